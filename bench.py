@@ -1,0 +1,233 @@
+"""Per-layer latency of value projection + multi-scale deformable attention on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 1000] [--warmup 50] [--workload rtdetr640-fp16-b1-q300] [--no-cpu]
+
+A step is one ma_deform_attn call (mode='auto', the default) on one batch of synthetic inputs already resident
+in HBM. Like the reference's bench (bench/bench.py:40-61) the calls are captured in a HIP graph, so Python launch
+overhead is excluded: W warm-up steps (one graph replay), then EXACTLY K steps (one replay of a K-call graph)
+bracketed by torch.cuda.synchronize() and timed with events on the replay stream.
+
+Prints diagnostics on stderr and ONE JSON line on stdout: value = µs per layer call (auto mode), with per-mode
+times, the roofline of the dominant kernel (algorithmic bytes per launch / its average launch duration, measured
+the same way on its own stream) and the CPU baseline (the oracle's torch restatement of the reference's PyTorch
+path, float32, on this host's cores, timed on a bounded sample).
+"""
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, 'tests'))
+
+import marearts_tinydeform_amd as td  # noqa: E402
+from marearts_tinydeform_amd import _native  # noqa: E402
+from inputs import DINO_LEVELS, LIMIT_LEVELS, RTDETR_LEVELS, workload  # noqa: E402
+
+HBM_PEAK = 8.0e12        # bytes/s, MI355X HBM3E
+MFMA_PEAK_16 = 2.5e15    # flop/s, dense fp16/bf16
+
+WORKLOADS = {
+    # name: (B, Q, H, D, C, levels, P, dtype, bias, loc_dist)
+    'rtdetr640-fp16-b1-q300': (1, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.float16, True, 'uniform'),
+    'rtdetr640-fp16-b1-q100': (1, 100, 8, 32, 256, RTDETR_LEVELS, 4, torch.float16, True, 'uniform'),
+    'rtdetr640-fp16-b1-q50': (1, 50, 8, 32, 256, RTDETR_LEVELS, 4, torch.float16, True, 'uniform'),
+    'rtdetr640-fp32-b1-q300': (1, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.float32, True, 'uniform'),
+    'rtdetr640-bf16-b8-q300': (8, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.bfloat16, True, 'uniform'),
+    'dino4l-fp16-b4-q900': (4, 900, 8, 32, 256, DINO_LEVELS, 4, torch.float16, True, 'outside10'),
+    'limit-bf16-c1024-b2-q50': (2, 50, 16, 64, 1024, LIMIT_LEVELS, 16, torch.bfloat16, False, 'uniform'),
+    'limit-bf16-c1024-b2-q300': (2, 300, 16, 64, 1024, LIMIT_LEVELS, 16, torch.bfloat16, False, 'uniform'),
+    'limit-bf16-c1024-b2-q900': (2, 900, 16, 64, 1024, LIMIT_LEVELS, 16, torch.bfloat16, False, 'uniform'),
+    'rtdetr640-fp16-b1-q300-clustered': (1, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.float16, True, 'clustered'),
+}
+
+DTYPE_NAMES = {torch.float16: 'f16', torch.bfloat16: 'bf16', torch.float32: 'f32', torch.float64: 'f64'}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def graph_time_us(fn, steps, warmup):
+    """µs per call: W warm-up calls (eager on a side stream, then one replay of a W-call graph), then one timed
+    replay of a graph of exactly `steps` calls, events recorded on the replay stream."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(stream)
+    warm = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(warm):
+        for _ in range(max(warmup, 1)):
+            fn()
+    timed = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(timed):
+        for _ in range(steps):
+            fn()
+    warm.replay()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(cur)
+    timed.replay()
+    end.record(cur)
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / steps
+    del warm, timed
+    return us
+
+
+def algorithmic(B, Q, H, D, C, N, L, P, s):
+    """Algorithmic bytes / flops per launch of each kernel (element size s)."""
+    HD = H * D
+    samples = B * Q * H * L * P
+    fused = samples * 4 * C * s + samples * 3 * s + HD * C * s + HD * s + B * Q * HD * s
+    sample = samples * 4 * D * s + samples * 3 * s + B * Q * HD * s
+    gemm_bytes = B * N * C * s + HD * C * s + B * N * HD * s + HD * s
+    gemm_flops = 2 * B * N * C * HD
+    return {'fused_bytes': fused, 'sample_bytes': sample, 'gemm_bytes': gemm_bytes, 'gemm_flops': gemm_flops}
+
+
+def cpu_baseline(spec, budget_s):
+    """The oracle's torch restatement of the reference's PyTorch path, float32, on this host's cores."""
+    from oracle import gridsample
+    B, Q, H, D, C, levels, P, _, bias, loc_dist = spec
+    args = workload(B, Q, H, D, C, levels, P, torch.float32, bias=bias, loc_dist=loc_dist)
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    with torch.inference_mode():
+        for _ in range(3):
+            gridsample.deform_attn(*args)
+        best, calls, t0 = float('inf'), 0, time.perf_counter()
+        while True:
+            t = time.perf_counter()
+            for _ in range(10):
+                gridsample.deform_attn(*args)
+            best = min(best, (time.perf_counter() - t) / 10)
+            calls += 10
+            if calls >= 70 and time.perf_counter() - t0 >= budget_s:
+                break
+            if time.perf_counter() - t0 >= 3 * budget_s:
+                break
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    cpu = line.split(':', 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {'value': round(best * 1e6, 1), 'unit': 'µs per layer call', 'cores': threads, 'kind': 'port',
+            'sample': f'float32 {B}x{Q} queries, same shapes and seed; best of {calls // 10} x 10 calls '
+                      f'({time.perf_counter() - t0:.1f} s) on {cpu}'}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=1000)
+    ap.add_argument('--warmup', type=int, default=50)
+    ap.add_argument('--workload', default='rtdetr640-fp16-b1-q300', choices=sorted(WORKLOADS))
+    ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
+    ap.add_argument('--cpu-seconds', type=float, default=10.0)
+    ap.add_argument('--modes-only', action='store_true', help='time the modes, skip per-kernel legs')
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
+        print('bench.py measures one GPU: this operator has no multi-GPU path to time (every (batch, query, head) '
+              'row is independent; sharding is data parallel with no exchange). Run with --gpus 1.', file=sys.stderr)
+        sys.exit(2)
+    if _native.lib is None:
+        raise SystemExit(f'HIP extension missing: {_native.load_error}')
+    assert torch.cuda.is_available(), 'no HIP device'
+
+    spec = WORKLOADS[args.workload]
+    B, Q, H, D, C, levels, P, dtype, bias, loc_dist = spec
+    cpu_args = workload(B, Q, H, D, C, levels, P, dtype, bias=bias, loc_dist=loc_dist)
+    dev = [None if t is None else t.cuda() for t in cpu_args]
+    N, L = dev[0].shape[1], len(levels)
+    s = dev[0].element_size()
+    alg = algorithmic(B, Q, H, D, C, N, L, P, s)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    log(f'{torch.cuda.get_device_name()} ({torch.cuda.get_device_properties(0).gcnArchName}), torch '
+        f'{torch.__version__}, workload {args.workload}: B={B} Q={Q} N={N} C={C} H={H} D={D} L={L} P={P}')
+
+    pick = td.choose_mode(dev[0], dev[1], dev[5])
+    times = {}
+    with torch.inference_mode():
+        for mode in ('fused', 'project'):
+            times[mode] = graph_time_us(lambda m=mode: td.ma_deform_attn(*dev, mode=m), args.steps, args.warmup)
+            log(f'  {mode:8s} {times[mode]:9.2f} µs/call')
+        times['auto'] = graph_time_us(lambda: td.ma_deform_attn(*dev), args.steps, args.warmup)
+        log(f'  auto     {times["auto"]:9.2f} µs/call (picks {pick})')
+        kern = {}
+        if not args.modes_only:
+            value = _native.value_proj(dev[0], dev[1], dev[2])
+            kern['value_proj'] = graph_time_us(lambda: _native.value_proj(dev[0], dev[1], dev[2]), args.steps,
+                                               args.warmup)
+            kern['sample'] = graph_time_us(lambda: _native.sample_forward(value, H, *dev[3:]), args.steps,
+                                           args.warmup)
+            kern['fused'] = times['fused']
+            log(f'  kernels: value_proj {kern["value_proj"]:.2f} µs, sample {kern["sample"]:.2f} µs')
+
+    if pick == 'fused':
+        dom, bytes_, t = 'fused', alg['fused_bytes'], times['fused']
+        roof = {'kernel': 'fused_vec_kernel', 'bound': 'hbm', 'achieved': bytes_ / (t * 1e-6) / 1e9, 'peak': 8000.0,
+                'unit': 'GB/s'}
+    else:
+        t_gemm, t_smp = kern.get('value_proj', times['project']), kern.get('sample', 0.0)
+        if t_gemm >= t_smp:
+            flops = alg['gemm_flops']
+            if dtype in (torch.float16, torch.bfloat16) and flops / alg['gemm_bytes'] > MFMA_PEAK_16 / HBM_PEAK:
+                roof = {'kernel': 'gemm_mfma_kernel', 'bound': 'mfma', 'achieved': flops / (t_gemm * 1e-6) / 1e12,
+                        'peak': 2500.0, 'unit': 'TFLOP/s'}
+            else:
+                roof = {'kernel': 'gemm_mfma_kernel', 'bound': 'hbm',
+                        'achieved': alg['gemm_bytes'] / (t_gemm * 1e-6) / 1e9, 'peak': 8000.0, 'unit': 'GB/s'}
+        else:
+            roof = {'kernel': 'sample_kernel', 'bound': 'hbm', 'achieved': alg['sample_bytes'] / (t_smp * 1e-6) / 1e9,
+                    'peak': 8000.0, 'unit': 'GB/s'}
+    roof['achieved'] = round(roof['achieved'], 1)
+    roof['frac'] = round(roof['achieved'] / roof['peak'], 4)
+    roof['traffic'] = None
+
+    path_bytes = alg['fused_bytes'] if pick == 'fused' else alg['gemm_bytes'] + alg['sample_bytes']
+    result = {
+        'metric': 'µs per layer call (value_proj+MSDeformAttn) RT-DETR-640 fp16 B=1 Q=300; HBM GB/s',
+        'value': round(times['auto'], 2),
+        'unit': 'µs',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': round(times['auto'] / 1e3, 5),
+        'higher_is_better': False,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': DTYPE_NAMES[dtype],
+        'data': f'synthetic (seeded CPU generator; locations {loc_dist})',
+        'config': {'workload': args.workload, 'B': B, 'Q': Q, 'N': N, 'C': C, 'H': H, 'D': D, 'L': L, 'P': P,
+                   'mode': 'auto'},
+        'modes_us': {k: round(v, 2) for k, v in times.items()},
+        'auto_pick': pick,
+        'kernels_us': {k: round(v, 2) for k, v in kern.items()},
+        'queries_per_s': round(B * Q / (times['auto'] * 1e-6)),
+        'hbm_gbps': round(path_bytes / (times['auto'] * 1e-6) / 1e9, 1),
+        'roofline': roof,
+    }
+    if not args.no_cpu:
+        log('CPU baseline ...')
+        result['cpu_baseline'] = cpu_baseline(spec, args.cpu_seconds)
+        log(f'  cpu {result["cpu_baseline"]["value"]} µs/call on {result["cpu_baseline"]["cores"]} threads')
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == '__main__':
+    main()

@@ -1,0 +1,92 @@
+/*
+ * tinydeform.h -- C ABI of the MI355X (gfx950) value-projection + multi-scale deformable attention library
+ * (libtinydeform.so, built from marearts_tinydeform_amd/csrc).
+ *
+ * Every entry point takes plain device pointers, element counts and a hipStream_t passed as void*.
+ * The library never allocates or frees device memory and never synchronises: callers own every buffer,
+ * kernels run asynchronously on the given stream, and each call may be captured in a HIP graph.
+ * The level geometry (spatial_shapes, level_start_index) is read on the device, never on the host.
+ *
+ * Tensor layouts (all row-major, contiguous, one element type `dtype` for every floating tensor):
+ *   memory              [B, N, C]
+ *   value_weight        [H*D, C]          (an nn.Linear weight)
+ *   value_bias          [H*D] or NULL
+ *   value               [B, N, H*D]       (memory @ value_weight^T + value_bias)
+ *   spatial_shapes      [L, 2] int64      (height, width) per level, tokens laid out level by level
+ *   level_start_index   [L] int64         first token of each level
+ *   sampling_locations  [B, Q, H, L, P, 2] (x, y) normalised to [0, 1]
+ *   attention_weights   [B, Q, H, L, P]
+ *   out                 [B, Q, H*D]
+ *
+ * Return value: TD_OK (0) or a negative TD_E* code; td_last_error() then describes the failure
+ * (thread-local, valid until the next call on the same thread).
+ */
+#ifndef TINYDEFORM_H
+#define TINYDEFORM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types: codes for the `dtype` argument */
+#define TD_F32 0
+#define TD_F16 1
+#define TD_BF16 2
+#define TD_F64 3
+
+/* error codes */
+#define TD_OK 0
+#define TD_E_ARG -1    /* invalid shape, limit or pointer (the same cases the reference rejects) */
+#define TD_E_DTYPE -2  /* unknown dtype code */
+#define TD_E_LAUNCH -3 /* the HIP runtime refused a kernel launch */
+
+/* limits shared with the reference operator (csrc/ma_deform_fused.cu:26-28) */
+#define TD_MAX_LEVEL_POINTS 64 /* L * P */
+#define TD_MAX_CHANNELS 8192   /* C, fused mode */
+
+/* Library version, e.g. 100 for 0.1.0. */
+int td_version(void);
+
+/* Message for the last non-zero return on this thread ("" if none). */
+const char* td_last_error(void);
+
+/*
+ * Fused mode: out[b,q,h*D+d] = W[h*D+d] . (sum_s w_s memory[b,t_s]) + bias[h*D+d] * sum_s w_s,
+ * s over the L*P*4 bilinear corners inside the map (align_corners=False, zero padding).
+ * Replaces the pybind entry `fused_forward(memory, weight, bias, spatial_shapes, level_start_index,
+ * sampling_locations, attention_weights)` of the reference (csrc/ma_deform_fused.cu:291-325).
+ * dtype: TD_F32, TD_F16, TD_BF16 (float32 accumulation) or TD_F64 (float64 accumulation).
+ * Limits: L*P <= 64, C <= 8192, N <= INT32_MAX, B*Q*H <= INT32_MAX.
+ */
+int td_fused_forward(int dtype, const void* memory, const void* value_weight, const void* value_bias,
+                     const int64_t* spatial_shapes, const int64_t* level_start_index,
+                     const void* sampling_locations, const void* attention_weights, void* out,
+                     int64_t B, int64_t Q, int64_t N, int64_t C, int64_t H, int64_t D, int64_t L, int64_t P,
+                     void* stream);
+
+/*
+ * Sampling on projected values (the second half of project mode):
+ * out[b,q,h*D+d] = sum_s w_s value[b,t_s,h*D+d].
+ * Replaces the pybind entry `sample_forward(value, heads, spatial_shapes, level_start_index,
+ * sampling_locations, attention_weights)` of the reference (csrc/ma_deform_fused.cu:327-350).
+ */
+int td_sample_forward(int dtype, const void* value, const int64_t* spatial_shapes,
+                      const int64_t* level_start_index, const void* sampling_locations,
+                      const void* attention_weights, void* out, int64_t B, int64_t Q, int64_t N, int64_t H,
+                      int64_t D, int64_t L, int64_t P, void* stream);
+
+/*
+ * Value projection (the first half of project mode): value[M, NO] = memory[M, K] @ weight[NO, K]^T + bias[NO],
+ * float32 accumulation, one rounding to dtype. M = B*N tokens, K = C, NO = H*D.
+ * Replaces the reference's F.linear(memory, value_weight, value_bias) call (marearts_tinydeform/__init__.py:77).
+ */
+int td_value_proj(int dtype, const void* memory, const void* weight, const void* bias, void* value, int64_t M,
+                  int64_t K, int64_t NO, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TINYDEFORM_H */

@@ -1,0 +1,110 @@
+"""marearts_tinydeform_amd: value projection + multi-scale deformable attention for DETR-style decoders on MI355X.
+
+Drop-in for marearts_tinydeform (same functions, arguments, results and errors; reference
+marearts_tinydeform/__init__.py:12-79). GPU tensors run hand-written HIP kernels for gfx950 through the C ABI of
+libtinydeform.so; CPU tensors run the PyTorch reference path. Inference only.
+"""
+
+import functools
+
+import torch
+
+from . import _native
+from .reference import ma_deform_attn_reference
+
+__all__ = ['ma_deform_attn', 'ma_deform_attn_reference', 'choose_mode', 'ma_deform_sample']
+__version__ = '0.1.0'
+
+MODES = ('auto', 'fused', 'project')
+
+# 'fused' gathers C-wide memory rows for every (query, head) sample corner: its cost grows with
+# batch * queries * heads * samples * C. 'project' runs the value GEMM over every token (batch * tokens * C * H * D
+# flops) and then gathers D-wide rows, plus a fixed cost of two launches. 'auto' picks 'fused' while
+#     queries * levels * points * 4 / (tokens * head_dim)  <  a + b / batch
+# (the reference's rule, marearts_tinydeform/__init__.py:21-30) with (a, b) per dtype fitted to MI355X (gfx950)
+# measurements of both modes over queries 50..900 and batch 1..8 at RT-DETR 640 shapes.
+FUSED_LIMIT = {torch.float32: (0.073, 0.032), torch.float16: (0.023, 0.031), torch.bfloat16: (0.023, 0.031)}
+
+# crossover tables by GPU architecture (gcnArchName without feature suffixes)
+ARCH_LIMITS = {'gfx950': FUSED_LIMIT}
+
+
+def _arch(device_index):
+    return torch.cuda.get_device_properties(device_index).gcnArchName.split(':')[0]
+
+
+@functools.lru_cache(maxsize=None)
+def _limits(device_index):
+    return ARCH_LIMITS.get(_arch(device_index), FUSED_LIMIT)
+
+
+def choose_mode(memory, value_weight, sampling_locations):
+    """The mode 'auto' runs: 'fused' for few queries per image, 'project' (project every token first) for many."""
+    B, N, _ = memory.shape
+    _, Q, H, L, P, _ = sampling_locations.shape
+    D = value_weight.shape[0] // H
+    limits = _limits(memory.get_device()) if memory.is_cuda else FUSED_LIMIT
+    a, b = limits.get(memory.dtype, limits[torch.float16])
+    return 'fused' if Q * L * P * 4 / (max(N, 1) * max(D, 1)) < a + b / max(B, 1) else 'project'
+
+
+def _reject_grad(*tensors):
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        raise RuntimeError('ma_deform_attn is inference only: run it under torch.no_grad() / '
+                           'torch.inference_mode(), or use ma_deform_attn_reference for training')
+
+
+def _on_device(t, fn, *args):
+    if t.device.index is None or t.device.index == torch.cuda.current_device():
+        return fn(*args)
+    with torch.cuda.device(t.device):
+        return fn(*args)
+
+
+def ma_deform_attn(memory, value_weight, value_bias, spatial_shapes, level_start_index,
+                   sampling_locations, attention_weights, mode='auto'):
+    """value = memory @ value_weight.T + value_bias, then multi-scale deformable attention; [B, Q, H * D].
+
+    Same arguments, shapes and result as ma_deform_attn_reference (grid_sample, bilinear, zero padding,
+    align_corners=False). GPU tensors (float32, float16, bfloat16, float64; float32 accumulation for the
+    16/32-bit types):
+      mode='fused'    gather the sampled memory rows first, then project per (query, head) on MFMA
+      mode='project'  project all tokens (the library's MFMA GEMM), then sample
+      mode='auto'     choose_mode() picks one by size (default)
+    CPU tensors run the reference. Inference only: inputs that require grad are rejected.
+    """
+    if mode not in MODES:
+        raise ValueError(f'mode must be one of {MODES}, got {mode!r}')
+    if not memory.is_cuda:
+        return ma_deform_attn_reference(memory, value_weight, value_bias, spatial_shapes, level_start_index,
+                                        sampling_locations, attention_weights)
+    _native._require()
+    _reject_grad(memory, value_weight, value_bias, sampling_locations, attention_weights)
+    if mode == 'auto':
+        mode = choose_mode(memory, value_weight, sampling_locations)
+    if mode == 'fused':
+        return _on_device(memory, _native.fused_forward, memory, value_weight, value_bias, spatial_shapes,
+                          level_start_index, sampling_locations, attention_weights)
+    return _on_device(memory, _project, memory, value_weight, value_bias, spatial_shapes, level_start_index,
+                      sampling_locations, attention_weights)
+
+
+def _project(memory, value_weight, value_bias, spatial_shapes, level_start_index, sampling_locations,
+             attention_weights):
+    H = sampling_locations.shape[2] if sampling_locations.dim() == 6 else 0
+    _native.check_geometry(memory, spatial_shapes, level_start_index, sampling_locations, attention_weights)
+    value = _native.value_proj(memory, value_weight, value_bias)
+    return _native.sample_forward(value, H, spatial_shapes, level_start_index, sampling_locations, attention_weights)
+
+
+def ma_deform_sample(value, spatial_shapes, level_start_index, sampling_locations, attention_weights):
+    """Multi-scale deformable attention on already projected values [B, N, H * D] -> [B, Q, H * D].
+
+    The sampling half of mode='project' on its own (for decoders whose value projection is done elsewhere).
+    GPU tensors only.
+    """
+    _native._require()
+    _reject_grad(value, sampling_locations, attention_weights)
+    H = sampling_locations.shape[2] if sampling_locations.dim() == 6 else 0
+    return _on_device(value, _native.sample_forward, value, H, spatial_shapes, level_start_index,
+                      sampling_locations, attention_weights)

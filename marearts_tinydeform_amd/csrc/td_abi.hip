@@ -1,0 +1,138 @@
+// C ABI of libtinydeform.so (declared in include/tinydeform.h): argument checks, then the kernel launchers.
+// The checks restate the reference's size and limit checks (csrc/ma_deform_fused.cu:236-266, 298-308, 333);
+// dtype and device agreement between tensors is the caller's job (the Python layer checks it).
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/tinydeform.h"
+#include "td_internal.h"
+
+namespace td {
+
+namespace {
+thread_local std::string g_last_error;
+
+__global__ void zero_kernel(unsigned* p, int64_t words) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < words; i += stride) p[i] = 0u;
+}
+__global__ void zero_bytes_kernel(unsigned char* p, int64_t bytes) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < bytes) p[i] = 0;
+}
+}  // namespace
+
+int set_error(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int launch_zero(void* out, int64_t bytes, hipStream_t stream) {
+    if (bytes <= 0) return 0;
+    if (reinterpret_cast<uintptr_t>(out) % 4 == 0 && bytes % 4 == 0) {
+        const int64_t words = bytes / 4;
+        int64_t blocks = (words + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        hipLaunchKernelGGL(zero_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                           static_cast<unsigned*>(out), words);
+    } else {
+        hipLaunchKernelGGL(zero_bytes_kernel, dim3(static_cast<unsigned>((bytes + 255) / 256)), dim3(256), 0, stream,
+                           static_cast<unsigned char*>(out), bytes);
+    }
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : set_error(TD_E_LAUNCH, "zero fill launch failed: %s", hipGetErrorString(e));
+}
+
+namespace {
+
+constexpr int64_t kInt32Max = 2147483647;
+
+bool dtype_ok(int dtype) { return dtype == TD_F32 || dtype == TD_F16 || dtype == TD_BF16 || dtype == TD_F64; }
+
+// Sizes and limits common to fused and sample mode (reference csrc/ma_deform_fused.cu:236-266).
+int check_geometry(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D, int64_t L, int64_t P,
+                   const int64_t* shapes, const int64_t* starts, const void* loc, const void* attn, const void* out) {
+    g_last_error.clear();
+    if (!dtype_ok(dtype)) return set_error(TD_E_DTYPE, "unknown dtype code %d", dtype);
+    if (B < 0 || Q < 0 || N < 0 || H < 0 || D < 0 || L < 0 || P < 0)
+        return set_error(TD_E_ARG, "sizes must be non-negative");
+    if (N > kInt32Max) return set_error(TD_E_ARG, "too many memory tokens");
+    if (H <= 0) return set_error(TD_E_ARG, "need at least one head");
+    if (L * P > kMaxLevelPoints) return set_error(TD_E_ARG, "levels x points must be <= %d", kMaxLevelPoints);
+    if (B * Q * H > kInt32Max) return set_error(TD_E_ARG, "too many (batch, query, head) rows");
+    if (H * D > kInt32Max) return set_error(TD_E_ARG, "too many output channels");
+    if (B * Q * H * D > 0) {
+        if (out == nullptr || loc == nullptr || attn == nullptr || (L > 0 && (shapes == nullptr || starts == nullptr)))
+            return set_error(TD_E_ARG, "null pointer argument");
+    }
+    return TD_OK;
+}
+
+}  // namespace
+}  // namespace td
+
+using namespace td;
+
+extern "C" int td_version(void) { return 100; }
+
+extern "C" const char* td_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" int td_fused_forward(int dtype, const void* memory, const void* value_weight, const void* value_bias,
+                                const int64_t* spatial_shapes, const int64_t* level_start_index,
+                                const void* sampling_locations, const void* attention_weights, void* out, int64_t B,
+                                int64_t Q, int64_t N, int64_t C, int64_t H, int64_t D, int64_t L, int64_t P,
+                                void* stream) {
+    int rc = check_geometry(dtype, B, Q, N, H, D, L, P, spatial_shapes, level_start_index, sampling_locations,
+                            attention_weights, out);
+    if (rc != TD_OK) return rc;
+    if (C < 0 || C > kMaxChannels) return set_error(TD_E_ARG, "channels must be <= %d", kMaxChannels);
+    if (B * N * C > 0 && memory == nullptr) return set_error(TD_E_ARG, "null pointer argument");
+    if (H * D * C > 0 && value_weight == nullptr) return set_error(TD_E_ARG, "null pointer argument");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (B * Q * H * D == 0) return TD_OK;
+    const int64_t bytes = B * Q * H * D * elem_size(dtype);
+    // no tokens: every corner is outside, so the output is exactly zero (the bias share included)
+    if (N == 0 || L * P == 0) return launch_zero(out, bytes, s);
+    const Geom g{spatial_shapes, level_start_index, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N),
+                 static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), static_cast<int>(P)};
+    FusedTune tune;
+    return launch_fused(dtype, memory, value_weight, value_bias, g, static_cast<int>(C), sampling_locations,
+                        attention_weights, out, s, tune);
+}
+
+extern "C" int td_sample_forward(int dtype, const void* value, const int64_t* spatial_shapes,
+                                 const int64_t* level_start_index, const void* sampling_locations,
+                                 const void* attention_weights, void* out, int64_t B, int64_t Q, int64_t N,
+                                 int64_t H, int64_t D, int64_t L, int64_t P, void* stream) {
+    int rc = check_geometry(dtype, B, Q, N, H, D, L, P, spatial_shapes, level_start_index, sampling_locations,
+                            attention_weights, out);
+    if (rc != TD_OK) return rc;
+    if (B * N * H * D > 0 && value == nullptr) return set_error(TD_E_ARG, "null pointer argument");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (B * Q * H * D == 0) return TD_OK;
+    const int64_t bytes = B * Q * H * D * elem_size(dtype);
+    if (N == 0 || L * P == 0) return launch_zero(out, bytes, s);
+    const Geom g{spatial_shapes, level_start_index, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N),
+                 static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), static_cast<int>(P)};
+    SampleTune tune;
+    return launch_sample(dtype, value, g, sampling_locations, attention_weights, out, s, tune);
+}
+
+extern "C" int td_value_proj(int dtype, const void* memory, const void* weight, const void* bias, void* value,
+                             int64_t M, int64_t K, int64_t NO, void* stream) {
+    g_last_error.clear();
+    if (!dtype_ok(dtype)) return set_error(TD_E_DTYPE, "unknown dtype code %d", dtype);
+    if (M < 0 || K < 0 || NO < 0) return set_error(TD_E_ARG, "sizes must be non-negative");
+    if (M > kInt32Max || K > kInt32Max || NO > kInt32Max) return set_error(TD_E_ARG, "GEMM size exceeds int32");
+    if (M * NO == 0) return TD_OK;
+    if (value == nullptr || (K > 0 && (memory == nullptr || weight == nullptr)))
+        return set_error(TD_E_ARG, "null pointer argument");
+    return launch_value_proj(dtype, memory, weight, bias, value, M, K, NO, static_cast<hipStream_t>(stream), 0);
+}

@@ -1,0 +1,182 @@
+// Shared device code for the gfx950 kernels: element types, vector loads, the bilinear corner rule and
+// wavefront (64-lane) cross-lane helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace td {
+
+constexpr int kWave = 64;
+constexpr int kMaxLevelPoints = 64;  // L * P per head (reference csrc/ma_deform_fused.cu:27)
+constexpr int kMaxChannels = 8192;   // C in fused mode (reference csrc/ma_deform_fused.cu:28)
+
+typedef _Float16 f16;
+typedef __bf16 bf16;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// Accumulation type: float for float/half/bfloat16, double for double.
+template <typename T>
+struct AccOf {
+    using type = float;
+};
+template <>
+struct AccOf<double> {
+    using type = double;
+};
+
+template <typename A, typename T>
+__device__ __forceinline__ A cvt(T v) {
+    return static_cast<A>(v);
+}
+
+// Level geometry and sizes shared by all kernels. shapes/starts are device pointers (int64), read on the
+// device so that a call never reads level sizes on the host (safe under stream capture).
+struct Geom {
+    const int64_t* shapes;  // [L, 2] (height, width)
+    const int64_t* starts;  // [L] first token of each level
+    int B, Q, N, H, D, L, P;
+};
+
+// One gathered corner: token index (-1 when the corner lies outside its level map or outside [0, N)) and
+// its weight (attention weight x bilinear weight; 0 when outside).
+template <typename A>
+struct Corner {
+    int tok;
+    A w;
+};
+
+// The four bilinear corners of sample j (j = l * P + p) of row `row` = (b * Q + q) * H + h.
+// Restates the reference's corner rule (csrc/ma_deform_fused.cu:81-100): pixel coordinate
+// x = loc_x * W_l - 0.5 (align_corners=False), clamped to [-2, W_l + 1] before the integer conversion so that
+// far-away, infinite or NaN locations sample nothing; corner k has dx = k & 1, dy = k >> 1; a corner counts only
+// if it lies inside the level map and its token t = start_l + y * W_l + x lies in [0, N).
+template <typename T, typename A>
+__device__ __forceinline__ void corner4(const T* __restrict__ loc, const T* __restrict__ attn, const Geom& g,
+                                        int64_t row, int j, Corner<A>* out) {
+    const int LP = g.L * g.P;
+    const int l = j / g.P;
+    const int hl = static_cast<int>(g.shapes[2 * l]);
+    const int wl = static_cast<int>(g.shapes[2 * l + 1]);
+    const int64_t st = g.starts[l];
+    const int64_t idx = row * LP + j;
+    const A w = cvt<A>(attn[idx]);
+    A x = cvt<A>(loc[2 * idx]) * static_cast<A>(wl) - static_cast<A>(0.5);
+    A y = cvt<A>(loc[2 * idx + 1]) * static_cast<A>(hl) - static_cast<A>(0.5);
+    // fmax returns the non-NaN operand, so a NaN coordinate becomes -2 (outside the map)
+    x = fmin(fmax(x, static_cast<A>(-2)), static_cast<A>(wl) + static_cast<A>(1));
+    y = fmin(fmax(y, static_cast<A>(-2)), static_cast<A>(hl) + static_cast<A>(1));
+    const A xf = floor(x), yf = floor(y);
+    const int x0 = static_cast<int>(xf), y0 = static_cast<int>(yf);
+    const A fx = x - xf, fy = y - yf;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int dx = k & 1, dy = k >> 1, xi = x0 + dx, yi = y0 + dy;
+        const int64_t t = st + static_cast<int64_t>(yi) * wl + xi;
+        const bool in = xi >= 0 && xi < wl && yi >= 0 && yi < hl && t >= 0 && t < g.N;
+        out[k].tok = in ? static_cast<int>(t) : -1;
+        out[k].w = in ? w * (dx ? fx : static_cast<A>(1) - fx) * (dy ? fy : static_cast<A>(1) - fy)
+                      : static_cast<A>(0);
+    }
+}
+
+// ---- vector loads: Bytes-wide raw loads unpacked to float ------------------------------------------------
+
+template <int Bytes>
+struct Raw;
+template <>
+struct Raw<16> {
+    using type = u32x4;
+};
+template <>
+struct Raw<8> {
+    using type = u32x2;
+};
+template <>
+struct Raw<4> {
+    using type = unsigned;
+};
+template <>
+struct Raw<2> {
+    using type = unsigned short;
+};
+
+// V elements of T loaded with one V * sizeof(T)-byte load (V * sizeof(T) in {2, 4, 8, 16}).
+template <typename T, int V>
+struct VecIO {
+    static constexpr int kBytes = V * static_cast<int>(sizeof(T));
+    using raw_t = typename Raw<kBytes>::type;
+    __device__ __forceinline__ static raw_t load(const T* p) { return *reinterpret_cast<const raw_t*>(p); }
+    __device__ __forceinline__ static raw_t zero() { return raw_t{}; }
+    __device__ __forceinline__ static void unpack(const raw_t& r, float* o) {
+        const T* e = reinterpret_cast<const T*>(&r);
+#pragma unroll
+        for (int i = 0; i < V; ++i) o[i] = static_cast<float>(e[i]);
+    }
+    __device__ __forceinline__ static void store(T* p, const float* v) {
+        raw_t r;
+        T* e = reinterpret_cast<T*>(&r);
+#pragma unroll
+        for (int i = 0; i < V; ++i) e[i] = static_cast<T>(v[i]);
+        *reinterpret_cast<raw_t*>(p) = r;
+    }
+};
+
+// bfloat16 -> float is a 16-bit shift; do it on the packed dwords.
+template <int V>
+struct VecIO<bf16, V> {
+    static constexpr int kBytes = V * 2;
+    using raw_t = typename Raw<kBytes>::type;
+    __device__ __forceinline__ static raw_t load(const bf16* p) { return *reinterpret_cast<const raw_t*>(p); }
+    __device__ __forceinline__ static raw_t zero() { return raw_t{}; }
+    __device__ __forceinline__ static void unpack(const raw_t& r, float* o) {
+        if constexpr (V == 1) {
+            o[0] = __builtin_bit_cast(float, static_cast<unsigned>(r) << 16);
+        } else {
+            const unsigned* u = reinterpret_cast<const unsigned*>(&r);
+#pragma unroll
+            for (int i = 0; i < V / 2; ++i) {
+                o[2 * i] = __builtin_bit_cast(float, u[i] << 16);
+                o[2 * i + 1] = __builtin_bit_cast(float, u[i] & 0xffff0000u);
+            }
+        }
+    }
+    __device__ __forceinline__ static void store(bf16* p, const float* v) {
+        raw_t r;
+        bf16* e = reinterpret_cast<bf16*>(&r);
+#pragma unroll
+        for (int i = 0; i < V; ++i) e[i] = static_cast<bf16>(v[i]);
+        *reinterpret_cast<raw_t*>(p) = r;
+    }
+};
+
+// ---- cross-lane ----------------------------------------------------------------------------------------
+
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
+
+// Value of `v` in lane (lane ^ mask) of the same wavefront.
+__device__ __forceinline__ float xor_lane(float v, int mask) {
+    const int src = (lane_id() ^ mask) << 2;
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, v)));
+}
+__device__ __forceinline__ double xor_lane(double v, int mask) {
+    const int src = (lane_id() ^ mask) << 2;
+    const long long u = __builtin_bit_cast(long long, v);
+    const int lo = __builtin_amdgcn_ds_bpermute(src, static_cast<int>(u));
+    const int hi = __builtin_amdgcn_ds_bpermute(src, static_cast<int>(u >> 32));
+    return __builtin_bit_cast(double, (static_cast<long long>(hi) << 32) | static_cast<unsigned>(lo));
+}
+
+// Sum over the 64 lanes of a wavefront (every lane receives the total).
+template <typename A>
+__device__ __forceinline__ A wave_sum(A v) {
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) v += xor_lane(v, m);
+    return v;
+}
+
+}  // namespace td

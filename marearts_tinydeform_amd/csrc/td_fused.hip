@@ -1,0 +1,406 @@
+// Fused mode: gather the sampled memory rows, then project one C-vector per (batch, query, head).
+//
+// For one row (b, q, h), with s over the L*P*4 bilinear corners inside the map,
+//   g      = sum_s w_s * memory[b, t_s, :]                  (C values, float32)
+//   out[d] = W[h*D+d, :] . g + bias[h*D+d] * sum_s w_s      (d < D)
+// which equals projecting every token first and sampling afterwards, because sampling and the weighted sum
+// are linear (reference csrc/ma_deform_fused.cu:6-14, README.md:16-22).
+//
+// fused_vec_kernel (float / half / bfloat16, C a multiple of 16 bytes, 16-byte aligned memory and weight):
+//   workgroup = (b, tile of QT queries, h); heads vary fastest across workgroups.
+//   phase 1  corner table of the QT rows into LDS.
+//   phase 2  gather: CV*SG lanes per row, lane = (corner group sg, 16-byte channel chunk ch); each lane sums
+//            every SG-th corner of its row with float32 FMAs, the SG partial sums meet by cross-lane adds,
+//            and g lands in LDS as float32.
+//   phase 3  projection on MFMA: out[16 x D] = g[16 x C] . W_h^T, split over (N tile, K slice) jobs, one per
+//            wavefront. 16-bit types use v_mfma_f32_16x16x32_{f16,bf16} with g split as hi + lo (two
+//            16-bit values whose sum carries 22 / 16 significant bits), so rounding g to the MFMA input type
+//            costs no accuracy; float32 uses v_mfma_f32_16x16x4_f32.
+// fused_generic_kernel: any C, any alignment, float64 (float64 accumulation); scalar loads, VALU projection.
+#include <stdio.h>
+
+#include "td_internal.h"
+
+namespace td {
+namespace {
+
+struct FusedParams {
+    const void* mem;
+    const void* w;
+    const void* bias;
+    const void* loc;
+    const void* attn;
+    void* out;
+    Geom g;
+    int C, QT, SG, KS, qtiles;
+};
+
+template <typename T>
+struct MfmaOp;
+template <>
+struct MfmaOp<f16> {
+    typedef f16x8 frag;
+    __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+template <>
+struct MfmaOp<bf16> {
+    typedef bf16x8 frag;
+    __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+// Workgroup index -> (b, query tile, h), heads fastest.
+struct BlockRow {
+    int b, qt, h;
+};
+__device__ __forceinline__ BlockRow decode_block(int bid, int H, int qtiles) {
+    BlockRow r;
+    r.h = bid % H;
+    const int rest = bid / H;
+    r.qt = rest % qtiles;
+    r.b = rest / qtiles;
+    return r;
+}
+
+template <typename T, int WAVES>
+__global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) {
+    constexpr int NTH = WAVES * kWave;
+    constexpr int V = 16 / static_cast<int>(sizeof(T));
+    using IO = VecIO<T, V>;
+    const Geom& g = p.g;
+    const int C = p.C, QT = p.QT, SG = p.SG, CV = C / V;
+    const int LP = g.L * g.P, S = 4 * LP, D = g.D;
+    const int GP = C + 4;  // float pitch of a g row in LDS: 16-byte aligned, rows offset by 4 banks
+    const int NTILE = (D + 15) >> 4, PW = NTILE * 16;
+
+    extern __shared__ __align__(16) unsigned char smem[];
+    Corner<float>* cw = reinterpret_cast<Corner<float>*>(smem);  // [QT][S]
+    float* gs = reinterpret_cast<float*>(cw + QT * S);           // [QT][GP]
+    float* wsum = gs + QT * GP;                                   // [16]
+    float* part = wsum + 16;                                      // [KS][16][PW]
+
+    const T* __restrict__ mem = static_cast<const T*>(p.mem);
+    const T* __restrict__ w = static_cast<const T*>(p.w);
+    const T* __restrict__ bias = static_cast<const T*>(p.bias);
+    const T* __restrict__ loc = static_cast<const T*>(p.loc);
+    const T* __restrict__ attn = static_cast<const T*>(p.attn);
+    T* __restrict__ out = static_cast<T*>(p.out);
+
+    const int tid = threadIdx.x;
+    const BlockRow br = decode_block(blockIdx.x, g.H, p.qtiles);
+    const int q0 = br.qt * QT;
+
+    // phase 1: corner table
+    for (int i = tid; i < QT * LP; i += NTH) {
+        const int r = i / LP, j = i - r * LP, q = q0 + r;
+        Corner<float>* c4 = cw + r * S + 4 * j;
+        if (q < g.Q) {
+            corner4<T, float>(loc, attn, g, (static_cast<int64_t>(br.b) * g.Q + q) * g.H + br.h, j, c4);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) c4[k] = Corner<float>{-1, 0.f};
+        }
+    }
+    __syncthreads();
+
+    // phase 2: gather C-wide rows, float32 accumulation
+    const T* mb = mem + static_cast<size_t>(br.b) * g.N * C;
+    const int GS = CV * SG;
+    for (int it = tid; it < QT * GS; it += NTH) {
+        const int r = it / GS, rem = it - r * GS, sg = rem / CV, ch = rem - sg * CV;
+        const Corner<float>* cr = cw + r * S;
+        const T* col = mb + ch * V;
+        float acc[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] = 0.f;
+        float ws = 0.f;
+#pragma unroll 8
+        for (int s = sg; s < S; s += SG) {
+            const Corner<float> c = cr[s];
+            ws += c.w;
+            typename IO::raw_t raw = IO::load(col + static_cast<size_t>(c.tok < 0 ? 0 : c.tok) * C);
+            if (c.tok < 0) raw = IO::zero();  // outside the map: contributes exactly 0 (zero padding)
+            float v[V];
+            IO::unpack(raw, v);
+#pragma unroll
+            for (int i = 0; i < V; ++i) acc[i] = fmaf(c.w, v[i], acc[i]);
+        }
+        for (int m = CV; m < GS; m <<= 1) {
+#pragma unroll
+            for (int i = 0; i < V; ++i) acc[i] += xor_lane(acc[i], m);
+            ws += xor_lane(ws, m);
+        }
+        if (sg == 0) {
+            float* dst = gs + r * GP + ch * V;
+#pragma unroll
+            for (int i = 0; i < V; i += 4)
+                *reinterpret_cast<f32x4*>(dst + i) = f32x4{acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
+            if (ch == 0) wsum[r] = ws;
+        }
+    }
+    __syncthreads();
+
+    // phase 3: out[16 x D] = g[16 x C] . W_h^T on MFMA; job = (N tile, K slice)
+    const int wave = tid / kWave, lane = tid & (kWave - 1);
+    const int n16 = lane & 15, kg = lane >> 4;
+    const bool av = n16 < QT;
+    const float* ga = gs + (av ? n16 : 0) * GP;
+    if constexpr (sizeof(T) == 2) {
+        using M = MfmaOp<T>;
+        using frag = typename M::frag;
+        const int nk = (C + 31) >> 5;
+        for (int job = wave; job < NTILE * p.KS; job += WAVES) {
+            const int nt = job % NTILE, ks = job / NTILE;
+            const int kb = ks * nk / p.KS, ke = (ks + 1) * nk / p.KS;
+            const int d = nt * 16 + n16;
+            const bool dv = d < D;
+            const T* wr = w + (static_cast<size_t>(br.h) * D + (dv ? d : 0)) * C;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+            for (int kk = kb; kk < ke; ++kk) {
+                const int k = kk * 32 + kg * 8;
+                const bool kv = k < C;
+                u32x4 braw = {0u, 0u, 0u, 0u};
+                if (dv && kv) braw = *reinterpret_cast<const u32x4*>(wr + k);
+                f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
+                if (av && kv) {
+                    a0 = *reinterpret_cast<const f32x4*>(ga + k);
+                    a1 = *reinterpret_cast<const f32x4*>(ga + k + 4);
+                }
+                frag hi, lo;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const T x0 = static_cast<T>(a0[i]), x1 = static_cast<T>(a1[i]);
+                    hi[i] = x0;
+                    hi[4 + i] = x1;
+                    lo[i] = static_cast<T>(a0[i] - static_cast<float>(x0));
+                    lo[4 + i] = static_cast<T>(a1[i] - static_cast<float>(x1));
+                }
+                const frag bf = __builtin_bit_cast(frag, braw);
+                acc = M::mma(hi, bf, acc);
+                acc = M::mma(lo, bf, acc);
+            }
+            float* pp = part + ks * 16 * PW;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pp[(4 * kg + i) * PW + nt * 16 + n16] = acc[i];
+        }
+    } else {
+        const int nk = (C + 15) >> 4;
+        for (int job = wave; job < NTILE * p.KS; job += WAVES) {
+            const int nt = job % NTILE, ks = job / NTILE;
+            const int kb = ks * nk / p.KS, ke = (ks + 1) * nk / p.KS;
+            const int d = nt * 16 + n16;
+            const bool dv = d < D;
+            const T* wr = w + (static_cast<size_t>(br.h) * D + (dv ? d : 0)) * C;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+            for (int kk = kb; kk < ke; ++kk) {
+                const int k = kk * 16 + kg * 4;
+                const bool kv = k < C;
+                f32x4 bq = {0.f, 0.f, 0.f, 0.f}, aq = bq;
+                if (dv && kv) bq = *reinterpret_cast<const f32x4*>(wr + k);
+                if (av && kv) aq = *reinterpret_cast<const f32x4*>(ga + k);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[j], bq[j], acc, 0, 0, 0);
+            }
+            float* pp = part + ks * 16 * PW;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pp[(4 * kg + i) * PW + nt * 16 + n16] = acc[i];
+        }
+    }
+    __syncthreads();
+
+    // epilogue: sum the K slices, add bias * sum of in-map weights, round once
+    for (int o = tid; o < QT * D; o += NTH) {
+        const int r = o / D, d = o - r * D, q = q0 + r;
+        if (q >= g.Q) continue;
+        float v = part[r * PW + d];
+        for (int ks = 1; ks < p.KS; ++ks) v += part[(ks * 16 + r) * PW + d];
+        if (bias != nullptr) v = fmaf(cvt<float>(bias[static_cast<size_t>(br.h) * D + d]), wsum[r], v);
+        out[((static_cast<size_t>(br.b) * g.Q + q) * g.H + br.h) * D + d] = static_cast<T>(v);
+    }
+}
+
+template <typename T, int WAVES>
+__global__ __launch_bounds__(WAVES* kWave) void fused_generic_kernel(FusedParams p) {
+    using A = typename AccOf<T>::type;
+    constexpr int NTH = WAVES * kWave;
+    const Geom& g = p.g;
+    const int C = p.C, QT = p.QT;
+    const int LP = g.L * g.P, S = 4 * LP, D = g.D;
+
+    extern __shared__ __align__(16) unsigned char smem[];
+    Corner<A>* cw = reinterpret_cast<Corner<A>*>(smem);  // [QT][S]
+    A* gs = reinterpret_cast<A*>(cw + QT * S);           // [QT][C]
+    A* wsum = gs + QT * C;                                // [QT]
+
+    const T* __restrict__ mem = static_cast<const T*>(p.mem);
+    const T* __restrict__ w = static_cast<const T*>(p.w);
+    const T* __restrict__ bias = static_cast<const T*>(p.bias);
+    const T* __restrict__ loc = static_cast<const T*>(p.loc);
+    const T* __restrict__ attn = static_cast<const T*>(p.attn);
+    T* __restrict__ out = static_cast<T*>(p.out);
+
+    const int tid = threadIdx.x;
+    const BlockRow br = decode_block(blockIdx.x, g.H, p.qtiles);
+    const int q0 = br.qt * QT;
+
+    for (int i = tid; i < QT * LP; i += NTH) {
+        const int r = i / LP, j = i - r * LP, q = q0 + r;
+        Corner<A>* c4 = cw + r * S + 4 * j;
+        if (q < g.Q) {
+            corner4<T, A>(loc, attn, g, (static_cast<int64_t>(br.b) * g.Q + q) * g.H + br.h, j, c4);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) c4[k] = Corner<A>{-1, static_cast<A>(0)};
+        }
+    }
+    __syncthreads();
+
+    for (int r = tid; r < QT; r += NTH) {
+        A s = 0;
+        for (int k = 0; k < S; ++k) s += cw[r * S + k].w;
+        wsum[r] = s;
+    }
+    const T* mb = mem + static_cast<size_t>(br.b) * g.N * C;
+    for (int it = tid; it < QT * C; it += NTH) {
+        const int r = it / C, c = it - r * C;
+        const Corner<A>* cr = cw + r * S;
+        A acc = 0;
+#pragma unroll 4
+        for (int s = 0; s < S; ++s) {
+            const Corner<A> cc = cr[s];
+            const T v = mb[static_cast<size_t>(cc.tok < 0 ? 0 : cc.tok) * C + c];
+            acc = fma(cc.w, cc.tok < 0 ? static_cast<A>(0) : cvt<A>(v), acc);
+        }
+        gs[r * C + c] = acc;
+    }
+    __syncthreads();
+
+    const int wave = tid / kWave, lane = tid & (kWave - 1);
+    for (int o = wave; o < QT * D; o += WAVES) {  // o is uniform across the wavefront
+        const int r = o / D, d = o - r * D, q = q0 + r;
+        if (q >= g.Q) continue;
+        const T* wr = w + (static_cast<size_t>(br.h) * D + d) * C;
+        A s = 0;
+        for (int c = lane; c < C; c += kWave) s = fma(cvt<A>(wr[c]), gs[r * C + c], s);
+        s = wave_sum(s);
+        if (lane == 0) {
+            if (bias != nullptr) s = fma(cvt<A>(bias[static_cast<size_t>(br.h) * D + d]), wsum[r], s);
+            out[((static_cast<size_t>(br.b) * g.Q + q) * g.H + br.h) * D + d] = static_cast<T>(s);
+        }
+    }
+}
+
+constexpr size_t kLdsBudget = 65536;
+
+inline bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+
+template <typename T, int WAVES>
+int go_vec(const FusedParams& p, size_t lds, hipStream_t stream) {
+    const int64_t blocks = static_cast<int64_t>(p.g.B) * p.g.H * p.qtiles;
+    hipLaunchKernelGGL((fused_vec_kernel<T, WAVES>), dim3(static_cast<unsigned>(blocks)), dim3(WAVES * kWave), lds,
+                       stream, p);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : set_error(-3, "fused_vec launch failed: %s", hipGetErrorString(e));
+}
+
+template <typename T, int WAVES>
+int go_generic(const FusedParams& p, size_t lds, hipStream_t stream) {
+    const int64_t blocks = static_cast<int64_t>(p.g.B) * p.g.H * p.qtiles;
+    hipLaunchKernelGGL((fused_generic_kernel<T, WAVES>), dim3(static_cast<unsigned>(blocks)), dim3(WAVES * kWave),
+                       lds, stream, p);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : set_error(-3, "fused_generic launch failed: %s", hipGetErrorString(e));
+}
+
+template <typename T>
+int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune) {
+    using A = typename AccOf<T>::type;
+    const Geom& g = p.g;
+    const int LP = g.L * g.P, S = 4 * LP, C = p.C, D = g.D;
+    const int qmax = g.Q < 16 ? g.Q : 16;
+
+    if constexpr (!std::is_same<T, double>::value) {
+        constexpr int V = 16 / static_cast<int>(sizeof(T));
+        const bool aligned = reinterpret_cast<uintptr_t>(p.mem) % 16 == 0 &&
+                             reinterpret_cast<uintptr_t>(p.w) % 16 == 0 && C % V == 0 && C > 0;
+        if (aligned && !tune.generic) {
+            const int CV = C / V;
+            const int waves = tune.waves ? tune.waves : 4;
+            const int nth = waves * kWave;
+            int sg = tune.sg;
+            if (sg <= 0) {
+                sg = 1;
+                if (is_pow2(CV) && CV < kWave) {
+                    sg = kWave / CV;
+                    while (sg > 1 && S / sg < 4) sg >>= 1;
+                }
+            }
+            if (sg > 1 && !(is_pow2(CV) && is_pow2(sg) && CV * sg <= kWave)) sg = 1;
+            const int GS = CV * sg;
+            const int rows_per_pass = nth / GS > 0 ? nth / GS : 1;
+            int qt = tune.qt > 0 ? tune.qt : 2 * rows_per_pass;
+            if (qt > qmax) qt = qmax;
+            if (qt < 1) qt = 1;
+            const int NTILE = (D + 15) / 16;
+            const int nk = sizeof(T) == 2 ? (C + 31) / 32 : (C + 15) / 16;
+            int ks = waves / NTILE;
+            if (ks < 1) ks = 1;
+            if (ks > nk) ks = nk;
+            auto lds = [&](int q) {
+                return static_cast<size_t>(q) * S * sizeof(Corner<float>) + static_cast<size_t>(q) * (C + 4) * 4 +
+                       16 * 4 + static_cast<size_t>(ks) * 16 * NTILE * 16 * 4;
+            };
+            while (qt > 1 && lds(qt) > kLdsBudget) --qt;
+            if (lds(qt) <= kLdsBudget) {
+                p.QT = qt;
+                p.SG = sg;
+                p.KS = ks;
+                p.qtiles = (g.Q + qt - 1) / qt;
+                switch (waves) {
+                    case 1: return go_vec<T, 1>(p, lds(qt), stream);
+                    case 2: return go_vec<T, 2>(p, lds(qt), stream);
+                    case 4: return go_vec<T, 4>(p, lds(qt), stream);
+                    case 8: return go_vec<T, 8>(p, lds(qt), stream);
+                    default: return set_error(-1, "fused: waves must be 1, 2, 4 or 8 (got %d)", waves);
+                }
+            }
+        }
+    }
+    // generic kernel
+    auto lds = [&](int q) {
+        return static_cast<size_t>(q) * S * sizeof(Corner<A>) + static_cast<size_t>(q) * C * sizeof(A) +
+               static_cast<size_t>(q) * sizeof(A);
+    };
+    int qt = tune.qt > 0 ? tune.qt : 4;
+    if (qt > qmax) qt = qmax;
+    if (qt < 1) qt = 1;
+    while (qt > 1 && lds(qt) > kLdsBudget) --qt;
+    if (lds(qt) > kLdsBudget)
+        return set_error(-1, "channels (%d) too large for the %s fused kernel", C, sizeof(T) == 8 ? "float64" : "scalar");
+    p.QT = qt;
+    p.SG = 1;
+    p.KS = 1;
+    p.qtiles = (g.Q + qt - 1) / qt;
+    return go_generic<T, 4>(p, lds(qt), stream);
+}
+
+}  // namespace
+
+int launch_fused(int dtype, const void* mem, const void* w, const void* bias, const Geom& g, int C, const void* loc,
+                 const void* attn, void* out, hipStream_t stream, const FusedTune& tune) {
+    FusedParams p{mem, w, bias, loc, attn, out, g, C, 1, 1, 1, 1};
+    switch (dtype) {
+        case kF32: return launch_fused_t<float>(p, stream, tune);
+        case kF16: return launch_fused_t<f16>(p, stream, tune);
+        case kBF16: return launch_fused_t<bf16>(p, stream, tune);
+        case kF64: return launch_fused_t<double>(p, stream, tune);
+        default: return set_error(-2, "unknown dtype code %d", dtype);
+    }
+}
+
+}  // namespace td

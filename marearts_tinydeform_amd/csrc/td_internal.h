@@ -1,0 +1,44 @@
+// Host-side declarations shared by the kernel translation units and the C ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "td_common.h"
+
+namespace td {
+
+enum Dtype { kF32 = 0, kF16 = 1, kBF16 = 2, kF64 = 3 };
+
+inline int elem_size(int dtype) { return dtype == kF64 ? 8 : dtype == kF32 ? 4 : 2; }
+
+// Launch shape of the fused kernels; zero fields are chosen by the launcher.
+struct FusedTune {
+    int qt = 0;     // query rows per workgroup (1..16)
+    int sg = 0;     // corner split per row (power of two)
+    int waves = 0;  // wavefronts per workgroup (1, 2, 4 or 8)
+    int generic = 0;  // 1 forces the generic kernel
+};
+
+// Launch shape of the sampling kernel; zero fields are chosen by the launcher.
+struct SampleTune {
+    int sg = 0;
+    int waves = 0;
+    int vec = 0;  // elements per load
+};
+
+// Every launcher returns 0, or a negative TD_E* code after recording a message with set_error.
+int set_error(int code, const char* fmt, ...);
+
+int launch_fused(int dtype, const void* mem, const void* w, const void* bias, const Geom& g, int C,
+                 const void* loc, const void* attn, void* out, hipStream_t stream, const FusedTune& tune);
+
+int launch_sample(int dtype, const void* value, const Geom& g, const void* loc, const void* attn, void* out,
+                  hipStream_t stream, const SampleTune& tune);
+
+int launch_value_proj(int dtype, const void* a, const void* w, const void* bias, void* c, int64_t M, int64_t K,
+                      int64_t NO, hipStream_t stream, int force_generic);
+
+int launch_zero(void* out, int64_t bytes, hipStream_t stream);
+
+}  // namespace td

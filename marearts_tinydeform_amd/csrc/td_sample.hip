@@ -1,0 +1,224 @@
+// Project mode, second half: sample projected values.
+//   out[b, q, h*D + d] = sum_s w_s * value[b, t_s, h*D + d]
+// over the L*P*4 bilinear corners of row (b, q, h) that lie inside the map (same corner rule as fused mode).
+//
+// Rows (b, q, h) are independent and need no shared weights, so a workgroup takes RB consecutive rows.
+// Each row is served by DV*SG lanes: lane = (corner group sg, chunk ch of V elements), so one load
+// instruction of a wavefront fetches 64 / (DV*SG) * SG rows' D-wide corner rows at once; the SG partial sums
+// of a row meet by cross-lane adds (lanes DV, 2*DV, ... apart) and the row is stored with V-element stores.
+#include "td_internal.h"
+
+namespace td {
+namespace {
+
+struct SampleParams {
+    const void* value;
+    const void* loc;
+    const void* attn;
+    void* out;
+    Geom g;
+    int RB, SG;
+    int64_t rows;
+};
+
+template <typename T, int V, int WAVES>
+__global__ __launch_bounds__(WAVES* kWave) void sample_kernel(SampleParams p) {
+    constexpr int NTH = WAVES * kWave;
+    using IO = VecIO<T, V>;
+    const Geom& g = p.g;
+    const int LP = g.L * g.P, S = 4 * LP, D = g.D, HD = g.H * D;
+    const int DV = D / V, SG = p.SG, GS = DV * SG, RB = p.RB;
+    extern __shared__ __align__(16) unsigned char smem[];
+    Corner<float>* cw = reinterpret_cast<Corner<float>*>(smem);  // [RB][S]
+
+    const T* __restrict__ value = static_cast<const T*>(p.value);
+    const T* __restrict__ loc = static_cast<const T*>(p.loc);
+    const T* __restrict__ attn = static_cast<const T*>(p.attn);
+    T* __restrict__ out = static_cast<T*>(p.out);
+
+    const int tid = threadIdx.x;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * RB;
+
+    for (int i = tid; i < RB * LP; i += NTH) {
+        const int r = i / LP, j = i - r * LP;
+        const int64_t row = row0 + r;
+        Corner<float>* c4 = cw + r * S + 4 * j;
+        if (row < p.rows) {
+            corner4<T, float>(loc, attn, g, row, j, c4);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) c4[k] = Corner<float>{-1, 0.f};
+        }
+    }
+    __syncthreads();
+
+    const int64_t QH = static_cast<int64_t>(g.Q) * g.H;
+    for (int it = tid; it < RB * GS; it += NTH) {
+        const int r = it / GS, rem = it - r * GS, sg = rem / DV, ch = rem - sg * DV;
+        const int64_t row = row0 + r;
+        const bool valid = row < p.rows;
+        const int64_t b = valid ? row / QH : 0;
+        const int h = valid ? static_cast<int>(row % g.H) : 0;
+        const T* base = value + static_cast<size_t>(b) * g.N * HD + static_cast<size_t>(h) * D + ch * V;
+        const Corner<float>* cr = cw + r * S;
+        float acc[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] = 0.f;
+#pragma unroll 8
+        for (int s = sg; s < S; s += SG) {
+            const Corner<float> c = cr[s];
+            typename IO::raw_t raw = IO::load(base + static_cast<size_t>(c.tok < 0 ? 0 : c.tok) * HD);
+            if (c.tok < 0) raw = IO::zero();
+            float v[V];
+            IO::unpack(raw, v);
+#pragma unroll
+            for (int i = 0; i < V; ++i) acc[i] = fmaf(c.w, v[i], acc[i]);
+        }
+        for (int m = DV; m < GS; m <<= 1) {
+#pragma unroll
+            for (int i = 0; i < V; ++i) acc[i] += xor_lane(acc[i], m);
+        }
+        if (sg == 0 && valid) IO::store(out + static_cast<size_t>(row) * D + ch * V, acc);
+    }
+}
+
+// float64: float64 accumulation, scalar loads.
+template <int WAVES>
+__global__ __launch_bounds__(WAVES* kWave) void sample_f64_kernel(SampleParams p) {
+    constexpr int NTH = WAVES * kWave;
+    const Geom& g = p.g;
+    const int LP = g.L * g.P, S = 4 * LP, D = g.D, HD = g.H * D, RB = p.RB;
+    extern __shared__ __align__(16) unsigned char smem[];
+    Corner<double>* cw = reinterpret_cast<Corner<double>*>(smem);
+    const double* __restrict__ value = static_cast<const double*>(p.value);
+    const double* __restrict__ loc = static_cast<const double*>(p.loc);
+    const double* __restrict__ attn = static_cast<const double*>(p.attn);
+    double* __restrict__ out = static_cast<double*>(p.out);
+    const int tid = threadIdx.x;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * RB;
+    for (int i = tid; i < RB * LP; i += NTH) {
+        const int r = i / LP, j = i - r * LP;
+        const int64_t row = row0 + r;
+        Corner<double>* c4 = cw + r * S + 4 * j;
+        if (row < p.rows) {
+            corner4<double, double>(loc, attn, g, row, j, c4);
+        } else {
+            for (int k = 0; k < 4; ++k) c4[k] = Corner<double>{-1, 0.0};
+        }
+    }
+    __syncthreads();
+    const int64_t QH = static_cast<int64_t>(g.Q) * g.H;
+    for (int it = tid; it < RB * D; it += NTH) {
+        const int r = it / D, d = it - r * D;
+        const int64_t row = row0 + r;
+        if (row >= p.rows) continue;
+        const int64_t b = row / QH;
+        const int h = static_cast<int>(row % g.H);
+        const double* base = value + static_cast<size_t>(b) * g.N * HD + static_cast<size_t>(h) * D + d;
+        double acc = 0.0;
+        for (int s = 0; s < S; ++s) {
+            const Corner<double> c = cw[r * S + s];
+            const double v = base[static_cast<size_t>(c.tok < 0 ? 0 : c.tok) * HD];
+            acc = fma(c.w, c.tok < 0 ? 0.0 : v, acc);
+        }
+        out[static_cast<size_t>(row) * D + d] = acc;
+    }
+}
+
+constexpr size_t kLdsBudget = 65536;
+
+inline bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+
+template <typename T, int V, int WAVES>
+int go(SampleParams p, size_t lds, hipStream_t stream) {
+    const int64_t blocks = (p.rows + p.RB - 1) / p.RB;
+    hipLaunchKernelGGL((sample_kernel<T, V, WAVES>), dim3(static_cast<unsigned>(blocks)), dim3(WAVES * kWave), lds,
+                       stream, p);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : set_error(-3, "sample launch failed: %s", hipGetErrorString(e));
+}
+
+template <typename T, int V>
+int go_waves(SampleParams p, int waves, size_t lds, hipStream_t stream) {
+    switch (waves) {
+        case 1: return go<T, V, 1>(p, lds, stream);
+        case 2: return go<T, V, 2>(p, lds, stream);
+        case 4: return go<T, V, 4>(p, lds, stream);
+        default: return set_error(-1, "sample: waves must be 1, 2 or 4 (got %d)", waves);
+    }
+}
+
+template <typename T>
+int launch_sample_t(SampleParams p, hipStream_t stream, const SampleTune& tune) {
+    const Geom& g = p.g;
+    const int LP = g.L * g.P, S = 4 * LP, D = g.D;
+    constexpr int VMAX = 16 / static_cast<int>(sizeof(T));
+    const uintptr_t align = reinterpret_cast<uintptr_t>(p.value) | reinterpret_cast<uintptr_t>(p.out);
+    int V = tune.vec > 0 ? tune.vec : VMAX;
+    while (V > 1 && (D % V != 0 || align % (V * sizeof(T)) != 0)) V >>= 1;
+    if (V > VMAX || D % V != 0 || align % (V * sizeof(T)) != 0)
+        return set_error(-1, "sample: %d elements per load do not fit D=%d and the pointer alignment", V, D);
+    const int DV = D / V;
+    int sg = tune.sg;
+    if (sg <= 0) {
+        sg = 1;
+        if (is_pow2(DV) && DV < kWave) {
+            sg = kWave / DV;
+            while (sg > 1 && S / sg < 8) sg >>= 1;
+        }
+    }
+    if (sg > 1 && !(is_pow2(DV) && is_pow2(sg) && DV * sg <= kWave)) sg = 1;
+    const int GS = DV * sg;
+    int waves = tune.waves;
+    if (waves <= 0) {
+        // small problems: single-wavefront workgroups so that more CUs get work
+        const int64_t lanes = p.rows * GS;
+        waves = lanes >= int64_t(256) * 64 * 8 ? 4 : 1;
+    }
+    const int nth = waves * kWave;
+    int rb = nth / GS;
+    if (rb < 1) rb = 1;
+    auto lds = [&](int r) { return static_cast<size_t>(r) * S * sizeof(Corner<float>); };
+    while (rb > 1 && lds(rb) > kLdsBudget) --rb;
+    p.RB = rb;
+    p.SG = sg;
+    switch (V) {
+        case 1: return go_waves<T, 1>(p, waves, lds(rb), stream);
+        case 2: return go_waves<T, 2>(p, waves, lds(rb), stream);
+        case 4: return go_waves<T, 4>(p, waves, lds(rb), stream);
+        case 8:
+            if constexpr (VMAX >= 8) return go_waves<T, 8>(p, waves, lds(rb), stream);
+            break;
+        default: break;
+    }
+    return set_error(-1, "sample: unsupported vector width %d", V);
+}
+
+int launch_sample_f64(SampleParams p, hipStream_t stream) {
+    const int S = 4 * p.g.L * p.g.P;
+    int rb = 4;
+    while (rb > 1 && static_cast<size_t>(rb) * S * sizeof(Corner<double>) > kLdsBudget) --rb;
+    p.RB = rb;
+    p.SG = 1;
+    const int64_t blocks = (p.rows + rb - 1) / rb;
+    hipLaunchKernelGGL((sample_f64_kernel<4>), dim3(static_cast<unsigned>(blocks)), dim3(4 * kWave),
+                       static_cast<size_t>(rb) * S * sizeof(Corner<double>), stream, p);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : set_error(-3, "sample launch failed: %s", hipGetErrorString(e));
+}
+
+}  // namespace
+
+int launch_sample(int dtype, const void* value, const Geom& g, const void* loc, const void* attn, void* out,
+                  hipStream_t stream, const SampleTune& tune) {
+    SampleParams p{value, loc, attn, out, g, 1, 1, static_cast<int64_t>(g.B) * g.Q * g.H};
+    switch (dtype) {
+        case kF32: return launch_sample_t<float>(p, stream, tune);
+        case kF16: return launch_sample_t<f16>(p, stream, tune);
+        case kBF16: return launch_sample_t<bf16>(p, stream, tune);
+        case kF64: return launch_sample_f64(p, stream);
+        default: return set_error(-2, "unknown dtype code %d", dtype);
+    }
+}
+
+}  // namespace td

@@ -1,0 +1,30 @@
+"""Torch restatement of the reference's PyTorch path. TEST INFRASTRUCTURE ONLY: imported by tests/ and by
+bench.py's cpu_baseline leg (it is the CPU path the reference runs for CPU tensors), never by the product.
+
+Follows marearts_tinydeform/reference.py:13-40: value = F.linear(memory, W, b), then for each level
+F.grid_sample(bilinear, zeros, align_corners=False) of that level's [B*H, D, h, w] map at 2 * loc - 1, then the
+attention-weighted sum over levels and points. Runs in the dtype it is given (float32 for the CPU baseline,
+float64 to cross-check the brute force).
+"""
+
+import torch
+import torch.nn.functional as F
+
+
+def deform_attn(memory, value_weight, value_bias, spatial_shapes, level_start_index, sampling_locations,
+                attention_weights):
+    B, N, _ = memory.shape
+    _, Q, H, L, P, _ = sampling_locations.shape
+    value = F.linear(memory, value_weight, value_bias).view(B, N, H, -1)
+    D = value.shape[-1]
+    grids = 2 * sampling_locations - 1
+    acc = torch.zeros(B * H, D, Q, dtype=value.dtype)
+    for lvl in range(L):
+        h, w = int(spatial_shapes[lvl, 0]), int(spatial_shapes[lvl, 1])
+        s = int(level_start_index[lvl])
+        v = value[:, s:s + h * w].permute(0, 2, 3, 1).reshape(B * H, D, h, w)
+        g = grids[:, :, :, lvl].transpose(1, 2).reshape(B * H, Q, P, 2)
+        smp = F.grid_sample(v, g, mode='bilinear', padding_mode='zeros', align_corners=False)  # [B*H, D, Q, P]
+        a = attention_weights[:, :, :, lvl].transpose(1, 2).reshape(B * H, 1, Q, P)
+        acc = acc + torch.einsum('ndqp,ndqp->ndq', smp, a.expand_as(smp))
+    return acc.view(B, H * D, Q).transpose(1, 2).contiguous()

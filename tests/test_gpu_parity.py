@@ -1,0 +1,283 @@
+"""HIP kernels vs the float64 oracle on seeded inputs (GPU). Mirrors the reference's differential tests
+(tests/test_correctness.py:46-146) and adds the benchmark configurations at full size.
+
+Tolerances: float32 atol 2e-5 / rtol 1e-4 and float16 3e-3 / bfloat16 2e-2 (atol = rtol) against float64, as the
+reference's tests use (tests/test_correctness.py:70,76); float64 1e-10. At the benchmark configurations the
+relative error max|got - ref| / max|ref| must also stay within 1e-4 (float32) / 2e-2 (float16, bfloat16).
+"""
+
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import marearts_tinydeform_amd as td
+from marearts_tinydeform_amd import _native
+from oracle import bruteforce
+from inputs import CASES, DINO_LEVELS, LIMIT_LEVELS, RTDETR_LEVELS, as_f64, make, to, workload
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: (2e-5, 1e-4), torch.float16: (3e-3, 3e-3), torch.bfloat16: (2e-2, 2e-2),
+       torch.float64: (1e-10, 1e-10)}
+REL = {torch.float32: 1e-4, torch.float16: 2e-2, torch.bfloat16: 2e-2, torch.float64: 1e-10}
+MODES = ('fused', 'project', 'auto')
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def run(args, mode):
+    with torch.inference_mode():
+        out = td.ma_deform_attn(*args, mode=mode)
+    torch.cuda.synchronize()
+    return out
+
+
+def assert_close(name, got, ref, atol, rtol):
+    got = got.double().cpu().numpy() if hasattr(got, 'cpu') else got
+    assert got.shape == ref.shape, f'{name}: shape {got.shape} != {ref.shape}'
+    err = np.abs(got - ref)
+    bad = err > atol + rtol * np.abs(ref)
+    assert not bad.any(), (f'{name}: {int(bad.sum())} elements out of tolerance, max |diff| {err.max():.3g} '
+                           f'(max |ref| {np.abs(ref).max():.3g})')
+    return float(err.max()) if err.size else 0.0
+
+
+def check_modes(name, cpu_args, dtype, modes=MODES):
+    ref = bruteforce.deform_attn(*cpu_args)
+    dev = to(cpu_args, 'cuda')
+    atol, rtol = TOL[dtype]
+    for mode in modes:
+        say(f'  {name} [{mode}]')
+        assert_close(f'{name} [{mode}]', run(dev, mode), ref, atol, rtol)
+
+
+def test_native_library_is_loaded():
+    assert _native.lib is not None, _native.load_error
+    assert os.path.dirname(_native.lib._name) == os.path.dirname(os.path.abspath(td.__file__))
+    assert torch.cuda.is_available()
+    say(f'device {torch.cuda.get_device_name()} arch {torch.cuda.get_device_properties(0).gcnArchName}')
+
+
+@pytest.mark.parametrize('bias', [True, False])
+def test_float32_cases(bias):
+    for name, *shape in CASES:
+        check_modes(f'{name} fp32 bias={bias}', make(*shape, bias=bias), torch.float32)
+
+
+@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
+def test_half_and_bfloat16_cases(dtype):
+    for name, *shape in CASES:
+        check_modes(f'{name} {dtype}', make(*shape, dtype=dtype), dtype)
+
+
+def test_float64_cases():
+    for name, *shape in CASES[3:]:
+        check_modes(f'{name} fp64', make(*shape, dtype=torch.float64), torch.float64)
+
+
+def test_unaligned_memory_uses_generic_kernel():
+    # reference tests/test_correctness.py:83-95: memory 2 or 4 bytes off a 16-byte boundary
+    for dtype in (torch.float32, torch.float16, torch.bfloat16):
+        args = make(1, 40, 8, 32, 256, [(20, 20), (10, 10)], 4, dtype=dtype)
+        ref = bruteforce.deform_attn(*args)
+        mem = args[0].cuda()
+        buf = torch.empty(mem.numel() + 1, dtype=dtype, device='cuda')
+        shifted = buf[1:].view(mem.shape)
+        shifted.copy_(mem)
+        assert shifted.is_contiguous() and shifted.data_ptr() % 16 != 0
+        dev = [shifted] + to(args[1:], 'cuda')
+        atol, rtol = TOL[dtype]
+        for mode in MODES:
+            say(f'  unaligned {dtype} [{mode}]')
+            assert_close(f'unaligned {dtype} [{mode}]', run(dev, mode), ref, atol, rtol)
+
+
+def test_far_outside_and_empty():
+    # reference tests/test_correctness.py:98-106
+    args = make(2, 20, 4, 8, 32, [(9, 11), (5, 6)], 4, spread=200.0)
+    ref = bruteforce.deform_attn(*args)
+    dev = to(args, 'cuda')
+    for mode in MODES:
+        assert_close(f'far outside [{mode}]', run(dev, mode), ref, 1e-5, 1e-4)
+    # every sample outside: exactly zero, bias included
+    allout = list(args)
+    allout[5] = torch.full_like(args[5], 7.0)
+    dev = to(allout, 'cuda')
+    for mode in MODES:
+        out = run(dev, mode)
+        assert torch.count_nonzero(out) == 0, mode
+    empty = to(make(1, 0, 4, 8, 32, [(9, 11)], 4), 'cuda')
+    for mode in MODES:
+        assert run(empty, mode).shape == (1, 0, 32)
+
+
+def test_nonfinite_locations_sample_nothing():
+    # clamp-before-convert rule (reference csrc/ma_deform_fused.cu:87-89): inf, -inf and NaN coordinates and
+    # huge finite ones contribute nothing and never overflow the integer conversion
+    for dtype in (torch.float32, torch.float16, torch.bfloat16):
+        args = make(1, 16, 2, 16, 32, [(7, 9), (4, 5)], 2, dtype=dtype)
+        loc = args[5].clone()
+        loc[0, 0, :, :, :, 0] = float('inf')
+        loc[0, 1, :, :, :, 1] = float('-inf')
+        loc[0, 2, :, 0, 0, 0] = float('nan')
+        loc[0, 3, :, :, :, :] = 3e4 if dtype == torch.float16 else 1e30
+        args[5] = loc
+        ref = bruteforce.deform_attn(*args)
+        assert np.isfinite(ref).all()
+        assert np.abs(ref[0, 0]).max() == 0 and np.abs(ref[0, 3]).max() == 0
+        dev = to(args, 'cuda')
+        atol, rtol = TOL[dtype]
+        for mode in MODES:
+            assert_close(f'nonfinite {dtype} [{mode}]', run(dev, mode), ref, atol, rtol)
+
+
+def test_rejects_bad_input():
+    # reference tests/test_correctness.py:109-146 (project mode checks the weight too here: our GEMM, not F.linear)
+    args = to(make(1, 8, 2, 8, 16, [(6, 7), (3, 4)], 2), 'cuda')
+    bad = [
+        ('weight cols', 1, args[1][:, :8].contiguous()),
+        ('dtype', 1, args[1].half()),
+        ('bias size', 2, args[2][:4]),
+        ('shapes dtype', 3, args[3].int()),
+        ('starts dtype', 4, args[4].int()),
+        ('too many points', 6, torch.ones(1, 8, 2, 2, 40, device='cuda') / 80),
+        ('attn shape', 6, torch.ones(1, 8, 2, 2, 3, device='cuda')),
+        ('loc dtype', 5, args[5].double()),
+        ('batch', 0, args[0][:0]),
+    ]
+    for what, i, value in bad:
+        a = list(args)
+        a[i] = value
+        if what == 'too many points':
+            a[5] = torch.rand(1, 8, 2, 2, 40, 2, device='cuda')
+        for mode in ('fused', 'project'):
+            with pytest.raises(RuntimeError):
+                with torch.inference_mode():
+                    td.ma_deform_attn(*a, mode=mode)
+    grad = [t.clone().requires_grad_(True) if i == 0 else t for i, t in enumerate(args)]
+    with pytest.raises(RuntimeError):
+        td.ma_deform_attn(*grad)
+    with pytest.raises(ValueError):
+        td.ma_deform_attn(*args, mode='nope')
+    with pytest.raises(RuntimeError):  # C > 8192 in fused mode
+        big = to(make(1, 2, 1, 8, 8200, [(2, 2)], 1, bias=False), 'cuda')
+        with torch.inference_mode():
+            td.ma_deform_attn(*big, mode='fused')
+
+
+def test_value_proj_matches_oracle():
+    # the GEMM alone, with M, N, K off the tile sizes
+    g = torch.Generator().manual_seed(3)
+    for dtype in (torch.float16, torch.bfloat16, torch.float32, torch.float64):
+        for (B, N, C, HD) in ((1, 8400, 256, 256), (2, 77, 40, 48), (1, 130, 96, 72), (3, 5, 8, 16)):
+            mem = torch.randn(B, N, C, generator=g).to(dtype)
+            w = (torch.randn(HD, C, generator=g) / C ** 0.5).to(dtype)
+            b = (torch.randn(HD, generator=g) * 0.1).to(dtype)
+            ref = bruteforce.project(mem, w, b)
+            with torch.inference_mode():
+                got = _native.value_proj(mem.cuda(), w.cuda(), b.cuda())
+            torch.cuda.synchronize()
+            # one rounding to dtype after float32 accumulation
+            eps = {torch.float16: 2e-3, torch.bfloat16: 1e-2, torch.float32: 1e-5, torch.float64: 1e-12}[dtype]
+            assert_close(f'value_proj {dtype} {(B, N, C, HD)}', got, ref, eps, eps)
+
+
+def test_sample_alone_matches_oracle():
+    for dtype in (torch.float16, torch.bfloat16, torch.float32):
+        for name, B, Q, H, D, C, levels, P in CASES:
+            args = make(B, Q, H, D, C, levels, P, dtype=dtype)
+            g = torch.Generator().manual_seed(5)
+            value = torch.randn(B, args[0].shape[1], H * D, generator=g).to(dtype)
+            ref = bruteforce.sample(value, H, *args[3:])
+            with torch.inference_mode():
+                got = td.ma_deform_sample(value.cuda(), *to(args[3:], 'cuda'))
+            torch.cuda.synchronize()
+            atol, rtol = TOL[dtype]
+            assert_close(f'sample {name} {dtype}', got, ref, atol, rtol)
+
+
+def test_graph_capture_replays_match_eager():
+    args = to(workload(1, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.float16), 'cuda')
+    for mode in MODES:
+        with torch.inference_mode():
+            eager = td.ma_deform_attn(*args, mode=mode)
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                for _ in range(2):
+                    td.ma_deform_attn(*args, mode=mode)
+            torch.cuda.current_stream().wait_stream(s)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                out = td.ma_deform_attn(*args, mode=mode)
+            for i in range(4):
+                out.zero_()
+                torch.cuda.synchronize()
+                graph.replay()
+                torch.cuda.synchronize()
+                assert torch.equal(out, eager), f'graph replay {i} [{mode}] differs from eager'
+                _ = eager.sum().item()  # eager work between replays
+
+
+# ---- the benchmark configurations at full size ---------------------------------------------------------------
+
+def full_size_check(name, args, dtype, rows=None, modes=('fused', 'project')):
+    H = args[5].shape[2]
+    B, Q = args[5].shape[:2]
+    if rows is None:
+        ref = bruteforce.deform_attn(*args)
+    else:
+        ref = bruteforce.deform_attn(*args, rows=rows)
+    dev = to(args, 'cuda')
+    atol, rtol = TOL[dtype]
+    outs = {}
+    for mode in modes:
+        say(f'  {name} [{mode}]')
+        out = run(dev, mode)
+        assert out.shape == (B, Q, args[1].shape[0])
+        assert torch.isfinite(out).all()
+        outs[mode] = out
+        got = out.double().cpu().numpy()
+        if rows is not None:
+            D = got.shape[-1] // H
+            got = got.reshape(-1, D)[rows]
+        err = assert_close(f'{name} [{mode}]', got, ref, atol, rtol)
+        rel = err / max(np.abs(ref).max(), 1e-30)
+        assert rel <= REL[dtype], f'{name} [{mode}]: relative error {rel:.3g}'
+    if len(outs) == 2:  # linear reordering: both orders agree over the whole output
+        a, b = (o.double() for o in outs.values())
+        assert torch.allclose(a, b, atol=2 * atol, rtol=2 * rtol), f'{name}: fused and project disagree'
+
+
+@pytest.mark.parametrize('Q', [50, 100, 300])
+def test_rtdetr640_fp16_b1(Q):
+    full_size_check(f'rtdetr640 fp16 B1 Q{Q}', workload(1, Q, 8, 32, 256, RTDETR_LEVELS, 4, torch.float16),
+                    torch.float16)
+
+
+def test_rtdetr640_fp32_b1_q300():
+    full_size_check('rtdetr640 fp32 B1 Q300', workload(1, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.float32),
+                    torch.float32)
+
+
+def test_rtdetr640_bf16_b8_q300():
+    full_size_check('rtdetr640 bf16 B8 Q300', workload(8, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.bfloat16),
+                    torch.bfloat16)
+
+
+def test_dino_4level_fp16_b4_q900():
+    full_size_check('dino fp16 B4 Q900',
+                    workload(4, 900, 8, 32, 256, DINO_LEVELS, 4, torch.float16, loc_dist='outside10'),
+                    torch.float16)
+
+
+@pytest.mark.parametrize('Q', [50, 300])
+def test_limit_case_bf16_c1024(Q):
+    args = workload(2, Q, 16, 64, 1024, LIMIT_LEVELS, 16, torch.bfloat16, bias=False)
+    rows = np.random.default_rng(Q).choice(2 * Q * 16, size=min(1024, 2 * Q * 16), replace=False)
+    full_size_check(f'limit bf16 C1024 B2 Q{Q}', args, torch.bfloat16, rows=np.sort(rows))
