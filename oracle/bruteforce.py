@@ -60,8 +60,8 @@ def corner_table(spatial_shapes, level_start_index, sampling_locations, attentio
         wts.append(np.where(inside, attn * bw, 0.0))
     tok = np.stack(toks, axis=-1)  # [B, Q, H, L, P, 4]
     wt = np.stack(wts, axis=-1)
-    B, Q, H = tok.shape[:3]
-    return tok.reshape(B, Q, H, -1), wt.reshape(B, Q, H, -1)
+    B, Q, H, L, P = tok.shape[:5]
+    return tok.reshape(B, Q, H, L * P * 4), wt.reshape(B, Q, H, L * P * 4)
 
 
 def project(memory, value_weight, value_bias):

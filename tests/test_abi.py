@@ -1,0 +1,106 @@
+"""The C ABI library (CPU only: no kernel is launched). libtinydeform.so must load, export every function
+include/tinydeform.h declares, agree with the header's constants, and reject invalid arguments on the host with
+the reference's messages (csrc/ma_deform_fused.cu:236-266, 298-308) before touching a device."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from marearts_tinydeform_amd import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, 'include', 'tinydeform.h')
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r'^\s*(?:const\s+)?\w+\*?\s+\*?(td_\w+)\s*\(', text, flags=re.M)))
+
+
+def header_defines():
+    return {k: int(v) for k, v in re.findall(r'#define\s+(TD_\w+)\s+(-?\d+)', open(HEADER).read())}
+
+
+@pytest.fixture(scope='module')
+def lib():
+    assert os.path.exists(_native.LIB_PATH), 'libtinydeform.so is not built: run __graft_entry__.build()'
+    lib = _native.load()
+    assert lib is not None, _native.load_error
+    return lib
+
+
+def test_header_declares_the_entry_points():
+    assert header_functions() == ['td_fused_forward', 'td_last_error', 'td_sample_forward', 'td_value_proj',
+                                  'td_version']
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(_native.LIB_PATH)
+    for name in header_functions():
+        assert hasattr(raw, name), name
+    assert set(header_functions()) == set(_native.SIGNATURES)
+
+
+def test_header_constants_match_python(lib):
+    d = header_defines()
+    assert d['TD_MAX_LEVEL_POINTS'] == _native.MAX_LEVEL_POINTS
+    assert d['TD_MAX_CHANNELS'] == _native.MAX_CHANNELS
+    assert {d['TD_F32'], d['TD_F16'], d['TD_BF16'], d['TD_F64']} == set(_native.DTYPE_CODES.values())
+    import torch
+    assert _native.DTYPE_CODES[torch.float32] == d['TD_F32']
+    assert _native.DTYPE_CODES[torch.float16] == d['TD_F16']
+    assert _native.DTYPE_CODES[torch.bfloat16] == d['TD_BF16']
+    assert _native.DTYPE_CODES[torch.float64] == d['TD_F64']
+
+
+def test_version(lib):
+    assert lib.td_version() == 100
+
+
+def fused(lib, dtype=1, B=1, Q=4, N=100, C=256, H=8, D=32, L=3, P=4, ptr=16):
+    p = ptr
+    return lib.td_fused_forward(dtype, p, p, None, p, p, p, p, p, B, Q, N, C, H, D, L, P, None)
+
+
+def sample(lib, dtype=1, B=1, Q=4, N=100, H=8, D=32, L=3, P=4, ptr=16):
+    p = ptr
+    return lib.td_sample_forward(dtype, p, p, p, p, p, p, B, Q, N, H, D, L, P, None)
+
+
+@pytest.mark.parametrize('kwargs,message', [
+    (dict(L=4, P=20), 'levels x points must be <= 64'),
+    (dict(H=0), 'need at least one head'),
+    (dict(C=8200), 'channels must be <= 8192'),
+    (dict(N=2 ** 31), 'too many memory tokens'),
+    (dict(B=2 ** 16, Q=2 ** 13, H=2 ** 3), r'too many \(batch, query, head\) rows'),
+    (dict(Q=-1), 'sizes must be non-negative'),
+    (dict(ptr=None), 'null pointer argument'),
+])
+def test_fused_rejects_on_host(lib, kwargs, message):
+    assert fused(lib, **kwargs) == header_defines()['TD_E_ARG']
+    assert re.search(message, lib.td_last_error().decode())
+
+
+def test_unknown_dtype(lib):
+    assert fused(lib, dtype=9) == header_defines()['TD_E_DTYPE']
+    assert sample(lib, dtype=-1) == header_defines()['TD_E_DTYPE']
+    assert lib.td_value_proj(7, 16, 16, None, 16, 4, 4, 4, None) == header_defines()['TD_E_DTYPE']
+
+
+def test_sample_and_proj_reject_on_host(lib):
+    assert sample(lib, L=8, P=9) == header_defines()['TD_E_ARG']
+    assert 'levels x points' in lib.td_last_error().decode()
+    assert sample(lib, ptr=None) == header_defines()['TD_E_ARG']
+    assert lib.td_value_proj(1, None, None, None, None, 4, 4, 4, None) == header_defines()['TD_E_ARG']
+    assert lib.td_value_proj(1, 16, 16, None, 16, -1, 4, 4, None) == header_defines()['TD_E_ARG']
+
+
+def test_empty_work_returns_ok_without_launching(lib):
+    # zero rows: nothing to launch, so no device is needed
+    assert fused(lib, Q=0) == 0
+    assert fused(lib, B=0) == 0
+    assert sample(lib, Q=0) == 0
+    assert lib.td_value_proj(1, 16, 16, None, 16, 0, 4, 4, None) == 0
+    assert lib.td_last_error().decode() == ''

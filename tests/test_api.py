@@ -1,0 +1,141 @@
+"""Python API and host logic (CPU only): the reference's CPU-runnable tests (tests/test_correctness.py:56-59,
+141-163) and the host-side validation of csrc/ma_deform_fused.cu:236-266, 298-308, 333, exercised without a GPU."""
+
+import numpy as np
+import pytest
+import torch
+
+import marearts_tinydeform_amd as td
+from marearts_tinydeform_amd import _native
+from oracle import bruteforce
+from inputs import RTDETR_LEVELS, make
+
+
+def test_public_names():
+    assert set(td.__all__) >= {'ma_deform_attn', 'ma_deform_attn_reference', 'choose_mode'}
+    assert td.MODES == ('auto', 'fused', 'project')
+
+
+def test_cpu_path_is_reference():
+    # reference tests/test_correctness.py:56-59
+    args = make(1, 10, 2, 8, 16, [(6, 7), (3, 4)], 2)
+    with torch.inference_mode():
+        for mode in td.MODES:
+            assert torch.equal(td.ma_deform_attn(*args, mode=mode), td.ma_deform_attn_reference(*args))
+
+
+def test_reference_path_matches_oracle():
+    args = make(2, 12, 4, 8, 32, [(10, 15), (5, 8)], 4)
+    f64 = [t if t is None or t.dtype == torch.long else t.double() for t in args]
+    assert np.abs(td.ma_deform_attn_reference(*f64).numpy() - bruteforce.deform_attn(*args)).max() <= 1e-12
+    # float32 within float32 rounding
+    got = td.ma_deform_attn_reference(*args).double().numpy()
+    assert np.abs(got - bruteforce.deform_attn(*args)).max() <= 1e-5
+
+
+def test_reference_path_supports_autograd():
+    args = make(1, 4, 2, 4, 8, [(5, 6)], 2)
+    args[0].requires_grad_(True)
+    td.ma_deform_attn(*args).sum().backward()  # CPU tensors: the reference, with autograd
+    assert args[0].grad is not None and args[0].grad.abs().sum() > 0
+
+
+def test_unknown_mode_raises_value_error():
+    args = make(1, 4, 2, 4, 8, [(5, 6)], 2)
+    with pytest.raises(ValueError):
+        td.ma_deform_attn(*args, mode='nope')
+
+
+def test_auto_picks_fused_for_few_queries():
+    # reference tests/test_correctness.py:149-153
+    few = make(1, 50, 8, 32, 256, RTDETR_LEVELS, 4)
+    many = make(8, 900, 8, 32, 256, RTDETR_LEVELS, 4)
+    assert td.choose_mode(few[0], few[1], few[5]) == 'fused'
+    assert td.choose_mode(many[0], many[1], many[5]) == 'project'
+
+
+def test_auto_limits_follow_the_gpu_architecture(monkeypatch):
+    # the reference keys its table by compute capability (tests/test_correctness.py:156-163); here by gcnArchName
+    class Props:
+        def __init__(self, arch):
+            self.gcnArchName = arch
+
+    for arch, table in (('gfx950:sramecc+:xnack-', td.FUSED_LIMIT), ('gfx942', td.FUSED_LIMIT)):
+        monkeypatch.setattr(torch.cuda, 'get_device_properties', lambda i, arch=arch: Props(arch))
+        assert td._limits.__wrapped__(0) is table
+    assert td.ARCH_LIMITS['gfx950'] is td.FUSED_LIMIT
+
+
+def test_fused_limit_tables_are_sane():
+    for dtype in (torch.float32, torch.float16, torch.bfloat16):
+        a, b = td.FUSED_LIMIT[dtype]
+        assert a >= 0 and b >= 0
+
+
+# ---- host validation (same rules and messages as the reference's host checks) ---------------------------------
+
+def geometry_args():
+    return make(1, 8, 2, 8, 16, [(6, 7), (3, 4)], 2)
+
+
+@pytest.mark.parametrize('what,index,make_bad,message', [
+    ('memory rank', 0, lambda a: a[0][0], 'memory / value must be [B, N, C]'),
+    ('loc rank', 5, lambda a: a[5][..., 0], 'sampling_locations must be [B, Q, H, L, P, 2]'),
+    ('attn rank', 6, lambda a: a[6][..., 0], 'attention_weights must be [B, Q, H, L, P]'),
+    ('attn shape', 6, lambda a: a[6][:, :4], 'attention_weights must be [B, Q, H, L, P] like sampling_locations'),
+    ('batch', 0, lambda a: torch.cat([a[0], a[0]]), 'batch size mismatch'),
+    ('shapes dtype', 3, lambda a: a[3].int(), 'spatial_shapes must be int64 [L, 2]'),
+    ('shapes size', 3, lambda a: a[3][:1], 'spatial_shapes must be int64 [L, 2]'),
+    ('starts dtype', 4, lambda a: a[4].int(), 'level_start_index must be int64 [L]'),
+    ('loc dtype', 5, lambda a: a[5].double(), 'all float tensors must have the same dtype'),
+    ('attn dtype', 6, lambda a: a[6].half(), 'all float tensors must have the same dtype'),
+])
+def test_check_geometry_rejects(what, index, make_bad, message):
+    a = geometry_args()
+    a[index] = make_bad(a)
+    with pytest.raises(RuntimeError, match=message.replace('[', r'\[').replace(']', r'\]')):
+        _native.check_geometry(a[0], a[3], a[4], a[5], a[6], require_gpu=False)
+
+
+def test_check_geometry_limits():
+    a = geometry_args()
+    loc = torch.rand(1, 8, 2, 2, 40, 2)
+    attn = torch.ones(1, 8, 2, 2, 40) / 80
+    with pytest.raises(RuntimeError, match='levels x points must be <= 64'):
+        _native.check_geometry(a[0], a[3], a[4], loc, attn, require_gpu=False)
+    loc0 = torch.rand(1, 8, 0, 2, 2, 2)
+    with pytest.raises(RuntimeError, match='need at least one head'):
+        _native.check_geometry(a[0], a[3], a[4], loc0, loc0[..., 0], require_gpu=False)
+    assert _native.check_geometry(a[0], a[3], a[4], a[5], a[6], require_gpu=False) == (1, 8, 2, 2, 2)
+    with pytest.raises(RuntimeError, match='inputs must be GPU tensors'):
+        _native.check_geometry(a[0], a[3], a[4], a[5], a[6])
+
+
+def test_check_projection_rejects():
+    a = geometry_args()
+    mem, w, b = a[0], a[1], a[2]
+    assert _native.check_projection(mem, w, b, 2) == 16
+    with pytest.raises(RuntimeError, match='value_weight must be'):
+        _native.check_projection(mem, w[:, :8], b, 2)
+    with pytest.raises(RuntimeError, match='multiple of the head count'):
+        _native.check_projection(mem, w[:15], None, 2)
+    with pytest.raises(RuntimeError, match='device and dtype'):
+        _native.check_projection(mem, w.half(), b, 2)
+    with pytest.raises(RuntimeError, match='value_bias must be'):
+        _native.check_projection(mem, w, b[:4], 2)
+    with pytest.raises(RuntimeError, match='value_bias must be'):
+        _native.check_projection(mem, w, b.double(), 2)
+
+
+def test_missing_extension_raises_for_device_entries(monkeypatch):
+    monkeypatch.setattr(_native, 'lib', None)
+    monkeypatch.setattr(_native, 'load_error', 'not built')
+    a = geometry_args()
+    with pytest.raises(RuntimeError, match='without its HIP extension'):
+        _native.fused_forward(*a)
+    with pytest.raises(RuntimeError, match='without its HIP extension'):
+        _native.value_proj(a[0], a[1], a[2])
+    with pytest.raises(RuntimeError, match='without its HIP extension'):
+        td.ma_deform_sample(a[0], a[3], a[4], a[5], a[6])
+    # CPU tensors still run the reference path (reference marearts_tinydeform/__init__.py:15-18, 62-64)
+    assert td.ma_deform_attn(*a).shape == (1, 8, 16)
