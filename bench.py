@@ -130,6 +130,114 @@ def cpu_baseline(spec, budget_s):
                       f'({time.perf_counter() - t0:.1f} s) on {cpu}'}
 
 
+COPY_BYTES = 256 << 20  # plain copy used to scale FETCH_SIZE / WRITE_SIZE to bytes
+
+
+def measured_traffic(workload_name, kernel):
+    """HBM bytes per launch of `kernel` (FETCH_SIZE + WRITE_SIZE, each scaled by the plain-copy calibration) from
+    the rocprofv3 --pmc summary committed for this workload, or None when there is none."""
+    path = os.path.join(ROOT, 'profiles', f'pmc_{workload_name}.json')
+    try:
+        with open(path) as f:
+            k = json.load(f)['kernels'][kernel]
+        return int(k['fetch_bytes'] + k['write_bytes'])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def pmc_run(dev, H, steps):
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device='cuda')
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    with torch.inference_mode():
+        for _ in range(steps):
+            td.ma_deform_attn(*dev, mode='fused')
+        torch.cuda.synchronize()
+        for _ in range(steps):
+            value = _native.value_proj(dev[0], dev[1], dev[2])
+        torch.cuda.synchronize()
+        for _ in range(steps):
+            _native.sample_forward(value, H, *dev[3:])
+        torch.cuda.synchronize()
+    log(f'pmc run done: copy of {COPY_BYTES} bytes, {steps} calls of fused / value_proj / sample')
+
+
+def auto_grid():
+    """The shapes the auto selector is fitted on: RT-DETR 640 (the reference's bench grid: 3 dtypes x batch 1/4/8
+    x 50..900 queries), DINO 4-level and the C=1024 / 64-sample limit shape."""
+    cases = []
+    for dt in (torch.float32, torch.float16, torch.bfloat16):
+        for B in (1, 4, 8):
+            for Q in (50, 100, 200, 300, 600, 900):
+                cases.append(('rtdetr640', B, Q, 8, 32, 256, RTDETR_LEVELS, 4, dt, True, 'uniform'))
+    for dt in (torch.float16, torch.bfloat16):
+        for B, Q in ((1, 300), (4, 300), (4, 900), (8, 900)):
+            cases.append(('dino4l', B, Q, 8, 32, 256, DINO_LEVELS, 4, dt, True, 'outside10'))
+    for Q in (50, 300, 900):
+        for B in (1, 2):
+            cases.append(('limit', B, Q, 16, 64, 1024, LIMIT_LEVELS, 16, torch.bfloat16, False, 'uniform'))
+    return cases
+
+
+def cost_features(B, Q, H, D, C, N, L, P, s):
+    samples = B * Q * H * L * P * 4
+    HD = H * D
+    return ([1.0, samples * C * s / 1e6],
+            [1.0, B * N * (C + HD) * s / 1e6, 2 * B * N * C * HD / 1e9, samples * D * s / 1e6])
+
+
+def fit_auto(out_path):
+    """Measure both modes over auto_grid(), fit FUSED_LIMIT's linear cost model per dtype family by non-negative
+    least squares on relative error, and report every case's loss of the fitted and the current selector."""
+    import numpy as np
+    from scipy.optimize import nnls
+    rows = []
+    with torch.inference_mode():
+        for name, B, Q, H, D, C, levels, P, dt, bias, ld in auto_grid():
+            dev = [None if t is None else t.cuda() for t in workload(B, Q, H, D, C, levels, P, dt, bias=bias,
+                                                                      loc_dist=ld)]
+            N, L = dev[0].shape[1], len(levels)
+            steps = 100 if B * Q * C < 2_000_000 else 20
+            t = {m: graph_time_us(lambda m=m: td.ma_deform_attn(*dev, mode=m), steps, 5) for m in ('fused', 'project')}
+            cur = td.choose_mode(dev[0], dev[1], dev[5])
+            rows.append(dict(case=name, dtype=DTYPE_NAMES[dt], B=B, Q=Q, H=H, D=D, C=C, N=N, L=L, P=P,
+                             s=dev[0].element_size(), fused=t['fused'], project=t['project'], current_pick=cur))
+            log(f'{name:9s} {DTYPE_NAMES[dt]:4s} B={B} Q={Q:3d} fused {t["fused"]:8.2f} project {t["project"]:8.2f}'
+                f' auto now picks {cur}')
+            del dev
+            torch.cuda.empty_cache()
+    table = {}
+    for fam in (('f32',), ('f16', 'bf16')):
+        xs = [r for r in rows if r['dtype'] in fam]
+        feats = [cost_features(r['B'], r['Q'], r['H'], r['D'], r['C'], r['N'], r['L'], r['P'], r['s']) for r in xs]
+        Ff = np.array([f[0] for f in feats])
+        Fp = np.array([f[1] for f in feats])
+        tf = np.array([r['fused'] for r in xs])
+        tp = np.array([r['project'] for r in xs])
+        cf, _ = nnls(Ff / tf[:, None], np.ones(len(xs)))
+        cp, _ = nnls(Fp / tp[:, None], np.ones(len(xs)))
+        for fd in fam:
+            table[fd] = {'fused': [round(float(c), 4) for c in cf], 'project': [round(float(c), 4) for c in cp]}
+        for r, a, b in zip(xs, Ff @ cf, Fp @ cp):
+            r['fitted_pick'] = 'fused' if a <= b else 'project'
+    for r in rows:
+        best = min(r['fused'], r['project'])
+        r['fitted_loss'] = round(r[r['fitted_pick']] / best, 3)
+        r['current_loss'] = round(r[r['current_pick']] / best, 3)
+    worst_fit = max(r['fitted_loss'] for r in rows)
+    worst_cur = max(r['current_loss'] for r in rows)
+    within = sum(r['current_loss'] <= 1.10 for r in rows)
+    log(f'fitted table: {json.dumps(table)}')
+    log(f'worst auto/best ratio: fitted {worst_fit:.3f}, current table {worst_cur:.3f}; '
+        f'current within 10%: {within}/{len(rows)}')
+    with open(out_path, 'w') as f:
+        json.dump({'table': table, 'rows': rows, 'worst_fitted': worst_fit, 'worst_current': worst_cur,
+                   'current_within_10pct': within, 'cases': len(rows)}, f, indent=1)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -139,6 +247,12 @@ def main():
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
     ap.add_argument('--cpu-seconds', type=float, default=10.0)
     ap.add_argument('--modes-only', action='store_true', help='time the modes, skip per-kernel legs')
+    ap.add_argument('--fit-auto', metavar='OUT.json', default=None,
+                    help='time fused and project over the auto grid, fit the per-dtype cost model of '
+                         'marearts_tinydeform_amd.FUSED_LIMIT and report how far auto is from the faster mode')
+    ap.add_argument('--pmc-run', action='store_true',
+                    help='for rocprofv3 --pmc: one plain copy of COPY_BYTES (the counter calibration), then '
+                         '--steps eager calls of the fused kernel, the value projection and the sampling kernel')
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
@@ -148,6 +262,9 @@ def main():
     if _native.lib is None:
         raise SystemExit(f'HIP extension missing: {_native.load_error}')
     assert torch.cuda.is_available(), 'no HIP device'
+    if args.fit_auto:
+        fit_auto(args.fit_auto)
+        return
 
     spec = WORKLOADS[args.workload]
     B, Q, H, D, C, levels, P, dtype, bias, loc_dist = spec
@@ -159,6 +276,10 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     log(f'{torch.cuda.get_device_name()} ({torch.cuda.get_device_properties(0).gcnArchName}), torch '
         f'{torch.__version__}, workload {args.workload}: B={B} Q={Q} N={N} C={C} H={H} D={D} L={L} P={P}')
+
+    if args.pmc_run:
+        pmc_run(dev, H, args.steps)
+        return
 
     pick = td.choose_mode(dev[0], dev[1], dev[5])
     times = {}
@@ -197,7 +318,7 @@ def main():
                     'peak': 8000.0, 'unit': 'GB/s'}
     roof['achieved'] = round(roof['achieved'], 1)
     roof['frac'] = round(roof['achieved'] / roof['peak'], 4)
-    roof['traffic'] = None
+    roof['traffic'] = measured_traffic(args.workload, roof['kernel'])
 
     path_bytes = alg['fused_bytes'] if pick == 'fused' else alg['gemm_bytes'] + alg['sample_bytes']
     result = {

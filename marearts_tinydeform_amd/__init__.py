@@ -12,20 +12,29 @@ import torch
 from . import _native
 from .reference import ma_deform_attn_reference
 
-__all__ = ['ma_deform_attn', 'ma_deform_attn_reference', 'choose_mode', 'ma_deform_sample']
+__all__ = ['ma_deform_attn', 'ma_deform_attn_reference', 'choose_mode', 'ma_deform_sample', 'predict_us']
 __version__ = '0.1.0'
 
 MODES = ('auto', 'fused', 'project')
 
-# 'fused' gathers C-wide memory rows for every (query, head) sample corner: its cost grows with
-# batch * queries * heads * samples * C. 'project' runs the value GEMM over every token (batch * tokens * C * H * D
-# flops) and then gathers D-wide rows, plus a fixed cost of two launches. 'auto' picks 'fused' while
-#     queries * levels * points * 4 / (tokens * head_dim)  <  a + b / batch
-# (the reference's rule, marearts_tinydeform/__init__.py:21-30) with (a, b) per dtype fitted to MI355X (gfx950)
-# measurements of both modes over queries 50..900 and batch 1..8 at RT-DETR 640 shapes.
-FUSED_LIMIT = {torch.float32: (0.073, 0.032), torch.float16: (0.023, 0.031), torch.bfloat16: (0.023, 0.031)}
+# 'auto' compares predicted times of the two orders (reference marearts_tinydeform/__init__.py:21-46 uses one
+# threshold on queries * levels * points * 4 / (tokens * head_dim); on MI355X the value GEMM is cheap next to
+# gathering C-wide rows, so the crossover also moves with C and one threshold cannot place it). Per dtype, each
+# mode's time in µs is a linear function, fitted to MI355X (gfx950) measurements of both modes
+# (bench.py --fit-auto: RT-DETR 640 shapes at batch 1/4/8 and 50..900 queries, DINO 4-level and C=1024 shapes), of
+#   gathered_mb  B*Q*H*L*P*4*C*s / 1e6   C-wide corner rows read by 'fused'          (s = element bytes)
+#   gemm_mb      B*N*(C + H*D)*s / 1e6   value GEMM traffic of 'project'
+#   gemm_gflop   2*B*N*C*H*D / 1e9       value GEMM work of 'project'
+#   sample_mb    B*Q*H*L*P*4*D*s / 1e6   D-wide corner rows read by 'project'
+#   fused   = f0 + f1 * gathered_mb
+#   project = p0 + p1 * gemm_mb + p2 * gemm_gflop + p3 * sample_mb
+FUSED_LIMIT = {
+    torch.float32: {'fused': (8.0544, 0.0642), 'project': (18.9109, 0.6264, 0.0000, 0.1113)},
+    torch.float16: {'fused': (6.2928, 0.0675), 'project': (8.9357, 0.3726, 0.8518, 0.0953)},
+    torch.bfloat16: {'fused': (6.2928, 0.0675), 'project': (8.9357, 0.3726, 0.8518, 0.0953)},
+}
 
-# crossover tables by GPU architecture (gcnArchName without feature suffixes)
+# cost tables by GPU architecture (gcnArchName without feature suffixes)
 ARCH_LIMITS = {'gfx950': FUSED_LIMIT}
 
 
@@ -38,14 +47,28 @@ def _limits(device_index):
     return ARCH_LIMITS.get(_arch(device_index), FUSED_LIMIT)
 
 
+def predict_us(memory, value_weight, sampling_locations, table=None):
+    """Predicted µs of mode 'fused' and 'project' for these shapes: {'fused': t, 'project': t}."""
+    B, N, C = memory.shape
+    _, Q, H, L, P, _ = sampling_locations.shape
+    HD = value_weight.shape[0]
+    D = HD // max(H, 1)
+    s = memory.element_size()
+    if table is None:
+        table = _limits(memory.get_device()) if memory.is_cuda else FUSED_LIMIT
+    coef = table.get(memory.dtype, table[torch.float16])
+    samples = B * Q * H * L * P * 4
+    f0, f1 = coef['fused']
+    p0, p1, p2, p3 = coef['project']
+    fused = f0 + f1 * samples * C * s / 1e6
+    project = p0 + p1 * B * N * (C + HD) * s / 1e6 + p2 * 2 * B * N * C * HD / 1e9 + p3 * samples * D * s / 1e6
+    return {'fused': fused, 'project': project}
+
+
 def choose_mode(memory, value_weight, sampling_locations):
     """The mode 'auto' runs: 'fused' for few queries per image, 'project' (project every token first) for many."""
-    B, N, _ = memory.shape
-    _, Q, H, L, P, _ = sampling_locations.shape
-    D = value_weight.shape[0] // H
-    limits = _limits(memory.get_device()) if memory.is_cuda else FUSED_LIMIT
-    a, b = limits.get(memory.dtype, limits[torch.float16])
-    return 'fused' if Q * L * P * 4 / (max(N, 1) * max(D, 1)) < a + b / max(B, 1) else 'project'
+    t = predict_us(memory, value_weight, sampling_locations)
+    return 'fused' if t['fused'] <= t['project'] else 'project'
 
 
 def _reject_grad(*tensors):

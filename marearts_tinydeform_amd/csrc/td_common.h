@@ -154,6 +154,38 @@ struct VecIO<bf16, V> {
     }
 };
 
+// Weighted sum of gathered rows: acc[0..V) += w_s * row(tok_s)[0..V) for corners s = first, first + step, ...
+// below S, where row(t) = col + t * stride; ws += w_s. Loads are issued NB at a time before any of them is
+// consumed, so NB row reads per lane are in flight together. Corners outside the map (tok < 0) and the padding
+// slots of the last batch read row 0 (always valid) and contribute exactly 0.
+template <typename T, int V, int NB>
+__device__ __forceinline__ void gather_sum(const Corner<float>* __restrict__ cr, int S, int first, int step,
+                                           const T* __restrict__ col, size_t stride, float* acc, float& ws) {
+    using IO = VecIO<T, V>;
+    for (int s0 = first; s0 < S; s0 += step * NB) {
+        typename IO::raw_t raw[NB];
+        float w[NB];
+        bool in[NB];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int s = s0 + u * step;
+            const Corner<float> c = s < S ? cr[s] : Corner<float>{-1, 0.f};
+            w[u] = c.w;
+            in[u] = c.tok >= 0;
+            raw[u] = IO::load(col + static_cast<size_t>(in[u] ? c.tok : 0) * stride);
+        }
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const typename IO::raw_t r = in[u] ? raw[u] : IO::zero();
+            float v[V];
+            IO::unpack(r, v);
+            ws += w[u];
+#pragma unroll
+            for (int i = 0; i < V; ++i) acc[i] = fmaf(w[u], v[i], acc[i]);
+        }
+    }
+}
+
 // ---- cross-lane ----------------------------------------------------------------------------------------
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }

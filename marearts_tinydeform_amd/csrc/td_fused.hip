@@ -65,11 +65,10 @@ __device__ __forceinline__ BlockRow decode_block(int bid, int H, int qtiles) {
     return r;
 }
 
-template <typename T, int WAVES>
+template <typename T, int WAVES, int NB>
 __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) {
     constexpr int NTH = WAVES * kWave;
     constexpr int V = 16 / static_cast<int>(sizeof(T));
-    using IO = VecIO<T, V>;
     const Geom& g = p.g;
     const int C = p.C, QT = p.QT, SG = p.SG, CV = C / V;
     const int LP = g.L * g.P, S = 4 * LP, D = g.D;
@@ -111,23 +110,11 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     const int GS = CV * SG;
     for (int it = tid; it < QT * GS; it += NTH) {
         const int r = it / GS, rem = it - r * GS, sg = rem / CV, ch = rem - sg * CV;
-        const Corner<float>* cr = cw + r * S;
-        const T* col = mb + ch * V;
         float acc[V];
 #pragma unroll
         for (int i = 0; i < V; ++i) acc[i] = 0.f;
         float ws = 0.f;
-#pragma unroll 8
-        for (int s = sg; s < S; s += SG) {
-            const Corner<float> c = cr[s];
-            ws += c.w;
-            typename IO::raw_t raw = IO::load(col + static_cast<size_t>(c.tok < 0 ? 0 : c.tok) * C);
-            if (c.tok < 0) raw = IO::zero();  // outside the map: contributes exactly 0 (zero padding)
-            float v[V];
-            IO::unpack(raw, v);
-#pragma unroll
-            for (int i = 0; i < V; ++i) acc[i] = fmaf(c.w, v[i], acc[i]);
-        }
+        gather_sum<T, V, NB>(cw + r * S, S, sg, SG, mb + ch * V, static_cast<size_t>(C), acc, ws);
         for (int m = CV; m < GS; m <<= 1) {
 #pragma unroll
             for (int i = 0; i < V; ++i) acc[i] += xor_lane(acc[i], m);
@@ -299,13 +286,19 @@ constexpr size_t kLdsBudget = 65536;
 
 inline bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
-template <typename T, int WAVES>
+template <typename T, int WAVES, int NB>
 int go_vec(const FusedParams& p, size_t lds, hipStream_t stream) {
     const int64_t blocks = static_cast<int64_t>(p.g.B) * p.g.H * p.qtiles;
-    hipLaunchKernelGGL((fused_vec_kernel<T, WAVES>), dim3(static_cast<unsigned>(blocks)), dim3(WAVES * kWave), lds,
-                       stream, p);
+    hipLaunchKernelGGL((fused_vec_kernel<T, WAVES, NB>), dim3(static_cast<unsigned>(blocks)), dim3(WAVES * kWave),
+                       lds, stream, p);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : set_error(-3, "fused_vec launch failed: %s", hipGetErrorString(e));
+}
+
+// nb = corner loads in flight per lane: 8 measured best on MI355X at every benchmark shape; 16 for tuning.
+template <typename T, int WAVES>
+int go_vec_nb(const FusedParams& p, int nb, size_t lds, hipStream_t stream) {
+    return nb == 16 ? go_vec<T, WAVES, 16>(p, lds, stream) : go_vec<T, WAVES, 8>(p, lds, stream);
 }
 
 template <typename T, int WAVES>
@@ -330,12 +323,16 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune) {
                              reinterpret_cast<uintptr_t>(p.w) % 16 == 0 && C % V == 0 && C > 0;
         if (aligned && !tune.generic) {
             const int CV = C / V;
-            const int waves = tune.waves ? tune.waves : 4;
+            // Launch shape (measured on MI355X): small problems want one row per wavefront and one pass per
+            // workgroup (more workgroups in flight); large ones 8-wave workgroups of 16 rows.
+            const int64_t rows = static_cast<int64_t>(g.B) * g.Q * g.H;
+            const bool big = rows >= 8192;
+            const int waves = tune.waves ? tune.waves : big ? 8 : 4;
             const int nth = waves * kWave;
             int sg = tune.sg;
             if (sg <= 0) {
                 sg = 1;
-                if (is_pow2(CV) && CV < kWave) {
+                if (!big && is_pow2(CV) && CV < kWave) {
                     sg = kWave / CV;
                     while (sg > 1 && S / sg < 4) sg >>= 1;
                 }
@@ -343,7 +340,11 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune) {
             if (sg > 1 && !(is_pow2(CV) && is_pow2(sg) && CV * sg <= kWave)) sg = 1;
             const int GS = CV * sg;
             const int rows_per_pass = nth / GS > 0 ? nth / GS : 1;
-            int qt = tune.qt > 0 ? tune.qt : 2 * rows_per_pass;
+            int qt = tune.qt;
+            if (qt <= 0) {
+                qt = big ? 2 * rows_per_pass : rows_per_pass;
+                if (!big && qt > 1 && rows / qt < 300) qt /= 2;
+            }
             if (qt > qmax) qt = qmax;
             if (qt < 1) qt = 1;
             const int NTILE = (D + 15) / 16;
@@ -361,11 +362,12 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune) {
                 p.SG = sg;
                 p.KS = ks;
                 p.qtiles = (g.Q + qt - 1) / qt;
+                const int nb = tune.nb;
                 switch (waves) {
-                    case 1: return go_vec<T, 1>(p, lds(qt), stream);
-                    case 2: return go_vec<T, 2>(p, lds(qt), stream);
-                    case 4: return go_vec<T, 4>(p, lds(qt), stream);
-                    case 8: return go_vec<T, 8>(p, lds(qt), stream);
+                    case 1: return go_vec_nb<T, 1>(p, nb, lds(qt), stream);
+                    case 2: return go_vec_nb<T, 2>(p, nb, lds(qt), stream);
+                    case 4: return go_vec_nb<T, 4>(p, nb, lds(qt), stream);
+                    case 8: return go_vec_nb<T, 8>(p, nb, lds(qt), stream);
                     default: return set_error(-1, "fused: waves must be 1, 2, 4 or 8 (got %d)", waves);
                 }
             }

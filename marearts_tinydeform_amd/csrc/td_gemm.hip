@@ -1,11 +1,10 @@
 // Project mode, first half: value[M, NO] = memory[M, K] . weight[NO, K]^T + bias[NO]
 // (M = B*N tokens, K = C channels, NO = H*D), float32 accumulation, one rounding to the element type.
 //
-// gemm_mfma_kernel (half / bfloat16, K % 8 == 0, 16-byte aligned operands): 128 x 64 output tile per
-// 256-thread workgroup, K in steps of 32 through double-buffered LDS; wavefront w owns rows 32w..32w+31 of the
-// tile (2 x 4 tiles of v_mfma_f32_16x16x32). Tiles are numbered so that the N tiles of one M tile go to the same
-// XCD (workgroups are dealt to the 8 XCDs round-robin), which keeps the memory rows in that XCD's L2.
-// gemm_generic_kernel: any type/alignment (float, double, unaligned 16-bit); 64 x 64 tile, VALU FMAs.
+// gemm_mfma_kernel (half / bfloat16 / float, K a multiple of 16 bytes, 16-byte aligned operands): see below.
+// Tiles are numbered so that the N tiles of one M tile go to the same XCD (workgroups are dealt to the 8 XCDs
+// round-robin), which keeps the memory rows in that XCD's L2.
+// gemm_generic_kernel: double, unaligned or odd-K operands; 64 x 64 tile, VALU FMAs.
 #include "td_internal.h"
 
 namespace td {
@@ -30,30 +29,62 @@ __device__ __forceinline__ int tile_of(const GemmParams& p) {
     return tile < p.mt * p.nt ? tile : -1;
 }
 
+// One 16-byte K block of an MFMA: 16-bit types take one v_mfma_f32_16x16x32 (K = 32 = 4 lane groups x 8),
+// float32 takes four v_mfma_f32_16x16x4_f32 on the components of a float4 (K = 16 = 4 lane groups x 4, lane group
+// g holding k = 4g..4g+3; A and B use the same k order, so the sum covers each k once).
 template <typename T>
-struct Mma16;
+struct KBlock;
 template <>
-struct Mma16<f16> {
-    typedef f16x8 frag;
-    __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+struct KBlock<f16> {
+    static constexpr int kK = 32;
+    __device__ __forceinline__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                      0, 0, 0);
     }
 };
 template <>
-struct Mma16<bf16> {
-    typedef bf16x8 frag;
-    __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+struct KBlock<bf16> {
+    static constexpr int kK = 32;
+    __device__ __forceinline__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       c, 0, 0, 0);
+    }
+};
+template <>
+struct KBlock<float> {
+    static constexpr int kK = 16;
+    __device__ __forceinline__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+        const f32x4 x = __builtin_bit_cast(f32x4, a), y = __builtin_bit_cast(f32x4, b);
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(x[0], y[0], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(x[1], y[1], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(x[2], y[2], c, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(x[3], y[3], c, 0, 0, 0);
     }
 };
 
-template <typename T>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
-    constexpr int BM = 128, BN = 64, BK = 32, LDK = BK + 8;  // LDS row pitch in elements (80 bytes)
-    using MM = Mma16<T>;
-    using frag = typename MM::frag;
-    __shared__ __align__(16) T As[2][BM * LDK];
-    __shared__ __align__(16) T Bs[2][BN * LDK];
+// MFMA GEMM, both operands K-contiguous (C = A . W^T). WM x WN wavefronts per workgroup; wavefront (wm, wn) owns a
+// TM x TN grid of 16x16 output tiles. K advances in chunks of NKB 16-byte blocks:
+//   A  each wavefront loads its own rows straight from global memory into MFMA fragments (one chunk ahead);
+//   W  the workgroup stages the BN x chunk slice in LDS (two buffers, filled from registers one chunk ahead).
+// STAGES = 2 overlaps the next chunk's loads with this chunk's MFMAs; STAGES = 1 (one LDS buffer) suits K that fits
+// one chunk, where the whole product costs a single round trip to memory.
+// Epilogue: bias, one rounding to T, the tile transposed through LDS and written with 16-byte stores.
+template <typename T, int WM, int WN, int TM, int TN, int NKB, int STAGES>
+__global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma_kernel(GemmParams p) {
+    constexpr int NTH = WM * WN * kWave;
+    constexpr int E = 16 / static_cast<int>(sizeof(T));  // elements per 16 bytes
+    constexpr int KBK = KBlock<T>::kK;                   // K per 16-byte block (4 lane groups)
+    constexpr int KC = NKB * KBK;                         // K per chunk
+    constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
+    constexpr int LDK = KC + E;                           // LDS pitch (elements) of a staged W row
+    constexpr int B_CHUNKS = BN * KC / E;                 // 16-byte pieces of one staged W slice
+    constexpr int B_PER_T = (B_CHUNKS + NTH - 1) / NTH;
+    constexpr int LDC = BN + E;                           // LDS pitch of the output tile
+    constexpr size_t kStage = static_cast<size_t>(BN) * LDK * sizeof(T);
+    constexpr size_t kOut = static_cast<size_t>(BM) * LDC * sizeof(T);
+    constexpr size_t kLds = STAGES * kStage > kOut ? STAGES * kStage : kOut;
+    __shared__ __align__(16) unsigned char lds[kLds];
+    auto stage = [&](int i) { return reinterpret_cast<T*>(lds + (STAGES == 2 ? (i & 1) * kStage : 0)); };
 
     const int tile = tile_of(p);
     if (tile < 0) return;
@@ -64,73 +95,124 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     T* __restrict__ Cm = static_cast<T*>(p.c);
     const int M = p.M, K = p.K, NO = p.NO;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    // global -> register staging: A tile = 512 chunks of 8 elements (2 per thread), B tile = 256 chunks
-    u32x4 ra[2], rb;
-    auto gload = [&](int k0) {
+    const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+    const int wm = wave / WN, wn = wave % WN;
+    const int r16 = lane & 15, kg = lane >> 4;
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+
+    // A fragments of one chunk: row m0 + wm*TM*16 + i*16 + r16, k = k0 + j*KBK + kg*E
+    auto load_a = [&](u32x4 (&a)[TM][NKB], int k0) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int cidx = tid + i * 256, row = cidx >> 2, kc = (cidx & 3) * 8;
-            const int gm = m0 + row, gk = k0 + kc;
-            ra[i] = u32x4{0u, 0u, 0u, 0u};
-            if (gm < M && gk < K) ra[i] = *reinterpret_cast<const u32x4*>(A + static_cast<size_t>(gm) * K + gk);
+        for (int i = 0; i < TM; ++i) {
+            const int m = m0 + (wm * TM + i) * 16 + r16;
+#pragma unroll
+            for (int j = 0; j < NKB; ++j) {
+                const int k = k0 + j * KBK + kg * E;
+                a[i][j] = (m < M && k < K) ? *reinterpret_cast<const u32x4*>(A + static_cast<size_t>(m) * K + k) : zero;
+            }
         }
-        const int row = tid >> 2, kc = (tid & 3) * 8;
-        const int gn = n0 + row, gk = k0 + kc;
-        rb = u32x4{0u, 0u, 0u, 0u};
-        if (gn < NO && gk < K) rb = *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(gn) * K + gk);
     };
-    auto sstore = [&](int buf) {
+    u32x4 rb[B_PER_T];
+    auto load_b = [&](int k0) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int cidx = tid + i * 256, row = cidx >> 2, kc = (cidx & 3) * 8;
-            *reinterpret_cast<u32x4*>(&As[buf][row * LDK + kc]) = ra[i];
+        for (int u = 0; u < B_PER_T; ++u) {
+            const int c = tid + u * NTH;
+            const int row = c / (KC / E), kc = (c % (KC / E)) * E;
+            const int n = n0 + row, k = k0 + kc;
+            rb[u] = (c < B_CHUNKS && n < NO && k < K) ? *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(n) * K + k)
+                                                      : zero;
         }
-        const int row = tid >> 2, kc = (tid & 3) * 8;
-        *reinterpret_cast<u32x4*>(&Bs[buf][row * LDK + kc]) = rb;
+    };
+    auto store_b = [&](T* buf) {
+#pragma unroll
+        for (int u = 0; u < B_PER_T; ++u) {
+            const int c = tid + u * NTH;
+            if (c < B_CHUNKS) {
+                const int row = c / (KC / E), kc = (c % (KC / E)) * E;
+                *reinterpret_cast<u32x4*>(buf + row * LDK + kc) = rb[u];
+            }
+        }
     };
 
-    f32x4 acc[2][4];
+    f32x4 acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int nk = (K + BK - 1) / BK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    const int r16 = lane & 15, kg = (lane >> 4) * 8;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) gload((kt + 1) * BK);
-        frag a[2], b[4];
+    const int nc = (K + KC - 1) / KC;
+    auto mma_chunk = [&](const u32x4 (&a)[TM][NKB], const T* bs) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            a[i] = *reinterpret_cast<const frag*>(&As[cur][(wave * 32 + i * 16 + r16) * LDK + kg]);
+        for (int j = 0; j < NKB; ++j) {
+            u32x4 b[TN];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const frag*>(&Bs[cur][(j * 16 + r16) * LDK + kg]);
+            for (int t = 0; t < TN; ++t)
+                b[t] = *reinterpret_cast<const u32x4*>(bs + ((wn * TN + t) * 16 + r16) * LDK + j * KBK + kg * E);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = MM::mma(a[i], b[j], acc[i][j]);
-        if (kt + 1 < nk) sstore(cur ^ 1);
+                for (int t = 0; t < TN; ++t) acc[i][t] = KBlock<T>::mma(a[i][j], b[t], acc[i][t]);
+        }
+    };
+    if constexpr (STAGES == 1) {
+        u32x4 a_cur[TM][NKB];
+        for (int c = 0; c < nc; ++c) {
+            load_a(a_cur, c * KC);
+            load_b(c * KC);
+            if (c > 0) __syncthreads();  // every wavefront is done with the previous chunk's slice
+            store_b(stage(0));
+            __syncthreads();
+            mma_chunk(a_cur, stage(0));
+        }
         __syncthreads();
+    } else {
+        u32x4 a_cur[TM][NKB], a_next[TM][NKB];
+        load_a(a_cur, 0);
+        load_b(0);
+        store_b(stage(0));
+        __syncthreads();
+        for (int c = 0; c < nc; ++c) {
+            const bool more = c + 1 < nc;
+            if (more) {
+                load_a(a_next, (c + 1) * KC);
+                load_b((c + 1) * KC);
+            }
+            mma_chunk(a_cur, stage(c));
+            if (more) store_b(stage(c + 1));
+            __syncthreads();
+            if (more) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < NKB; ++j) a_cur[i][j] = a_next[i][j];
+            }
+        }
     }
 
-    // epilogue: lane holds rows 4*(lane/16)+e of each 16x16 tile, column lane%16
+    // epilogue through LDS (every wavefront has passed the last barrier, so the W buffers are free)
+    T* Ct = reinterpret_cast<T*>(lds);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int n = n0 + j * 16 + r16;
-        if (n >= NO) continue;
-        const float bv = bias != nullptr ? static_cast<float>(bias[n]) : 0.f;
+    for (int t = 0; t < TN; ++t) {
+        const int nl = (wn * TN + t) * 16 + r16;
+        const float bv = (bias != nullptr && n0 + nl < NO) ? static_cast<float>(bias[n0 + nl]) : 0.f;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int m = m0 + wave * 32 + i * 16 + (lane >> 4) * 4 + e;
-                if (m < M) Cm[static_cast<size_t>(m) * NO + n] = static_cast<T>(acc[i][j][e] + bv);
-            }
+            for (int e = 0; e < 4; ++e)
+                Ct[((wm * TM + i) * 16 + kg * 4 + e) * LDC + nl] = static_cast<T>(acc[i][t][e] + bv);
+    }
+    __syncthreads();
+    const bool vec_ok = NO % E == 0 && (reinterpret_cast<uintptr_t>(Cm) % 16) == 0;
+    for (int c = tid; c < BM * (BN / E); c += NTH) {
+        const int row = c / (BN / E), col = (c % (BN / E)) * E;
+        const int m = m0 + row, n = n0 + col;
+        if (m >= M || n >= NO) continue;
+        const T* src = Ct + row * LDC + col;
+        T* dst = Cm + static_cast<size_t>(m) * NO + n;
+        if (vec_ok && n + E <= NO) {
+            *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
+        } else {
+            for (int e = 0; e < E && n + e < NO; ++e) dst[e] = src[e];
         }
     }
 }
@@ -182,41 +264,73 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmParams p) {
     }
 }
 
-template <typename T, bool MFMA>
-int go(GemmParams p, int bm, int bn, hipStream_t stream) {
+template <typename Kernel>
+int go(Kernel kernel, GemmParams p, int bm, int bn, int threads, hipStream_t stream) {
     p.mt = (p.M + bm - 1) / bm;
     p.nt = (p.NO + bn - 1) / bn;
     const int64_t tiles = static_cast<int64_t>(p.mt) * p.nt;
     p.per_xcd = static_cast<int>((tiles + kXcds - 1) / kXcds);
     const unsigned grid = static_cast<unsigned>(static_cast<int64_t>(p.per_xcd) * kXcds);
-    if constexpr (MFMA) {
-        hipLaunchKernelGGL((gemm_mfma_kernel<T>), dim3(grid), dim3(256), 0, stream, p);
-    } else {
-        hipLaunchKernelGGL((gemm_generic_kernel<T>), dim3(grid), dim3(256), 0, stream, p);
-    }
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), 0, stream, p);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : set_error(-3, "value_proj launch failed: %s", hipGetErrorString(e));
 }
 
+template <typename T, int WM, int WN, int TM, int TN, int NKB, int STAGES>
+int go_mfma(GemmParams p, hipStream_t stream) {
+    return go(gemm_mfma_kernel<T, WM, WN, TM, TN, NKB, STAGES>, p, WM * TM * 16, WN * TN * 16, WM * WN * kWave,
+              stream);
+}
+
+// Tile shape by problem size (variant > 0 forces one, for tuning). K per chunk = NKB 16-byte blocks
+// (32 elements each for 16-bit types, 16 for float32).
+//   1  64 x 64   4 waves of 16 x 64,  K chunks of 64/32, two stages
+//   2  64 x 128  4 waves of 16 x 128, K chunks of 64/32, two stages
+//   3  128 x 128 2 x 2 waves of 64 x 64, two stages
+//   4  128 x 64  4 waves of 32 x 64, two stages
+//   5  64 x 64   one chunk of 256/128 (K <= 256 for 16-bit: a single round trip), one stage
+//   6  64 x 128  one chunk of 256/128, one stage
 template <typename T>
-int launch_t(GemmParams p, hipStream_t stream, int force_generic) {
-    if constexpr (sizeof(T) == 2) {
-        const uintptr_t al = reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.w);
-        if (!force_generic && p.K % 8 == 0 && al % 16 == 0) return go<T, true>(p, 128, 64, stream);
+int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
+    if (variant <= 0) {
+        constexpr int one_chunk = 8 * KBlock<T>::kK;
+        const int64_t tiles_64x128 = ((p.M + 63) / 64) * static_cast<int64_t>((p.NO + 127) / 128);
+        if (p.K <= one_chunk)
+            variant = tiles_64x128 >= 1024 ? 6 : 5;
+        else
+            variant = 2;
     }
-    return go<T, false>(p, 64, 64, stream);
+    switch (variant) {
+        case 1: return go_mfma<T, 4, 1, 1, 4, 2, 2>(p, stream);
+        case 2: return go_mfma<T, 4, 1, 1, 8, 2, 2>(p, stream);
+        case 3: return go_mfma<T, 2, 2, 4, 4, 2, 2>(p, stream);
+        case 4: return go_mfma<T, 4, 1, 2, 4, 2, 2>(p, stream);
+        case 5: return go_mfma<T, 4, 1, 1, 4, 8, 1>(p, stream);
+        case 6: return go_mfma<T, 4, 1, 1, 8, 8, 1>(p, stream);
+        default: return set_error(-1, "value_proj: unknown tile variant %d", variant);
+    }
+}
+
+template <typename T>
+int launch_t(GemmParams p, hipStream_t stream, int variant) {
+    if constexpr (!std::is_same<T, double>::value) {
+        constexpr int E = 16 / static_cast<int>(sizeof(T));
+        const uintptr_t al = reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.w);
+        if (variant >= 0 && p.K % E == 0 && al % 16 == 0) return launch_mfma<T>(p, stream, variant);
+    }
+    return go(gemm_generic_kernel<T>, p, 64, 64, 256, stream);
 }
 
 }  // namespace
 
 int launch_value_proj(int dtype, const void* a, const void* w, const void* bias, void* c, int64_t M, int64_t K,
-                      int64_t NO, hipStream_t stream, int force_generic) {
+                      int64_t NO, hipStream_t stream, int variant) {
     GemmParams p{a, w, bias, c, static_cast<int>(M), static_cast<int>(K), static_cast<int>(NO), 0, 0, 0};
     switch (dtype) {
-        case kF32: return launch_t<float>(p, stream, force_generic);
-        case kF16: return launch_t<f16>(p, stream, force_generic);
-        case kBF16: return launch_t<bf16>(p, stream, force_generic);
-        case kF64: return launch_t<double>(p, stream, force_generic);
+        case kF32: return launch_t<float>(p, stream, variant);
+        case kF16: return launch_t<f16>(p, stream, variant);
+        case kBF16: return launch_t<bf16>(p, stream, variant);
+        case kF64: return launch_t<double>(p, stream, variant);
         default: return set_error(-2, "unknown dtype code %d", dtype);
     }
 }

@@ -17,6 +17,7 @@ struct FusedTune {
     int qt = 0;     // query rows per workgroup (1..16)
     int sg = 0;     // corner split per row (power of two)
     int waves = 0;  // wavefronts per workgroup (1, 2, 4 or 8)
+    int nb = 0;     // corner loads in flight per lane (8 or 16)
     int generic = 0;  // 1 forces the generic kernel
 };
 
@@ -25,6 +26,7 @@ struct SampleTune {
     int sg = 0;
     int waves = 0;
     int vec = 0;  // elements per load
+    int nb = 0;   // corner loads in flight per lane (8 or 16)
 };
 
 // Every launcher returns 0, or a negative TD_E* code after recording a message with set_error.
@@ -36,8 +38,9 @@ int launch_fused(int dtype, const void* mem, const void* w, const void* bias, co
 int launch_sample(int dtype, const void* value, const Geom& g, const void* loc, const void* attn, void* out,
                   hipStream_t stream, const SampleTune& tune);
 
+// variant: 0 picks the tile shape by size, > 0 forces an MFMA tile variant, -1 forces the generic kernel.
 int launch_value_proj(int dtype, const void* a, const void* w, const void* bias, void* c, int64_t M, int64_t K,
-                      int64_t NO, hipStream_t stream, int force_generic);
+                      int64_t NO, hipStream_t stream, int variant);
 
 int launch_zero(void* out, int64_t bytes, hipStream_t stream);
 

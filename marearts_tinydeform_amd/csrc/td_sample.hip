@@ -21,7 +21,7 @@ struct SampleParams {
     int64_t rows;
 };
 
-template <typename T, int V, int WAVES>
+template <typename T, int V, int WAVES, int NB>
 __global__ __launch_bounds__(WAVES* kWave) void sample_kernel(SampleParams p) {
     constexpr int NTH = WAVES * kWave;
     using IO = VecIO<T, V>;
@@ -60,20 +60,11 @@ __global__ __launch_bounds__(WAVES* kWave) void sample_kernel(SampleParams p) {
         const int64_t b = valid ? row / QH : 0;
         const int h = valid ? static_cast<int>(row % g.H) : 0;
         const T* base = value + static_cast<size_t>(b) * g.N * HD + static_cast<size_t>(h) * D + ch * V;
-        const Corner<float>* cr = cw + r * S;
         float acc[V];
 #pragma unroll
         for (int i = 0; i < V; ++i) acc[i] = 0.f;
-#pragma unroll 8
-        for (int s = sg; s < S; s += SG) {
-            const Corner<float> c = cr[s];
-            typename IO::raw_t raw = IO::load(base + static_cast<size_t>(c.tok < 0 ? 0 : c.tok) * HD);
-            if (c.tok < 0) raw = IO::zero();
-            float v[V];
-            IO::unpack(raw, v);
-#pragma unroll
-            for (int i = 0; i < V; ++i) acc[i] = fmaf(c.w, v[i], acc[i]);
-        }
+        float ws = 0.f;
+        gather_sum<T, V, NB>(cw + r * S, S, sg, SG, base, static_cast<size_t>(HD), acc, ws);
         for (int m = DV; m < GS; m <<= 1) {
 #pragma unroll
             for (int i = 0; i < V; ++i) acc[i] += xor_lane(acc[i], m);
@@ -129,21 +120,27 @@ constexpr size_t kLdsBudget = 65536;
 
 inline bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
-template <typename T, int V, int WAVES>
+template <typename T, int V, int WAVES, int NB>
 int go(SampleParams p, size_t lds, hipStream_t stream) {
     const int64_t blocks = (p.rows + p.RB - 1) / p.RB;
-    hipLaunchKernelGGL((sample_kernel<T, V, WAVES>), dim3(static_cast<unsigned>(blocks)), dim3(WAVES * kWave), lds,
+    hipLaunchKernelGGL((sample_kernel<T, V, WAVES, NB>), dim3(static_cast<unsigned>(blocks)), dim3(WAVES * kWave), lds,
                        stream, p);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : set_error(-3, "sample launch failed: %s", hipGetErrorString(e));
 }
 
+// nb = corner loads in flight per lane: 8 measured best on MI355X; 16 for tuning.
+template <typename T, int V, int WAVES>
+int go_nb(SampleParams p, int nb, size_t lds, hipStream_t stream) {
+    return nb == 16 ? go<T, V, WAVES, 16>(p, lds, stream) : go<T, V, WAVES, 8>(p, lds, stream);
+}
+
 template <typename T, int V>
-int go_waves(SampleParams p, int waves, size_t lds, hipStream_t stream) {
+int go_waves(SampleParams p, int waves, int nb, size_t lds, hipStream_t stream) {
     switch (waves) {
-        case 1: return go<T, V, 1>(p, lds, stream);
-        case 2: return go<T, V, 2>(p, lds, stream);
-        case 4: return go<T, V, 4>(p, lds, stream);
+        case 1: return go_nb<T, V, 1>(p, nb, lds, stream);
+        case 2: return go_nb<T, V, 2>(p, nb, lds, stream);
+        case 4: return go_nb<T, V, 4>(p, nb, lds, stream);
         default: return set_error(-1, "sample: waves must be 1, 2 or 4 (got %d)", waves);
     }
 }
@@ -159,22 +156,20 @@ int launch_sample_t(SampleParams p, hipStream_t stream, const SampleTune& tune) 
     if (V > VMAX || D % V != 0 || align % (V * sizeof(T)) != 0)
         return set_error(-1, "sample: %d elements per load do not fit D=%d and the pointer alignment", V, D);
     const int DV = D / V;
+    // Launch shape (measured on MI355X): up to 8 corner groups per row, at least 4 corners per lane;
+    // 2-wave workgroups for small problems, 1-wave ones for large.
     int sg = tune.sg;
     if (sg <= 0) {
         sg = 1;
         if (is_pow2(DV) && DV < kWave) {
-            sg = kWave / DV;
-            while (sg > 1 && S / sg < 8) sg >>= 1;
+            sg = kWave / DV < 8 ? kWave / DV : 8;
+            while (sg > 1 && S / sg < 4) sg >>= 1;
         }
     }
     if (sg > 1 && !(is_pow2(DV) && is_pow2(sg) && DV * sg <= kWave)) sg = 1;
     const int GS = DV * sg;
     int waves = tune.waves;
-    if (waves <= 0) {
-        // small problems: single-wavefront workgroups so that more CUs get work
-        const int64_t lanes = p.rows * GS;
-        waves = lanes >= int64_t(256) * 64 * 8 ? 4 : 1;
-    }
+    if (waves <= 0) waves = p.rows <= 12000 ? 2 : 1;
     const int nth = waves * kWave;
     int rb = nth / GS;
     if (rb < 1) rb = 1;
@@ -182,12 +177,13 @@ int launch_sample_t(SampleParams p, hipStream_t stream, const SampleTune& tune) 
     while (rb > 1 && lds(rb) > kLdsBudget) --rb;
     p.RB = rb;
     p.SG = sg;
+    const int nb = tune.nb;
     switch (V) {
-        case 1: return go_waves<T, 1>(p, waves, lds(rb), stream);
-        case 2: return go_waves<T, 2>(p, waves, lds(rb), stream);
-        case 4: return go_waves<T, 4>(p, waves, lds(rb), stream);
+        case 1: return go_waves<T, 1>(p, waves, nb, lds(rb), stream);
+        case 2: return go_waves<T, 2>(p, waves, nb, lds(rb), stream);
+        case 4: return go_waves<T, 4>(p, waves, nb, lds(rb), stream);
         case 8:
-            if constexpr (VMAX >= 8) return go_waves<T, 8>(p, waves, lds(rb), stream);
+            if constexpr (VMAX >= 8) return go_waves<T, 8>(p, waves, nb, lds(rb), stream);
             break;
         default: break;
     }

@@ -66,10 +66,28 @@ def test_auto_limits_follow_the_gpu_architecture(monkeypatch):
     assert td.ARCH_LIMITS['gfx950'] is td.FUSED_LIMIT
 
 
-def test_fused_limit_tables_are_sane():
+def test_cost_tables_are_sane():
     for dtype in (torch.float32, torch.float16, torch.bfloat16):
-        a, b = td.FUSED_LIMIT[dtype]
-        assert a >= 0 and b >= 0
+        coef = td.FUSED_LIMIT[dtype]
+        assert len(coef['fused']) == 2 and len(coef['project']) == 4
+        assert all(c >= 0 for c in coef['fused'] + coef['project'])
+
+
+def test_auto_crossover_moves_with_queries_batch_and_channels():
+    # RT-DETR 640, 16-bit: fused at batch 1 up to 600 queries, project at 900; batch 8 switches earlier;
+    # C=1024 / 16 heads / 64 samples (the limit shape) switches to project by 300 queries
+    def pick(B, Q, H, D, C, levels, P, dtype=torch.float16):
+        mem = torch.empty(B, sum(h * w for h, w in levels), C, dtype=dtype)
+        w = torch.empty(H * D, C, dtype=dtype)
+        loc = torch.empty(B, Q, H, len(levels), P, 2, dtype=dtype)
+        return td.choose_mode(mem, w, loc)
+    assert pick(1, 300, 8, 32, 256, RTDETR_LEVELS, 4) == 'fused'
+    assert pick(1, 600, 8, 32, 256, RTDETR_LEVELS, 4) == 'fused'
+    assert pick(1, 900, 8, 32, 256, RTDETR_LEVELS, 4) == 'project'
+    assert pick(8, 900, 8, 32, 256, RTDETR_LEVELS, 4) == 'project'
+    limit = [(128, 128), (64, 64), (32, 32), (16, 16)]
+    assert pick(2, 50, 16, 64, 1024, limit, 16, torch.bfloat16) == 'fused'
+    assert pick(2, 300, 16, 64, 1024, limit, 16, torch.bfloat16) == 'project'
 
 
 # ---- host validation (same rules and messages as the reference's host checks) ---------------------------------

@@ -174,7 +174,9 @@ def test_value_proj_matches_oracle():
     # the GEMM alone, with M, N, K off the tile sizes
     g = torch.Generator().manual_seed(3)
     for dtype in (torch.float16, torch.bfloat16, torch.float32, torch.float64):
-        for (B, N, C, HD) in ((1, 8400, 256, 256), (2, 77, 40, 48), (1, 130, 96, 72), (3, 5, 8, 16)):
+        # tile variants by size: small (1 x 8400), medium (4 x 9000), large (2 x 8192 x 1024 outputs), ragged edges
+        for (B, N, C, HD) in ((1, 8400, 256, 256), (4, 9000, 256, 256), (2, 8192, 128, 1024), (2, 77, 40, 48),
+                              (1, 130, 96, 72), (3, 5, 8, 16), (1, 33, 1024, 64)):
             mem = torch.randn(B, N, C, generator=g).to(dtype)
             w = (torch.randn(HD, C, generator=g) / C ** 0.5).to(dtype)
             b = (torch.randn(HD, generator=g) * 0.1).to(dtype)
