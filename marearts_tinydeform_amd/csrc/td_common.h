@@ -8,6 +8,7 @@
 namespace td {
 
 constexpr int kWave = 64;
+constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (each with its own L2) round-robin
 constexpr int kMaxLevelPoints = 64;  // L * P per head (reference csrc/ma_deform_fused.cu:27)
 constexpr int kMaxChannels = 8192;   // C in fused mode (reference csrc/ma_deform_fused.cu:28)
 

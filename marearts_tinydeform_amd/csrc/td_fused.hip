@@ -33,6 +33,7 @@ struct FusedParams {
     void* out;
     Geom g;
     int C, QT, SG, KS, qtiles;
+    int per_xcd, units;  // work-unit mapping (decode_block)
 };
 
 template <typename T>
@@ -52,14 +53,20 @@ struct MfmaOp<bf16> {
     }
 };
 
-// Workgroup index -> (b, query tile, h), heads fastest.
+// Workgroup index -> work unit (b, query tile, h) with heads fastest. Workgroups are dealt to the 8 XCDs
+// round-robin, so unit = (bid % 8) * per_xcd + bid / 8 gives each XCD a contiguous range of units: with a batch of
+// 8 images each XCD's L2 holds one image's memory rows instead of all eight. valid = false for the at most 7
+// workgroups past the last unit.
 struct BlockRow {
     int b, qt, h;
+    bool valid;
 };
-__device__ __forceinline__ BlockRow decode_block(int bid, int H, int qtiles) {
+__device__ __forceinline__ BlockRow decode_block(int bid, int H, int qtiles, int per_xcd, int units) {
+    const int unit = (bid % kXcds) * per_xcd + bid / kXcds;
     BlockRow r;
-    r.h = bid % H;
-    const int rest = bid / H;
+    r.valid = unit < units;
+    r.h = unit % H;
+    const int rest = unit / H;
     r.qt = rest % qtiles;
     r.b = rest / qtiles;
     return r;
@@ -89,7 +96,8 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     T* __restrict__ out = static_cast<T*>(p.out);
 
     const int tid = threadIdx.x;
-    const BlockRow br = decode_block(blockIdx.x, g.H, p.qtiles);
+    const BlockRow br = decode_block(blockIdx.x, g.H, p.qtiles, p.per_xcd, p.units);
+    if (!br.valid) return;
     const int q0 = br.qt * QT;
 
     // phase 1: corner table
@@ -232,7 +240,8 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_generic_kernel(FusedParams
     T* __restrict__ out = static_cast<T*>(p.out);
 
     const int tid = threadIdx.x;
-    const BlockRow br = decode_block(blockIdx.x, g.H, p.qtiles);
+    const BlockRow br = decode_block(blockIdx.x, g.H, p.qtiles, p.per_xcd, p.units);
+    if (!br.valid) return;
     const int q0 = br.qt * QT;
 
     for (int i = tid; i < QT * LP; i += NTH) {
@@ -286,9 +295,17 @@ constexpr size_t kLdsBudget = 65536;
 
 inline bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
+// Sets the work-unit mapping and returns the grid size (a multiple of the XCD count).
+inline int64_t map_units(FusedParams& p) {
+    const int64_t units = static_cast<int64_t>(p.g.B) * p.g.H * p.qtiles;
+    p.units = static_cast<int>(units);
+    p.per_xcd = static_cast<int>((units + kXcds - 1) / kXcds);
+    return static_cast<int64_t>(p.per_xcd) * kXcds;
+}
+
 template <typename T, int WAVES, int NB>
-int go_vec(const FusedParams& p, size_t lds, hipStream_t stream) {
-    const int64_t blocks = static_cast<int64_t>(p.g.B) * p.g.H * p.qtiles;
+int go_vec(FusedParams p, size_t lds, hipStream_t stream) {
+    const int64_t blocks = map_units(p);
     hipLaunchKernelGGL((fused_vec_kernel<T, WAVES, NB>), dim3(static_cast<unsigned>(blocks)), dim3(WAVES * kWave),
                        lds, stream, p);
     const hipError_t e = hipGetLastError();
@@ -302,8 +319,8 @@ int go_vec_nb(const FusedParams& p, int nb, size_t lds, hipStream_t stream) {
 }
 
 template <typename T, int WAVES>
-int go_generic(const FusedParams& p, size_t lds, hipStream_t stream) {
-    const int64_t blocks = static_cast<int64_t>(p.g.B) * p.g.H * p.qtiles;
+int go_generic(FusedParams p, size_t lds, hipStream_t stream) {
+    const int64_t blocks = map_units(p);
     hipLaunchKernelGGL((fused_generic_kernel<T, WAVES>), dim3(static_cast<unsigned>(blocks)), dim3(WAVES * kWave),
                        lds, stream, p);
     const hipError_t e = hipGetLastError();
@@ -395,7 +412,7 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune) {
 
 int launch_fused(int dtype, const void* mem, const void* w, const void* bias, const Geom& g, int C, const void* loc,
                  const void* attn, void* out, hipStream_t stream, const FusedTune& tune) {
-    FusedParams p{mem, w, bias, loc, attn, out, g, C, 1, 1, 1, 1};
+    FusedParams p{mem, w, bias, loc, attn, out, g, C, 1, 1, 1, 1, 0, 0};
     switch (dtype) {
         case kF32: return launch_fused_t<float>(p, stream, tune);
         case kF16: return launch_fused_t<f16>(p, stream, tune);

@@ -10,8 +10,6 @@
 namespace td {
 namespace {
 
-constexpr int kXcds = 8;
-
 struct GemmParams {
     const void* a;
     const void* w;
@@ -293,12 +291,11 @@ int go_mfma(GemmParams p, hipStream_t stream) {
 template <typename T>
 int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
     if (variant <= 0) {
+        // measured on MI355X: one round trip (5) wins while the grid is small; 64 x 128 double-buffered (2) wins
+        // once there are >= 1024 of its tiles or K spans several chunks
         constexpr int one_chunk = 8 * KBlock<T>::kK;
         const int64_t tiles_64x128 = ((p.M + 63) / 64) * static_cast<int64_t>((p.NO + 127) / 128);
-        if (p.K <= one_chunk)
-            variant = tiles_64x128 >= 1024 ? 6 : 5;
-        else
-            variant = 2;
+        variant = (p.K <= one_chunk && tiles_64x128 < 1024) ? 5 : 2;
     }
     switch (variant) {
         case 1: return go_mfma<T, 4, 1, 1, 4, 2, 2>(p, stream);

@@ -19,6 +19,7 @@ struct SampleParams {
     Geom g;
     int RB, SG;
     int64_t rows;
+    int per_xcd, blocks;  // workgroup -> row-block mapping: XCD x takes a contiguous range of row blocks
 };
 
 template <typename T, int V, int WAVES, int NB>
@@ -37,7 +38,9 @@ __global__ __launch_bounds__(WAVES* kWave) void sample_kernel(SampleParams p) {
     T* __restrict__ out = static_cast<T*>(p.out);
 
     const int tid = threadIdx.x;
-    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * RB;
+    const int rblock = (blockIdx.x % kXcds) * p.per_xcd + blockIdx.x / kXcds;
+    if (rblock >= p.blocks) return;
+    const int64_t row0 = static_cast<int64_t>(rblock) * RB;
 
     for (int i = tid; i < RB * LP; i += NTH) {
         const int r = i / LP, j = i - r * LP;
@@ -123,8 +126,10 @@ inline bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 template <typename T, int V, int WAVES, int NB>
 int go(SampleParams p, size_t lds, hipStream_t stream) {
     const int64_t blocks = (p.rows + p.RB - 1) / p.RB;
-    hipLaunchKernelGGL((sample_kernel<T, V, WAVES, NB>), dim3(static_cast<unsigned>(blocks)), dim3(WAVES * kWave), lds,
-                       stream, p);
+    p.blocks = static_cast<int>(blocks);
+    p.per_xcd = static_cast<int>((blocks + kXcds - 1) / kXcds);
+    hipLaunchKernelGGL((sample_kernel<T, V, WAVES, NB>), dim3(static_cast<unsigned>(p.per_xcd) * kXcds),
+                       dim3(WAVES * kWave), lds, stream, p);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : set_error(-3, "sample launch failed: %s", hipGetErrorString(e));
 }
@@ -156,20 +161,22 @@ int launch_sample_t(SampleParams p, hipStream_t stream, const SampleTune& tune) 
     if (V > VMAX || D % V != 0 || align % (V * sizeof(T)) != 0)
         return set_error(-1, "sample: %d elements per load do not fit D=%d and the pointer alignment", V, D);
     const int DV = D / V;
-    // Launch shape (measured on MI355X): up to 8 corner groups per row, at least 4 corners per lane;
-    // 2-wave workgroups for small problems, 1-wave ones for large.
+    // Launch shape (measured on MI355X): small problems want 8 corner groups per row and 2-wave workgroups, large
+    // ones (>= 12k rows) 4 corner groups and 1-wave workgroups; at least 4 corners per lane.
+    const bool big = p.rows >= 12000;
     int sg = tune.sg;
     if (sg <= 0) {
         sg = 1;
         if (is_pow2(DV) && DV < kWave) {
-            sg = kWave / DV < 8 ? kWave / DV : 8;
+            const int cap = big ? 4 : 8;
+            sg = kWave / DV < cap ? kWave / DV : cap;
             while (sg > 1 && S / sg < 4) sg >>= 1;
         }
     }
     if (sg > 1 && !(is_pow2(DV) && is_pow2(sg) && DV * sg <= kWave)) sg = 1;
     const int GS = DV * sg;
     int waves = tune.waves;
-    if (waves <= 0) waves = p.rows <= 12000 ? 2 : 1;
+    if (waves <= 0) waves = big ? 1 : 2;
     const int nth = waves * kWave;
     int rb = nth / GS;
     if (rb < 1) rb = 1;
@@ -207,7 +214,7 @@ int launch_sample_f64(SampleParams p, hipStream_t stream) {
 
 int launch_sample(int dtype, const void* value, const Geom& g, const void* loc, const void* attn, void* out,
                   hipStream_t stream, const SampleTune& tune) {
-    SampleParams p{value, loc, attn, out, g, 1, 1, static_cast<int64_t>(g.B) * g.Q * g.H};
+    SampleParams p{value, loc, attn, out, g, 1, 1, static_cast<int64_t>(g.B) * g.Q * g.H, 0, 0};
     switch (dtype) {
         case kF32: return launch_sample_t<float>(p, stream, tune);
         case kF16: return launch_sample_t<f16>(p, stream, tune);
