@@ -78,6 +78,24 @@ int td_sample_forward(int dtype, const void* value, const int64_t* spatial_shape
                       int64_t D, int64_t L, int64_t P, void* stream);
 
 /*
+ * td_fused_forward / td_sample_forward with a value padding mask: padding_mask is a device array of B*N bytes,
+ * non-zero marking a padded token whose value row is zero (value.masked_fill(padding_mask[..., None], 0) after the
+ * projection, as Deformable-DETR decoders do); NULL means no mask. A corner on a padded token contributes nothing,
+ * bias share included. No counterpart in the reference, which does not support a padding mask (README.md:62);
+ * needed by batches of images padded to one size.
+ */
+int td_fused_forward_masked(int dtype, const void* memory, const void* value_weight, const void* value_bias,
+                            const int64_t* spatial_shapes, const int64_t* level_start_index,
+                            const void* sampling_locations, const void* attention_weights,
+                            const uint8_t* padding_mask, void* out, int64_t B, int64_t Q, int64_t N, int64_t C,
+                            int64_t H, int64_t D, int64_t L, int64_t P, void* stream);
+
+int td_sample_forward_masked(int dtype, const void* value, const int64_t* spatial_shapes,
+                             const int64_t* level_start_index, const void* sampling_locations,
+                             const void* attention_weights, const uint8_t* padding_mask, void* out, int64_t B,
+                             int64_t Q, int64_t N, int64_t H, int64_t D, int64_t L, int64_t P, void* stream);
+
+/*
  * Value projection (the first half of project mode): value[M, NO] = memory[M, K] @ weight[NO, K]^T + bias[NO],
  * float32 accumulation, one rounding to dtype. M = B*N tokens, K = C, NO = H*D.
  * Replaces the reference's F.linear(memory, value_weight, value_bias) call (marearts_tinydeform/__init__.py:77).

@@ -85,7 +85,7 @@ def _on_device(t, fn, *args):
 
 
 def ma_deform_attn(memory, value_weight, value_bias, spatial_shapes, level_start_index,
-                   sampling_locations, attention_weights, mode='auto'):
+                   sampling_locations, attention_weights, mode='auto', padding_mask=None):
     """value = memory @ value_weight.T + value_bias, then multi-scale deformable attention; [B, Q, H * D].
 
     Same arguments, shapes and result as ma_deform_attn_reference (grid_sample, bilinear, zero padding,
@@ -94,40 +94,47 @@ def ma_deform_attn(memory, value_weight, value_bias, spatial_shapes, level_start
       mode='fused'    gather the sampled memory rows first, then project per (query, head) on MFMA
       mode='project'  project all tokens (the library's MFMA GEMM), then sample
       mode='auto'     choose_mode() picks one by size (default)
+    padding_mask: optional bool [B, N], True for padded tokens, whose value is zero
+    (value.masked_fill(padding_mask[..., None], 0) after the projection, as Deformable-DETR decoders do; HF RT-DETR
+    passes ~attention_mask). Not in the reference operator, which has no mask.
     CPU tensors run the reference. Inference only: inputs that require grad are rejected.
     """
     if mode not in MODES:
         raise ValueError(f'mode must be one of {MODES}, got {mode!r}')
     if not memory.is_cuda:
         return ma_deform_attn_reference(memory, value_weight, value_bias, spatial_shapes, level_start_index,
-                                        sampling_locations, attention_weights)
+                                        sampling_locations, attention_weights, padding_mask=padding_mask)
     _native._require()
     _reject_grad(memory, value_weight, value_bias, sampling_locations, attention_weights)
     if mode == 'auto':
         mode = choose_mode(memory, value_weight, sampling_locations)
     if mode == 'fused':
         return _on_device(memory, _native.fused_forward, memory, value_weight, value_bias, spatial_shapes,
-                          level_start_index, sampling_locations, attention_weights)
+                          level_start_index, sampling_locations, attention_weights, padding_mask)
     return _on_device(memory, _project, memory, value_weight, value_bias, spatial_shapes, level_start_index,
-                      sampling_locations, attention_weights)
+                      sampling_locations, attention_weights, padding_mask)
 
 
 def _project(memory, value_weight, value_bias, spatial_shapes, level_start_index, sampling_locations,
-             attention_weights):
+             attention_weights, padding_mask):
     H = sampling_locations.shape[2] if sampling_locations.dim() == 6 else 0
     _native.check_geometry(memory, spatial_shapes, level_start_index, sampling_locations, attention_weights)
+    _native.check_padding_mask(memory, padding_mask)
     value = _native.value_proj(memory, value_weight, value_bias)
-    return _native.sample_forward(value, H, spatial_shapes, level_start_index, sampling_locations, attention_weights)
+    # padded tokens: the sampler drops their corners, the same as zeroing their value rows
+    return _native.sample_forward(value, H, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+                                  padding_mask)
 
 
-def ma_deform_sample(value, spatial_shapes, level_start_index, sampling_locations, attention_weights):
+def ma_deform_sample(value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+                     padding_mask=None):
     """Multi-scale deformable attention on already projected values [B, N, H * D] -> [B, Q, H * D].
 
-    The sampling half of mode='project' on its own (for decoders whose value projection is done elsewhere).
-    GPU tensors only.
+    The sampling half of mode='project' on its own (for decoders whose value projection is done elsewhere, e.g.
+    D-FINE). padding_mask as in ma_deform_attn. GPU tensors only.
     """
     _native._require()
     _reject_grad(value, sampling_locations, attention_weights)
     H = sampling_locations.shape[2] if sampling_locations.dim() == 6 else 0
     return _on_device(value, _native.sample_forward, value, H, spatial_shapes, level_start_index,
-                      sampling_locations, attention_weights)
+                      sampling_locations, attention_weights, padding_mask)

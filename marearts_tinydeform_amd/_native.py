@@ -27,6 +27,8 @@ SIGNATURES = {
     'td_last_error': (ctypes.c_char_p, []),
     'td_fused_forward': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 8 + [_vp]),
     'td_sample_forward': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 7 + [_vp]),
+    'td_fused_forward_masked': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 8 + [_vp]),
+    'td_sample_forward_masked': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 7 + [_vp]),
     'td_value_proj': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
 }
 
@@ -131,12 +133,26 @@ def check_projection(memory, weight, bias, H=None):
     return HD
 
 
-def fused_forward(memory, weight, bias, spatial_shapes, level_start_index, sampling_locations, attention_weights):
+def check_padding_mask(ref, padding_mask):
+    """padding_mask: None or bool/uint8 [B, N] on the device of ref (non-zero = padded token); returns it contiguous
+    as uint8 bytes, or None."""
+    if padding_mask is None:
+        return None
+    if padding_mask.dtype not in (torch.bool, torch.uint8) or padding_mask.shape != ref.shape[:2]:
+        raise RuntimeError('padding_mask must be bool [B, N] like memory / value')
+    if padding_mask.device != ref.device:
+        raise RuntimeError('all tensors must be on the same device')
+    return padding_mask.contiguous()
+
+
+def fused_forward(memory, weight, bias, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+                  padding_mask=None):
     """Fused mode (replaces the reference's _C.fused_forward, csrc/ma_deform_fused.cu:291-325)."""
     lib_ = _require()
     B, Q, H, L, P = check_geometry(memory, spatial_shapes, level_start_index, sampling_locations, attention_weights)
     N, C = memory.size(1), memory.size(2)
     HD = check_projection(memory, weight, bias, H)
+    mask = check_padding_mask(memory, padding_mask)
     if C > MAX_CHANNELS:
         raise RuntimeError(f'channels must be <= {MAX_CHANNELS}')
     dev = memory.device
@@ -147,19 +163,21 @@ def fused_forward(memory, weight, bias, spatial_shapes, level_start_index, sampl
     out = torch.empty((B, Q, HD), dtype=memory.dtype, device=dev)
     if out.numel() == 0:
         return out
-    _check(lib_.td_fused_forward(DTYPE_CODES[memory.dtype], mem.data_ptr(), w.data_ptr(), _ptr(b), sh.data_ptr(),
-                                 st.data_ptr(), lc.data_ptr(), aw.data_ptr(), out.data_ptr(), B, Q, N, C, H, HD // H,
-                                 L, P, _stream(dev)))
+    _check(lib_.td_fused_forward_masked(DTYPE_CODES[memory.dtype], mem.data_ptr(), w.data_ptr(), _ptr(b),
+                                        sh.data_ptr(), st.data_ptr(), lc.data_ptr(), aw.data_ptr(), _ptr(mask),
+                                        out.data_ptr(), B, Q, N, C, H, HD // H, L, P, _stream(dev)))
     return out
 
 
-def sample_forward(value, heads, spatial_shapes, level_start_index, sampling_locations, attention_weights):
+def sample_forward(value, heads, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+                   padding_mask=None):
     """Sampling of projected values (replaces the reference's _C.sample_forward, csrc/ma_deform_fused.cu:327-350)."""
     lib_ = _require()
     B, Q, H, L, P = check_geometry(value, spatial_shapes, level_start_index, sampling_locations, attention_weights)
     N, HD = value.size(1), value.size(2)
     if heads != H or HD % H != 0:
         raise RuntimeError('value must be [B, N, H * D] with H = sampling_locations.size(2)')
+    mask = check_padding_mask(value, padding_mask)
     dev = value.device
     v = value.contiguous()
     lc, aw = sampling_locations.contiguous(), attention_weights.contiguous()
@@ -167,9 +185,9 @@ def sample_forward(value, heads, spatial_shapes, level_start_index, sampling_loc
     out = torch.empty((B, Q, HD), dtype=value.dtype, device=dev)
     if out.numel() == 0:
         return out
-    _check(lib_.td_sample_forward(DTYPE_CODES[value.dtype], v.data_ptr(), sh.data_ptr(), st.data_ptr(),
-                                  lc.data_ptr(), aw.data_ptr(), out.data_ptr(), B, Q, N, H, HD // H, L, P,
-                                  _stream(dev)))
+    _check(lib_.td_sample_forward_masked(DTYPE_CODES[value.dtype], v.data_ptr(), sh.data_ptr(), st.data_ptr(),
+                                         lc.data_ptr(), aw.data_ptr(), _ptr(mask), out.data_ptr(), B, Q, N, H, HD // H,
+                                         L, P, _stream(dev)))
     return out
 
 

@@ -84,11 +84,12 @@ extern "C" int td_version(void) { return 100; }
 
 extern "C" const char* td_last_error(void) { return g_last_error.c_str(); }
 
-extern "C" int td_fused_forward(int dtype, const void* memory, const void* value_weight, const void* value_bias,
-                                const int64_t* spatial_shapes, const int64_t* level_start_index,
-                                const void* sampling_locations, const void* attention_weights, void* out, int64_t B,
-                                int64_t Q, int64_t N, int64_t C, int64_t H, int64_t D, int64_t L, int64_t P,
-                                void* stream) {
+extern "C" int td_fused_forward_masked(int dtype, const void* memory, const void* value_weight,
+                                       const void* value_bias, const int64_t* spatial_shapes,
+                                       const int64_t* level_start_index, const void* sampling_locations,
+                                       const void* attention_weights, const uint8_t* padding_mask, void* out,
+                                       int64_t B, int64_t Q, int64_t N, int64_t C, int64_t H, int64_t D, int64_t L,
+                                       int64_t P, void* stream) {
     int rc = check_geometry(dtype, B, Q, N, H, D, L, P, spatial_shapes, level_start_index, sampling_locations,
                             attention_weights, out);
     if (rc != TD_OK) return rc;
@@ -101,16 +102,17 @@ extern "C" int td_fused_forward(int dtype, const void* memory, const void* value
     // no tokens: every corner is outside, so the output is exactly zero (the bias share included)
     if (N == 0 || L * P == 0) return launch_zero(out, bytes, s);
     const Geom g{spatial_shapes, level_start_index, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N),
-                 static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), static_cast<int>(P)};
+                 static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), static_cast<int>(P), padding_mask};
     FusedTune tune;
     return launch_fused(dtype, memory, value_weight, value_bias, g, static_cast<int>(C), sampling_locations,
                         attention_weights, out, s, tune);
 }
 
-extern "C" int td_sample_forward(int dtype, const void* value, const int64_t* spatial_shapes,
-                                 const int64_t* level_start_index, const void* sampling_locations,
-                                 const void* attention_weights, void* out, int64_t B, int64_t Q, int64_t N,
-                                 int64_t H, int64_t D, int64_t L, int64_t P, void* stream) {
+extern "C" int td_sample_forward_masked(int dtype, const void* value, const int64_t* spatial_shapes,
+                                        const int64_t* level_start_index, const void* sampling_locations,
+                                        const void* attention_weights, const uint8_t* padding_mask, void* out,
+                                        int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D, int64_t L, int64_t P,
+                                        void* stream) {
     int rc = check_geometry(dtype, B, Q, N, H, D, L, P, spatial_shapes, level_start_index, sampling_locations,
                             attention_weights, out);
     if (rc != TD_OK) return rc;
@@ -120,9 +122,26 @@ extern "C" int td_sample_forward(int dtype, const void* value, const int64_t* sp
     const int64_t bytes = B * Q * H * D * elem_size(dtype);
     if (N == 0 || L * P == 0) return launch_zero(out, bytes, s);
     const Geom g{spatial_shapes, level_start_index, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N),
-                 static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), static_cast<int>(P)};
+                 static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), static_cast<int>(P), padding_mask};
     SampleTune tune;
     return launch_sample(dtype, value, g, sampling_locations, attention_weights, out, s, tune);
+}
+
+extern "C" int td_fused_forward(int dtype, const void* memory, const void* value_weight, const void* value_bias,
+                                const int64_t* spatial_shapes, const int64_t* level_start_index,
+                                const void* sampling_locations, const void* attention_weights, void* out, int64_t B,
+                                int64_t Q, int64_t N, int64_t C, int64_t H, int64_t D, int64_t L, int64_t P,
+                                void* stream) {
+    return td_fused_forward_masked(dtype, memory, value_weight, value_bias, spatial_shapes, level_start_index,
+                                   sampling_locations, attention_weights, nullptr, out, B, Q, N, C, H, D, L, P, stream);
+}
+
+extern "C" int td_sample_forward(int dtype, const void* value, const int64_t* spatial_shapes,
+                                 const int64_t* level_start_index, const void* sampling_locations,
+                                 const void* attention_weights, void* out, int64_t B, int64_t Q, int64_t N,
+                                 int64_t H, int64_t D, int64_t L, int64_t P, void* stream) {
+    return td_sample_forward_masked(dtype, value, spatial_shapes, level_start_index, sampling_locations,
+                                    attention_weights, nullptr, out, B, Q, N, H, D, L, P, stream);
 }
 
 extern "C" int td_value_proj(int dtype, const void* memory, const void* weight, const void* bias, void* value,

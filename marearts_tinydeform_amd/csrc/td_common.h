@@ -41,6 +41,7 @@ struct Geom {
     const int64_t* shapes;  // [L, 2] (height, width)
     const int64_t* starts;  // [L] first token of each level
     int B, Q, N, H, D, L, P;
+    const uint8_t* mask = nullptr;  // [B, N] padding mask (non-zero = padded token, value zero) or null
 };
 
 // One gathered corner: token index (-1 when the corner lies outside its level map or outside [0, N)) and
@@ -55,7 +56,9 @@ struct Corner {
 // Restates the reference's corner rule (csrc/ma_deform_fused.cu:81-100): pixel coordinate
 // x = loc_x * W_l - 0.5 (align_corners=False), clamped to [-2, W_l + 1] before the integer conversion so that
 // far-away, infinite or NaN locations sample nothing; corner k has dx = k & 1, dy = k >> 1; a corner counts only
-// if it lies inside the level map and its token t = start_l + y * W_l + x lies in [0, N).
+// if it lies inside the level map and its token t = start_l + y * W_l + x lies in [0, N). With a padding mask, a
+// corner on a padded token counts as outside too: its value row is zero (value.masked_fill(mask, 0) after the
+// projection), so in fused mode it drops both W . memory[t] and its share of the bias.
 template <typename T, typename A>
 __device__ __forceinline__ void corner4(const T* __restrict__ loc, const T* __restrict__ attn, const Geom& g,
                                         int64_t row, int j, Corner<A>* out) {
@@ -78,7 +81,8 @@ __device__ __forceinline__ void corner4(const T* __restrict__ loc, const T* __re
     for (int k = 0; k < 4; ++k) {
         const int dx = k & 1, dy = k >> 1, xi = x0 + dx, yi = y0 + dy;
         const int64_t t = st + static_cast<int64_t>(yi) * wl + xi;
-        const bool in = xi >= 0 && xi < wl && yi >= 0 && yi < hl && t >= 0 && t < g.N;
+        bool in = xi >= 0 && xi < wl && yi >= 0 && yi < hl && t >= 0 && t < g.N;
+        if (in && g.mask != nullptr) in = g.mask[(row / (static_cast<int64_t>(g.Q) * g.H)) * g.N + t] == 0;
         out[k].tok = in ? static_cast<int>(t) : -1;
         out[k].w = in ? w * (dx ? fx : static_cast<A>(1) - fx) * (dy ? fy : static_cast<A>(1) - fy)
                       : static_cast<A>(0);

@@ -215,6 +215,133 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma_kernel(GemmParams p) 
     }
 }
 
+// MFMA GEMM for large problems: both operands staged through LDS (each element read from memory once per
+// workgroup), two stages, WM x WN wavefronts each owning TM x TN 16x16 tiles (64 x 64 per wavefront), so a K block
+// costs TM + TN fragment reads from LDS for TM * TN MFMAs.
+template <typename T, int WM, int WN, int TM, int TN, int NKB>
+__global__ __launch_bounds__(WM* WN* kWave) void gemm_lds_kernel(GemmParams p) {
+    constexpr int NTH = WM * WN * kWave;
+    constexpr int E = 16 / static_cast<int>(sizeof(T));
+    constexpr int KBK = KBlock<T>::kK;
+    constexpr int KC = NKB * KBK;
+    constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
+    constexpr int LDK = KC + E;
+    constexpr int A_CHUNKS = BM * KC / E, B_CHUNKS = BN * KC / E;
+    constexpr int A_PER_T = (A_CHUNKS + NTH - 1) / NTH, B_PER_T = (B_CHUNKS + NTH - 1) / NTH;
+    constexpr int LDC = BN + E;
+    constexpr size_t kA = static_cast<size_t>(BM) * LDK * sizeof(T), kB = static_cast<size_t>(BN) * LDK * sizeof(T);
+    constexpr size_t kStage = kA + kB;
+    constexpr size_t kOut = static_cast<size_t>(BM) * LDC * sizeof(T);
+    constexpr size_t kLds = 2 * kStage > kOut ? 2 * kStage : kOut;
+    __shared__ __align__(16) unsigned char lds[kLds];
+    auto as = [&](int i) { return reinterpret_cast<T*>(lds + (i & 1) * kStage); };
+    auto bs = [&](int i) { return reinterpret_cast<T*>(lds + (i & 1) * kStage + kA); };
+
+    const int tile = tile_of(p);
+    if (tile < 0) return;
+    const int m0 = (tile / p.nt) * BM, n0 = (tile % p.nt) * BN;
+    const T* __restrict__ A = static_cast<const T*>(p.a);
+    const T* __restrict__ W = static_cast<const T*>(p.w);
+    const T* __restrict__ bias = static_cast<const T*>(p.bias);
+    T* __restrict__ Cm = static_cast<T*>(p.c);
+    const int M = p.M, K = p.K, NO = p.NO;
+    const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+    const int wm = wave / WN, wn = wave % WN;
+    const int r16 = lane & 15, kg = lane >> 4;
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+
+    u32x4 ra[A_PER_T], rb[B_PER_T];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < A_PER_T; ++u) {
+            const int c = tid + u * NTH, row = c / (KC / E), kc = (c % (KC / E)) * E;
+            const int m = m0 + row, k = k0 + kc;
+            ra[u] = (c < A_CHUNKS && m < M && k < K) ? *reinterpret_cast<const u32x4*>(A + static_cast<size_t>(m) * K + k)
+                                                     : zero;
+        }
+#pragma unroll
+        for (int u = 0; u < B_PER_T; ++u) {
+            const int c = tid + u * NTH, row = c / (KC / E), kc = (c % (KC / E)) * E;
+            const int n = n0 + row, k = k0 + kc;
+            rb[u] = (c < B_CHUNKS && n < NO && k < K) ? *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(n) * K + k)
+                                                      : zero;
+        }
+    };
+    auto store = [&](int stage) {
+        T* a = as(stage);
+        T* b = bs(stage);
+#pragma unroll
+        for (int u = 0; u < A_PER_T; ++u) {
+            const int c = tid + u * NTH;
+            if (c < A_CHUNKS) *reinterpret_cast<u32x4*>(a + (c / (KC / E)) * LDK + (c % (KC / E)) * E) = ra[u];
+        }
+#pragma unroll
+        for (int u = 0; u < B_PER_T; ++u) {
+            const int c = tid + u * NTH;
+            if (c < B_CHUNKS) *reinterpret_cast<u32x4*>(b + (c / (KC / E)) * LDK + (c % (KC / E)) * E) = rb[u];
+        }
+    };
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int nc = (K + KC - 1) / KC;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int c = 0; c < nc; ++c) {
+        const bool more = c + 1 < nc;
+        if (more) load((c + 1) * KC);
+        const T* a = as(c);
+        const T* b = bs(c);
+#pragma unroll
+        for (int j = 0; j < NKB; ++j) {
+            u32x4 fa[TM], fb[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+                fa[i] = *reinterpret_cast<const u32x4*>(a + ((wm * TM + i) * 16 + r16) * LDK + j * KBK + kg * E);
+#pragma unroll
+            for (int t = 0; t < TN; ++t)
+                fb[t] = *reinterpret_cast<const u32x4*>(b + ((wn * TN + t) * 16 + r16) * LDK + j * KBK + kg * E);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int t = 0; t < TN; ++t) acc[i][t] = KBlock<T>::mma(fa[i], fb[t], acc[i][t]);
+        }
+        if (more) store(c + 1);
+        __syncthreads();
+    }
+
+    T* Ct = reinterpret_cast<T*>(lds);
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+        const int nl = (wn * TN + t) * 16 + r16;
+        const float bv = (bias != nullptr && n0 + nl < NO) ? static_cast<float>(bias[n0 + nl]) : 0.f;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                Ct[((wm * TM + i) * 16 + kg * 4 + e) * LDC + nl] = static_cast<T>(acc[i][t][e] + bv);
+    }
+    __syncthreads();
+    const bool vec_ok = NO % E == 0 && (reinterpret_cast<uintptr_t>(Cm) % 16) == 0;
+    for (int c = tid; c < BM * (BN / E); c += NTH) {
+        const int row = c / (BN / E), col = (c % (BN / E)) * E;
+        const int m = m0 + row, n = n0 + col;
+        if (m >= M || n >= NO) continue;
+        const T* src = Ct + row * LDC + col;
+        T* dst = Cm + static_cast<size_t>(m) * NO + n;
+        if (vec_ok && n + E <= NO) {
+            *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
+        } else {
+            for (int e = 0; e < E && n + e < NO; ++e) dst[e] = src[e];
+        }
+    }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmParams p) {
     using A = typename AccOf<T>::type;
@@ -274,6 +401,11 @@ int go(Kernel kernel, GemmParams p, int bm, int bn, int threads, hipStream_t str
     return e == hipSuccess ? 0 : set_error(-3, "value_proj launch failed: %s", hipGetErrorString(e));
 }
 
+template <typename T, int WM, int WN, int TM, int TN, int NKB>
+int go_lds(GemmParams p, hipStream_t stream) {
+    return go(gemm_lds_kernel<T, WM, WN, TM, TN, NKB>, p, WM * TM * 16, WN * TN * 16, WM * WN * kWave, stream);
+}
+
 template <typename T, int WM, int WN, int TM, int TN, int NKB, int STAGES>
 int go_mfma(GemmParams p, hipStream_t stream) {
     return go(gemm_mfma_kernel<T, WM, WN, TM, TN, NKB, STAGES>, p, WM * TM * 16, WN * TN * 16, WM * WN * kWave,
@@ -288,14 +420,21 @@ int go_mfma(GemmParams p, hipStream_t stream) {
 //   4  128 x 64  4 waves of 32 x 64, two stages
 //   5  64 x 64   one chunk of 256/128 (K <= 256 for 16-bit: a single round trip), one stage
 //   6  64 x 128  one chunk of 256/128, one stage
+//   7  128 x 128 A and W both through LDS (2 x 2 waves of 64 x 64), K chunks of 64/32
+//   8  256 x 128 A and W through LDS (4 x 2 waves of 64 x 64)
+//   9  128 x 128 A and W through LDS, K chunks of 128/64
+//   10 128 x 256 A and W through LDS (2 x 4 waves of 64 x 64)
 template <typename T>
 int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
     if (variant <= 0) {
-        // measured on MI355X: one round trip (5) wins while the grid is small; 64 x 128 double-buffered (2) wins
-        // once there are >= 1024 of its tiles or K spans several chunks
+        // measured on MI355X: one round trip (5) while the grid is small; for large 16-bit problems both operands
+        // through LDS in 128 x 128 tiles (7); float32 keeps A direct in 64 x 128 tiles (2)
         constexpr int one_chunk = 8 * KBlock<T>::kK;
-        const int64_t tiles_64x128 = ((p.M + 63) / 64) * static_cast<int64_t>((p.NO + 127) / 128);
-        variant = (p.K <= one_chunk && tiles_64x128 < 1024) ? 5 : 2;
+        const int64_t tiles_128 = ((p.M + 127) / 128) * static_cast<int64_t>((p.NO + 127) / 128);
+        if (p.K <= one_chunk && tiles_128 < 512)
+            variant = 5;
+        else
+            variant = sizeof(T) == 2 ? 7 : 2;
     }
     switch (variant) {
         case 1: return go_mfma<T, 4, 1, 1, 4, 2, 2>(p, stream);
@@ -304,6 +443,10 @@ int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
         case 4: return go_mfma<T, 4, 1, 2, 4, 2, 2>(p, stream);
         case 5: return go_mfma<T, 4, 1, 1, 4, 8, 1>(p, stream);
         case 6: return go_mfma<T, 4, 1, 1, 8, 8, 1>(p, stream);
+        case 7: return go_lds<T, 2, 2, 4, 4, 2>(p, stream);
+        case 8: return go_lds<T, 4, 2, 4, 4, 2>(p, stream);
+        case 9: return go_lds<T, 2, 2, 4, 4, 4>(p, stream);
+        case 10: return go_lds<T, 2, 4, 4, 4, 2>(p, stream);
         default: return set_error(-1, "value_proj: unknown tile variant %d", variant);
     }
 }

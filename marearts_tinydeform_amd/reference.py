@@ -10,7 +10,7 @@ import torch.nn.functional as F
 
 
 def ma_deform_attn_reference(memory, value_weight, value_bias, spatial_shapes, level_start_index,
-                             sampling_locations, attention_weights):
+                             sampling_locations, attention_weights, padding_mask=None):
     """value = memory @ value_weight.T + value_bias, then multi-scale deformable attention.
 
     memory              [B, N, C]
@@ -20,11 +20,14 @@ def ma_deform_attn_reference(memory, value_weight, value_bias, spatial_shapes, l
     level_start_index   [L] int64       first token of each level
     sampling_locations  [B, Q, H, L, P, 2]  (x, y) normalised to [0, 1]
     attention_weights   [B, Q, H, L, P]     already normalised (softmax over L * P)
+    padding_mask        [B, N] bool or None  True = padded token: its value row is zeroed after the projection
     returns             [B, Q, H * D]
     """
     B, N, _ = memory.shape
     _, Q, H, L, P, _ = sampling_locations.shape
     value = F.linear(memory, value_weight, value_bias)  # [B, N, H * D]
+    if padding_mask is not None:
+        value = value.masked_fill(padding_mask.bool()[..., None], 0)
     D = value.shape[-1] // H
     # heads to the batch dimension: [B * H, D, N]
     per_head = value.view(B, N, H, D).permute(0, 2, 3, 1).reshape(B * H, D, N)

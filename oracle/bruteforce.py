@@ -26,11 +26,13 @@ def _i64(a):
     return np.asarray(a, dtype=np.int64)
 
 
-def corner_table(spatial_shapes, level_start_index, sampling_locations, attention_weights, num_tokens):
+def corner_table(spatial_shapes, level_start_index, sampling_locations, attention_weights, num_tokens,
+                 padding_mask=None):
     """Token index and weight of every bilinear corner: tok, wt of shape [B, Q, H, L * P * 4].
 
     Corner order is (level, point, k) with k = dy * 2 + dx (reference csrc/ma_deform_fused.cu:93-99).
-    tok is -1 and wt is 0 for corners outside the level map or outside [0, num_tokens).
+    tok is -1 and wt is 0 for corners outside the level map or outside [0, num_tokens), and for corners on tokens
+    that padding_mask ([B, N], True = padded) marks.
     """
     shapes = _i64(spatial_shapes)
     starts = _i64(level_start_index)
@@ -61,6 +63,12 @@ def corner_table(spatial_shapes, level_start_index, sampling_locations, attentio
     tok = np.stack(toks, axis=-1)  # [B, Q, H, L, P, 4]
     wt = np.stack(wts, axis=-1)
     B, Q, H, L, P = tok.shape[:5]
+    if padding_mask is not None:
+        pm = np.asarray(padding_mask.detach().cpu().numpy() if hasattr(padding_mask, 'detach') else padding_mask,
+                        dtype=bool)
+        padded = pm[np.arange(B)[:, None, None, None, None, None], np.maximum(tok, 0)] & (tok >= 0)
+        tok = np.where(padded, -1, tok)
+        wt = np.where(padded, 0.0, wt)
     return tok.reshape(B, Q, H, L * P * 4), wt.reshape(B, Q, H, L * P * 4)
 
 
@@ -73,7 +81,7 @@ def project(memory, value_weight, value_bias):
 
 
 def sample(value, heads, spatial_shapes, level_start_index, sampling_locations, attention_weights, rows=None,
-           chunk=None):
+           chunk=None, padding_mask=None):
     """out[b, q, h*D + d] = sum over in-map corners of wt * value[b, tok, h*D + d], float64: [B, Q, H * D].
 
     rows: optional array of flat row indices ((b * Q + q) * H + h); then only those rows are computed and the
@@ -83,7 +91,7 @@ def sample(value, heads, spatial_shapes, level_start_index, sampling_locations, 
     B, N, HD = value.shape
     H = heads
     D = HD // H
-    tok, wt = corner_table(spatial_shapes, level_start_index, sampling_locations, attention_weights, N)
+    tok, wt = corner_table(spatial_shapes, level_start_index, sampling_locations, attention_weights, N, padding_mask)
     Q = tok.shape[1]
     S = tok.shape[-1]
     tok = tok.reshape(-1, S)
@@ -104,11 +112,13 @@ def sample(value, heads, spatial_shapes, level_start_index, sampling_locations, 
 
 
 def deform_attn(memory, value_weight, value_bias, spatial_shapes, level_start_index, sampling_locations,
-                attention_weights, rows=None):
-    """The whole op in float64, project order (reference marearts_tinydeform/reference.py:13-40)."""
+                attention_weights, rows=None, padding_mask=None):
+    """The whole op in float64, project order (reference marearts_tinydeform/reference.py:13-40); padded tokens'
+    corners are dropped (padding_mask, [B, N], True = padded)."""
     heads = sampling_locations.shape[2]
     value = project(memory, value_weight, value_bias)
-    return sample(value, heads, spatial_shapes, level_start_index, sampling_locations, attention_weights, rows=rows)
+    return sample(value, heads, spatial_shapes, level_start_index, sampling_locations, attention_weights, rows=rows,
+                  padding_mask=padding_mask)
 
 
 def deform_attn_fused_order(memory, value_weight, value_bias, spatial_shapes, level_start_index,

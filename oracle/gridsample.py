@@ -12,10 +12,15 @@ import torch.nn.functional as F
 
 
 def deform_attn(memory, value_weight, value_bias, spatial_shapes, level_start_index, sampling_locations,
-                attention_weights):
+                attention_weights, padding_mask=None):
+    """padding_mask ([B, N] bool, True = padded) zeroes those value rows after the projection, the way
+    Deformable-DETR decoders mask padded tokens."""
     B, N, _ = memory.shape
     _, Q, H, L, P, _ = sampling_locations.shape
-    value = F.linear(memory, value_weight, value_bias).view(B, N, H, -1)
+    value = F.linear(memory, value_weight, value_bias)
+    if padding_mask is not None:
+        value = value.masked_fill(padding_mask.bool()[..., None], 0)
+    value = value.view(B, N, H, -1)
     D = value.shape[-1]
     grids = 2 * sampling_locations - 1
     acc = torch.zeros(B * H, D, Q, dtype=value.dtype)

@@ -32,8 +32,8 @@ def lib():
 
 
 def test_header_declares_the_entry_points():
-    assert header_functions() == ['td_fused_forward', 'td_last_error', 'td_sample_forward', 'td_value_proj',
-                                  'td_version']
+    assert header_functions() == ['td_fused_forward', 'td_fused_forward_masked', 'td_last_error',
+                                  'td_sample_forward', 'td_sample_forward_masked', 'td_value_proj', 'td_version']
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -95,6 +95,14 @@ def test_sample_and_proj_reject_on_host(lib):
     assert sample(lib, ptr=None) == header_defines()['TD_E_ARG']
     assert lib.td_value_proj(1, None, None, None, None, 4, 4, 4, None) == header_defines()['TD_E_ARG']
     assert lib.td_value_proj(1, 16, 16, None, 16, -1, 4, 4, None) == header_defines()['TD_E_ARG']
+
+
+def test_masked_entries_reject_on_host(lib):
+    p = 16
+    assert lib.td_fused_forward_masked(1, p, p, None, p, p, p, p, None, p, 1, 4, 100, 256, 8, 32, 4, 20, None) == \
+        header_defines()['TD_E_ARG']
+    assert 'levels x points' in lib.td_last_error().decode()
+    assert lib.td_sample_forward_masked(1, p, p, p, p, p, None, p, 1, 0, 100, 8, 32, 3, 4, None) == 0
 
 
 def test_empty_work_returns_ok_without_launching(lib):

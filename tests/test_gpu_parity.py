@@ -283,3 +283,71 @@ def test_limit_case_bf16_c1024(Q):
     args = workload(2, Q, 16, 64, 1024, LIMIT_LEVELS, 16, torch.bfloat16, bias=False)
     rows = np.random.default_rng(Q).choice(2 * Q * 16, size=min(1024, 2 * Q * 16), replace=False)
     full_size_check(f'limit bf16 C1024 B2 Q{Q}', args, torch.bfloat16, rows=np.sort(rows))
+
+
+# ---- value padding mask ---------------------------------------------------------------------------------------
+
+def padded_images_mask(B, levels, seed):
+    """Padding as a batch of different-size images produces: per image and level, the right and bottom part of
+    the map is padding (True)."""
+    g = torch.Generator().manual_seed(seed)
+    masks = []
+    for b in range(B):
+        keep_w, keep_h = 0.5 + 0.5 * torch.rand(2, generator=g).tolist()[0], 0.5 + 0.5 * torch.rand(1, generator=g).item()
+        per_level = []
+        for h, w in levels:
+            m = torch.zeros(h, w, dtype=torch.bool)
+            m[:, max(1, int(round(w * keep_w))):] = True
+            m[max(1, int(round(h * keep_h))):, :] = True
+            per_level.append(m.flatten())
+        masks.append(torch.cat(per_level))
+    return torch.stack(masks)
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16, torch.bfloat16])
+def test_padding_mask_cases(dtype):
+    for name, B, Q, H, D, C, levels, P in CASES:
+        args = make(B, Q, H, D, C, levels, P, dtype=dtype)
+        mask = torch.rand(B, args[0].shape[1], generator=torch.Generator().manual_seed(7)) < 0.3
+        ref = bruteforce.deform_attn(*args, padding_mask=mask)
+        dev = to(args, 'cuda')
+        atol, rtol = TOL[dtype]
+        for mode in MODES:
+            with torch.inference_mode():
+                out = td.ma_deform_attn(*dev, mode=mode, padding_mask=mask.cuda())
+            assert_close(f'mask {name} {dtype} [{mode}]', out, ref, atol, rtol)
+        # sampling alone on projected values
+        value = bruteforce.project(args[0], args[1], args[2])
+        vdev = torch.from_numpy(value).to(dtype).cuda()
+        with torch.inference_mode():
+            out = td.ma_deform_sample(vdev, *dev[3:], padding_mask=mask.cuda())
+        ref_s = bruteforce.sample(vdev.double().cpu(), H, *args[3:], padding_mask=mask)
+        assert_close(f'mask sample {name} {dtype}', out, ref_s, atol, rtol)
+
+
+def test_padding_mask_everything_padded_is_zero():
+    args = to(make(2, 9, 4, 8, 32, [(9, 11), (5, 6)], 4), 'cuda')
+    mask = torch.ones(2, args[0].shape[1], dtype=torch.bool, device='cuda')
+    for mode in MODES:
+        with torch.inference_mode():
+            out = td.ma_deform_attn(*args, mode=mode, padding_mask=mask)
+        assert torch.count_nonzero(out) == 0, mode
+    with pytest.raises(RuntimeError):
+        td.ma_deform_attn(*args, padding_mask=mask[:, :5])
+
+
+def test_padding_mask_rtdetr640_fp16_b4_padded_images():
+    args = workload(4, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.float16)
+    mask = padded_images_mask(4, RTDETR_LEVELS, 11)
+    assert 0.1 < mask.float().mean() < 0.7
+    ref = bruteforce.deform_attn(*args, padding_mask=mask)
+    dev = to(args, 'cuda')
+    atol, rtol = TOL[torch.float16]
+    outs = []
+    for mode in ('fused', 'project'):
+        with torch.inference_mode():
+            out = td.ma_deform_attn(*dev, mode=mode, padding_mask=mask.cuda())
+        err = assert_close(f'padded images [{mode}]', out, ref, atol, rtol)
+        assert err / np.abs(ref).max() <= REL[torch.float16]
+        outs.append(out.double())
+    assert torch.allclose(outs[0], outs[1], atol=2 * atol, rtol=2 * rtol)

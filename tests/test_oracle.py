@@ -225,27 +225,27 @@ def test_token_range_guard_drops_tokens_past_n():
 def _mutants():
     orig = bruteforce.corner_table
 
-    def no_half_pixel(shapes, starts, loc, attn, n):  # x = loc * W (align_corners mix-up)
+    def no_half_pixel(shapes, starts, loc, attn, n, mask=None):  # x = loc * W (align_corners mix-up)
         wh = torch.as_tensor(np.asarray(shapes))[:, [1, 0]].double()
-        return orig(shapes, starts, torch.as_tensor(np.asarray(loc)) + 0.5 / wh[:, None, :], attn, n)
+        return orig(shapes, starts, torch.as_tensor(np.asarray(loc)) + 0.5 / wh[:, None, :], attn, n, mask)
 
-    def swapped_xy(shapes, starts, loc, attn, n):
-        return orig(shapes, starts, torch.as_tensor(np.asarray(loc)).flip(-1), attn, n)
+    def swapped_xy(shapes, starts, loc, attn, n, mask=None):
+        return orig(shapes, starts, torch.as_tensor(np.asarray(loc)).flip(-1), attn, n, mask)
 
-    def dropped_corner(shapes, starts, loc, attn, n):
-        tok, wt = orig(shapes, starts, loc, attn, n)
+    def dropped_corner(shapes, starts, loc, attn, n, mask=None):
+        tok, wt = orig(shapes, starts, loc, attn, n, mask)
         wt = wt.copy()
         wt[..., 3::4] = 0.0
         return tok, wt
 
-    def transposed_bilinear(shapes, starts, loc, attn, n):  # corner k=1 and k=2 weights exchanged
-        tok, wt = orig(shapes, starts, loc, attn, n)
+    def transposed_bilinear(shapes, starts, loc, attn, n, mask=None):  # corner k=1 and k=2 weights exchanged
+        tok, wt = orig(shapes, starts, loc, attn, n, mask)
         wt = wt.copy()
         wt[..., 1::4], wt[..., 2::4] = wt[..., 2::4].copy(), wt[..., 1::4].copy()
         return tok, wt
 
-    def wrong_level_start(shapes, starts, loc, attn, n):
-        return orig(shapes, np.roll(np.asarray(starts), 1), loc, attn, n)
+    def wrong_level_start(shapes, starts, loc, attn, n, mask=None):
+        return orig(shapes, np.roll(np.asarray(starts), 1), loc, attn, n, mask)
 
     return {'no half-pixel offset': no_half_pixel, 'swapped x/y': swapped_xy, 'dropped corner': dropped_corner,
             'transposed bilinear weights': transposed_bilinear, 'wrong level start': wrong_level_start}
@@ -268,3 +268,37 @@ def test_planted_bias_mistake_fails_outside_zero_pin():
     wrong = bruteforce.deform_attn_fused_order(*no_bias) + args[2].double().numpy()
     assert wrong.any()  # the closed form (exact zero) rejects it
     assert not bruteforce.deform_attn_fused_order(*args).any()
+
+
+# ---- value padding mask -------------------------------------------------------------------------------------
+
+def random_mask(B, N, seed, frac=0.3):
+    g = torch.Generator().manual_seed(seed)
+    return torch.rand(B, N, generator=g) < frac
+
+
+@pytest.mark.parametrize('case', CASES[:4], ids=[c[0] for c in CASES[:4]])
+def test_padding_mask_drops_corners_like_zeroed_values(case):
+    # dropping corners on padded tokens == zeroing their value rows after the projection (the decoder's
+    # value.masked_fill(mask[..., None], 0)), checked three ways: corner-dropping brute force, zeroed-value brute
+    # force, grid_sample on zeroed values
+    name, B, Q, H, D, C, levels, P = case
+    args = make(B, min(Q, 16), H, D, C, levels, P, seed=21)
+    mask = random_mask(B, args[0].shape[1], 22)
+    dropped = bruteforce.deform_attn(*args, padding_mask=mask)
+    value = bruteforce.project(args[0], args[1], args[2])
+    value[mask.numpy()] = 0.0
+    zeroed = bruteforce.sample(value, H, *args[3:])
+    gs = gridsample.deform_attn(*as_f64(args), padding_mask=mask).numpy()
+    assert np.abs(dropped - zeroed).max() <= 1e-13
+    assert np.abs(dropped - gs).max() <= 1e-12
+    assert np.abs(dropped - bruteforce.deform_attn(*args)).max() > 1e-3  # the mask matters
+
+
+def test_padding_mask_all_and_none():
+    args = make(2, 6, 2, 4, 8, [(5, 6), (3, 3)], 2, seed=23)
+    N = args[0].shape[1]
+    full = bruteforce.deform_attn(*args, padding_mask=torch.ones(2, N, dtype=torch.bool))
+    assert not full.any()  # every token padded: exact zero, bias included
+    none = bruteforce.deform_attn(*args, padding_mask=torch.zeros(2, N, dtype=torch.bool))
+    assert np.abs(none - bruteforce.deform_attn(*args)).max() == 0
