@@ -96,6 +96,21 @@ int td_sample_forward_masked(int dtype, const void* value, const int64_t* spatia
                              int64_t Q, int64_t N, int64_t H, int64_t D, int64_t L, int64_t P, void* stream);
 
 /*
+ * Sampling with per-level point counts and a choice of sampling method (the deformable attention core of D-FINE:
+ * transformers models/d_fine/modeling_d_fine.py:150-216, multi_scale_deformable_attention_v2). Level l has
+ * points_per_level[l] samples (a host array of L entries, sum <= 64), so sampling_locations is
+ * [B, Q, H, sum, 2] and attention_weights [B, Q, H, sum]. discrete = 0: bilinear with zero padding
+ * (align_corners=False); discrete = 1: the nearest-pixel rule of D-FINE's "discrete" method. padding_mask as in
+ * td_sample_forward_masked (NULL for none). No counterpart in the reference (README.md:62 lists discrete sampling
+ * as unsupported); needed by D-FINE / RT-DETRv2-style decoders, which have no value projection.
+ */
+int td_sample_forward_v2(int dtype, const void* value, const int64_t* spatial_shapes,
+                         const int64_t* level_start_index, const void* sampling_locations,
+                         const void* attention_weights, const uint8_t* padding_mask, void* out, int64_t B, int64_t Q,
+                         int64_t N, int64_t H, int64_t D, int64_t L, const int64_t* points_per_level, int discrete,
+                         void* stream);
+
+/*
  * Value projection (the first half of project mode): value[M, NO] = memory[M, K] @ weight[NO, K]^T + bias[NO],
  * float32 accumulation, one rounding to dtype. M = B*N tokens, K = C, NO = H*D.
  * Replaces the reference's F.linear(memory, value_weight, value_bias) call (marearts_tinydeform/__init__.py:77).

@@ -12,7 +12,8 @@ import torch
 from . import _native
 from .reference import ma_deform_attn_reference
 
-__all__ = ['ma_deform_attn', 'ma_deform_attn_reference', 'choose_mode', 'ma_deform_sample', 'predict_us']
+__all__ = ['ma_deform_attn', 'ma_deform_attn_reference', 'choose_mode', 'ma_deform_sample', 'ma_deform_sample_v2',
+           'predict_us']
 __version__ = '0.1.0'
 
 MODES = ('auto', 'fused', 'project')
@@ -138,3 +139,21 @@ def ma_deform_sample(value, spatial_shapes, level_start_index, sampling_location
     H = sampling_locations.shape[2] if sampling_locations.dim() == 6 else 0
     return _on_device(value, _native.sample_forward, value, H, spatial_shapes, level_start_index,
                       sampling_locations, attention_weights, padding_mask)
+
+
+def ma_deform_sample_v2(value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+                        num_points_list, method='default', padding_mask=None):
+    """D-FINE's deformable attention core on the GPU: per-level point counts and the 'default' (bilinear, zero
+    padding, align_corners=False) or 'discrete' (nearest pixel, clamped) method; the result of transformers'
+    multi_scale_deformable_attention_v2 (models/d_fine/modeling_d_fine.py:150-216) with the value padding already
+    applied by padding_mask.
+
+    value               [B, N, H, D] or [B, N, H * D]   (D-FINE has no value projection)
+    sampling_locations  [B, Q, H, sum(num_points_list), 2]
+    attention_weights   [B, Q, H, sum(num_points_list)]
+    returns             [B, Q, H * D]
+    """
+    _native._require()
+    _reject_grad(value, sampling_locations, attention_weights)
+    return _on_device(value, _native.sample_forward_v2, value, spatial_shapes, level_start_index, sampling_locations,
+                      attention_weights, num_points_list, method, padding_mask)

@@ -29,6 +29,7 @@ SIGNATURES = {
     'td_sample_forward': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 7 + [_vp]),
     'td_fused_forward_masked': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 8 + [_vp]),
     'td_sample_forward_masked': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 7 + [_vp]),
+    'td_sample_forward_v2': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 6 + [_vp, _int, _vp]),
     'td_value_proj': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
 }
 
@@ -188,6 +189,61 @@ def sample_forward(value, heads, spatial_shapes, level_start_index, sampling_loc
     _check(lib_.td_sample_forward_masked(DTYPE_CODES[value.dtype], v.data_ptr(), sh.data_ptr(), st.data_ptr(),
                                          lc.data_ptr(), aw.data_ptr(), _ptr(mask), out.data_ptr(), B, Q, N, H, HD // H,
                                          L, P, _stream(dev)))
+    return out
+
+
+def sample_forward_v2(value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+                      num_points_list, method='default', padding_mask=None):
+    """Sampling with per-level point counts and D-FINE's methods (td_sample_forward_v2)."""
+    lib_ = _require()
+    if method not in ('default', 'discrete'):
+        raise ValueError(f"method must be 'default' or 'discrete', got {method!r}")
+    if not value.is_cuda:
+        raise RuntimeError('inputs must be GPU tensors')
+    if value.dim() == 4:
+        value = value.flatten(2)
+    if value.dim() != 3:
+        raise RuntimeError('value must be [B, N, H * D] or [B, N, H, D]')
+    if sampling_locations.dim() != 5 or sampling_locations.size(4) != 2:
+        raise RuntimeError('sampling_locations must be [B, Q, H, sum(num_points_list), 2]')
+    B, Q, H, J = sampling_locations.shape[:4]
+    points = [int(n) for n in num_points_list]
+    L = len(points)
+    if sum(points) != J or any(n < 0 for n in points):
+        raise RuntimeError('sampling_locations must have sum(num_points_list) samples per head')
+    if J > MAX_LEVEL_POINTS:
+        raise RuntimeError(f'levels x points must be <= {MAX_LEVEL_POINTS}')
+    if attention_weights.shape != sampling_locations.shape[:4]:
+        raise RuntimeError('attention_weights must be [B, Q, H, sum(num_points_list)] like sampling_locations')
+    if value.size(0) != B:
+        raise RuntimeError('batch size mismatch')
+    N, HD = value.size(1), value.size(2)
+    if H <= 0 or HD % H != 0:
+        raise RuntimeError('value must be [B, N, H * D] with H = sampling_locations.size(2)')
+    if spatial_shapes.dtype != torch.int64 or spatial_shapes.shape != (L, 2):
+        raise RuntimeError('spatial_shapes must be int64 [L, 2]')
+    if level_start_index.dtype != torch.int64 or level_start_index.shape != (L,):
+        raise RuntimeError('level_start_index must be int64 [L]')
+    for t in (sampling_locations, attention_weights, spatial_shapes, level_start_index):
+        if t.device != value.device:
+            raise RuntimeError('all tensors must be on the same device')
+    for t in (sampling_locations, attention_weights):
+        if t.dtype != value.dtype:
+            raise RuntimeError('all float tensors must have the same dtype')
+    if value.dtype not in DTYPE_CODES:
+        raise RuntimeError(f'unsupported dtype {value.dtype}')
+    mask = check_padding_mask(value, padding_mask)
+    dev = value.device
+    v = value.contiguous()
+    lc, aw = sampling_locations.contiguous(), attention_weights.contiguous()
+    sh, st = spatial_shapes.contiguous(), level_start_index.contiguous()
+    out = torch.empty((B, Q, HD), dtype=value.dtype, device=dev)
+    if out.numel() == 0:
+        return out
+    pts = (ctypes.c_int64 * max(L, 1))(*points)
+    _check(lib_.td_sample_forward_v2(DTYPE_CODES[value.dtype], v.data_ptr(), sh.data_ptr(), st.data_ptr(),
+                                     lc.data_ptr(), aw.data_ptr(), _ptr(mask), out.data_ptr(), B, Q, N, H, HD // H, L,
+                                     ctypes.cast(pts, ctypes.c_void_p), int(method == 'discrete'), _stream(dev)))
     return out
 
 

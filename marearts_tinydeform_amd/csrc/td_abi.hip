@@ -101,8 +101,9 @@ extern "C" int td_fused_forward_masked(int dtype, const void* memory, const void
     const int64_t bytes = B * Q * H * D * elem_size(dtype);
     // no tokens: every corner is outside, so the output is exactly zero (the bias share included)
     if (N == 0 || L * P == 0) return launch_zero(out, bytes, s);
-    const Geom g{spatial_shapes, level_start_index, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N),
-                 static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), static_cast<int>(P), padding_mask};
+    Geom g{spatial_shapes, level_start_index, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N),
+           static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), static_cast<int>(P), padding_mask};
+    set_levels(g, nullptr);
     FusedTune tune;
     return launch_fused(dtype, memory, value_weight, value_bias, g, static_cast<int>(C), sampling_locations,
                         attention_weights, out, s, tune);
@@ -121,8 +122,37 @@ extern "C" int td_sample_forward_masked(int dtype, const void* value, const int6
     if (B * Q * H * D == 0) return TD_OK;
     const int64_t bytes = B * Q * H * D * elem_size(dtype);
     if (N == 0 || L * P == 0) return launch_zero(out, bytes, s);
-    const Geom g{spatial_shapes, level_start_index, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N),
-                 static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), static_cast<int>(P), padding_mask};
+    Geom g{spatial_shapes, level_start_index, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N),
+           static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), static_cast<int>(P), padding_mask};
+    set_levels(g, nullptr);
+    SampleTune tune;
+    return launch_sample(dtype, value, g, sampling_locations, attention_weights, out, s, tune);
+}
+
+extern "C" int td_sample_forward_v2(int dtype, const void* value, const int64_t* spatial_shapes,
+                                    const int64_t* level_start_index, const void* sampling_locations,
+                                    const void* attention_weights, const uint8_t* padding_mask, void* out, int64_t B,
+                                    int64_t Q, int64_t N, int64_t H, int64_t D, int64_t L,
+                                    const int64_t* points_per_level, int discrete, void* stream) {
+    g_last_error.clear();
+    if (L < 0) return set_error(TD_E_ARG, "sizes must be non-negative");
+    if (L > kMaxLevelPoints) return set_error(TD_E_ARG, "levels x points must be <= %d", kMaxLevelPoints);
+    if (L > 0 && points_per_level == nullptr) return set_error(TD_E_ARG, "null pointer argument");
+    if (discrete != 0 && discrete != 1) return set_error(TD_E_ARG, "method must be 0 (bilinear) or 1 (discrete)");
+    Geom g{spatial_shapes, level_start_index, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N),
+           static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), 1, padding_mask};
+    if (!set_levels(g, points_per_level))
+        return set_error(TD_E_ARG, "levels x points must be <= %d (and point counts non-negative)", kMaxLevelPoints);
+    g.discrete = discrete;
+    // the shared checks see the samples of a row as L levels of one point each plus the total
+    int rc = check_geometry(dtype, B, Q, N, H, D, 1, g.LP, spatial_shapes, level_start_index, sampling_locations,
+                            attention_weights, out);
+    if (rc != TD_OK) return rc;
+    if (B * N * H * D > 0 && value == nullptr) return set_error(TD_E_ARG, "null pointer argument");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (B * Q * H * D == 0) return TD_OK;
+    const int64_t bytes = B * Q * H * D * elem_size(dtype);
+    if (N == 0 || g.LP == 0) return launch_zero(out, bytes, s);
     SampleTune tune;
     return launch_sample(dtype, value, g, sampling_locations, attention_weights, out, s, tune);
 }

@@ -42,7 +42,40 @@ struct Geom {
     const int64_t* starts;  // [L] first token of each level
     int B, Q, N, H, D, L, P;
     const uint8_t* mask = nullptr;  // [B, N] padding mask (non-zero = padded token, value zero) or null
+    int LP = 0;                     // samples per row: L * P, or the sum of per-level point counts
+    int discrete = 0;               // 1: nearest-pixel sampling (D-FINE's "discrete" method) instead of bilinear
+    uint8_t level_end[kMaxLevelPoints] = {};  // per-level point counts (P == 0): first sample after level l
+
+    // true when the general corner rule is needed (padding mask, per-level point counts or discrete sampling)
+    bool general() const { return mask != nullptr || P == 0 || discrete != 0; }
 };
+
+// Fills Geom::LP (and Geom::level_end with P = 0 when `points` gives per-level counts; points == nullptr keeps P
+// points on every level). Returns false when the total exceeds kMaxLevelPoints.
+inline bool set_levels(Geom& g, const int64_t* points) {
+    if (points == nullptr) {
+        g.LP = g.L * g.P;
+        return g.LP <= kMaxLevelPoints;
+    }
+    int64_t j = 0;
+    for (int l = 0; l < g.L; ++l) {
+        if (points[l] < 0 || j + points[l] > kMaxLevelPoints) return false;
+        j += points[l];
+        g.level_end[l] = static_cast<uint8_t>(j);
+    }
+    g.P = 0;
+    g.LP = static_cast<int>(j);
+    return true;
+}
+
+// Level of sample j: j / P for P points per level; otherwise the number of levels that end at or before j
+// (uniform loop over levels, so the counts are read as scalars).
+__device__ __forceinline__ int level_of(const Geom& g, int j) {
+    if (g.P > 0) return j / g.P;
+    int l = 0;
+    for (int i = 0; i + 1 < g.L; ++i) l += j >= g.level_end[i];
+    return l;
+}
 
 // One gathered corner: token index (-1 when the corner lies outside its level map or outside [0, N)) and
 // its weight (attention weight x bilinear weight; 0 when outside).
@@ -59,16 +92,41 @@ struct Corner {
 // if it lies inside the level map and its token t = start_l + y * W_l + x lies in [0, N). With a padding mask, a
 // corner on a padded token counts as outside too: its value row is zero (value.masked_fill(mask, 0) after the
 // projection), so in fused mode it drops both W . memory[t] and its share of the bias.
-template <typename T, typename A>
+//
+// Discrete method (D-FINE, transformers models/d_fine/modeling_d_fine.py:168-206): one tap at pixel
+// (int(loc_x * W_l + 0.5), int(loc_y * H_l + 0.5)) truncated toward zero and clamped into the map, weight = the
+// attention weight; corners 1..3 are empty. A NaN coordinate takes pixel 0.
+//
+// GENERAL = false compiles the reference's case only (P points on every level, bilinear, no mask); kernels are
+// instantiated both ways and the launchers pick GENERAL = true only when a mask, per-level point counts or the
+// discrete method is in use, so the common path carries none of their cost.
+template <typename T, typename A, bool GENERAL>
 __device__ __forceinline__ void corner4(const T* __restrict__ loc, const T* __restrict__ attn, const Geom& g,
                                         int64_t row, int j, Corner<A>* out) {
-    const int LP = g.L * g.P;
-    const int l = j / g.P;
+    const int LP = g.LP;
+    const int l = GENERAL ? level_of(g, j) : j / g.P;
     const int hl = static_cast<int>(g.shapes[2 * l]);
     const int wl = static_cast<int>(g.shapes[2 * l + 1]);
     const int64_t st = g.starts[l];
     const int64_t idx = row * LP + j;
     const A w = cvt<A>(attn[idx]);
+    if (GENERAL && g.discrete) {
+        const A fx = fmin(fmax(cvt<A>(loc[2 * idx]) * static_cast<A>(wl) + static_cast<A>(0.5), static_cast<A>(-1)),
+                          static_cast<A>(wl));
+        const A fy = fmin(fmax(cvt<A>(loc[2 * idx + 1]) * static_cast<A>(hl) + static_cast<A>(0.5), static_cast<A>(-1)),
+                          static_cast<A>(hl));
+        int xi = static_cast<int>(fx), yi = static_cast<int>(fy);  // truncation toward zero
+        xi = xi < 0 ? 0 : xi > wl - 1 ? wl - 1 : xi;
+        yi = yi < 0 ? 0 : yi > hl - 1 ? hl - 1 : yi;
+        const int64_t t = st + static_cast<int64_t>(yi) * wl + xi;
+        bool in = wl > 0 && hl > 0 && t >= 0 && t < g.N;
+        if (in && g.mask != nullptr) in = g.mask[(row / (static_cast<int64_t>(g.Q) * g.H)) * g.N + t] == 0;
+        out[0].tok = in ? static_cast<int>(t) : -1;
+        out[0].w = in ? w : static_cast<A>(0);
+#pragma unroll
+        for (int k = 1; k < 4; ++k) out[k] = Corner<A>{-1, static_cast<A>(0)};
+        return;
+    }
     A x = cvt<A>(loc[2 * idx]) * static_cast<A>(wl) - static_cast<A>(0.5);
     A y = cvt<A>(loc[2 * idx + 1]) * static_cast<A>(hl) - static_cast<A>(0.5);
     // fmax returns the non-NaN operand, so a NaN coordinate becomes -2 (outside the map)
@@ -82,7 +140,7 @@ __device__ __forceinline__ void corner4(const T* __restrict__ loc, const T* __re
         const int dx = k & 1, dy = k >> 1, xi = x0 + dx, yi = y0 + dy;
         const int64_t t = st + static_cast<int64_t>(yi) * wl + xi;
         bool in = xi >= 0 && xi < wl && yi >= 0 && yi < hl && t >= 0 && t < g.N;
-        if (in && g.mask != nullptr) in = g.mask[(row / (static_cast<int64_t>(g.Q) * g.H)) * g.N + t] == 0;
+        if (GENERAL && in && g.mask != nullptr) in = g.mask[(row / (static_cast<int64_t>(g.Q) * g.H)) * g.N + t] == 0;
         out[k].tok = in ? static_cast<int>(t) : -1;
         out[k].w = in ? w * (dx ? fx : static_cast<A>(1) - fx) * (dy ? fy : static_cast<A>(1) - fy)
                       : static_cast<A>(0);

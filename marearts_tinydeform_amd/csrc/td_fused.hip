@@ -72,13 +72,13 @@ __device__ __forceinline__ BlockRow decode_block(int bid, int H, int qtiles, int
     return r;
 }
 
-template <typename T, int WAVES, int NB>
+template <typename T, int WAVES, int NB, bool GENERAL>
 __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) {
     constexpr int NTH = WAVES * kWave;
     constexpr int V = 16 / static_cast<int>(sizeof(T));
     const Geom& g = p.g;
     const int C = p.C, QT = p.QT, SG = p.SG, CV = C / V;
-    const int LP = g.L * g.P, S = 4 * LP, D = g.D;
+    const int LP = g.LP, S = 4 * LP, D = g.D;
     const int GP = C + 4;  // float pitch of a g row in LDS: 16-byte aligned, rows offset by 4 banks
     const int NTILE = (D + 15) >> 4, PW = NTILE * 16;
 
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
         const int r = i / LP, j = i - r * LP, q = q0 + r;
         Corner<float>* c4 = cw + r * S + 4 * j;
         if (q < g.Q) {
-            corner4<T, float>(loc, attn, g, (static_cast<int64_t>(br.b) * g.Q + q) * g.H + br.h, j, c4);
+            corner4<T, float, GENERAL>(loc, attn, g, (static_cast<int64_t>(br.b) * g.Q + q) * g.H + br.h, j, c4);
         } else {
 #pragma unroll
             for (int k = 0; k < 4; ++k) c4[k] = Corner<float>{-1, 0.f};
@@ -219,13 +219,13 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     }
 }
 
-template <typename T, int WAVES>
+template <typename T, int WAVES, bool GENERAL>
 __global__ __launch_bounds__(WAVES* kWave) void fused_generic_kernel(FusedParams p) {
     using A = typename AccOf<T>::type;
     constexpr int NTH = WAVES * kWave;
     const Geom& g = p.g;
     const int C = p.C, QT = p.QT;
-    const int LP = g.L * g.P, S = 4 * LP, D = g.D;
+    const int LP = g.LP, S = 4 * LP, D = g.D;
 
     extern __shared__ __align__(16) unsigned char smem[];
     Corner<A>* cw = reinterpret_cast<Corner<A>*>(smem);  // [QT][S]
@@ -248,7 +248,7 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_generic_kernel(FusedParams
         const int r = i / LP, j = i - r * LP, q = q0 + r;
         Corner<A>* c4 = cw + r * S + 4 * j;
         if (q < g.Q) {
-            corner4<T, A>(loc, attn, g, (static_cast<int64_t>(br.b) * g.Q + q) * g.H + br.h, j, c4);
+            corner4<T, A, GENERAL>(loc, attn, g, (static_cast<int64_t>(br.b) * g.Q + q) * g.H + br.h, j, c4);
         } else {
 #pragma unroll
             for (int k = 0; k < 4; ++k) c4[k] = Corner<A>{-1, static_cast<A>(0)};
@@ -303,26 +303,28 @@ inline int64_t map_units(FusedParams& p) {
     return static_cast<int64_t>(p.per_xcd) * kXcds;
 }
 
-template <typename T, int WAVES, int NB>
+template <typename T, int WAVES>
 int go_vec(FusedParams p, size_t lds, hipStream_t stream) {
     const int64_t blocks = map_units(p);
-    hipLaunchKernelGGL((fused_vec_kernel<T, WAVES, NB>), dim3(static_cast<unsigned>(blocks)), dim3(WAVES * kWave),
-                       lds, stream, p);
+    if (p.g.general())
+        hipLaunchKernelGGL((fused_vec_kernel<T, WAVES, 8, true>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(WAVES * kWave), lds, stream, p);
+    else
+        hipLaunchKernelGGL((fused_vec_kernel<T, WAVES, 8, false>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(WAVES * kWave), lds, stream, p);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : set_error(-3, "fused_vec launch failed: %s", hipGetErrorString(e));
-}
-
-// nb = corner loads in flight per lane: 8 measured best on MI355X at every benchmark shape; 16 for tuning.
-template <typename T, int WAVES>
-int go_vec_nb(const FusedParams& p, int nb, size_t lds, hipStream_t stream) {
-    return nb == 16 ? go_vec<T, WAVES, 16>(p, lds, stream) : go_vec<T, WAVES, 8>(p, lds, stream);
 }
 
 template <typename T, int WAVES>
 int go_generic(FusedParams p, size_t lds, hipStream_t stream) {
     const int64_t blocks = map_units(p);
-    hipLaunchKernelGGL((fused_generic_kernel<T, WAVES>), dim3(static_cast<unsigned>(blocks)), dim3(WAVES * kWave),
-                       lds, stream, p);
+    if (p.g.general())
+        hipLaunchKernelGGL((fused_generic_kernel<T, WAVES, true>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(WAVES * kWave), lds, stream, p);
+    else
+        hipLaunchKernelGGL((fused_generic_kernel<T, WAVES, false>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(WAVES * kWave), lds, stream, p);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : set_error(-3, "fused_generic launch failed: %s", hipGetErrorString(e));
 }
@@ -331,7 +333,7 @@ template <typename T>
 int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune) {
     using A = typename AccOf<T>::type;
     const Geom& g = p.g;
-    const int LP = g.L * g.P, S = 4 * LP, C = p.C, D = g.D;
+    const int LP = g.LP, S = 4 * LP, C = p.C, D = g.D;
     const int qmax = g.Q < 16 ? g.Q : 16;
 
     if constexpr (!std::is_same<T, double>::value) {
@@ -379,12 +381,12 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune) {
                 p.SG = sg;
                 p.KS = ks;
                 p.qtiles = (g.Q + qt - 1) / qt;
-                const int nb = tune.nb;
+                // 8 corner loads in flight per lane: measured best on MI355X at every benchmark shape
                 switch (waves) {
-                    case 1: return go_vec_nb<T, 1>(p, nb, lds(qt), stream);
-                    case 2: return go_vec_nb<T, 2>(p, nb, lds(qt), stream);
-                    case 4: return go_vec_nb<T, 4>(p, nb, lds(qt), stream);
-                    case 8: return go_vec_nb<T, 8>(p, nb, lds(qt), stream);
+                    case 1: return go_vec<T, 1>(p, lds(qt), stream);
+                    case 2: return go_vec<T, 2>(p, lds(qt), stream);
+                    case 4: return go_vec<T, 4>(p, lds(qt), stream);
+                    case 8: return go_vec<T, 8>(p, lds(qt), stream);
                     default: return set_error(-1, "fused: waves must be 1, 2, 4 or 8 (got %d)", waves);
                 }
             }

@@ -17,7 +17,6 @@ struct FusedTune {
     int qt = 0;     // query rows per workgroup (1..16)
     int sg = 0;     // corner split per row (power of two)
     int waves = 0;  // wavefronts per workgroup (1, 2, 4 or 8)
-    int nb = 0;     // corner loads in flight per lane (8 or 16)
     int generic = 0;  // 1 forces the generic kernel
 };
 
@@ -26,7 +25,6 @@ struct SampleTune {
     int sg = 0;
     int waves = 0;
     int vec = 0;  // elements per load
-    int nb = 0;   // corner loads in flight per lane (8 or 16)
 };
 
 // Every launcher returns 0, or a negative TD_E* code after recording a message with set_error.

@@ -22,12 +22,12 @@ struct SampleParams {
     int per_xcd, blocks;  // workgroup -> row-block mapping: XCD x takes a contiguous range of row blocks
 };
 
-template <typename T, int V, int WAVES, int NB>
+template <typename T, int V, int WAVES, int NB, bool GENERAL>
 __global__ __launch_bounds__(WAVES* kWave) void sample_kernel(SampleParams p) {
     constexpr int NTH = WAVES * kWave;
     using IO = VecIO<T, V>;
     const Geom& g = p.g;
-    const int LP = g.L * g.P, S = 4 * LP, D = g.D, HD = g.H * D;
+    const int LP = g.LP, S = 4 * LP, D = g.D, HD = g.H * D;
     const int DV = D / V, SG = p.SG, GS = DV * SG, RB = p.RB;
     extern __shared__ __align__(16) unsigned char smem[];
     Corner<float>* cw = reinterpret_cast<Corner<float>*>(smem);  // [RB][S]
@@ -47,7 +47,7 @@ __global__ __launch_bounds__(WAVES* kWave) void sample_kernel(SampleParams p) {
         const int64_t row = row0 + r;
         Corner<float>* c4 = cw + r * S + 4 * j;
         if (row < p.rows) {
-            corner4<T, float>(loc, attn, g, row, j, c4);
+            corner4<T, float, GENERAL>(loc, attn, g, row, j, c4);
         } else {
 #pragma unroll
             for (int k = 0; k < 4; ++k) c4[k] = Corner<float>{-1, 0.f};
@@ -81,7 +81,7 @@ template <int WAVES>
 __global__ __launch_bounds__(WAVES* kWave) void sample_f64_kernel(SampleParams p) {
     constexpr int NTH = WAVES * kWave;
     const Geom& g = p.g;
-    const int LP = g.L * g.P, S = 4 * LP, D = g.D, HD = g.H * D, RB = p.RB;
+    const int LP = g.LP, S = 4 * LP, D = g.D, HD = g.H * D, RB = p.RB;
     extern __shared__ __align__(16) unsigned char smem[];
     Corner<double>* cw = reinterpret_cast<Corner<double>*>(smem);
     const double* __restrict__ value = static_cast<const double*>(p.value);
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(WAVES* kWave) void sample_f64_kernel(SampleParams p
         const int64_t row = row0 + r;
         Corner<double>* c4 = cw + r * S + 4 * j;
         if (row < p.rows) {
-            corner4<double, double>(loc, attn, g, row, j, c4);
+            corner4<double, double, true>(loc, attn, g, row, j, c4);
         } else {
             for (int k = 0; k < 4; ++k) c4[k] = Corner<double>{-1, 0.0};
         }
@@ -123,29 +123,28 @@ constexpr size_t kLdsBudget = 65536;
 
 inline bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
-template <typename T, int V, int WAVES, int NB>
+template <typename T, int V, int WAVES>
 int go(SampleParams p, size_t lds, hipStream_t stream) {
     const int64_t blocks = (p.rows + p.RB - 1) / p.RB;
     p.blocks = static_cast<int>(blocks);
     p.per_xcd = static_cast<int>((blocks + kXcds - 1) / kXcds);
-    hipLaunchKernelGGL((sample_kernel<T, V, WAVES, NB>), dim3(static_cast<unsigned>(p.per_xcd) * kXcds),
-                       dim3(WAVES * kWave), lds, stream, p);
+    // 8 corner loads in flight per lane: measured best on MI355X
+    if (p.g.general())
+        hipLaunchKernelGGL((sample_kernel<T, V, WAVES, 8, true>), dim3(static_cast<unsigned>(p.per_xcd) * kXcds),
+                           dim3(WAVES * kWave), lds, stream, p);
+    else
+        hipLaunchKernelGGL((sample_kernel<T, V, WAVES, 8, false>), dim3(static_cast<unsigned>(p.per_xcd) * kXcds),
+                           dim3(WAVES * kWave), lds, stream, p);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : set_error(-3, "sample launch failed: %s", hipGetErrorString(e));
 }
 
-// nb = corner loads in flight per lane: 8 measured best on MI355X; 16 for tuning.
-template <typename T, int V, int WAVES>
-int go_nb(SampleParams p, int nb, size_t lds, hipStream_t stream) {
-    return nb == 16 ? go<T, V, WAVES, 16>(p, lds, stream) : go<T, V, WAVES, 8>(p, lds, stream);
-}
-
 template <typename T, int V>
-int go_waves(SampleParams p, int waves, int nb, size_t lds, hipStream_t stream) {
+int go_waves(SampleParams p, int waves, size_t lds, hipStream_t stream) {
     switch (waves) {
-        case 1: return go_nb<T, V, 1>(p, nb, lds, stream);
-        case 2: return go_nb<T, V, 2>(p, nb, lds, stream);
-        case 4: return go_nb<T, V, 4>(p, nb, lds, stream);
+        case 1: return go<T, V, 1>(p, lds, stream);
+        case 2: return go<T, V, 2>(p, lds, stream);
+        case 4: return go<T, V, 4>(p, lds, stream);
         default: return set_error(-1, "sample: waves must be 1, 2 or 4 (got %d)", waves);
     }
 }
@@ -153,7 +152,7 @@ int go_waves(SampleParams p, int waves, int nb, size_t lds, hipStream_t stream) 
 template <typename T>
 int launch_sample_t(SampleParams p, hipStream_t stream, const SampleTune& tune) {
     const Geom& g = p.g;
-    const int LP = g.L * g.P, S = 4 * LP, D = g.D;
+    const int LP = g.LP, S = 4 * LP, D = g.D;
     constexpr int VMAX = 16 / static_cast<int>(sizeof(T));
     const uintptr_t align = reinterpret_cast<uintptr_t>(p.value) | reinterpret_cast<uintptr_t>(p.out);
     int V = tune.vec > 0 ? tune.vec : VMAX;
@@ -184,13 +183,12 @@ int launch_sample_t(SampleParams p, hipStream_t stream, const SampleTune& tune) 
     while (rb > 1 && lds(rb) > kLdsBudget) --rb;
     p.RB = rb;
     p.SG = sg;
-    const int nb = tune.nb;
     switch (V) {
-        case 1: return go_waves<T, 1>(p, waves, nb, lds(rb), stream);
-        case 2: return go_waves<T, 2>(p, waves, nb, lds(rb), stream);
-        case 4: return go_waves<T, 4>(p, waves, nb, lds(rb), stream);
+        case 1: return go_waves<T, 1>(p, waves, lds(rb), stream);
+        case 2: return go_waves<T, 2>(p, waves, lds(rb), stream);
+        case 4: return go_waves<T, 4>(p, waves, lds(rb), stream);
         case 8:
-            if constexpr (VMAX >= 8) return go_waves<T, 8>(p, waves, nb, lds(rb), stream);
+            if constexpr (VMAX >= 8) return go_waves<T, 8>(p, waves, lds(rb), stream);
             break;
         default: break;
     }
@@ -198,7 +196,7 @@ int launch_sample_t(SampleParams p, hipStream_t stream, const SampleTune& tune) 
 }
 
 int launch_sample_f64(SampleParams p, hipStream_t stream) {
-    const int S = 4 * p.g.L * p.g.P;
+    const int S = 4 * p.g.LP;
     int rb = 4;
     while (rb > 1 && static_cast<size_t>(rb) * S * sizeof(Corner<double>) > kLdsBudget) --rb;
     p.RB = rb;

@@ -1,7 +1,7 @@
 """Torch restatement of the reference's PyTorch path. TEST INFRASTRUCTURE ONLY: imported by tests/ and by
 bench.py's cpu_baseline leg (it is the CPU path the reference runs for CPU tensors), never by the product.
 
-Follows marearts_tinydeform/reference.py:13-40: value = F.linear(memory, W, b), then for each level
+deform_attn follows marearts_tinydeform/reference.py:13-40: value = F.linear(memory, W, b), then for each level
 F.grid_sample(bilinear, zeros, align_corners=False) of that level's [B*H, D, h, w] map at 2 * loc - 1, then the
 attention-weighted sum over levels and points. Runs in the dtype it is given (float32 for the CPU baseline,
 float64 to cross-check the brute force).
@@ -33,3 +33,32 @@ def deform_attn(memory, value_weight, value_bias, spatial_shapes, level_start_in
         a = attention_weights[:, :, :, lvl].transpose(1, 2).reshape(B * H, 1, Q, P)
         acc = acc + torch.einsum('ndqp,ndqp->ndq', smp, a.expand_as(smp))
     return acc.view(B, H * D, Q).transpose(1, 2).contiguous()
+
+
+def deform_sample_v2(value, spatial_shapes, sampling_locations, attention_weights, num_points_list,
+                     method='default'):
+    """D-FINE's deformable attention core, restating transformers models/d_fine/modeling_d_fine.py:150-216
+    (multi_scale_deformable_attention_v2): value [B, N, H, D], loc [B, Q, H, sum(P), 2], attn [B, Q, H, sum(P)];
+    per level, grid_sample (method 'default') or the nearest-pixel gather of (loc * [W, H] + 0.5) cast to int64
+    and clamped into the map ('discrete'), then the attention-weighted sum -> [B, Q, H * D]."""
+    B, N, H, D = value.shape
+    _, Q, _, J, _ = sampling_locations.shape
+    levels = [(int(h), int(w)) for h, w in spatial_shapes]
+    per_level = value.permute(0, 2, 3, 1).flatten(0, 1).split([h * w for h, w in levels], dim=-1)
+    grids = 2 * sampling_locations - 1 if method == 'default' else sampling_locations
+    grids = grids.permute(0, 2, 1, 3, 4).flatten(0, 1).split(list(num_points_list), dim=-2)  # [B*H, Q, P_l, 2]
+    sampled = []
+    for lvl, (h, w) in enumerate(levels):
+        v = per_level[lvl].reshape(B * H, D, h, w)
+        g = grids[lvl]
+        if method == 'default':
+            sampled.append(F.grid_sample(v, g, mode='bilinear', padding_mode='zeros', align_corners=False))
+        else:
+            coord = (g * torch.tensor([[w, h]], dtype=g.dtype) + 0.5).to(torch.int64)
+            x = coord[..., 0].clamp(0, w - 1)
+            y = coord[..., 1].clamp(0, h - 1)
+            n = torch.arange(B * H)[:, None, None]
+            sampled.append(v[n, :, y, x].permute(0, 3, 1, 2))  # [B*H, D, Q, P_l]
+    a = attention_weights.permute(0, 2, 1, 3).reshape(B * H, 1, Q, J)
+    out = (torch.cat(sampled, dim=-1) * a).sum(-1)  # [B*H, D, Q]
+    return out.view(B, H * D, Q).transpose(1, 2).contiguous()

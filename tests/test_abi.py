@@ -33,7 +33,8 @@ def lib():
 
 def test_header_declares_the_entry_points():
     assert header_functions() == ['td_fused_forward', 'td_fused_forward_masked', 'td_last_error',
-                                  'td_sample_forward', 'td_sample_forward_masked', 'td_value_proj', 'td_version']
+                                  'td_sample_forward', 'td_sample_forward_masked', 'td_sample_forward_v2',
+                                  'td_value_proj', 'td_version']
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -103,6 +104,21 @@ def test_masked_entries_reject_on_host(lib):
         header_defines()['TD_E_ARG']
     assert 'levels x points' in lib.td_last_error().decode()
     assert lib.td_sample_forward_masked(1, p, p, p, p, p, None, p, 1, 0, 100, 8, 32, 3, 4, None) == 0
+
+
+def test_sample_v2_rejects_on_host(lib):
+    import ctypes as ct
+    p = 16
+    pts = (ct.c_int64 * 3)(30, 30, 10)  # 70 samples > 64
+    assert lib.td_sample_forward_v2(1, p, p, p, p, p, None, p, 1, 4, 100, 8, 32, 3, ct.cast(pts, ct.c_void_p), 0,
+                                    None) == header_defines()['TD_E_ARG']
+    assert 'levels x points' in lib.td_last_error().decode()
+    ok = (ct.c_int64 * 3)(3, 6, 3)
+    assert lib.td_sample_forward_v2(1, p, p, p, p, p, None, p, 1, 4, 100, 8, 32, 3, ct.cast(ok, ct.c_void_p), 2,
+                                    None) == header_defines()['TD_E_ARG']
+    assert 'method' in lib.td_last_error().decode()
+    assert lib.td_sample_forward_v2(1, p, p, p, p, p, None, p, 1, 0, 100, 8, 32, 3, ct.cast(ok, ct.c_void_p), 1,
+                                    None) == 0
 
 
 def test_empty_work_returns_ok_without_launching(lib):

@@ -351,3 +351,36 @@ def test_padding_mask_rtdetr640_fp16_b4_padded_images():
         assert err / np.abs(ref).max() <= REL[torch.float16]
         outs.append(out.double())
     assert torch.allclose(outs[0], outs[1], atol=2 * atol, rtol=2 * rtol)
+
+
+# ---- D-FINE core: per-level point counts, discrete method ---------------------------------------------------
+
+def dfine_case(B, Q, H, D, levels, points, dtype, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    shapes = torch.tensor(levels, dtype=torch.long)
+    sizes = shapes[:, 0] * shapes[:, 1]
+    starts = torch.cat([torch.zeros(1, dtype=torch.long), sizes.cumsum(0)[:-1]])
+    N, J = int(sizes.sum()), sum(points)
+    value = torch.randn(B, N, H, D, generator=g).to(dtype)
+    loc = (torch.rand(B, Q, 1, 1, 2, generator=g) + 0.3 * torch.randn(B, Q, H, J, 2, generator=g)).to(dtype)
+    attn = torch.randn(B, Q, H, J, generator=g).softmax(-1).to(dtype)
+    return value, shapes, starts, loc, attn
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize('method', ['default', 'discrete'])
+def test_dfine_sample_v2(dtype, method):
+    for points, levels in (([3, 6, 3], RTDETR_LEVELS), ([4, 4, 4], RTDETR_LEVELS), ([2, 1, 5, 3], DINO_LEVELS)):
+        value, shapes, starts, loc, attn = dfine_case(2, 120, 8, 32, levels, points, dtype)
+        mask = torch.rand(2, value.shape[1], generator=torch.Generator().manual_seed(3)) < 0.2
+        atol, rtol = TOL[dtype]
+        for m in (None, mask):
+            ref = bruteforce.sample_v2(value, shapes, starts, loc, attn, points, method, padding_mask=m)
+            with torch.inference_mode():
+                out = td.ma_deform_sample_v2(value.cuda(), shapes.cuda(), starts.cuda(), loc.cuda(), attn.cuda(),
+                                             points, method, padding_mask=None if m is None else m.cuda())
+            assert_close(f'dfine {points} {method} {dtype} mask={m is not None}', out, ref, atol, rtol)
+    with pytest.raises(RuntimeError):  # counts that do not add up to the sample dimension
+        td.ma_deform_sample_v2(value.cuda(), shapes.cuda(), starts.cuda(), loc.cuda(), attn.cuda(), [2, 2, 2, 2])
+    with pytest.raises(ValueError):
+        td.ma_deform_sample_v2(value.cuda(), shapes.cuda(), starts.cuda(), loc.cuda(), attn.cuda(), points, 'nope')

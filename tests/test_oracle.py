@@ -302,3 +302,65 @@ def test_padding_mask_all_and_none():
     assert not full.any()  # every token padded: exact zero, bias included
     none = bruteforce.deform_attn(*args, padding_mask=torch.zeros(2, N, dtype=torch.bool))
     assert np.abs(none - bruteforce.deform_attn(*args)).max() == 0
+
+
+# ---- per-level point counts and D-FINE's discrete method -----------------------------------------------------
+
+def dfine_inputs(B, Q, H, D, levels, points, seed, spread=0.4):
+    g = torch.Generator().manual_seed(seed)
+    shapes, starts, N = level_index(levels)
+    J = sum(points)
+    value = torch.randn(B, N, H, D, generator=g, dtype=torch.float64)
+    loc = (torch.rand(B, Q, 1, 1, 2, generator=g) + spread * torch.randn(B, Q, H, J, 2, generator=g)).double()
+    attn = torch.randn(B, Q, H, J, generator=g).softmax(-1).double()
+    return value, shapes, starts, loc, attn
+
+
+@pytest.mark.parametrize('points', [[3, 6, 3], [4, 4, 4], [2, 1, 5, 3], [8]])
+@pytest.mark.parametrize('method', ['default', 'discrete'])
+def test_sample_v2_matches_dfine_restatement(points, method):
+    levels = [(12, 9), (6, 5), (3, 3), (2, 2)][:len(points)]
+    value, shapes, starts, loc, attn = dfine_inputs(2, 7, 3, 4, levels, points, seed=31)
+    ref = gridsample.deform_sample_v2(value, shapes, loc, attn, points, method).numpy()
+    got = bruteforce.sample_v2(value, shapes, starts, loc, attn, points, method)
+    assert np.abs(got - ref).max() <= 1e-12
+
+
+def test_sample_v2_uniform_points_equals_sample():
+    levels = [(12, 9), (6, 5), (3, 3)]
+    value, shapes, starts, loc, attn = dfine_inputs(2, 5, 3, 4, levels, [4, 4, 4], seed=32)
+    v1 = bruteforce.sample(value.reshape(2, -1, 12), 3, shapes, starts, loc.reshape(2, 5, 3, 3, 4, 2),
+                           attn.reshape(2, 5, 3, 3, 4))
+    assert np.abs(bruteforce.sample_v2(value, shapes, starts, loc, attn, [4, 4, 4]) - v1).max() == 0
+
+
+def test_discrete_pixel_closed_form():
+    # a location inside pixel (i, j) reads exactly value[start + j * W + i]; outside the map it clamps to the edge
+    levels = [(4, 8)]
+    value, shapes, starts, loc, attn = dfine_inputs(1, 3, 1, 2, levels, [2], seed=33)
+    loc = loc.clone()
+    loc[0, 0, 0, 0] = torch.tensor([(5 + 0.3) / 8, (2 + 0.6) / 4])   # pixel x=5 (rounds up from 5.8: 5.3 + 0.5)
+    loc[0, 0, 0, 1] = torch.tensor([-3.0, 9.0])                       # clamps to x=0, y=3
+    attn = torch.zeros_like(attn)
+    attn[0, 0, 0, 0], attn[0, 0, 0, 1] = 0.25, 0.75
+    out = bruteforce.sample_v2(value, shapes, starts, loc, attn, [2], 'discrete')
+    # x = int(5.3 + 0.5) = 5, y = int(2.6 + 0.5) = 3
+    expect = 0.25 * value[0, 3 * 8 + 5, 0].numpy() + 0.75 * value[0, 3 * 8 + 0, 0].numpy()
+    assert np.abs(out[0, 0] - expect).max() <= 1e-15
+
+
+def test_planted_discrete_mistake_fails_restatement_pin(monkeypatch):
+    # rounding without the + 0.5 (floor instead of nearest) must disagree with the D-FINE restatement
+    levels = [(12, 9), (6, 5)]
+    value, shapes, starts, loc, attn = dfine_inputs(2, 7, 3, 4, levels, [3, 5], seed=34)
+    ref = gridsample.deform_sample_v2(value, shapes, loc, attn, [3, 5], 'discrete').numpy()
+    orig = bruteforce.corner_table_v2
+
+    def floor_not_round(shapes_, starts_, loc_, attn_, n, pts, method='default', mask=None):
+        wh = torch.as_tensor(np.asarray(shapes_))[:, [1, 0]].double()
+        level_of = np.repeat(np.arange(len(pts)), pts)
+        return orig(shapes_, starts_, torch.as_tensor(np.asarray(loc_)) - 0.5 / wh[level_of], attn_, n, pts, method,
+                    mask)
+
+    monkeypatch.setattr(bruteforce, 'corner_table_v2', floor_not_round)
+    assert np.abs(bruteforce.sample_v2(value, shapes, starts, loc, attn, [3, 5], 'discrete') - ref).max() > 1e-3
