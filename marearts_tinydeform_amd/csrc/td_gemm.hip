@@ -424,17 +424,20 @@ int go_mfma(GemmParams p, hipStream_t stream) {
 //   8  256 x 128 A and W through LDS (4 x 2 waves of 64 x 64)
 //   9  128 x 128 A and W through LDS, K chunks of 128/64
 //   10 128 x 256 A and W through LDS (2 x 4 waves of 64 x 64)
+//   11 128 x 256 A and W through LDS (2 x 2 waves of 64 x 128)
+//   12 256 x 128 A and W through LDS (2 x 2 waves of 128 x 64)
+//   13 128 x 128 A and W through LDS, K chunks of 32/16
 template <typename T>
 int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
     if (variant <= 0) {
         // measured on MI355X: one round trip (5) while the grid is small; for large 16-bit problems both operands
-        // through LDS in 128 x 128 tiles (7); float32 keeps A direct in 64 x 128 tiles (2)
+        // through LDS in 128 x 128 tiles with K chunks of 32 (13); float32 keeps A direct in 64 x 128 tiles (2)
         constexpr int one_chunk = 8 * KBlock<T>::kK;
         const int64_t tiles_128 = ((p.M + 127) / 128) * static_cast<int64_t>((p.NO + 127) / 128);
         if (p.K <= one_chunk && tiles_128 < 512)
             variant = 5;
         else
-            variant = sizeof(T) == 2 ? 7 : 2;
+            variant = sizeof(T) == 2 ? 13 : 2;
     }
     switch (variant) {
         case 1: return go_mfma<T, 4, 1, 1, 4, 2, 2>(p, stream);
@@ -447,6 +450,9 @@ int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
         case 8: return go_lds<T, 4, 2, 4, 4, 2>(p, stream);
         case 9: return go_lds<T, 2, 2, 4, 4, 4>(p, stream);
         case 10: return go_lds<T, 2, 4, 4, 4, 2>(p, stream);
+        case 11: return go_lds<T, 2, 2, 4, 8, 2>(p, stream);
+        case 12: return go_lds<T, 2, 2, 8, 4, 2>(p, stream);
+        case 13: return go_lds<T, 2, 2, 4, 4, 1>(p, stream);
         default: return set_error(-1, "value_proj: unknown tile variant %d", variant);
     }
 }
