@@ -41,6 +41,7 @@ extern "C" {
 #define TD_E_ARG -1    /* invalid shape, limit or pointer (the same cases the reference rejects) */
 #define TD_E_DTYPE -2  /* unknown dtype code */
 #define TD_E_LAUNCH -3 /* the HIP runtime refused a kernel launch */
+#define TD_E_WORKSPACE -4 /* td_layer_fused_forward: this problem needs loc_out and attn_out (see there) */
 
 /* limits shared with the reference operator (csrc/ma_deform_fused.cu:26-28) */
 #define TD_MAX_LEVEL_POINTS 64 /* L * P */
@@ -109,6 +110,56 @@ int td_sample_forward_v2(int dtype, const void* value, const int64_t* spatial_sh
                          const void* attention_weights, const uint8_t* padding_mask, void* out, int64_t B, int64_t Q,
                          int64_t N, int64_t H, int64_t D, int64_t L, const int64_t* points_per_level, int discrete,
                          void* stream);
+
+/*
+ * Decoder-layer entries: the query side of a deformable-attention layer computed on the device, restating
+ * HF transformers RTDetrMultiscaleDeformableAttention.forward (models/rt_detr/modeling_rt_detr.py:673-713):
+ *   x          = query[b,q] (+ position[b,q])                                  query, position: [B, Q, Cq]
+ *   offsets    = x @ offsets_weight^T + offsets_bias      offsets_weight [H*L*P*2, Cq], viewed [H, L, P, 2]
+ *   attention  = softmax over L*P of (x @ attn_weight^T + attn_bias), per head; attn_weight [H*L*P, Cq]
+ *   location   = ref[b,q,l] + offsets / (W_l, H_l)                        ref_dim = 2
+ *              = ref[b,q,l,0:2] + offsets / P * ref[b,q,l,2:4] * 0.5      ref_dim = 4 (box centre and size)
+ * reference_points is [B, Q, ref_levels, ref_dim] with ref_levels 1 (shared by every level) or L. Biases and
+ * position may be NULL. Locations and weights are computed in float32 (float64 for TD_F64) and never rounded to
+ * dtype. No counterpart in the reference, whose operator starts from ready locations and weights; these fuse the
+ * producers of those inputs into the operator (the sampling-offset and attention projections, the softmax and the
+ * reference-point arithmetic), so they need no HBM round trip and no separate launches.
+ */
+
+/*
+ * Query prologue alone: writes loc_out [B, Q, H, L, P, 2] and attn_out [B, Q, H, L, P], both float32 (float64 for
+ * TD_F64). Used ahead of td_layer_sample_forward in project mode.
+ */
+int td_layer_prologue(int dtype, const void* query, const void* position, const void* reference_points,
+                      int64_t ref_levels, int64_t ref_dim, const void* offsets_weight, const void* offsets_bias,
+                      const void* attn_weight, const void* attn_bias, const int64_t* spatial_shapes, void* loc_out,
+                      void* attn_out, int64_t B, int64_t Q, int64_t Cq, int64_t H, int64_t L, int64_t P,
+                      void* stream);
+
+/*
+ * Fused layer: the query prologue inside the fused-mode kernel (td_fused_forward_masked with the locations and
+ * weights computed in-kernel). out [B, Q, H*D] as td_fused_forward; padding_mask as td_fused_forward_masked.
+ * loc_out / attn_out (float32, float64 for TD_F64; NULL for none) receive the locations and weights when given.
+ * Problems the in-kernel prologue cannot take (TD_F64; C or Cq not a multiple of 16 bytes; rows not 16-byte
+ * aligned) run the standalone prologue into loc_out / attn_out and then the fused kernel: for those both buffers
+ * are required, and without them the call returns TD_E_WORKSPACE having launched nothing.
+ */
+int td_layer_fused_forward(int dtype, const void* query, const void* position, const void* reference_points,
+                           int64_t ref_levels, int64_t ref_dim, const void* offsets_weight, const void* offsets_bias,
+                           const void* attn_weight, const void* attn_bias, const void* memory,
+                           const void* value_weight, const void* value_bias, const int64_t* spatial_shapes,
+                           const int64_t* level_start_index, const uint8_t* padding_mask, void* out, void* loc_out,
+                           void* attn_out, int64_t B, int64_t Q, int64_t N, int64_t Cq, int64_t C, int64_t H,
+                           int64_t D, int64_t L, int64_t P, void* stream);
+
+/*
+ * td_sample_forward_masked with locations and weights in float32 (float64 for TD_F64), as td_layer_prologue
+ * writes them: the second half of the layer's project mode.
+ */
+int td_layer_sample_forward(int dtype, const void* value, const int64_t* spatial_shapes,
+                            const int64_t* level_start_index, const void* loc, const void* attn,
+                            const uint8_t* padding_mask, void* out, int64_t B, int64_t Q, int64_t N, int64_t H,
+                            int64_t D, int64_t L, int64_t P, void* stream);
 
 /*
  * Value projection (the first half of project mode): value[M, NO] = memory[M, K] @ weight[NO, K]^T + bias[NO],

@@ -10,10 +10,11 @@ import functools
 import torch
 
 from . import _native
-from .reference import ma_deform_attn_reference
+from .reference import layer_locations_reference, ma_deform_attn_layer_reference, ma_deform_attn_reference
 
 __all__ = ['ma_deform_attn', 'ma_deform_attn_reference', 'choose_mode', 'ma_deform_sample', 'ma_deform_sample_v2',
-           'predict_us']
+           'predict_us', 'ma_deform_attn_layer', 'ma_deform_attn_layer_reference', 'layer_locations_reference',
+           'MSDeformAttnLayer']
 __version__ = '0.1.0'
 
 MODES = ('auto', 'fused', 'project')
@@ -50,8 +51,12 @@ def _limits(device_index):
 
 def predict_us(memory, value_weight, sampling_locations, table=None):
     """Predicted µs of mode 'fused' and 'project' for these shapes: {'fused': t, 'project': t}."""
-    B, N, C = memory.shape
     _, Q, H, L, P, _ = sampling_locations.shape
+    return _predict(memory, value_weight, Q, H, L, P, table)
+
+
+def _predict(memory, value_weight, Q, H, L, P, table=None):
+    B, N, C = memory.shape
     HD = value_weight.shape[0]
     D = HD // max(H, 1)
     s = memory.element_size()
@@ -157,3 +162,123 @@ def ma_deform_sample_v2(value, spatial_shapes, level_start_index, sampling_locat
     _reject_grad(value, sampling_locations, attention_weights)
     return _on_device(value, _native.sample_forward_v2, value, spatial_shapes, level_start_index, sampling_locations,
                       attention_weights, num_points_list, method, padding_mask)
+
+
+def ma_deform_attn_layer(hidden_states, encoder_hidden_states, reference_points, spatial_shapes, level_start_index,
+                         sampling_offsets_weight, sampling_offsets_bias, attention_weights_weight,
+                         attention_weights_bias, value_weight, value_bias, output_weight, output_bias, num_heads,
+                         num_points, position_embeddings=None, padding_mask=None, mode='auto',
+                         return_attention_weights=False):
+    """One deformable cross-attention layer of a DETR decoder (HF transformers RTDetrMultiscaleDeformableAttention,
+    models/rt_detr/modeling_rt_detr.py:673-727) with its producers fused on the GPU:
+
+      x          = hidden_states (+ position_embeddings)                        [B, Q, C]
+      offsets    = x @ sampling_offsets_weight.T + bias    -> [B, Q, H, L, P, 2]
+      attention  = softmax over L * P of (x @ attention_weights_weight.T + bias)
+      locations  = reference_points + offsets / (W_l, H_l)          (points, [B, Q, 1 or L, 2])
+                 = ref[..., :2] + offsets / P * ref[..., 2:] * 0.5  (boxes, [B, Q, 1 or L, 4])
+      out        = output_proj(ma_deform_attn(encoder_hidden_states, value_weight, value_bias, ...))
+
+    mode='fused': one kernel computes each (query tile, head)'s offsets and attention on MFMA, keeps the locations
+    in float32 in LDS and gathers the memory rows; mode='project': the query prologue kernel, the value GEMM and
+    the sampler; 'auto' picks by size as ma_deform_attn does. output_proj runs on the library's GEMM (skipped when
+    output_weight is None). padding_mask: bool [B, N], True = padded token (HF passes ~attention_mask).
+    Returns [B, Q, C_out], and the attention weights [B, Q, H, L, P] too with return_attention_weights.
+    CPU tensors run ma_deform_attn_layer_reference. Inference only.
+    """
+    if mode not in MODES:
+        raise ValueError(f'mode must be one of {MODES}, got {mode!r}')
+    args = (hidden_states, encoder_hidden_states, reference_points, spatial_shapes, level_start_index,
+            sampling_offsets_weight, sampling_offsets_bias, attention_weights_weight, attention_weights_bias,
+            value_weight, value_bias, output_weight, output_bias, num_heads, num_points)
+    if not encoder_hidden_states.is_cuda:
+        return ma_deform_attn_layer_reference(*args, position_embeddings=position_embeddings,
+                                              padding_mask=padding_mask,
+                                              return_attention_weights=return_attention_weights)
+    _native._require()
+    _reject_grad(hidden_states, encoder_hidden_states, reference_points, sampling_offsets_weight,
+                 sampling_offsets_bias, attention_weights_weight, attention_weights_bias, value_weight, value_bias,
+                 output_weight, output_bias, position_embeddings)
+    return _on_device(encoder_hidden_states, _layer, *args, position_embeddings, padding_mask, mode,
+                      return_attention_weights)
+
+
+def _layer(hidden_states, memory, reference_points, spatial_shapes, level_start_index, ow, ob, aw, ab, value_weight,
+           value_bias, output_weight, output_bias, num_heads, num_points, position, padding_mask, mode, want_attn):
+    B, Q, Cq, H, L, P = _native.check_layer(memory, hidden_states, reference_points, ow, ob, aw, ab, position,
+                                            spatial_shapes, num_heads, num_points)
+    if mode == 'auto':
+        t = _predict(memory, value_weight, Q, H, L, P)
+        mode = 'fused' if t['fused'] <= t['project'] else 'project'
+    if mode == 'fused':
+        core, la = _native.layer_fused_forward(hidden_states, position, reference_points, ow, ob, aw, ab, memory,
+                                               value_weight, value_bias, spatial_shapes, level_start_index, H, P,
+                                               padding_mask, return_locations=want_attn)
+        attn = la[1] if want_attn else None
+    else:
+        _native.check_projection(memory, value_weight, value_bias, H)
+        _native.check_padding_mask(memory, padding_mask)
+        loc, attn = _native.layer_prologue(hidden_states, position, reference_points, ow, ob, aw, ab, spatial_shapes,
+                                           H, P)
+        value = _native.value_proj(memory, value_weight, value_bias)
+        core = _native.layer_sample_forward(value, H, spatial_shapes, level_start_index, loc, attn, padding_mask)
+    out = core if output_weight is None else _native.value_proj(core, output_weight, output_bias)
+    if want_attn:
+        return out, attn.to(memory.dtype)
+    return out
+
+
+def _grid_offsets_bias(n_heads, n_levels, n_points):
+    """Deformable-DETR's initial sampling-offset bias: head h looks along direction 2 pi h / H (scaled so the larger
+    coordinate is 1), point p at distance p + 1, on every level."""
+    theta = torch.arange(n_heads, dtype=torch.float32) * (2.0 * torch.pi / n_heads)
+    grid = torch.stack([theta.cos(), theta.sin()], -1)
+    grid = grid / grid.abs().max(-1, keepdim=True)[0]
+    grid = grid.view(n_heads, 1, 1, 2).repeat(1, n_levels, n_points, 1)
+    grid = grid * torch.arange(1, n_points + 1, dtype=torch.float32).view(1, 1, n_points, 1)
+    return grid.flatten()
+
+
+class MSDeformAttnLayer(torch.nn.Module):
+    """Deformable cross-attention module of a DETR decoder, running ma_deform_attn_layer.
+
+    Same submodules as HF transformers' RTDetrMultiscaleDeformableAttention (sampling_offsets, attention_weights,
+    value_proj, output_proj; models/rt_detr/modeling_rt_detr.py:623-658), so its state dict loads unchanged, and the
+    same forward arguments and results: (output [B, Q, d_model], attention_weights [B, Q, H, L, P]).
+    attention_mask is the encoder's validity mask (True = real token), as HF passes it.
+    """
+
+    def __init__(self, d_model=256, n_levels=4, n_heads=8, n_points=4, mode='auto'):
+        super().__init__()
+        if d_model % n_heads != 0:
+            raise ValueError(f'd_model ({d_model}) must be divisible by n_heads ({n_heads})')
+        self.d_model, self.n_levels, self.n_heads, self.n_points, self.mode = d_model, n_levels, n_heads, n_points, mode
+        self.sampling_offsets = torch.nn.Linear(d_model, n_heads * n_levels * n_points * 2)
+        self.attention_weights = torch.nn.Linear(d_model, n_heads * n_levels * n_points)
+        self.value_proj = torch.nn.Linear(d_model, d_model)
+        self.output_proj = torch.nn.Linear(d_model, d_model)
+        self.reset_parameters()
+
+    @torch.no_grad()
+    def reset_parameters(self):
+        torch.nn.init.zeros_(self.sampling_offsets.weight)
+        self.sampling_offsets.bias.copy_(_grid_offsets_bias(self.n_heads, self.n_levels, self.n_points))
+        torch.nn.init.zeros_(self.attention_weights.weight)
+        torch.nn.init.zeros_(self.attention_weights.bias)
+        for lin in (self.value_proj, self.output_proj):
+            torch.nn.init.xavier_uniform_(lin.weight)
+            torch.nn.init.zeros_(lin.bias)
+
+    def forward(self, hidden_states, attention_mask=None, encoder_hidden_states=None, encoder_attention_mask=None,
+                position_embeddings=None, reference_points=None, spatial_shapes=None, spatial_shapes_list=None,
+                level_start_index=None, **kwargs):
+        if level_start_index is None:
+            sizes = spatial_shapes[:, 0] * spatial_shapes[:, 1]
+            level_start_index = torch.cat([sizes.new_zeros(1), sizes.cumsum(0)[:-1]])
+        padding_mask = None if attention_mask is None else ~attention_mask.bool()
+        return ma_deform_attn_layer(
+            hidden_states, encoder_hidden_states, reference_points, spatial_shapes, level_start_index,
+            self.sampling_offsets.weight, self.sampling_offsets.bias, self.attention_weights.weight,
+            self.attention_weights.bias, self.value_proj.weight, self.value_proj.bias, self.output_proj.weight,
+            self.output_proj.bias, self.n_heads, self.n_points, position_embeddings=position_embeddings,
+            padding_mask=padding_mask, mode=self.mode, return_attention_weights=True)

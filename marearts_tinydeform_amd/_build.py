@@ -20,7 +20,7 @@ BUILD = os.path.join(HERE, '_build')
 LIB = os.path.join(HERE, 'libtinydeform.so')
 ARCH = 'gfx950'
 
-SOURCES = ['td_abi.hip', 'td_fused.hip', 'td_sample.hip', 'td_gemm.hip']
+SOURCES = ['td_abi.hip', 'td_fused.hip', 'td_sample.hip', 'td_gemm.hip', 'td_layer.hip']
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in the generated code (the host pass warns that it does not know
 # the feature; that warning is expected).

@@ -1,6 +1,6 @@
 """ctypes binding of libtinydeform.so (C ABI: include/tinydeform.h) and the tensor-level host entries.
 
-fused_forward / sample_forward / value_proj take torch tensors on a HIP device, check them the way the reference's
+fused_forward / sample_forward / value_proj (and the decoder-layer entries layer_*) take torch tensors on a HIP device, check them the way the reference's
 host code does (csrc/ma_deform_fused.cu:236-266, 298-308, 333; same messages, RuntimeError), make them contiguous,
 allocate the output with torch.empty on the caching allocator, and launch on the current stream of the tensors'
 device. Nothing here computes on the CPU: without the library these functions raise.
@@ -31,7 +31,12 @@ SIGNATURES = {
     'td_sample_forward_masked': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 7 + [_vp]),
     'td_sample_forward_v2': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 6 + [_vp, _int, _vp]),
     'td_value_proj': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    'td_layer_prologue': (_int, [_int, _vp, _vp, _vp, _i64, _i64] + [_vp] * 7 + [_i64] * 6 + [_vp]),
+    'td_layer_fused_forward': (_int, [_int, _vp, _vp, _vp, _i64, _i64] + [_vp] * 13 + [_i64] * 9 + [_vp]),
+    'td_layer_sample_forward': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 7 + [_vp]),
 }
+
+TD_E_WORKSPACE = -4  # td_layer_fused_forward: the problem needs loc_out / attn_out
 
 load_error = None
 
@@ -273,3 +278,176 @@ def value_proj(memory, weight, bias):
     _check(lib_.td_value_proj(DTYPE_CODES[memory.dtype], mem.data_ptr(), w.data_ptr(), _ptr(b), value.data_ptr(),
                               B * N, C, HD, _stream(dev)))
     return value
+
+
+def acc_dtype(dtype):
+    """Type the layer entries compute locations and attention weights in: float32, or float64 for float64."""
+    return torch.float64 if dtype == torch.float64 else torch.float32
+
+
+def check_layer(memory, query, reference_points, offsets_weight, offsets_bias, attn_weight, attn_bias, position,
+                spatial_shapes, num_heads, num_points, require_gpu=True):
+    """Query-side checks of the decoder-layer entries; returns B, Q, Cq, H, L, P.
+
+    query [B, Q, Cq] (and position, same shape, or None), reference_points [B, Q, 1 or L, 2 or 4],
+    offsets_weight [H * L * P * 2, Cq] / offsets_bias [H * L * P * 2] or None, attn_weight [H * L * P, Cq] /
+    attn_bias [H * L * P] or None, all on memory's device and in its dtype; L = spatial_shapes.size(0).
+    """
+    if require_gpu and not memory.is_cuda:
+        raise RuntimeError('inputs must be GPU tensors')
+    if memory.dim() != 3:
+        raise RuntimeError('memory / value must be [B, N, C]')
+    if query.dim() != 3:
+        raise RuntimeError('hidden_states must be [B, Q, C]')
+    B, Q, Cq = query.shape
+    if memory.size(0) != B:
+        raise RuntimeError('batch size mismatch')
+    H, P = int(num_heads), int(num_points)
+    if H <= 0:
+        raise RuntimeError('need at least one head')
+    if P < 0:
+        raise RuntimeError('num_points must be non-negative')
+    if spatial_shapes.dtype != torch.int64 or spatial_shapes.dim() != 2 or spatial_shapes.size(1) != 2:
+        raise RuntimeError('spatial_shapes must be int64 [L, 2]')
+    L = spatial_shapes.size(0)
+    if L * P > MAX_LEVEL_POINTS:
+        raise RuntimeError(f'levels x points must be <= {MAX_LEVEL_POINTS}')
+    if Cq > MAX_CHANNELS:
+        raise RuntimeError(f'query channels must be <= {MAX_CHANNELS}')
+    if (reference_points.dim() != 4 or reference_points.shape[:2] != (B, Q) or reference_points.size(2) not in (1, L)
+            or reference_points.size(3) not in (2, 4)):
+        raise RuntimeError('reference_points must be [B, Q, 1 or L, 2 or 4]')
+    if offsets_weight.shape != (H * L * P * 2, Cq):
+        raise RuntimeError('sampling_offsets weight must be [H * L * P * 2, C]')
+    if attn_weight.shape != (H * L * P, Cq):
+        raise RuntimeError('attention_weights weight must be [H * L * P, C]')
+    if offsets_bias is not None and offsets_bias.shape != (H * L * P * 2,):
+        raise RuntimeError('sampling_offsets bias must be [H * L * P * 2]')
+    if attn_bias is not None and attn_bias.shape != (H * L * P,):
+        raise RuntimeError('attention_weights bias must be [H * L * P]')
+    if position is not None and position.shape != query.shape:
+        raise RuntimeError('position_embeddings must be [B, Q, C] like hidden_states')
+    for t in (query, reference_points, offsets_weight, offsets_bias, attn_weight, attn_bias, position):
+        if t is None:
+            continue
+        if t.device != memory.device:
+            raise RuntimeError('all tensors must be on the same device')
+        if t.dtype != memory.dtype:
+            raise RuntimeError('all float tensors must have the same dtype')
+    if spatial_shapes.device != memory.device:
+        raise RuntimeError('all tensors must be on the same device')
+    if memory.dtype not in DTYPE_CODES:
+        raise RuntimeError(f'unsupported dtype {memory.dtype}')
+    if B * Q * H > INT32_MAX:
+        raise RuntimeError('too many (batch, query, head) rows')
+    return B, Q, Cq, H, L, P
+
+
+def _contig(*ts):
+    return [None if t is None else t.contiguous() for t in ts]
+
+
+def layer_prologue(query, position, reference_points, offsets_weight, offsets_bias, attn_weight, attn_bias,
+                   spatial_shapes, num_heads, num_points):
+    """Query prologue alone (td_layer_prologue): sampling locations [B, Q, H, L, P, 2] and attention weights
+    [B, Q, H, L, P] in float32 (float64 for float64 inputs)."""
+    lib_ = _require()
+    B, Q, Cq, H, L, P = check_layer(query, query, reference_points, offsets_weight, offsets_bias, attn_weight,
+                                    attn_bias, position, spatial_shapes, num_heads, num_points)
+    dev = query.device
+    acc = acc_dtype(query.dtype)
+    loc = torch.empty((B, Q, H, L, P, 2), dtype=acc, device=dev)
+    attn = torch.empty((B, Q, H, L, P), dtype=acc, device=dev)
+    if attn.numel() == 0:
+        return loc, attn
+    q, pos, ref, ow, ob, aw, ab, sh = _contig(query, position, reference_points, offsets_weight, offsets_bias,
+                                              attn_weight, attn_bias, spatial_shapes)
+    _check(lib_.td_layer_prologue(DTYPE_CODES[query.dtype], q.data_ptr(), _ptr(pos), ref.data_ptr(), ref.size(2),
+                                  ref.size(3), ow.data_ptr(), _ptr(ob), aw.data_ptr(), _ptr(ab), sh.data_ptr(),
+                                  loc.data_ptr(), attn.data_ptr(), B, Q, Cq, H, L, P, _stream(dev)))
+    return loc, attn
+
+
+def layer_fused_forward(query, position, reference_points, offsets_weight, offsets_bias, attn_weight, attn_bias,
+                        memory, value_weight, value_bias, spatial_shapes, level_start_index, num_heads, num_points,
+                        padding_mask=None, return_locations=False):
+    """Fused decoder layer core (td_layer_fused_forward): the query prologue inside the fused kernel.
+
+    Returns out [B, Q, H * D] and, with return_locations, (loc, attn) in float32 (float64 for float64 inputs),
+    else None. Problems the in-kernel prologue cannot take get location buffers and a second call."""
+    lib_ = _require()
+    B, Q, Cq, H, L, P = check_layer(memory, query, reference_points, offsets_weight, offsets_bias, attn_weight,
+                                    attn_bias, position, spatial_shapes, num_heads, num_points)
+    N, C = memory.size(1), memory.size(2)
+    HD = check_projection(memory, value_weight, value_bias, H)
+    if C > MAX_CHANNELS:
+        raise RuntimeError(f'channels must be <= {MAX_CHANNELS}')
+    if level_start_index.dtype != torch.int64 or level_start_index.shape != (L,):
+        raise RuntimeError('level_start_index must be int64 [L]')
+    if level_start_index.device != memory.device:
+        raise RuntimeError('all tensors must be on the same device')
+    mask = check_padding_mask(memory, padding_mask)
+    dev = memory.device
+    acc = acc_dtype(memory.dtype)
+    out = torch.empty((B, Q, HD), dtype=memory.dtype, device=dev)
+    loc = attn = None
+    if return_locations:
+        loc = torch.empty((B, Q, H, L, P, 2), dtype=acc, device=dev)
+        attn = torch.empty((B, Q, H, L, P), dtype=acc, device=dev)
+    if B * Q * H == 0:
+        return out, ((loc, attn) if return_locations else None)
+    q, pos, ref, ow, ob, aw, ab = _contig(query, position, reference_points, offsets_weight, offsets_bias, attn_weight,
+                                          attn_bias)
+    mem, w, b, sh, st = _contig(memory, value_weight, value_bias, spatial_shapes, level_start_index)
+
+    def call(lo, at):
+        return lib_.td_layer_fused_forward(DTYPE_CODES[memory.dtype], q.data_ptr(), _ptr(pos), ref.data_ptr(),
+                                           ref.size(2), ref.size(3), ow.data_ptr(), _ptr(ob), aw.data_ptr(), _ptr(ab),
+                                           mem.data_ptr(), w.data_ptr(), _ptr(b), sh.data_ptr(), st.data_ptr(),
+                                           _ptr(mask), out.data_ptr(), _ptr(lo), _ptr(at), B, Q, N, Cq, C, H, HD // H,
+                                           L, P, _stream(dev))
+
+    rc = call(loc, attn)
+    if rc == TD_E_WORKSPACE and loc is None:
+        loc = torch.empty((B, Q, H, L, P, 2), dtype=acc, device=dev)
+        attn = torch.empty((B, Q, H, L, P), dtype=acc, device=dev)
+        rc = call(loc, attn)
+    _check(rc)
+    return out, ((loc, attn) if return_locations else None)
+
+
+def layer_sample_forward(value, heads, spatial_shapes, level_start_index, loc, attn, padding_mask=None):
+    """Sampling of projected values with float32 (float64) locations and weights (td_layer_sample_forward)."""
+    lib_ = _require()
+    if not value.is_cuda:
+        raise RuntimeError('inputs must be GPU tensors')
+    if value.dim() != 3:
+        raise RuntimeError('memory / value must be [B, N, C]')
+    if loc.dim() != 6 or loc.size(5) != 2 or attn.shape != loc.shape[:5]:
+        raise RuntimeError('sampling_locations must be [B, Q, H, L, P, 2]')
+    B, Q, H, L, P = loc.shape[:5]
+    N, HD = value.size(1), value.size(2)
+    if heads != H or HD % H != 0 or value.size(0) != B:
+        raise RuntimeError('value must be [B, N, H * D] with H = sampling_locations.size(2)')
+    acc = acc_dtype(value.dtype)
+    if loc.dtype != acc or attn.dtype != acc:
+        raise RuntimeError(f'locations and weights must be {acc} for {value.dtype} values')
+    if spatial_shapes.dtype != torch.int64 or spatial_shapes.shape != (L, 2):
+        raise RuntimeError('spatial_shapes must be int64 [L, 2]')
+    if level_start_index.dtype != torch.int64 or level_start_index.shape != (L,):
+        raise RuntimeError('level_start_index must be int64 [L]')
+    for t in (loc, attn, spatial_shapes, level_start_index):
+        if t.device != value.device:
+            raise RuntimeError('all tensors must be on the same device')
+    if value.dtype not in DTYPE_CODES:
+        raise RuntimeError(f'unsupported dtype {value.dtype}')
+    mask = check_padding_mask(value, padding_mask)
+    dev = value.device
+    v, lc, aw, sh, st = _contig(value, loc, attn, spatial_shapes, level_start_index)
+    out = torch.empty((B, Q, HD), dtype=value.dtype, device=dev)
+    if out.numel() == 0:
+        return out
+    _check(lib_.td_layer_sample_forward(DTYPE_CODES[value.dtype], v.data_ptr(), sh.data_ptr(), st.data_ptr(),
+                                        lc.data_ptr(), aw.data_ptr(), _ptr(mask), out.data_ptr(), B, Q, N, H, HD // H,
+                                        L, P, _stream(dev)))
+    return out

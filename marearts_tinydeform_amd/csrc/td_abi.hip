@@ -157,6 +157,129 @@ extern "C" int td_sample_forward_v2(int dtype, const void* value, const int64_t*
     return launch_sample(dtype, value, g, sampling_locations, attention_weights, out, s, tune);
 }
 
+namespace {
+
+// Query-side checks of the layer entries.
+int check_layer(int64_t Cq, int64_t ref_levels, int64_t ref_dim, int64_t L, int64_t P, const void* query,
+                const void* ref, const void* off_w, const void* aw_w, int64_t rows) {
+    if (Cq < 0 || Cq > kMaxChannels) return set_error(TD_E_ARG, "query channels must be <= %d", kMaxChannels);
+    if (ref_dim != 2 && ref_dim != 4) return set_error(TD_E_ARG, "reference points must have 2 or 4 coordinates");
+    if (ref_levels != 1 && ref_levels != L)
+        return set_error(TD_E_ARG, "reference points must have 1 or L (= %lld) levels", static_cast<long long>(L));
+    if (rows > 0 && L * P > 0 && (query == nullptr || ref == nullptr || (Cq > 0 && (off_w == nullptr || aw_w == nullptr))))
+        return set_error(TD_E_ARG, "null pointer argument");
+    return TD_OK;
+}
+
+LayerArgs layer_args(const void* query, const void* position, const void* ref, int64_t ref_levels, int64_t ref_dim,
+                     const void* off_w, const void* off_b, const void* aw_w, const void* aw_b, void* loc_out,
+                     void* attn_out, int64_t Cq) {
+    LayerArgs la;
+    la.query = query;
+    la.pos = position;
+    la.ref = ref;
+    la.off_w = off_w;
+    la.off_b = off_b;
+    la.aw_w = aw_w;
+    la.aw_b = aw_b;
+    la.loc_out = loc_out;
+    la.attn_out = attn_out;
+    la.Cq = static_cast<int>(Cq);
+    la.RL = static_cast<int>(ref_levels);
+    la.RD = static_cast<int>(ref_dim);
+    return la;
+}
+
+}  // namespace
+
+extern "C" int td_layer_prologue(int dtype, const void* query, const void* position, const void* reference_points,
+                                 int64_t ref_levels, int64_t ref_dim, const void* offsets_weight,
+                                 const void* offsets_bias, const void* attn_weight, const void* attn_bias,
+                                 const int64_t* spatial_shapes, void* loc_out, void* attn_out, int64_t B, int64_t Q,
+                                 int64_t Cq, int64_t H, int64_t L, int64_t P, void* stream) {
+    // the level starts are not needed here: pass the shapes in their place for the shared checks
+    int rc = check_geometry(dtype, B, Q, 0, H, 1, L, P, spatial_shapes, spatial_shapes, loc_out, attn_out, loc_out);
+    if (rc != TD_OK) return rc;
+    rc = check_layer(Cq, ref_levels, ref_dim, L, P, query, reference_points, offsets_weight, attn_weight, B * Q * H);
+    if (rc != TD_OK) return rc;
+    if (B * Q * H * L * P == 0) return TD_OK;
+    Geom g{spatial_shapes, spatial_shapes, static_cast<int>(B), static_cast<int>(Q), 0, static_cast<int>(H), 1,
+           static_cast<int>(L), static_cast<int>(P)};
+    set_levels(g, nullptr);
+    const LayerArgs la = layer_args(query, position, reference_points, ref_levels, ref_dim, offsets_weight,
+                                    offsets_bias, attn_weight, attn_bias, loc_out, attn_out, Cq);
+    return launch_prologue(dtype, la, g, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int td_layer_fused_forward(int dtype, const void* query, const void* position,
+                                      const void* reference_points, int64_t ref_levels, int64_t ref_dim,
+                                      const void* offsets_weight, const void* offsets_bias, const void* attn_weight,
+                                      const void* attn_bias, const void* memory, const void* value_weight,
+                                      const void* value_bias, const int64_t* spatial_shapes,
+                                      const int64_t* level_start_index, const uint8_t* padding_mask, void* out,
+                                      void* loc_out, void* attn_out, int64_t B, int64_t Q, int64_t N, int64_t Cq,
+                                      int64_t C, int64_t H, int64_t D, int64_t L, int64_t P, void* stream) {
+    // the shared checks see the query and the reference points in place of ready locations and weights
+    int rc = check_geometry(dtype, B, Q, N, H, D, L, P, spatial_shapes, level_start_index, query, reference_points,
+                            out);
+    if (rc != TD_OK) return rc;
+    if (C < 0 || C > kMaxChannels) return set_error(TD_E_ARG, "channels must be <= %d", kMaxChannels);
+    if (B * N * C > 0 && memory == nullptr) return set_error(TD_E_ARG, "null pointer argument");
+    if (H * D * C > 0 && value_weight == nullptr) return set_error(TD_E_ARG, "null pointer argument");
+    rc = check_layer(Cq, ref_levels, ref_dim, L, P, query, reference_points, offsets_weight, attn_weight, B * Q * H);
+    if (rc != TD_OK) return rc;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (B * Q * H == 0) return TD_OK;
+    Geom g{spatial_shapes, level_start_index, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N),
+           static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), static_cast<int>(P), padding_mask};
+    set_levels(g, nullptr);
+    const LayerArgs la = layer_args(query, position, reference_points, ref_levels, ref_dim, offsets_weight,
+                                    offsets_bias, attn_weight, attn_bias, loc_out, attn_out, Cq);
+    const bool want_prologue = L * P > 0 && (loc_out != nullptr || attn_out != nullptr);
+    if (D == 0 || N == 0 || L * P == 0) {
+        // nothing to gather: the output is exactly zero (bias share included); locations still go out if asked
+        if (want_prologue) {
+            if (loc_out == nullptr || attn_out == nullptr)
+                return set_error(TD_E_WORKSPACE, "layer: give both loc_out and attn_out, or neither");
+            rc = launch_prologue(dtype, la, g, s);
+            if (rc != TD_OK) return rc;
+        }
+        return launch_zero(out, B * Q * H * D * elem_size(dtype), s);
+    }
+    FusedTune tune;
+    rc = launch_fused(dtype, memory, value_weight, value_bias, g, static_cast<int>(C), nullptr, nullptr, out, s, tune,
+                      &la);
+    if (rc != 1) return rc;
+    // the in-kernel prologue cannot take this problem: standalone prologue, then the fused kernel on its output
+    if (loc_out == nullptr || attn_out == nullptr)
+        return set_error(TD_E_WORKSPACE,
+                         "layer: float64, or rows that are not 16-byte multiples or not 16-byte aligned, need "
+                         "loc_out and attn_out");
+    rc = launch_prologue(dtype, la, g, s);
+    if (rc != TD_OK) return rc;
+    g.loc_acc = 1;
+    return launch_fused(dtype, memory, value_weight, value_bias, g, static_cast<int>(C), loc_out, attn_out, out, s,
+                        tune);
+}
+
+extern "C" int td_layer_sample_forward(int dtype, const void* value, const int64_t* spatial_shapes,
+                                       const int64_t* level_start_index, const void* loc, const void* attn,
+                                       const uint8_t* padding_mask, void* out, int64_t B, int64_t Q, int64_t N,
+                                       int64_t H, int64_t D, int64_t L, int64_t P, void* stream) {
+    int rc = check_geometry(dtype, B, Q, N, H, D, L, P, spatial_shapes, level_start_index, loc, attn, out);
+    if (rc != TD_OK) return rc;
+    if (B * N * H * D > 0 && value == nullptr) return set_error(TD_E_ARG, "null pointer argument");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (B * Q * H * D == 0) return TD_OK;
+    if (N == 0 || L * P == 0) return launch_zero(out, B * Q * H * D * elem_size(dtype), s);
+    Geom g{spatial_shapes, level_start_index, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N),
+           static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), static_cast<int>(P), padding_mask};
+    set_levels(g, nullptr);
+    g.loc_acc = 1;
+    SampleTune tune;
+    return launch_sample(dtype, value, g, loc, attn, out, s, tune);
+}
+
 extern "C" int td_fused_forward(int dtype, const void* memory, const void* value_weight, const void* value_bias,
                                 const int64_t* spatial_shapes, const int64_t* level_start_index,
                                 const void* sampling_locations, const void* attention_weights, void* out, int64_t B,

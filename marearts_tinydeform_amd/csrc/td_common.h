@@ -44,10 +44,13 @@ struct Geom {
     const uint8_t* mask = nullptr;  // [B, N] padding mask (non-zero = padded token, value zero) or null
     int LP = 0;                     // samples per row: L * P, or the sum of per-level point counts
     int discrete = 0;               // 1: nearest-pixel sampling (D-FINE's "discrete" method) instead of bilinear
+    int loc_acc = 0;                // 1: locations and weights are in the accumulation type (float; double for
+                                    // float64) instead of the element type (computed by the query prologue)
     uint8_t level_end[kMaxLevelPoints] = {};  // per-level point counts (P == 0): first sample after level l
 
-    // true when the general corner rule is needed (padding mask, per-level point counts or discrete sampling)
-    bool general() const { return mask != nullptr || P == 0 || discrete != 0; }
+    // true when the general corner rule is needed (padding mask, per-level point counts, discrete sampling or
+    // locations in the accumulation type)
+    bool general() const { return mask != nullptr || P == 0 || discrete != 0 || loc_acc != 0; }
 };
 
 // Fills Geom::LP (and Geom::level_end with P = 0 when `points` gives per-level counts; points == nullptr keeps P
@@ -85,36 +88,29 @@ struct Corner {
     A w;
 };
 
-// The four bilinear corners of sample j (j = l * P + p) of row `row` = (b * Q + q) * H + h.
-// Restates the reference's corner rule (csrc/ma_deform_fused.cu:81-100): pixel coordinate
-// x = loc_x * W_l - 0.5 (align_corners=False), clamped to [-2, W_l + 1] before the integer conversion so that
-// far-away, infinite or NaN locations sample nothing; corner k has dx = k & 1, dy = k >> 1; a corner counts only
-// if it lies inside the level map and its token t = start_l + y * W_l + x lies in [0, N). With a padding mask, a
-// corner on a padded token counts as outside too: its value row is zero (value.masked_fill(mask, 0) after the
+// The four bilinear corners of one sample of row `row` = (b * Q + q) * H + h on level l, at normalised location
+// (lx, ly) with attention weight w. Restates the reference's corner rule (csrc/ma_deform_fused.cu:81-100): pixel
+// coordinate x = lx * W_l - 0.5 (align_corners=False), clamped to [-2, W_l + 1] before the integer conversion so
+// that far-away, infinite or NaN locations sample nothing; corner k has dx = k & 1, dy = k >> 1; a corner counts
+// only if it lies inside the level map and its token t = start_l + y * W_l + x lies in [0, N). With a padding mask,
+// a corner on a padded token counts as outside too: its value row is zero (value.masked_fill(mask, 0) after the
 // projection), so in fused mode it drops both W . memory[t] and its share of the bias.
 //
 // Discrete method (D-FINE, transformers models/d_fine/modeling_d_fine.py:168-206): one tap at pixel
-// (int(loc_x * W_l + 0.5), int(loc_y * H_l + 0.5)) truncated toward zero and clamped into the map, weight = the
+// (int(lx * W_l + 0.5), int(ly * H_l + 0.5)) truncated toward zero and clamped into the map, weight = the
 // attention weight; corners 1..3 are empty. A NaN coordinate takes pixel 0.
 //
 // GENERAL = false compiles the reference's case only (P points on every level, bilinear, no mask); kernels are
-// instantiated both ways and the launchers pick GENERAL = true only when a mask, per-level point counts or the
-// discrete method is in use, so the common path carries none of their cost.
-template <typename T, typename A, bool GENERAL>
-__device__ __forceinline__ void corner4(const T* __restrict__ loc, const T* __restrict__ attn, const Geom& g,
-                                        int64_t row, int j, Corner<A>* out) {
-    const int LP = g.LP;
-    const int l = GENERAL ? level_of(g, j) : j / g.P;
+// instantiated both ways and the launchers pick GENERAL = true only when a mask, per-level point counts, the
+// discrete method or accumulation-type locations are in use, so the common path carries none of their cost.
+template <typename A, bool GENERAL>
+__device__ __forceinline__ void corners_at(A lx, A ly, A w, int l, const Geom& g, int64_t row, Corner<A>* out) {
     const int hl = static_cast<int>(g.shapes[2 * l]);
     const int wl = static_cast<int>(g.shapes[2 * l + 1]);
     const int64_t st = g.starts[l];
-    const int64_t idx = row * LP + j;
-    const A w = cvt<A>(attn[idx]);
     if (GENERAL && g.discrete) {
-        const A fx = fmin(fmax(cvt<A>(loc[2 * idx]) * static_cast<A>(wl) + static_cast<A>(0.5), static_cast<A>(-1)),
-                          static_cast<A>(wl));
-        const A fy = fmin(fmax(cvt<A>(loc[2 * idx + 1]) * static_cast<A>(hl) + static_cast<A>(0.5), static_cast<A>(-1)),
-                          static_cast<A>(hl));
+        const A fx = fmin(fmax(lx * static_cast<A>(wl) + static_cast<A>(0.5), static_cast<A>(-1)), static_cast<A>(wl));
+        const A fy = fmin(fmax(ly * static_cast<A>(hl) + static_cast<A>(0.5), static_cast<A>(-1)), static_cast<A>(hl));
         int xi = static_cast<int>(fx), yi = static_cast<int>(fy);  // truncation toward zero
         xi = xi < 0 ? 0 : xi > wl - 1 ? wl - 1 : xi;
         yi = yi < 0 ? 0 : yi > hl - 1 ? hl - 1 : yi;
@@ -127,8 +123,8 @@ __device__ __forceinline__ void corner4(const T* __restrict__ loc, const T* __re
         for (int k = 1; k < 4; ++k) out[k] = Corner<A>{-1, static_cast<A>(0)};
         return;
     }
-    A x = cvt<A>(loc[2 * idx]) * static_cast<A>(wl) - static_cast<A>(0.5);
-    A y = cvt<A>(loc[2 * idx + 1]) * static_cast<A>(hl) - static_cast<A>(0.5);
+    A x = lx * static_cast<A>(wl) - static_cast<A>(0.5);
+    A y = ly * static_cast<A>(hl) - static_cast<A>(0.5);
     // fmax returns the non-NaN operand, so a NaN coordinate becomes -2 (outside the map)
     x = fmin(fmax(x, static_cast<A>(-2)), static_cast<A>(wl) + static_cast<A>(1));
     y = fmin(fmax(y, static_cast<A>(-2)), static_cast<A>(hl) + static_cast<A>(1));
@@ -145,6 +141,28 @@ __device__ __forceinline__ void corner4(const T* __restrict__ loc, const T* __re
         out[k].w = in ? w * (dx ? fx : static_cast<A>(1) - fx) * (dy ? fy : static_cast<A>(1) - fy)
                       : static_cast<A>(0);
     }
+}
+
+// The corners of sample j (j = l * P + p, or the running index over per-level point counts) of row `row`, with the
+// location and weight read from loc [rows, LP, 2] and attn [rows, LP] in the element type T (or in the
+// accumulation type A when g.loc_acc is set).
+template <typename T, typename A, bool GENERAL>
+__device__ __forceinline__ void corner4(const T* __restrict__ loc, const T* __restrict__ attn, const Geom& g,
+                                        int64_t row, int j, Corner<A>* out) {
+    const int l = GENERAL ? level_of(g, j) : j / g.P;
+    const int64_t idx = row * g.LP + j;
+    A lx, ly, w;
+    if (GENERAL && g.loc_acc) {
+        const A* la = reinterpret_cast<const A*>(loc);
+        lx = la[2 * idx];
+        ly = la[2 * idx + 1];
+        w = reinterpret_cast<const A*>(attn)[idx];
+    } else {
+        lx = cvt<A>(loc[2 * idx]);
+        ly = cvt<A>(loc[2 * idx + 1]);
+        w = cvt<A>(attn[idx]);
+    }
+    corners_at<A, GENERAL>(lx, ly, w, l, g, row, out);
 }
 
 // ---- vector loads: Bytes-wide raw loads unpacked to float ------------------------------------------------

@@ -20,6 +20,7 @@
 #include <stdio.h>
 
 #include "td_internal.h"
+#include "td_prologue.h"
 
 namespace td {
 namespace {
@@ -34,23 +35,7 @@ struct FusedParams {
     Geom g;
     int C, QT, SG, KS, qtiles;
     int per_xcd, units;  // work-unit mapping (decode_block)
-};
-
-template <typename T>
-struct MfmaOp;
-template <>
-struct MfmaOp<f16> {
-    typedef f16x8 frag;
-    __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-    }
-};
-template <>
-struct MfmaOp<bf16> {
-    typedef bf16x8 frag;
-    __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-    }
+    LayerArgs lay;       // query prologue (layer kernels only)
 };
 
 // Workgroup index -> work unit (b, query tile, h) with heads fastest. Workgroups are dealt to the 8 XCDs
@@ -72,21 +57,26 @@ __device__ __forceinline__ BlockRow decode_block(int bid, int H, int qtiles, int
     return r;
 }
 
-template <typename T, int WAVES, int NB, bool GENERAL>
+template <typename T, int WAVES, int NB, bool GENERAL, bool LAYER>
 __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) {
     constexpr int NTH = WAVES * kWave;
     constexpr int V = 16 / static_cast<int>(sizeof(T));
     const Geom& g = p.g;
     const int C = p.C, QT = p.QT, SG = p.SG, CV = C / V;
     const int LP = g.LP, S = 4 * LP, D = g.D;
-    const int GP = C + 4;  // float pitch of a g row in LDS: 16-byte aligned, rows offset by 4 banks
+    // float pitch of a g row (and, for the layer kernel, of a query row) in LDS: 16-byte aligned, rows offset
+    // by 4 banks
+    const int GP = (LAYER && p.lay.Cq > C ? p.lay.Cq : C) + 4;
     const int NTILE = (D + 15) >> 4, PW = NTILE * 16;
+    const int PP = ((3 * LP + 15) & ~15) + 4;  // pitch of a row of the query projections
 
     extern __shared__ __align__(16) unsigned char smem[];
     Corner<float>* cw = reinterpret_cast<Corner<float>*>(smem);  // [QT][S]
     float* gs = reinterpret_cast<float*>(cw + QT * S);           // [QT][GP]
     float* wsum = gs + QT * GP;                                   // [16]
     float* part = wsum + 16;                                      // [KS][16][PW]
+    float* pro = part + p.KS * 16 * PW;                           // layer: [16][PP] query projections
+    float* rstat = pro + 16 * PP;                                 // layer: [16][2] softmax max, 1 / sum
 
     const T* __restrict__ mem = static_cast<const T*>(p.mem);
     const T* __restrict__ w = static_cast<const T*>(p.w);
@@ -100,12 +90,30 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     if (!br.valid) return;
     const int q0 = br.qt * QT;
 
+    if constexpr (LAYER) {
+        // phase 0 (layer): sampling offsets and attention logits of the tile's queries for head h, on MFMA; the
+        // query rows are staged in the g rows' LDS, which phase 2 overwrites only after the corner table is built
+        stage_queries<T, float, true, NTH>(p.lay, br.b, q0, QT, g.Q, gs, GP);
+        __syncthreads();
+        prologue_mfma<T, WAVES>(p.lay, br.h, LP, QT, gs, GP, pro, PP);
+        __syncthreads();
+        prologue_stats<float, NTH>(LP, QT, pro, PP, rstat);
+        __syncthreads();
+    }
+
     // phase 1: corner table
     for (int i = tid; i < QT * LP; i += NTH) {
         const int r = i / LP, j = i - r * LP, q = q0 + r;
         Corner<float>* c4 = cw + r * S + 4 * j;
         if (q < g.Q) {
-            corner4<T, float, GENERAL>(loc, attn, g, (static_cast<int64_t>(br.b) * g.Q + q) * g.H + br.h, j, c4);
+            const int64_t row = (static_cast<int64_t>(br.b) * g.Q + q) * g.H + br.h;
+            if constexpr (LAYER) {
+                float lx, ly, a;
+                prologue_sample<T, float>(p.lay, g, br.b, q, br.h, r, j, pro, PP, rstat, lx, ly, a);
+                corners_at<float, GENERAL>(lx, ly, a, j / g.P, g, row, c4);
+            } else {
+                corner4<T, float, GENERAL>(loc, attn, g, row, j, c4);
+            }
         } else {
 #pragma unroll
             for (int k = 0; k < 4; ++k) c4[k] = Corner<float>{-1, 0.f};
@@ -303,14 +311,14 @@ inline int64_t map_units(FusedParams& p) {
     return static_cast<int64_t>(p.per_xcd) * kXcds;
 }
 
-template <typename T, int WAVES>
+template <typename T, int WAVES, bool LAYER>
 int go_vec(FusedParams p, size_t lds, hipStream_t stream) {
     const int64_t blocks = map_units(p);
     if (p.g.general())
-        hipLaunchKernelGGL((fused_vec_kernel<T, WAVES, 8, true>), dim3(static_cast<unsigned>(blocks)),
+        hipLaunchKernelGGL((fused_vec_kernel<T, WAVES, 8, true, LAYER>), dim3(static_cast<unsigned>(blocks)),
                            dim3(WAVES * kWave), lds, stream, p);
     else
-        hipLaunchKernelGGL((fused_vec_kernel<T, WAVES, 8, false>), dim3(static_cast<unsigned>(blocks)),
+        hipLaunchKernelGGL((fused_vec_kernel<T, WAVES, 8, false, LAYER>), dim3(static_cast<unsigned>(blocks)),
                            dim3(WAVES * kWave), lds, stream, p);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : set_error(-3, "fused_vec launch failed: %s", hipGetErrorString(e));
@@ -329,8 +337,13 @@ int go_generic(FusedParams p, size_t lds, hipStream_t stream) {
     return e == hipSuccess ? 0 : set_error(-3, "fused_generic launch failed: %s", hipGetErrorString(e));
 }
 
+inline bool aligned16(const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; }
+
+// layer: the query prologue runs inside the kernel (LayerArgs in p.lay); returns 1 without launching anything when
+// the vector kernel cannot take the problem (alignment, channel counts, LDS), so the caller can fall back to the
+// standalone prologue followed by the plain kernels.
 template <typename T>
-int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune) {
+int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, bool layer) {
     using A = typename AccOf<T>::type;
     const Geom& g = p.g;
     const int LP = g.LP, S = 4 * LP, C = p.C, D = g.D;
@@ -338,8 +351,12 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune) {
 
     if constexpr (!std::is_same<T, double>::value) {
         constexpr int V = 16 / static_cast<int>(sizeof(T));
-        const bool aligned = reinterpret_cast<uintptr_t>(p.mem) % 16 == 0 &&
-                             reinterpret_cast<uintptr_t>(p.w) % 16 == 0 && C % V == 0 && C > 0;
+        bool aligned = aligned16(p.mem) && aligned16(p.w) && C % V == 0 && C > 0;
+        if (layer) {
+            const LayerArgs& la = p.lay;
+            aligned = aligned && la.Cq > 0 && la.Cq % V == 0 && aligned16(la.query) && aligned16(la.off_w) &&
+                      aligned16(la.aw_w) && (la.pos == nullptr || aligned16(la.pos)) && g.P > 0;
+        }
         if (aligned && !tune.generic) {
             const int CV = C / V;
             // Launch shape (measured on MI355X): small problems want one row per wavefront and one pass per
@@ -371,9 +388,12 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune) {
             int ks = waves / NTILE;
             if (ks < 1) ks = 1;
             if (ks > nk) ks = nk;
+            const int GP = (layer && p.lay.Cq > C ? p.lay.Cq : C) + 4;
+            const int PP = ((3 * LP + 15) & ~15) + 4;
             auto lds = [&](int q) {
-                return static_cast<size_t>(q) * S * sizeof(Corner<float>) + static_cast<size_t>(q) * (C + 4) * 4 +
-                       16 * 4 + static_cast<size_t>(ks) * 16 * NTILE * 16 * 4;
+                return static_cast<size_t>(q) * S * sizeof(Corner<float>) + static_cast<size_t>(q) * GP * 4 +
+                       16 * 4 + static_cast<size_t>(ks) * 16 * NTILE * 16 * 4 +
+                       (layer ? static_cast<size_t>(16 * PP + 32) * 4 : 0);
             };
             while (qt > 1 && lds(qt) > kLdsBudget) --qt;
             if (lds(qt) <= kLdsBudget) {
@@ -382,16 +402,24 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune) {
                 p.KS = ks;
                 p.qtiles = (g.Q + qt - 1) / qt;
                 // 8 corner loads in flight per lane: measured best on MI355X at every benchmark shape
+                if (layer) {
+                    switch (waves) {
+                        case 4: return go_vec<T, 4, true>(p, lds(qt), stream);
+                        case 8: return go_vec<T, 8, true>(p, lds(qt), stream);
+                        default: return set_error(-1, "fused layer: waves must be 4 or 8 (got %d)", waves);
+                    }
+                }
                 switch (waves) {
-                    case 1: return go_vec<T, 1>(p, lds(qt), stream);
-                    case 2: return go_vec<T, 2>(p, lds(qt), stream);
-                    case 4: return go_vec<T, 4>(p, lds(qt), stream);
-                    case 8: return go_vec<T, 8>(p, lds(qt), stream);
+                    case 1: return go_vec<T, 1, false>(p, lds(qt), stream);
+                    case 2: return go_vec<T, 2, false>(p, lds(qt), stream);
+                    case 4: return go_vec<T, 4, false>(p, lds(qt), stream);
+                    case 8: return go_vec<T, 8, false>(p, lds(qt), stream);
                     default: return set_error(-1, "fused: waves must be 1, 2, 4 or 8 (got %d)", waves);
                 }
             }
         }
     }
+    if (layer) return 1;
     // generic kernel
     auto lds = [&](int q) {
         return static_cast<size_t>(q) * S * sizeof(Corner<A>) + static_cast<size_t>(q) * C * sizeof(A) +
@@ -413,13 +441,15 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune) {
 }  // namespace
 
 int launch_fused(int dtype, const void* mem, const void* w, const void* bias, const Geom& g, int C, const void* loc,
-                 const void* attn, void* out, hipStream_t stream, const FusedTune& tune) {
-    FusedParams p{mem, w, bias, loc, attn, out, g, C, 1, 1, 1, 1, 0, 0};
+                 const void* attn, void* out, hipStream_t stream, const FusedTune& tune, const LayerArgs* layer) {
+    FusedParams p{mem, w, bias, loc, attn, out, g, C, 1, 1, 1, 1, 0, 0, LayerArgs{}};
+    if (layer != nullptr) p.lay = *layer;
+    const bool lay = layer != nullptr;
     switch (dtype) {
-        case kF32: return launch_fused_t<float>(p, stream, tune);
-        case kF16: return launch_fused_t<f16>(p, stream, tune);
-        case kBF16: return launch_fused_t<bf16>(p, stream, tune);
-        case kF64: return launch_fused_t<double>(p, stream, tune);
+        case kF32: return launch_fused_t<float>(p, stream, tune, lay);
+        case kF16: return launch_fused_t<f16>(p, stream, tune, lay);
+        case kBF16: return launch_fused_t<bf16>(p, stream, tune, lay);
+        case kF64: return lay ? 1 : launch_fused_t<double>(p, stream, tune, false);
         default: return set_error(-2, "unknown dtype code %d", dtype);
     }
 }

@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "td_common.h"
+#include "td_prologue.h"
 
 namespace td {
 
@@ -30,8 +31,15 @@ struct SampleTune {
 // Every launcher returns 0, or a negative TD_E* code after recording a message with set_error.
 int set_error(int code, const char* fmt, ...);
 
+// layer != null: the decoder-layer kernel, whose query prologue computes locations and weights in-kernel (loc and
+// attn are then unused). Returns 1, launching nothing, when the vector kernel cannot take a layer problem.
 int launch_fused(int dtype, const void* mem, const void* w, const void* bias, const Geom& g, int C,
-                 const void* loc, const void* attn, void* out, hipStream_t stream, const FusedTune& tune);
+                 const void* loc, const void* attn, void* out, hipStream_t stream, const FusedTune& tune,
+                 const LayerArgs* layer = nullptr);
+
+// Standalone query prologue: locations [B, Q, H, L, P, 2] and attention weights [B, Q, H, L, P] in the
+// accumulation type (layer.loc_out / layer.attn_out, both required).
+int launch_prologue(int dtype, const LayerArgs& layer, const Geom& g, hipStream_t stream);
 
 int launch_sample(int dtype, const void* value, const Geom& g, const void* loc, const void* attn, void* out,
                   hipStream_t stream, const SampleTune& tune);

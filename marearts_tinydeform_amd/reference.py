@@ -46,3 +46,49 @@ def ma_deform_attn_reference(memory, value_weight, value_bias, spatial_shapes, l
     if out is None:  # no levels
         out = memory.new_zeros(B * H, D, Q)
     return out.view(B, H, D, Q).permute(0, 3, 1, 2).reshape(B, Q, H * D)
+
+
+def layer_locations_reference(hidden_states, reference_points, spatial_shapes, sampling_offsets_weight,
+                              sampling_offsets_bias, attention_weights_weight, attention_weights_bias, num_heads,
+                              num_points, position_embeddings=None):
+    """Sampling locations [B, Q, H, L, P, 2] and attention weights [B, Q, H, L, P] of a deformable-attention layer,
+    in PyTorch (HF transformers RTDetrMultiscaleDeformableAttention.forward, models/rt_detr/modeling_rt_detr.py:673-713).
+
+    reference_points [B, Q, 1 or L, 2] are points, [B, Q, 1 or L, 4] boxes (centre, size): a point's offsets are
+    divided by the level's (width, height); a box's by num_points, scaled by half its size.
+    """
+    if position_embeddings is not None:
+        hidden_states = hidden_states + position_embeddings
+    B, Q, _ = hidden_states.shape
+    H, P, L = num_heads, num_points, spatial_shapes.shape[0]
+    offsets = F.linear(hidden_states, sampling_offsets_weight, sampling_offsets_bias).view(B, Q, H, L, P, 2)
+    logits = F.linear(hidden_states, attention_weights_weight, attention_weights_bias).view(B, Q, H, L * P)
+    attention = F.softmax(logits, -1).view(B, Q, H, L, P)
+    ref = reference_points[:, :, None, :, None, :]  # [B, Q, 1, 1 or L, 1, 2 or 4]
+    if reference_points.shape[-1] == 2:
+        normalizer = torch.stack([spatial_shapes[..., 1], spatial_shapes[..., 0]], -1)  # (width, height)
+        locations = ref + offsets / normalizer[None, None, None, :, None, :]
+    elif reference_points.shape[-1] == 4:
+        locations = ref[..., :2] + offsets / P * ref[..., 2:] * 0.5
+    else:
+        raise ValueError(f'reference_points must end in 2 or 4 coordinates, got {reference_points.shape[-1]}')
+    return locations, attention
+
+
+def ma_deform_attn_layer_reference(hidden_states, encoder_hidden_states, reference_points, spatial_shapes,
+                                   level_start_index, sampling_offsets_weight, sampling_offsets_bias,
+                                   attention_weights_weight, attention_weights_bias, value_weight, value_bias,
+                                   output_weight, output_bias, num_heads, num_points, position_embeddings=None,
+                                   padding_mask=None, return_attention_weights=False):
+    """One deformable cross-attention layer of a DETR decoder in PyTorch: the query prologue
+    (layer_locations_reference), value projection and multi-scale deformable attention (ma_deform_attn_reference),
+    then output_proj (skipped when output_weight is None). Returns [B, Q, C_out] (and the attention weights with
+    return_attention_weights)."""
+    locations, attention = layer_locations_reference(
+        hidden_states, reference_points, spatial_shapes, sampling_offsets_weight, sampling_offsets_bias,
+        attention_weights_weight, attention_weights_bias, num_heads, num_points, position_embeddings)
+    out = ma_deform_attn_reference(encoder_hidden_states, value_weight, value_bias, spatial_shapes, level_start_index,
+                                   locations, attention, padding_mask=padding_mask)
+    if output_weight is not None:
+        out = F.linear(out, output_weight, output_bias)
+    return (out, attention) if return_attention_weights else out

@@ -81,3 +81,49 @@ def to(args, device):
 
 def as_f64(args):
     return [t if t is None or t.dtype == torch.long else t.double() for t in args]
+
+
+# name, B, Q, H, D, C, levels, P, ref_dim, ref_levels ('1' or 'L')
+LAYER_CASES = [
+    ('rt-detr decoder boxes', 1, 300, 8, 32, 256, [(80, 80), (40, 40), (20, 20)], 4, 4, '1'),
+    ('deformable-detr points per level', 2, 100, 8, 32, 256, [(100, 152), (50, 76), (25, 38), (13, 19)], 4, 2, 'L'),
+    ('points shared by levels', 2, 37, 4, 16, 64, [(32, 48), (16, 24)], 8, 2, '1'),
+    ('boxes per level, one level', 1, 50, 2, 64, 128, [(20, 30)], 16, 4, 'L'),
+    ('wide channels', 1, 40, 12, 64, 768, [(40, 40), (20, 20), (10, 10)], 4, 4, '1'),
+    ('odd channels (fallback)', 2, 33, 3, 10, 30, [(13, 17), (7, 9)], 4, 2, 'L'),
+]
+
+
+def make_layer(B, Q, H, D, C, levels, P, ref_dim=4, ref_levels='1', dtype=torch.float32, pos=True, bias=True,
+               out_proj=True, seed=0):
+    """Inputs of a deformable cross-attention layer (CPU tensors), in ma_deform_attn_layer's argument order up to
+    num_points: hidden, memory, reference points, shapes, starts, offsets W/b, attention W/b, value W/b,
+    output W/b, H, P; plus position embeddings (or None) last. Offsets are a few pixels (points) or a fraction
+    of the box (boxes); attention logits N(0, ~1)."""
+    g = torch.Generator().manual_seed(seed)
+    shapes, starts, N = level_index(levels)
+    L = len(levels)
+    HD = H * D
+    hidden = torch.randn(B, Q, C, generator=g)
+    memory = torch.randn(B, N, C, generator=g)
+    RL = 1 if ref_levels == '1' else L
+    if ref_dim == 2:
+        ref = torch.rand(B, Q, RL, 2, generator=g)
+        off_scale = 3.0
+    else:
+        centre = torch.rand(B, Q, RL, 2, generator=g)
+        size = torch.rand(B, Q, RL, 2, generator=g) * 0.3 + 0.02
+        ref = torch.cat([centre, size], -1)
+        off_scale = 1.0
+    off_w = torch.randn(H * L * P * 2, C, generator=g) * (off_scale / C ** 0.5)
+    off_b = torch.randn(H * L * P * 2, generator=g) * off_scale if bias else None
+    aw_w = torch.randn(H * L * P, C, generator=g) / C ** 0.5
+    aw_b = torch.randn(H * L * P, generator=g) * 0.3 if bias else None
+    v_w = torch.randn(HD, C, generator=g) / C ** 0.5
+    v_b = torch.randn(HD, generator=g) * 0.1 if bias else None
+    o_w = torch.randn(C, HD, generator=g) / HD ** 0.5 if out_proj else None
+    o_b = torch.randn(C, generator=g) * 0.1 if (out_proj and bias) else None
+    position = torch.randn(B, Q, C, generator=g) * 0.5 if pos else None
+    cast = [t if t is None or t.dtype == torch.long else t.to(dtype) for t in
+            (hidden, memory, ref, shapes, starts, off_w, off_b, aw_w, aw_b, v_w, v_b, o_w, o_b)]
+    return cast + [H, P, None if position is None else position.to(dtype)]

@@ -33,6 +33,7 @@ def lib():
 
 def test_header_declares_the_entry_points():
     assert header_functions() == ['td_fused_forward', 'td_fused_forward_masked', 'td_last_error',
+                                  'td_layer_fused_forward', 'td_layer_prologue', 'td_layer_sample_forward',
                                   'td_sample_forward', 'td_sample_forward_masked', 'td_sample_forward_v2',
                                   'td_value_proj', 'td_version']
 

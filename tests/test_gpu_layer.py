@@ -1,0 +1,168 @@
+"""The decoder-layer entries on the GPU against the float64 layer oracle (oracle/layer.py, itself pinned against
+HF transformers' RTDetrMultiscaleDeformableAttention in tests/test_layer.py).
+
+Tolerances: the output as the operator's tests (float32 atol 2e-5 / rtol 1e-4 scaled by max|ref|; float16 and
+bfloat16 2e-2 of max|ref| as relative error, and elementwise atol 3e-3 / 2e-2 + rtol); the attention weights and
+locations, computed in float32 from the same inputs, within 2e-5 (float32, float16) / 1e-4 (bfloat16, whose
+query split into two halves keeps 16 significant bits) of the oracle's.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import marearts_tinydeform_amd as td
+from marearts_tinydeform_amd import _native
+from oracle import layer as olayer
+from inputs import LAYER_CASES, RTDETR_LEVELS, make_layer, to
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: (2e-5, 1e-4), torch.float16: (3e-3, 3e-3), torch.bfloat16: (2e-2, 2e-2),
+       torch.float64: (1e-10, 1e-10)}
+REL = {torch.float32: 1e-4, torch.float16: 2e-2, torch.bfloat16: 2e-2, torch.float64: 1e-10}
+LOC_TOL = {torch.float32: 2e-5, torch.float16: 2e-5, torch.bfloat16: 1e-4, torch.float64: 1e-12}
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def check(name, got, ref, dtype):
+    got = got.double().cpu().numpy()
+    assert got.shape == ref.shape, f'{name}: shape {got.shape} != {ref.shape}'
+    atol, rtol = TOL[dtype]
+    scale = max(float(np.abs(ref).max()), 1.0) if ref.size else 1.0
+    err = np.abs(got - ref)
+    bad = err > atol * scale + rtol * np.abs(ref)
+    assert not bad.any(), f'{name}: {int(bad.sum())} out of tolerance, max |diff| {err.max():.3g}'
+    if ref.size:
+        assert err.max() / scale <= REL[dtype], f'{name}: relative error {err.max() / scale:.3g}'
+
+
+def run_layer(dev, mode, mask=None, want_attn=True):
+    with torch.inference_mode():
+        res = td.ma_deform_attn_layer(*dev[:15], position_embeddings=dev[15], padding_mask=mask, mode=mode,
+                                      return_attention_weights=want_attn)
+    torch.cuda.synchronize()
+    return res
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize('case', LAYER_CASES, ids=[c[0] for c in LAYER_CASES])
+def test_layer_cases(case, dtype):
+    name, B, Q, H, D, C, levels, P, rd, rl = case
+    a = make_layer(B, Q, H, D, C, levels, P, rd, rl, dtype=dtype)
+    ref, ref_attn = olayer.layer(*a[:15], position_embeddings=a[15])
+    dev = to(a[:13], 'cuda') + a[13:15] + to(a[15:], 'cuda')
+    for mode in ('fused', 'project', 'auto'):
+        say(f'  {name} {dtype} [{mode}]')
+        out, attn = run_layer(dev, mode)
+        check(f'{name} {dtype} [{mode}]', out, ref, dtype)
+        np.testing.assert_allclose(attn.double().cpu().numpy(), ref_attn, rtol=0,
+                                   atol=max(LOC_TOL[dtype], 2 ** -8 if dtype == torch.bfloat16 else
+                                            2 ** -11 if dtype == torch.float16 else 0))
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16, torch.bfloat16])
+def test_locations_in_float32(dtype):
+    """loc / attn as the kernels compute them (float32, before any rounding), fused and standalone prologue."""
+    a = make_layer(2, 45, 8, 32, 256, RTDETR_LEVELS, 4, 4, '1', dtype=dtype)
+    ref_loc, ref_attn = olayer.locations(a[0], a[2], a[3], a[5], a[6], a[7], a[8], a[13], a[14], a[15])
+    dev = to(a[:13], 'cuda') + a[13:15] + to(a[15:], 'cuda')
+    hidden, memory, rp, shapes, starts, ow, ob, aw, ab, vw, vb = dev[:11]
+    with torch.inference_mode():
+        loc, attn = _native.layer_prologue(hidden, dev[15], rp, ow, ob, aw, ab, shapes, 8, 4)
+        _, (floc, fattn) = _native.layer_fused_forward(hidden, dev[15], rp, ow, ob, aw, ab, memory, vw, vb, shapes,
+                                                       starts, 8, 4, return_locations=True)
+    torch.cuda.synchronize()
+    tol = LOC_TOL[dtype]
+    for nm, l_, a_ in (('prologue', loc, attn), ('fused', floc, fattn)):
+        say(f'  locations {dtype} [{nm}]')
+        assert l_.dtype == torch.float32 and a_.dtype == torch.float32
+        np.testing.assert_allclose(l_.double().cpu().numpy(), ref_loc, rtol=0, atol=tol)
+        np.testing.assert_allclose(a_.double().cpu().numpy(), ref_attn, rtol=0, atol=tol)
+
+
+def test_float64_layer_takes_the_standalone_prologue():
+    a = make_layer(2, 21, 4, 16, 64, [(12, 18), (6, 9)], 4, 2, 'L', dtype=torch.float64)
+    ref, ref_attn = olayer.layer(*a[:15], position_embeddings=a[15])
+    dev = to(a[:13], 'cuda') + a[13:15] + to(a[15:], 'cuda')
+    for mode in ('fused', 'project'):
+        say(f'  float64 [{mode}]')
+        out, attn = run_layer(dev, mode)
+        check(f'float64 [{mode}]', out, ref, torch.float64)
+        np.testing.assert_allclose(attn.cpu().numpy(), ref_attn, rtol=0, atol=1e-12)
+    # without location buffers the fused entry reports that it needs them, launching nothing
+    lib = _native.lib
+    hidden, memory, rp, shapes, starts, ow, ob, aw, ab, vw, vb = dev[:11]
+    out = torch.empty(2, 21, 64, dtype=torch.float64, device='cuda')
+    rc = lib.td_layer_fused_forward(3, hidden.data_ptr(), None, rp.data_ptr(), 2, 2, ow.data_ptr(), ob.data_ptr(),
+                                    aw.data_ptr(), ab.data_ptr(), memory.data_ptr(), vw.data_ptr(), vb.data_ptr(),
+                                    shapes.data_ptr(), starts.data_ptr(), None, out.data_ptr(), None, None,
+                                    2, 21, memory.shape[1], 64, 64, 4, 16, 2, 4, None)
+    assert rc == _native.TD_E_WORKSPACE
+
+
+@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
+def test_layer_padding_mask_and_no_bias(dtype):
+    a = make_layer(2, 60, 8, 32, 256, [(40, 40), (20, 20), (10, 10)], 4, 2, 'L', dtype=dtype, bias=False, pos=False)
+    N = a[1].shape[1]
+    mask = torch.zeros(2, N, dtype=torch.bool)
+    mask[1, :] = torch.rand(N, generator=torch.Generator().manual_seed(5)) < 0.4  # image 1 partly padded
+    ref, _ = olayer.layer(*a[:15], position_embeddings=None, padding_mask=mask)
+    dev = to(a[:13], 'cuda') + a[13:15] + [None]
+    for mode in ('fused', 'project'):
+        say(f'  mask {dtype} [{mode}]')
+        out = run_layer(dev, mode, mask=mask.cuda(), want_attn=False)
+        check(f'mask {dtype} [{mode}]', out, ref, dtype)
+
+
+def test_layer_without_output_projection():
+    a = make_layer(1, 40, 8, 32, 256, RTDETR_LEVELS, 4, 4, '1', dtype=torch.float16, out_proj=False)
+    ref, _ = olayer.layer(*a[:15], position_embeddings=a[15])
+    dev = to(a[:13], 'cuda') + a[13:15] + to(a[15:], 'cuda')
+    out = run_layer(dev, 'fused', want_attn=False)
+    assert out.shape == (1, 40, 256)
+    check('no output_proj', out, ref, torch.float16)
+
+
+def test_module_on_gpu_matches_cpu():
+    torch.manual_seed(0)
+    m = td.MSDeformAttnLayer(d_model=256, n_levels=3, n_heads=8, n_points=4)
+    with torch.no_grad():  # offsets and attention that depend on the query
+        m.sampling_offsets.weight.normal_(0, 0.05)
+        m.attention_weights.weight.normal_(0, 0.05)
+    a = make_layer(2, 50, 8, 32, 256, RTDETR_LEVELS, 4, 4, '1', dtype=torch.float32)
+    hidden, memory, ref, shapes, starts = a[:5]
+    kw = dict(hidden_states=hidden, encoder_hidden_states=memory, position_embeddings=a[15], reference_points=ref,
+              spatial_shapes=shapes, level_start_index=starts)
+    with torch.no_grad():
+        want, want_attn = m(**kw)
+        mg = m.cuda()
+        got, got_attn = mg(**{k: v.cuda() for k, v in kw.items()})
+    torch.cuda.synchronize()
+    scale = float(want.abs().max())
+    assert float((got.cpu() - want).abs().max()) <= 1e-4 * scale
+    assert float((got_attn.cpu() - want_attn).abs().max()) <= 2e-5
+
+
+def test_layer_graph_capture_replays_match_eager():
+    a = make_layer(1, 300, 8, 32, 256, RTDETR_LEVELS, 4, 4, '1', dtype=torch.float16)
+    dev = to(a[:13], 'cuda') + a[13:15] + to(a[15:], 'cuda')
+    with torch.inference_mode():
+        eager = run_layer(dev, 'fused', want_attn=False).clone()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            run_layer(dev, 'fused', want_attn=False)
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            static_out = td.ma_deform_attn_layer(*dev[:15], position_embeddings=dev[15], mode='fused')
+        for i in range(3):
+            static_out.zero_()
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(static_out, eager), f'replay {i}'
