@@ -95,6 +95,39 @@ def algorithmic(B, Q, H, D, C, N, L, P, s):
     return {'fused_bytes': fused, 'sample_bytes': sample, 'gemm_bytes': gemm_bytes, 'gemm_flops': gemm_flops}
 
 
+def layer_times(B, Q, H, D, C, levels, P, dtype, steps, warmup):
+    """µs per decoder-layer call (RT-DETR decoder cross-attention: box reference points shared by the levels,
+    position embeddings, output_proj) on the same shapes: the fused layer kernel, the layer's project mode, the
+    unfused sequence (PyTorch sampling-offset / attention Linear + softmax + reference-point arithmetic, then
+    ma_deform_attn and output_proj as separate calls) and the plain PyTorch layer (F.linear + grid_sample)."""
+    from inputs import make_layer
+    a = make_layer(B, Q, H, D, C, levels, P, ref_dim=4, ref_levels='1', dtype=dtype)
+    dev = [t.cuda() if isinstance(t, torch.Tensor) else t for t in a]
+    hidden, memory, ref, shapes, starts, ow, ob, aw, ab, vw, vb, o_w, o_b, nh, npt, pos = dev
+    shapes_cpu, starts_cpu = a[3], a[4]
+
+    def layer(mode):
+        return td.ma_deform_attn_layer(hidden, memory, ref, shapes, starts, ow, ob, aw, ab, vw, vb, o_w, o_b, nh, npt,
+                                       position_embeddings=pos, mode=mode)
+
+    def unfused():
+        loc, attn = td.layer_locations_reference(hidden, ref, shapes_cpu, ow, ob, aw, ab, nh, npt, pos)
+        core = td.ma_deform_attn(memory, vw, vb, shapes, starts, loc, attn)
+        return torch.nn.functional.linear(core, o_w, o_b)
+
+    def pytorch():
+        return td.ma_deform_attn_layer_reference(hidden, memory, ref, shapes_cpu, starts_cpu, ow, ob, aw, ab, vw, vb,
+                                                 o_w, o_b, nh, npt, position_embeddings=pos)
+
+    out = {}
+    with torch.inference_mode():
+        for mode in ('fused', 'project', 'auto'):
+            out[f'layer_{mode}'] = graph_time_us(lambda m=mode: layer(m), steps, warmup)
+        out['layer_unfused'] = graph_time_us(unfused, steps, warmup)
+        out['layer_pytorch'] = graph_time_us(pytorch, min(steps, 200), min(warmup, 10))
+    return out
+
+
 def gemm_kernel(M, K, NO, s):
     """Which value-projection kernel td_value_proj launches for an aligned [M, K] x [K, NO] problem (element size
     s): one K round trip in 64 x 64 tiles while the grid is small, otherwise both operands staged through LDS
@@ -315,6 +348,10 @@ def main():
             kern['pytorch_reference'] = graph_time_us(lambda: td.ma_deform_attn_reference(*ref_args),
                                                       min(args.steps, 200), min(args.warmup, 10))
             log(f'  PyTorch reference path on the GPU: {kern["pytorch_reference"]:.2f} µs/call')
+            lay = layer_times(B, Q, H, D, C, levels, P, dtype, args.steps, args.warmup)
+            log('  decoder layer (prologue + value_proj + MSDeformAttn + output_proj): ' +
+                ', '.join(f'{k[6:]} {v:.2f}' for k, v in lay.items()) + ' µs/call')
+            kern.update(lay)
 
     if pick == 'fused':
         dom, bytes_, t = 'fused', alg['fused_bytes'], times['fused']

@@ -20,7 +20,11 @@ BUILD = os.path.join(HERE, '_build')
 LIB = os.path.join(HERE, 'libtinydeform.so')
 ARCH = 'gfx950'
 
-SOURCES = ['td_abi.hip', 'td_fused.hip', 'td_sample.hip', 'td_gemm.hip', 'td_layer.hip']
+SOURCES = ['td_abi.hip', 'td_fused.hip', 'td_sample.hip', 'td_gemm.hip', 'td_gemm_dma.hip', 'td_layer.hip']
+
+# per-source additions: the direct-to-LDS GEMM keeps its MFMA accumulators in architectural VGPRs (in the
+# accumulator-register form the compiler copies every accumulator through a temporary in the inner loop)
+EXTRA_FLAGS = {'td_gemm_dma.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form=1']}
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in the generated code (the host pass warns that it does not know
 # the feature; that warning is expected).
@@ -40,7 +44,7 @@ def hipcc():
 
 def _compile(src):
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + '.o')
-    cmd = [hipcc()] + HIPCC_FLAGS + ['-c', os.path.join(CSRC, src), '-o', obj]
+    cmd = [hipcc()] + HIPCC_FLAGS + EXTRA_FLAGS.get(src, []) + ['-c', os.path.join(CSRC, src), '-o', obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f'hipcc failed on {src}:\n{res.stdout}\n{res.stderr}')

@@ -5,60 +5,10 @@
 // Tiles are numbered so that the N tiles of one M tile go to the same XCD (workgroups are dealt to the 8 XCDs
 // round-robin), which keeps the memory rows in that XCD's L2.
 // gemm_generic_kernel: double, unaligned or odd-K operands; 64 x 64 tile, VALU FMAs.
-#include "td_internal.h"
+#include "td_gemm.h"
 
 namespace td {
 namespace {
-
-struct GemmParams {
-    const void* a;
-    const void* w;
-    const void* bias;
-    void* c;
-    int M, K, NO;
-    int mt, nt;  // tile counts
-    int per_xcd;
-};
-
-// Linear tile index for this workgroup; -1 when the workgroup has no tile.
-__device__ __forceinline__ int tile_of(const GemmParams& p) {
-    const int id = blockIdx.x;
-    const int tile = (id % kXcds) * p.per_xcd + id / kXcds;
-    return tile < p.mt * p.nt ? tile : -1;
-}
-
-// One 16-byte K block of an MFMA: 16-bit types take one v_mfma_f32_16x16x32 (K = 32 = 4 lane groups x 8),
-// float32 takes four v_mfma_f32_16x16x4_f32 on the components of a float4 (K = 16 = 4 lane groups x 4, lane group
-// g holding k = 4g..4g+3; A and B use the same k order, so the sum covers each k once).
-template <typename T>
-struct KBlock;
-template <>
-struct KBlock<f16> {
-    static constexpr int kK = 32;
-    __device__ __forceinline__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
-                                                      0, 0, 0);
-    }
-};
-template <>
-struct KBlock<bf16> {
-    static constexpr int kK = 32;
-    __device__ __forceinline__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
-                                                       c, 0, 0, 0);
-    }
-};
-template <>
-struct KBlock<float> {
-    static constexpr int kK = 16;
-    __device__ __forceinline__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
-        const f32x4 x = __builtin_bit_cast(f32x4, a), y = __builtin_bit_cast(f32x4, b);
-        c = __builtin_amdgcn_mfma_f32_16x16x4f32(x[0], y[0], c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x4f32(x[1], y[1], c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x4f32(x[2], y[2], c, 0, 0, 0);
-        return __builtin_amdgcn_mfma_f32_16x16x4f32(x[3], y[3], c, 0, 0, 0);
-    }
-};
 
 // MFMA GEMM, both operands K-contiguous (C = A . W^T). WM x WN wavefronts per workgroup; wavefront (wm, wn) owns a
 // TM x TN grid of 16x16 output tiles. K advances in chunks of NKB 16-byte blocks:
@@ -342,6 +292,23 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_lds_kernel(GemmParams p) {
     }
 }
 
+// MFMA GEMM for large 16-bit problems with K a multiple of 64: 256 x BN tiles (BN = 256 or 128), four wavefronts
+// in a 2 x 2 grid, each owning 128 x BN/2 (8 x BN/32 tiles of 16 x 16: up to 256 accumulator registers per lane, one
+// wavefront per SIMD). The L2 → CU traffic per flop halves against 128 x 128 tiles, which is what lets the MFMAs
+// rather than the L2 set the pace.
+//
+// K streams through a ring of STAGES LDS buffers, STAGES - 1 chunks of 32 ahead of the MFMAs, by direct
+// global-to-LDS loads (global_load_lds_dwordx4: lane i's 16 bytes land at the wavefront's LDS base + 16 i), so the
+// staging costs no registers and no LDS store instructions. The compiler does not track these loads, so the
+// kernel orders them itself: `s_waitcnt vmcnt(n)` lets exactly the chunks after the one about to be read stay in
+// flight (8 loads per chunk per wavefront), and a plain `s_barrier` (no fence, which would drain every
+// outstanding load) then publishes the chunk (meet()); the same barrier tells every wavefront that the buffer refilled next
+// (the one read in the previous step) is no longer read.
+//
+// LDS layout of a staged operand: [rows][4 slots of 16 bytes]; row r's K piece kc (8 elements) sits in slot
+// kc ^ ((r >> 2) & 3), so each 16-lane phase of a fragment read (16 rows, one kc) touches 16 distinct 16-byte
+// bank groups. The swizzle is applied on the source side: the lane whose LDS slot is s loads piece s ^ f(row).
+// Rows past M or NO load the last valid row (their results are never stored), so no load is predicated.
 template <typename T>
 __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmParams p) {
     using A = typename AccOf<T>::type;
@@ -427,14 +394,21 @@ int go_mfma(GemmParams p, hipStream_t stream) {
 //   11 128 x 256 A and W through LDS (2 x 2 waves of 64 x 128)
 //   12 256 x 128 A and W through LDS (2 x 2 waves of 128 x 64)
 //   13 128 x 128 A and W through LDS, K chunks of 32/16
+//   14..21 256 x 128 / 256 x 256 tiles fed by direct-to-LDS loads (td_gemm_dma.hip; 16-bit, K % 64 == 0)
 template <typename T>
 int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
     if (variant <= 0) {
         // measured on MI355X: one round trip (5) while the grid is small; for large 16-bit problems both operands
-        // through LDS in 128 x 128 tiles with K chunks of 32 (13); float32 keeps A direct in 64 x 128 tiles (2)
+        // through LDS in 128 x 128 tiles with K chunks of 32 (13); float32 keeps A direct in 64 x 128 tiles (2).
+        // Deep 16-bit K (K >= 512, K % 64 == 0): the direct-to-LDS kernel, 256 x 256 tiles (16) when there are at
+        // least 2.5 rounds of them on 256 CUs, else 256 x 128 (14) (C = 1024, M = 43520: 101 µs against 122 µs for
+        // 13; M = 21760: 57 against 68).
         constexpr int one_chunk = 8 * KBlock<T>::kK;
         const int64_t tiles_128 = ((p.M + 127) / 128) * static_cast<int64_t>((p.NO + 127) / 128);
-        if (p.K <= one_chunk && tiles_128 < 512)
+        const int64_t tiles_256 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 255) / 256);
+        if (sizeof(T) == 2 && p.K >= 512 && p.K % 64 == 0)
+            variant = tiles_256 >= 640 ? 16 : 14;
+        else if (p.K <= one_chunk && tiles_128 < 512)
             variant = 5;
         else
             variant = sizeof(T) == 2 ? 13 : 2;
@@ -453,6 +427,9 @@ int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
         case 11: return go_lds<T, 2, 2, 4, 8, 2>(p, stream);
         case 12: return go_lds<T, 2, 2, 8, 4, 2>(p, stream);
         case 13: return go_lds<T, 2, 2, 4, 4, 1>(p, stream);
+        case 14: case 15: case 16: case 17: case 18: case 19: case 20: case 21:
+            return launch_gemm_dma(std::is_same<T, bf16>::value ? kBF16 : std::is_same<T, f16>::value ? kF16 : -1, p,
+                                   stream, variant);
         default: return set_error(-1, "value_proj: unknown tile variant %d", variant);
     }
 }

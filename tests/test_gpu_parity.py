@@ -189,6 +189,26 @@ def test_value_proj_matches_oracle():
             assert_close(f'value_proj {dtype} {(B, N, C, HD)}', got, ref, eps, eps)
 
 
+@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
+def test_value_proj_deep_k_matches_oracle(dtype):
+    # 16-bit, K >= 512 and K % 64 == 0: the direct-to-LDS kernel, 256 x 128 tiles for the small grids and 256 x 256
+    # tiles for >= 640 of them (the C=1024 limit shape, here with M and the output width off the tile sizes). Rows
+    # are checked on a sample that includes the last, partial M tile.
+    g = torch.Generator().manual_seed(11)
+    for (M, K, NO) in ((1037, 512, 200), (5000, 576, 136), (43557, 1024, 1000)):
+        say(f'  value_proj {dtype} M={M} K={K} NO={NO}')
+        mem = torch.randn(1, M, K, generator=g).to(dtype)
+        w = (torch.randn(NO, K, generator=g) / K ** 0.5).to(dtype)
+        b = (torch.randn(NO, generator=g) * 0.1).to(dtype)
+        with torch.inference_mode():
+            got = _native.value_proj(mem.cuda(), w.cuda(), b.cuda()).cpu()
+        rows = torch.cat([torch.arange(0, min(M, 300)), torch.randint(0, M, (700,), generator=g),
+                          torch.arange(max(M - 300, 0), M)]).unique()
+        ref = bruteforce.project(mem[:, rows], w, b)
+        eps = {torch.float16: 2e-3, torch.bfloat16: 1e-2}[dtype]
+        assert_close(f'value_proj {dtype} {(M, K, NO)}', got[:, rows], ref, eps, eps)
+
+
 def test_sample_alone_matches_oracle():
     for dtype in (torch.float16, torch.bfloat16, torch.float32):
         for name, B, Q, H, D, C, levels, P in CASES:
