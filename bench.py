@@ -130,13 +130,15 @@ def layer_times(B, Q, H, D, C, levels, P, dtype, steps, warmup):
 
 def gemm_kernel(M, K, NO, s):
     """Which value-projection kernel td_value_proj launches for an aligned [M, K] x [K, NO] problem (element size
-    s): one K round trip in 64 x 64 tiles while the grid is small, otherwise both operands staged through LDS
-    (16-bit) or direct A in 64 x 128 tiles (float32)."""
-    one_chunk = 8 * (32 if s == 2 else 16)
+    s), following its size rule: 16-bit deep K (K >= 512, K % 64 == 0) on a grid of >= 256 tiles of 256 x 128
+    takes the direct-to-LDS kernel; other 16-bit grids under 512 tiles of 128 x 128 take 64 x 64 tiles, larger ones
+    both operands through LDS; float32 takes 64 x 64 tiles for K <= 128 on small grids, else 64 x 128 tiles."""
     tiles_128 = -(-M // 128) * -(-NO // 128)
-    if K <= one_chunk and tiles_128 < 512:
-        return 'gemm_mfma_kernel'
-    return 'gemm_lds_kernel' if s == 2 else 'gemm_mfma_kernel'
+    if s == 2:
+        if K >= 512 and K % 64 == 0 and -(-M // 256) * -(-NO // 128) >= 256:
+            return 'gemm_dma_kernel'
+        return 'gemm_mfma_kernel' if tiles_128 < 512 else 'gemm_lds_kernel'
+    return 'gemm_mfma_kernel'
 
 
 def cpu_baseline(spec, budget_s):

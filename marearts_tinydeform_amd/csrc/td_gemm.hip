@@ -398,20 +398,26 @@ int go_mfma(GemmParams p, hipStream_t stream) {
 template <typename T>
 int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
     if (variant <= 0) {
-        // measured on MI355X: one round trip (5) while the grid is small; for large 16-bit problems both operands
-        // through LDS in 128 x 128 tiles with K chunks of 32 (13); float32 keeps A direct in 64 x 128 tiles (2).
-        // Deep 16-bit K (K >= 512, K % 64 == 0): the direct-to-LDS kernel, 256 x 256 tiles (16) when there are at
-        // least 2.5 rounds of them on 256 CUs, else 256 x 128 (14) (C = 1024, M = 43520: 101 µs against 122 µs for
-        // 13; M = 21760: 57 against 68).
+        // measured on MI355X (16-bit):
+        //   deep K (K >= 512, K % 64 == 0) on a grid of at least 256 tiles of 256 x 128: the direct-to-LDS kernel,
+        //     256 x 256 tiles (16) from 2.5 rounds of them on 256 CUs, else 256 x 128 (14) (C = 1024: M = 43520
+        //     101 µs against 122 µs for 13; M = 21760 57 against 68);
+        //   other grids under 512 tiles of 128 x 128: 64 x 64 tiles with K in chunks of 256 (5) (M = 600, K = 1024,
+        //     1024 outputs: 10.3 µs against 19-20 µs for 13, 14 or 16);
+        //   else both operands through LDS in 128 x 128 tiles with K chunks of 32 (13).
+        // float32: one round trip (5) for K <= 128 on small grids, else A direct in 64 x 128 tiles (2).
         constexpr int one_chunk = 8 * KBlock<T>::kK;
         const int64_t tiles_128 = ((p.M + 127) / 128) * static_cast<int64_t>((p.NO + 127) / 128);
+        const int64_t tiles_256x128 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 127) / 128);
         const int64_t tiles_256 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 255) / 256);
-        if (sizeof(T) == 2 && p.K >= 512 && p.K % 64 == 0)
-            variant = tiles_256 >= 640 ? 16 : 14;
-        else if (p.K <= one_chunk && tiles_128 < 512)
-            variant = 5;
-        else
-            variant = sizeof(T) == 2 ? 13 : 2;
+        if (sizeof(T) == 2) {
+            if (p.K >= 512 && p.K % 64 == 0 && tiles_256x128 >= 256)
+                variant = tiles_256 >= 640 ? 16 : 14;
+            else
+                variant = tiles_128 < 512 ? 5 : 13;
+        } else {
+            variant = p.K <= one_chunk && tiles_128 < 512 ? 5 : 2;
+        }
     }
     switch (variant) {
         case 1: return go_mfma<T, 4, 1, 1, 4, 2, 2>(p, stream);

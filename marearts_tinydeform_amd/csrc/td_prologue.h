@@ -125,41 +125,58 @@ __device__ __forceinline__ void prologue_mfma(const LayerArgs& a, int h, int LP,
         const bool nv = n < NP;
         const T* wr = proj_row<T>(a, h, LP, nv ? n : 0);
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        // the weight row streams from L2/HBM: KB K blocks of loads are issued before the first is used, so a
+        // wavefront waits one memory latency per KB blocks rather than per block
+        constexpr int KB = 8;
         if constexpr (sizeof(T) == 2) {
             using M = MfmaOp<T>;
             using frag = typename M::frag;
-            for (int k0 = 0; k0 < Cq; k0 += 32) {
-                const int k = k0 + kg * 8;
-                const bool kv = k < Cq;
-                u32x4 braw = {0u, 0u, 0u, 0u};
-                if (nv && kv) braw = *reinterpret_cast<const u32x4*>(wr + k);
-                f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
-                if (av && kv) {
-                    a0 = *reinterpret_cast<const f32x4*>(xa + k);
-                    a1 = *reinterpret_cast<const f32x4*>(xa + k + 4);
-                }
-                frag hi, lo;
+            for (int k0 = 0; k0 < Cq; k0 += 32 * KB) {
+                u32x4 braw[KB];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const T x0 = static_cast<T>(a0[i]), x1 = static_cast<T>(a1[i]);
-                    hi[i] = x0;
-                    hi[4 + i] = x1;
-                    lo[i] = static_cast<T>(a0[i] - static_cast<float>(x0));
-                    lo[4 + i] = static_cast<T>(a1[i] - static_cast<float>(x1));
+                for (int u = 0; u < KB; ++u) {
+                    const int k = k0 + u * 32 + kg * 8;
+                    braw[u] = (nv && k < Cq) ? *reinterpret_cast<const u32x4*>(wr + k) : u32x4{0u, 0u, 0u, 0u};
                 }
-                const frag bf = __builtin_bit_cast(frag, braw);
-                acc = M::mma(hi, bf, acc);
-                acc = M::mma(lo, bf, acc);
+#pragma unroll
+                for (int u = 0; u < KB; ++u) {
+                    const int k = k0 + u * 32 + kg * 8;
+                    f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
+                    if (av && k < Cq) {
+                        a0 = *reinterpret_cast<const f32x4*>(xa + k);
+                        a1 = *reinterpret_cast<const f32x4*>(xa + k + 4);
+                    }
+                    frag hi, lo;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const T x0 = static_cast<T>(a0[i]), x1 = static_cast<T>(a1[i]);
+                        hi[i] = x0;
+                        hi[4 + i] = x1;
+                        lo[i] = static_cast<T>(a0[i] - static_cast<float>(x0));
+                        lo[4 + i] = static_cast<T>(a1[i] - static_cast<float>(x1));
+                    }
+                    const frag bf = __builtin_bit_cast(frag, braw[u]);
+                    acc = M::mma(hi, bf, acc);
+                    acc = M::mma(lo, bf, acc);
+                }
             }
         } else {
-            for (int k0 = 0; k0 < Cq; k0 += 16) {
-                const int k = k0 + kg * 4;
-                const bool kv = k < Cq;
-                f32x4 bq = {0.f, 0.f, 0.f, 0.f}, aq = bq;
-                if (nv && kv) bq = *reinterpret_cast<const f32x4*>(wr + k);
-                if (av && kv) aq = *reinterpret_cast<const f32x4*>(xa + k);
+            for (int k0 = 0; k0 < Cq; k0 += 16 * KB) {
+                f32x4 bq[KB];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[j], bq[j], acc, 0, 0, 0);
+                for (int u = 0; u < KB; ++u) {
+                    const int k = k0 + u * 16 + kg * 4;
+                    bq[u] = (nv && k < Cq) ? *reinterpret_cast<const f32x4*>(wr + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+                for (int u = 0; u < KB; ++u) {
+                    const int k = k0 + u * 16 + kg * 4;
+                    f32x4 aq = {0.f, 0.f, 0.f, 0.f};
+                    if (av && k < Cq) aq = *reinterpret_cast<const f32x4*>(xa + k);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[j], bq[u][j], acc, 0, 0, 0);
+                }
             }
         }
         const float bn = nv ? proj_bias<T, float>(a, h, LP, n) : 0.f;
