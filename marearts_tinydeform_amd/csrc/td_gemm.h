@@ -14,6 +14,7 @@ struct GemmParams {
     int M, K, NO;
     int mt, nt;  // tile counts
     int per_xcd;
+    const void* a2 = nullptr;  // second A operand of the two-operand form (C = A . W^T + A2 . W^T + bias)
 };
 
 // Linear tile index for this workgroup; -1 when the workgroup has no tile. Workgroups are dealt to the 8 XCDs

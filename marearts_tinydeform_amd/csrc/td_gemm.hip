@@ -17,19 +17,23 @@ namespace {
 // STAGES = 2 overlaps the next chunk's loads with this chunk's MFMAs; STAGES = 1 (one LDS buffer) suits K that fits
 // one chunk, where the whole product costs a single round trip to memory.
 // Epilogue: bias, one rounding to T, the tile transposed through LDS and written with 16-byte stores.
-template <typename T, int WM, int WN, int TM, int TN, int NKB, int STAGES>
+// DUAL: C = A . W^T + A2 . W^T + bias with A2 the same shape as A (two MFMAs per block; the sum A + A2 is never
+// rounded to T). F32OUT: C is float32, the accumulators stored unrounded.
+template <typename T, int WM, int WN, int TM, int TN, int NKB, int STAGES, bool DUAL = false, bool F32OUT = false>
 __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma_kernel(GemmParams p) {
+    using O = typename std::conditional<F32OUT, float, T>::type;  // output element
     constexpr int NTH = WM * WN * kWave;
     constexpr int E = 16 / static_cast<int>(sizeof(T));  // elements per 16 bytes
+    constexpr int EO = 16 / static_cast<int>(sizeof(O));  // output elements per 16 bytes
     constexpr int KBK = KBlock<T>::kK;                   // K per 16-byte block (4 lane groups)
     constexpr int KC = NKB * KBK;                         // K per chunk
     constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
     constexpr int LDK = KC + E;                           // LDS pitch (elements) of a staged W row
     constexpr int B_CHUNKS = BN * KC / E;                 // 16-byte pieces of one staged W slice
     constexpr int B_PER_T = (B_CHUNKS + NTH - 1) / NTH;
-    constexpr int LDC = BN + E;                           // LDS pitch of the output tile
+    constexpr int LDC = BN + EO;                          // LDS pitch of the output tile
     constexpr size_t kStage = static_cast<size_t>(BN) * LDK * sizeof(T);
-    constexpr size_t kOut = static_cast<size_t>(BM) * LDC * sizeof(T);
+    constexpr size_t kOut = static_cast<size_t>(BM) * LDC * sizeof(O);
     constexpr size_t kLds = STAGES * kStage > kOut ? STAGES * kStage : kOut;
     __shared__ __align__(16) unsigned char lds[kLds];
     auto stage = [&](int i) { return reinterpret_cast<T*>(lds + (STAGES == 2 ? (i & 1) * kStage : 0)); };
@@ -38,9 +42,10 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma_kernel(GemmParams p) 
     if (tile < 0) return;
     const int m0 = (tile / p.nt) * BM, n0 = (tile % p.nt) * BN;
     const T* __restrict__ A = static_cast<const T*>(p.a);
+    const T* __restrict__ A2 = static_cast<const T*>(p.a2);
     const T* __restrict__ W = static_cast<const T*>(p.w);
     const T* __restrict__ bias = static_cast<const T*>(p.bias);
-    T* __restrict__ Cm = static_cast<T*>(p.c);
+    O* __restrict__ Cm = static_cast<O*>(p.c);
     const int M = p.M, K = p.K, NO = p.NO;
 
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
@@ -48,15 +53,19 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma_kernel(GemmParams p) 
     const int r16 = lane & 15, kg = lane >> 4;
     const u32x4 zero = {0u, 0u, 0u, 0u};
 
-    // A fragments of one chunk: row m0 + wm*TM*16 + i*16 + r16, k = k0 + j*KBK + kg*E
-    auto load_a = [&](u32x4 (&a)[TM][NKB], int k0) {
+    // A fragments of one chunk: row m0 + wm*TM*16 + i*16 + r16, k = k0 + j*KBK + kg*E (and the same of A2)
+    constexpr int NA = DUAL ? 2 : 1;
+    auto load_a = [&](u32x4 (&a)[NA][TM][NKB], int k0) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const int m = m0 + (wm * TM + i) * 16 + r16;
 #pragma unroll
             for (int j = 0; j < NKB; ++j) {
                 const int k = k0 + j * KBK + kg * E;
-                a[i][j] = (m < M && k < K) ? *reinterpret_cast<const u32x4*>(A + static_cast<size_t>(m) * K + k) : zero;
+                const bool in = m < M && k < K;
+                a[0][i][j] = in ? *reinterpret_cast<const u32x4*>(A + static_cast<size_t>(m) * K + k) : zero;
+                if constexpr (DUAL)
+                    a[NA - 1][i][j] = in ? *reinterpret_cast<const u32x4*>(A2 + static_cast<size_t>(m) * K + k) : zero;
             }
         }
     };
@@ -89,7 +98,7 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma_kernel(GemmParams p) 
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int nc = (K + KC - 1) / KC;
-    auto mma_chunk = [&](const u32x4 (&a)[TM][NKB], const T* bs) {
+    auto mma_chunk = [&](const u32x4 (&a)[NA][TM][NKB], const T* bs) {
 #pragma unroll
         for (int j = 0; j < NKB; ++j) {
             u32x4 b[TN];
@@ -97,13 +106,15 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma_kernel(GemmParams p) 
             for (int t = 0; t < TN; ++t)
                 b[t] = *reinterpret_cast<const u32x4*>(bs + ((wn * TN + t) * 16 + r16) * LDK + j * KBK + kg * E);
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+            for (int o = 0; o < NA; ++o)
 #pragma unroll
-                for (int t = 0; t < TN; ++t) acc[i][t] = KBlock<T>::mma(a[i][j], b[t], acc[i][t]);
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int t = 0; t < TN; ++t) acc[i][t] = KBlock<T>::mma(a[o][i][j], b[t], acc[i][t]);
         }
     };
     if constexpr (STAGES == 1) {
-        u32x4 a_cur[TM][NKB];
+        u32x4 a_cur[NA][TM][NKB];
         for (int c = 0; c < nc; ++c) {
             load_a(a_cur, c * KC);
             load_b(c * KC);
@@ -114,7 +125,7 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma_kernel(GemmParams p) 
         }
         __syncthreads();
     } else {
-        u32x4 a_cur[TM][NKB], a_next[TM][NKB];
+        u32x4 a_cur[NA][TM][NKB], a_next[NA][TM][NKB];
         load_a(a_cur, 0);
         load_b(0);
         store_b(stage(0));
@@ -130,15 +141,17 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma_kernel(GemmParams p) 
             __syncthreads();
             if (more) {
 #pragma unroll
-                for (int i = 0; i < TM; ++i)
+                for (int o = 0; o < NA; ++o)
 #pragma unroll
-                    for (int j = 0; j < NKB; ++j) a_cur[i][j] = a_next[i][j];
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < NKB; ++j) a_cur[o][i][j] = a_next[o][i][j];
             }
         }
     }
 
     // epilogue through LDS (every wavefront has passed the last barrier, so the W buffers are free)
-    T* Ct = reinterpret_cast<T*>(lds);
+    O* Ct = reinterpret_cast<O*>(lds);
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
         const int nl = (wn * TN + t) * 16 + r16;
@@ -147,20 +160,20 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma_kernel(GemmParams p) 
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                Ct[((wm * TM + i) * 16 + kg * 4 + e) * LDC + nl] = static_cast<T>(acc[i][t][e] + bv);
+                Ct[((wm * TM + i) * 16 + kg * 4 + e) * LDC + nl] = static_cast<O>(acc[i][t][e] + bv);
     }
     __syncthreads();
-    const bool vec_ok = NO % E == 0 && (reinterpret_cast<uintptr_t>(Cm) % 16) == 0;
-    for (int c = tid; c < BM * (BN / E); c += NTH) {
-        const int row = c / (BN / E), col = (c % (BN / E)) * E;
+    const bool vec_ok = NO % EO == 0 && (reinterpret_cast<uintptr_t>(Cm) % 16) == 0;
+    for (int c = tid; c < BM * (BN / EO); c += NTH) {
+        const int row = c / (BN / EO), col = (c % (BN / EO)) * EO;
         const int m = m0 + row, n = n0 + col;
         if (m >= M || n >= NO) continue;
-        const T* src = Ct + row * LDC + col;
-        T* dst = Cm + static_cast<size_t>(m) * NO + n;
-        if (vec_ok && n + E <= NO) {
+        const O* src = Ct + row * LDC + col;
+        O* dst = Cm + static_cast<size_t>(m) * NO + n;
+        if (vec_ok && n + EO <= NO) {
             *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
         } else {
-            for (int e = 0; e < E && n + e < NO; ++e) dst[e] = src[e];
+            for (int e = 0; e < EO && n + e < NO; ++e) dst[e] = src[e];
         }
     }
 }
@@ -450,7 +463,30 @@ int launch_t(GemmParams p, hipStream_t stream, int variant) {
     return go(gemm_generic_kernel<T>, p, 64, 64, 256, stream);
 }
 
+template <typename T>
+int launch_proj_f32_t(GemmParams p, hipStream_t stream) {
+    constexpr int E = 16 / static_cast<int>(sizeof(T));
+    const uintptr_t al = reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.w) |
+                         reinterpret_cast<uintptr_t>(p.a2) | reinterpret_cast<uintptr_t>(p.c);
+    if (p.K % E != 0 || al % 16 != 0) return 1;
+    // 64 x 64 tiles, K in chunks of 256 (16-bit) / 128 (float32): the projections are short and wide
+    if (p.a2 != nullptr)
+        return go(gemm_mfma_kernel<T, 4, 1, 1, 4, 8, 1, true, true>, p, 64, 64, 4 * kWave, stream);
+    return go(gemm_mfma_kernel<T, 4, 1, 1, 4, 8, 1, false, true>, p, 64, 64, 4 * kWave, stream);
+}
+
 }  // namespace
+
+int launch_proj_f32(int dtype, const void* a, const void* a2, const void* w, const void* bias, float* c, int64_t M,
+                    int64_t K, int64_t NO, hipStream_t stream) {
+    GemmParams p{a, w, bias, c, static_cast<int>(M), static_cast<int>(K), static_cast<int>(NO), 0, 0, 0, a2};
+    switch (dtype) {
+        case kF32: return launch_proj_f32_t<float>(p, stream);
+        case kF16: return launch_proj_f32_t<f16>(p, stream);
+        case kBF16: return launch_proj_f32_t<bf16>(p, stream);
+        default: return 1;
+    }
+}
 
 int launch_value_proj(int dtype, const void* a, const void* w, const void* bias, void* c, int64_t M, int64_t K,
                       int64_t NO, hipStream_t stream, int variant) {

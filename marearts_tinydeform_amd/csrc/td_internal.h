@@ -39,7 +39,9 @@ int launch_fused(int dtype, const void* mem, const void* w, const void* bias, co
 
 // Standalone query prologue: locations [B, Q, H, L, P, 2] and attention weights [B, Q, H, L, P] in the
 // accumulation type (layer.loc_out / layer.attn_out, both required).
-int launch_prologue(int dtype, const LayerArgs& layer, const Geom& g, hipStream_t stream);
+// route: 0 picks by size, 1 forces the single-kernel prologue, 2 the GEMM route (projections on the GEMM, then an
+// in-place finalize; falls back to the single kernel for float64 or unaligned operands).
+int launch_prologue(int dtype, const LayerArgs& layer, const Geom& g, hipStream_t stream, int route = 0);
 
 int launch_sample(int dtype, const void* value, const Geom& g, const void* loc, const void* attn, void* out,
                   hipStream_t stream, const SampleTune& tune);
@@ -47,6 +49,12 @@ int launch_sample(int dtype, const void* value, const Geom& g, const void* loc, 
 // variant: 0 picks the tile shape by size, > 0 forces an MFMA tile variant, -1 forces the generic kernel.
 int launch_value_proj(int dtype, const void* a, const void* w, const void* bias, void* c, int64_t M, int64_t K,
                       int64_t NO, hipStream_t stream, int variant);
+
+// Projection in float32 for the layer prologue: c[M, NO] = a[M, K] . w[NO, K]^T (+ a2[M, K] . w^T) + bias, float32
+// accumulation, stored unrounded; a2 may be null. 16/32-bit operands with K a multiple of 16 bytes and 16-byte
+// aligned a, a2, w and c. Returns 1, launching nothing, when the operands do not qualify.
+int launch_proj_f32(int dtype, const void* a, const void* a2, const void* w, const void* bias, float* c, int64_t M,
+                    int64_t K, int64_t NO, hipStream_t stream);
 
 int launch_zero(void* out, int64_t bytes, hipStream_t stream);
 

@@ -53,6 +53,68 @@ __global__ __launch_bounds__(WAVES* kWave) void layer_prologue_kernel(ProloguePa
     }
 }
 
+// Second half of the GEMM route (launch_prologue_gemm): loc_out holds the raw offsets [rows, LP, 2] and attn_out
+// the raw logits [rows, LP] (rows = (b, q, h)); each wavefront turns 64 / SEG rows in place into locations and
+// softmax weights (SEG = the power of two >= LP lanes per row, lane j of a segment taking sample j).
+template <typename T>
+__global__ __launch_bounds__(256) void layer_finalize_kernel(LayerArgs a, Geom g, int seg_log2) {
+    const int SEG = 1 << seg_log2, lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+    const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * (kWave >> seg_log2) +
+                        (lane >> seg_log2);
+    const int64_t rows = static_cast<int64_t>(g.B) * g.Q * g.H;
+    const int j = lane & (SEG - 1), LP = g.LP;
+    const bool on = row < rows && j < LP;
+    float* lg = static_cast<float*>(a.attn_out) + row * LP;
+    float* off = static_cast<float*>(a.loc_out) + row * LP * 2;
+    float x = -INFINITY, ox = 0.f, oy = 0.f;
+    if (on) {
+        x = lg[j];
+        ox = off[2 * j];
+        oy = off[2 * j + 1];
+    }
+    float m = x;
+    for (int k = SEG >> 1; k > 0; k >>= 1) m = fmaxf(m, xor_lane(m, k));
+    const float e = on ? exp_acc(x - m) : 0.f;
+    float sum = e;
+    for (int k = SEG >> 1; k > 0; k >>= 1) sum += xor_lane(sum, k);
+    if (!on) return;
+    lg[j] = e * (1.f / sum);
+    const int q = static_cast<int>((row / g.H) % g.Q), b = static_cast<int>(row / (static_cast<int64_t>(g.H) * g.Q));
+    float lx, ly;
+    layer_location<T, float>(a, g, b, q, j / g.P, ox, oy, lx, ly);
+    off[2 * j] = lx;
+    off[2 * j + 1] = ly;
+}
+
+// The prologue as two projections on the GEMM (x . W^T computed as hidden . W^T + pos . W^T, float32 out, straight
+// into loc_out and attn_out) and the in-place finalize. A workgroup of the single-kernel prologue owns 16 queries of
+// one head and streams that head's weights once per 16 queries, so for large problems the weights are read
+// B * Q / 16 times; the GEMM tiles 64 queries x 64 outputs and keeps them in LDS. Returns 1, launching nothing,
+// when the GEMM cannot take the operands.
+template <typename T>
+int launch_prologue_gemm(const LayerArgs& la, const Geom& g, hipStream_t stream) {
+    constexpr int V = 16 / static_cast<int>(sizeof(T));
+    const uintptr_t al = reinterpret_cast<uintptr_t>(la.query) | reinterpret_cast<uintptr_t>(la.pos) |
+                         reinterpret_cast<uintptr_t>(la.off_w) | reinterpret_cast<uintptr_t>(la.aw_w) |
+                         reinterpret_cast<uintptr_t>(la.loc_out) | reinterpret_cast<uintptr_t>(la.attn_out);
+    if (la.Cq <= 0 || la.Cq % V != 0 || al % 16 != 0 || g.P <= 0) return 1;
+    const int64_t M = static_cast<int64_t>(g.B) * g.Q, NO = static_cast<int64_t>(g.H) * g.LP;
+    int rc = launch_proj_f32(std::is_same<T, float>::value ? kF32 : std::is_same<T, f16>::value ? kF16 : kBF16,
+                             la.query, la.pos, la.off_w, la.off_b, static_cast<float*>(la.loc_out), M, la.Cq, 2 * NO,
+                             stream);
+    if (rc != 0) return rc;
+    rc = launch_proj_f32(std::is_same<T, float>::value ? kF32 : std::is_same<T, f16>::value ? kF16 : kBF16, la.query,
+                         la.pos, la.aw_w, la.aw_b, static_cast<float*>(la.attn_out), M, la.Cq, NO, stream);
+    if (rc != 0) return rc;
+    int seg_log2 = 0;
+    while ((1 << seg_log2) < g.LP) ++seg_log2;
+    const int64_t rows = M * g.H, per_wave = kWave >> seg_log2, waves = (rows + per_wave - 1) / per_wave;
+    hipLaunchKernelGGL(layer_finalize_kernel<T>, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, stream,
+                       la, g, seg_log2);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : set_error(-3, "layer prologue launch failed: %s", hipGetErrorString(e));
+}
+
 constexpr size_t kLdsBudget = 65536;
 
 template <typename T, bool MFMA>
@@ -93,9 +155,23 @@ int launch_prologue_t(PrologueParams p, hipStream_t stream) {
 
 }  // namespace
 
-int launch_prologue(int dtype, const LayerArgs& layer, const Geom& g, hipStream_t stream) {
+int launch_prologue(int dtype, const LayerArgs& layer, const Geom& g, hipStream_t stream, int route) {
     if (layer.loc_out == nullptr || layer.attn_out == nullptr)
         return set_error(-1, "layer prologue: locations and weights need output buffers");
+    // route 0: by the projections' multiply-adds. Measured on MI355X: the single kernel up to DINO-sized problems
+    // (3600 queries, Cq 256, 8 heads x 16 samples, 3.5e8: 14-17 µs against 25 µs for the GEMM route), the GEMM route
+    // for the C = 1024 shape (600 queries, 16 heads x 64 samples, 1.9e9: 45 µs against 72 µs).
+    const double macs = static_cast<double>(g.B) * g.Q * g.H * 3 * g.LP * layer.Cq;
+    if (dtype != kF64 && (route == 2 || (route == 0 && macs >= 8e8))) {
+        int rc = 1;
+        switch (dtype) {
+            case kF32: rc = launch_prologue_gemm<float>(layer, g, stream); break;
+            case kF16: rc = launch_prologue_gemm<f16>(layer, g, stream); break;
+            case kBF16: rc = launch_prologue_gemm<bf16>(layer, g, stream); break;
+            default: break;
+        }
+        if (rc <= 0) return rc;  // launched, or failed; 1: the GEMM cannot take the operands
+    }
     PrologueParams p{layer, g, 1, 1, 0, 0};
     switch (dtype) {
         case kF32: return launch_prologue_t<float>(p, stream);

@@ -216,14 +216,11 @@ __device__ __forceinline__ void prologue_stats(int LP, int QT, const A* pro, int
     }
 }
 
-// Location (lx, ly) and attention weight w of sample j of tile row r (query q of image b, head h); also stored
-// to a.loc_out / a.attn_out when those are set.
+// Reference-point arithmetic: location (lx, ly) of a sample on level l of query q of image b from its offsets
+// (ox, oy).
 template <typename T, typename A>
-__device__ __forceinline__ void prologue_sample(const LayerArgs& a, const Geom& g, int b, int q, int h, int r, int j,
-                                                const A* pro, int PP, const A* rstat, A& lx, A& ly, A& w) {
-    const int LP = g.LP, l = j / g.P;
-    w = exp_acc(pro[r * PP + 2 * LP + j] - rstat[2 * r]) * rstat[2 * r + 1];
-    const A ox = pro[r * PP + 2 * j], oy = pro[r * PP + 2 * j + 1];
+__device__ __forceinline__ void layer_location(const LayerArgs& a, const Geom& g, int b, int q, int l, A ox, A oy,
+                                               A& lx, A& ly) {
     const T* rp = static_cast<const T*>(a.ref) +
                   ((static_cast<size_t>(b) * g.Q + q) * a.RL + (a.RL == 1 ? 0 : l)) * a.RD;
     const A rx = cvt<A>(rp[0]), ry = cvt<A>(rp[1]);
@@ -234,6 +231,16 @@ __device__ __forceinline__ void prologue_sample(const LayerArgs& a, const Geom& 
         lx = rx + ox / static_cast<A>(g.P) * cvt<A>(rp[2]) * static_cast<A>(0.5);
         ly = ry + oy / static_cast<A>(g.P) * cvt<A>(rp[3]) * static_cast<A>(0.5);
     }
+}
+
+// Location (lx, ly) and attention weight w of sample j of tile row r (query q of image b, head h); also stored
+// to a.loc_out / a.attn_out when those are set.
+template <typename T, typename A>
+__device__ __forceinline__ void prologue_sample(const LayerArgs& a, const Geom& g, int b, int q, int h, int r, int j,
+                                                const A* pro, int PP, const A* rstat, A& lx, A& ly, A& w) {
+    const int LP = g.LP, l = j / g.P;
+    w = exp_acc(pro[r * PP + 2 * LP + j] - rstat[2 * r]) * rstat[2 * r + 1];
+    layer_location<T, A>(a, g, b, q, l, pro[r * PP + 2 * j], pro[r * PP + 2 * j + 1], lx, ly);
     const size_t idx = ((static_cast<size_t>(b) * g.Q + q) * g.H + h) * LP + j;
     if (a.loc_out != nullptr) {
         A* lo = static_cast<A*>(a.loc_out);

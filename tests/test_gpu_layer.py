@@ -84,6 +84,28 @@ def test_locations_in_float32(dtype):
         np.testing.assert_allclose(a_.double().cpu().numpy(), ref_attn, rtol=0, atol=tol)
 
 
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16, torch.bfloat16])
+def test_large_prologue_takes_the_gemm_route(dtype):
+    # >= 8e8 multiply-adds in the query projections: project mode runs them on the GEMM (hidden . W^T + pos . W^T in
+    # float32) and finalizes softmax and locations in place; boxes with 64 samples per head (one row per wavefront)
+    # and points per level with 12 (four rows per wavefront), with and without bias
+    for name, (B, Q, H, D, C, levels, P, rd, rl, bias) in {
+            'boxes': (2, 300, 16, 32, 512, [(40, 40), (20, 20), (10, 10), (5, 5)], 16, 4, '1', True),
+            'points per level': (2, 900, 16, 32, 1024, [(48, 40), (24, 20), (12, 10)], 4, 2, 'L', False)}.items():
+        a = make_layer(B, Q, H, D, C, levels, P, rd, rl, dtype=dtype, bias=bias)
+        ref, ref_attn = olayer.layer(*a[:15], position_embeddings=a[15])
+        ref_loc, _ = olayer.locations(a[0], a[2], a[3], a[5], a[6], a[7], a[8], H, P, position_embeddings=a[15])
+        dev = to(a[:13], 'cuda') + a[13:15] + to(a[15:], 'cuda')
+        say(f'  gemm route {name} {dtype}')
+        loc, attn = _native.layer_prologue(dev[0], dev[15], dev[2], dev[5], dev[6], dev[7], dev[8], dev[3], H, P)
+        torch.cuda.synchronize()
+        lt = LOC_TOL[dtype]
+        assert np.abs(loc.double().cpu().numpy() - ref_loc).max() <= lt, f'{name}: locations'
+        assert np.abs(attn.double().cpu().numpy() - ref_attn).max() <= lt, f'{name}: attention weights'
+        out, got_attn = run_layer(dev, 'project')
+        check(f'{name} {dtype} [project]', out, ref, dtype)
+
+
 def test_float64_layer_takes_the_standalone_prologue():
     a = make_layer(2, 21, 4, 16, 64, [(12, 18), (6, 9)], 4, 2, 'L', dtype=torch.float64)
     ref, ref_attn = olayer.layer(*a[:15], position_embeddings=a[15])
