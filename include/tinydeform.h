@@ -41,7 +41,8 @@ extern "C" {
 #define TD_E_ARG -1    /* invalid shape, limit or pointer (the same cases the reference rejects) */
 #define TD_E_DTYPE -2  /* unknown dtype code */
 #define TD_E_LAUNCH -3 /* the HIP runtime refused a kernel launch */
-#define TD_E_WORKSPACE -4 /* td_layer_fused_forward: this problem needs loc_out and attn_out (see there) */
+#define TD_E_WORKSPACE -4 /* td_layer_fused_forward: this problem needs loc_out and attn_out (see there);
+                              td_weight_grad: the workspace is smaller than td_weight_grad_workspace() */
 
 /* limits shared with the reference operator (csrc/ma_deform_fused.cu:26-28) */
 #define TD_MAX_LEVEL_POINTS 64 /* L * P */
@@ -168,6 +169,44 @@ int td_layer_sample_forward(int dtype, const void* value, const int64_t* spatial
  */
 int td_value_proj(int dtype, const void* memory, const void* weight, const void* bias, void* value, int64_t M,
                   int64_t K, int64_t NO, void* stream);
+
+/*
+ * Backward (training). No counterpart in the reference, whose operator is inference only (README.md:61); these are
+ * the gradients of its reference computation (reference.py:13-40: value = memory . W^T + b, then bilinear
+ * grid_sample with zero padding, align_corners=False, weighted by the attention), for callers that train through
+ * the operator. The caller owns every buffer, workspaces included.
+ */
+
+/*
+ * Sampling half: given grad_out [B, Q, H*D] and the forward's value, locations and weights,
+ *   grad_value_acc [B, N, H*D]  float32 (float64 for TD_F64): zeroed, then accumulated (the gradient of value);
+ *   grad_value     [B, N, H*D]  dtype, or NULL: grad_value_acc rounded to dtype (may be grad_value_acc itself for
+ *                               TD_F32 / TD_F64);
+ *   grad_loc [B, Q, H, L, P, 2], grad_attn [B, Q, H, L, P]: dtype.
+ * padding_mask as in td_sample_forward_masked. Limits as td_sample_forward, and D <= 256.
+ */
+int td_sample_backward(int dtype, const void* value, const int64_t* spatial_shapes, const int64_t* level_start_index,
+                       const void* sampling_locations, const void* attention_weights, const uint8_t* padding_mask,
+                       const void* grad_out, void* grad_value_acc, void* grad_value, void* grad_loc, void* grad_attn,
+                       int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D, int64_t L, int64_t P, void* stream);
+
+/*
+ * Projection, input side: grad_memory[M, C] = grad_value[M, HD] . value_weight[HD, C] on the library's GEMM.
+ * weight_t: a workspace of HD*C elements of dtype, which receives value_weight^T.
+ */
+int td_input_grad(int dtype, const void* grad_value, const void* value_weight, void* weight_t, void* grad_memory,
+                  int64_t M, int64_t HD, int64_t C, void* stream);
+
+/* Bytes of workspace td_weight_grad needs for these sizes. */
+int64_t td_weight_grad_workspace(int dtype, int64_t M, int64_t HD, int64_t C);
+
+/*
+ * Projection, weight side: grad_weight[HD, C] = grad_value[M, HD]^T . memory[M, C] and grad_bias[HD] = the column
+ * sums of grad_value (NULL: not computed). Split over the M tokens, with per-split float32 (float64) partials in
+ * the workspace summed in a fixed order, so the result is the same on every run.
+ */
+int td_weight_grad(int dtype, const void* grad_value, const void* memory, void* grad_weight, void* grad_bias,
+                   int64_t M, int64_t HD, int64_t C, void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

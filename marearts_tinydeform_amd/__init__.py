@@ -14,7 +14,7 @@ from .reference import layer_locations_reference, ma_deform_attn_layer_reference
 
 __all__ = ['ma_deform_attn', 'ma_deform_attn_reference', 'choose_mode', 'ma_deform_sample', 'ma_deform_sample_v2',
            'predict_us', 'ma_deform_attn_layer', 'ma_deform_attn_layer_reference', 'layer_locations_reference',
-           'MSDeformAttnLayer']
+           'MSDeformAttnLayer', 'ma_deform_attn_train', 'ma_deform_sample_train']
 __version__ = '0.1.0'
 
 MODES = ('auto', 'fused', 'project')
@@ -228,6 +228,81 @@ def _layer(hidden_states, memory, reference_points, spatial_shapes, level_start_
     return out
 
 
+class _DeformAttnFunction(torch.autograd.Function):
+    """value = memory @ W^T + b, then sampling, on the library's kernels, with gradients for memory, W, b, the
+    locations and the attention weights (td_sample_backward, td_input_grad, td_weight_grad)."""
+
+    @staticmethod
+    def forward(ctx, memory, value_weight, value_bias, spatial_shapes, level_start_index, sampling_locations,
+                attention_weights, padding_mask):
+        H = sampling_locations.shape[2] if sampling_locations.dim() == 6 else 0
+        _native.check_geometry(memory, spatial_shapes, level_start_index, sampling_locations, attention_weights)
+        _native.check_padding_mask(memory, padding_mask)
+        value = _native.value_proj(memory, value_weight, value_bias)
+        out = _native.sample_forward(value, H, spatial_shapes, level_start_index, sampling_locations,
+                                     attention_weights, padding_mask)
+        ctx.save_for_backward(memory, value_weight, value, spatial_shapes, level_start_index, sampling_locations,
+                              attention_weights, padding_mask)
+        ctx.has_bias = value_bias is not None
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        memory, weight, value, shapes, starts, loc, attn, mask = ctx.saved_tensors
+        need = ctx.needs_input_grad
+        gv, gl, ga = _native.sample_backward(value, loc.shape[2], shapes, starts, loc, attn, grad_out, mask)
+        gm = _native.input_grad(gv, weight) if need[0] else None
+        gw = gb = None
+        if need[1] or (need[2] and ctx.has_bias):
+            gw, gb = _native.weight_grad(gv, memory, with_bias=ctx.has_bias and need[2])
+        return (gm, gw if need[1] else None, gb, None, None, gl if need[5] else None, ga if need[6] else None, None)
+
+
+class _DeformSampleFunction(torch.autograd.Function):
+    """Sampling of projected values with gradients for the values, the locations and the attention weights."""
+
+    @staticmethod
+    def forward(ctx, value, spatial_shapes, level_start_index, sampling_locations, attention_weights, padding_mask):
+        H = sampling_locations.shape[2] if sampling_locations.dim() == 6 else 0
+        out = _native.sample_forward(value, H, spatial_shapes, level_start_index, sampling_locations,
+                                     attention_weights, padding_mask)
+        ctx.save_for_backward(value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+                              padding_mask)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        value, shapes, starts, loc, attn, mask = ctx.saved_tensors
+        need = ctx.needs_input_grad
+        gv, gl, ga = _native.sample_backward(value, loc.shape[2], shapes, starts, loc, attn, grad_out, mask)
+        return gv if need[0] else None, None, None, gl if need[3] else None, ga if need[4] else None, None
+
+
+def ma_deform_attn_train(memory, value_weight, value_bias, spatial_shapes, level_start_index, sampling_locations,
+                         attention_weights, padding_mask=None):
+    """ma_deform_attn with autograd, for training: the same arguments and result (project order: the value
+    projection, then sampling), differentiable in memory, value_weight, value_bias, sampling_locations and
+    attention_weights. GPU tensors run the library's forward and backward kernels (float32 accumulation for the
+    16/32-bit types); CPU tensors run ma_deform_attn_reference under PyTorch's autograd. ma_deform_attn itself stays
+    inference only, as in the reference."""
+    if not memory.is_cuda:
+        return ma_deform_attn_reference(memory, value_weight, value_bias, spatial_shapes, level_start_index,
+                                        sampling_locations, attention_weights, padding_mask=padding_mask)
+    _native._require()
+    return _on_device(memory, _DeformAttnFunction.apply, memory, value_weight, value_bias, spatial_shapes,
+                      level_start_index, sampling_locations, attention_weights, padding_mask)
+
+
+def ma_deform_sample_train(value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+                           padding_mask=None):
+    """ma_deform_sample with autograd: differentiable in value [B, N, H * D], sampling_locations and
+    attention_weights (Deformable-DETR's MSDeformAttnFunction, for decoders that project the values themselves).
+    GPU tensors only."""
+    _native._require()
+    return _on_device(value, _DeformSampleFunction.apply, value, spatial_shapes, level_start_index,
+                      sampling_locations, attention_weights, padding_mask)
+
+
 def _grid_offsets_bias(n_heads, n_levels, n_points):
     """Deformable-DETR's initial sampling-offset bias: head h looks along direction 2 pi h / H (scaled so the larger
     coordinate is 1), point p at distance p + 1, on every level."""
@@ -276,6 +351,18 @@ class MSDeformAttnLayer(torch.nn.Module):
             sizes = spatial_shapes[:, 0] * spatial_shapes[:, 1]
             level_start_index = torch.cat([sizes.new_zeros(1), sizes.cumsum(0)[:-1]])
         padding_mask = None if attention_mask is None else ~attention_mask.bool()
+        if torch.is_grad_enabled() and (any(t.requires_grad for t in self.parameters()) or any(
+                t is not None and t.requires_grad for t in (hidden_states, encoder_hidden_states, position_embeddings,
+                                                            reference_points))):
+            # training: the query prologue and output_proj under PyTorch's autograd, the operator on the library's
+            # forward and backward kernels
+            loc, attn = layer_locations_reference(
+                hidden_states, reference_points, spatial_shapes, self.sampling_offsets.weight,
+                self.sampling_offsets.bias, self.attention_weights.weight, self.attention_weights.bias, self.n_heads,
+                self.n_points, position_embeddings)
+            core = ma_deform_attn_train(encoder_hidden_states, self.value_proj.weight, self.value_proj.bias,
+                                        spatial_shapes, level_start_index, loc, attn, padding_mask=padding_mask)
+            return self.output_proj(core), attn
         return ma_deform_attn_layer(
             hidden_states, encoder_hidden_states, reference_points, spatial_shapes, level_start_index,
             self.sampling_offsets.weight, self.sampling_offsets.bias, self.attention_weights.weight,

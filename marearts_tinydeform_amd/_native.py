@@ -34,6 +34,10 @@ SIGNATURES = {
     'td_layer_prologue': (_int, [_int, _vp, _vp, _vp, _i64, _i64] + [_vp] * 7 + [_i64] * 6 + [_vp]),
     'td_layer_fused_forward': (_int, [_int, _vp, _vp, _vp, _i64, _i64] + [_vp] * 13 + [_i64] * 9 + [_vp]),
     'td_layer_sample_forward': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 7 + [_vp]),
+    'td_sample_backward': (_int, [_int] + [_vp] * 11 + [_i64] * 7 + [_vp]),
+    'td_input_grad': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    'td_weight_grad_workspace': (_i64, [_int, _i64, _i64, _i64]),
+    'td_weight_grad': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
 }
 
 TD_E_WORKSPACE = -4  # td_layer_fused_forward: the problem needs loc_out / attn_out
@@ -278,6 +282,76 @@ def value_proj(memory, weight, bias):
     _check(lib_.td_value_proj(DTYPE_CODES[memory.dtype], mem.data_ptr(), w.data_ptr(), _ptr(b), value.data_ptr(),
                               B * N, C, HD, _stream(dev)))
     return value
+
+
+def sample_backward(value, heads, spatial_shapes, level_start_index, sampling_locations, attention_weights, grad_out,
+                    padding_mask=None):
+    """Gradients of sample_forward (td_sample_backward): (grad_value [B, N, H * D], grad_loc, grad_attn), each in the
+    input dtype; grad_value is accumulated in float32 (float64) and rounded once."""
+    lib_ = _require()
+    B, Q, H, L, P = check_geometry(value, spatial_shapes, level_start_index, sampling_locations, attention_weights)
+    N, HD = value.size(1), value.size(2)
+    if heads != H or HD % H != 0:
+        raise RuntimeError('value must be [B, N, H * D] with H = sampling_locations.size(2)')
+    if HD // H > 256:
+        raise RuntimeError('sample backward: head dim must be <= 256')
+    if grad_out.shape != (B, Q, HD) or grad_out.dtype != value.dtype or grad_out.device != value.device:
+        raise RuntimeError('grad_out must be [B, Q, H * D] like the forward output')
+    mask = check_padding_mask(value, padding_mask)
+    dev, dt = value.device, value.dtype
+    v, go = value.contiguous(), grad_out.contiguous()
+    lc, aw = sampling_locations.contiguous(), attention_weights.contiguous()
+    sh, st = spatial_shapes.contiguous(), level_start_index.contiguous()
+    acc = torch.empty((B, N, HD), dtype=acc_dtype(dt), device=dev)
+    gv = acc if acc.dtype == dt else torch.empty((B, N, HD), dtype=dt, device=dev)
+    gl = torch.empty_like(lc)
+    ga = torch.empty_like(aw)
+    if acc.numel() == 0 and gl.numel() == 0:
+        return gv, gl, ga
+    _check(lib_.td_sample_backward(DTYPE_CODES[dt], v.data_ptr(), sh.data_ptr(), st.data_ptr(), lc.data_ptr(),
+                                   aw.data_ptr(), _ptr(mask), go.data_ptr(), acc.data_ptr(), gv.data_ptr(),
+                                   gl.data_ptr(), ga.data_ptr(), B, Q, N, H, HD // H, L, P, _stream(dev)))
+    return gv, gl, ga
+
+
+def input_grad(grad_value, weight):
+    """grad_memory = grad_value @ weight on the library's GEMM (td_input_grad): [B, N, C]."""
+    lib_ = _require()
+    B, N, HD = grad_value.shape
+    C = weight.size(1)
+    if weight.shape != (HD, C) or weight.dtype != grad_value.dtype or weight.device != grad_value.device:
+        raise RuntimeError('weight must be [H * D, C] like value_weight')
+    dev = grad_value.device
+    g, w = grad_value.contiguous(), weight.contiguous()
+    wt = torch.empty((C, HD), dtype=w.dtype, device=dev)
+    out = torch.empty((B, N, C), dtype=g.dtype, device=dev)
+    if out.numel() == 0:
+        return out
+    if HD == 0:
+        return out.zero_()
+    _check(lib_.td_input_grad(DTYPE_CODES[g.dtype], g.data_ptr(), w.data_ptr(), wt.data_ptr(), out.data_ptr(), B * N,
+                              HD, C, _stream(dev)))
+    return out
+
+
+def weight_grad(grad_value, memory, with_bias=True):
+    """(grad_weight [H * D, C] = grad_value^T @ memory, grad_bias [H * D] or None) over all B * N tokens
+    (td_weight_grad), with its float32 (float64) split-K workspace from the caching allocator."""
+    lib_ = _require()
+    B, N, HD = grad_value.shape
+    C = memory.size(2)
+    if memory.shape[:2] != (B, N) or memory.dtype != grad_value.dtype or memory.device != grad_value.device:
+        raise RuntimeError('memory must be [B, N, C] with the tokens of grad_value')
+    dev, dt = grad_value.device, grad_value.dtype
+    g, mem = grad_value.contiguous(), memory.contiguous()
+    gw = torch.empty((HD, C), dtype=dt, device=dev)
+    gb = torch.empty((HD,), dtype=dt, device=dev) if with_bias else None
+    code = DTYPE_CODES[dt]
+    ws_bytes = int(lib_.td_weight_grad_workspace(code, B * N, HD, C))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    _check(lib_.td_weight_grad(code, g.data_ptr(), mem.data_ptr(), gw.data_ptr(), _ptr(gb), B * N, HD, C,
+                               ws.data_ptr(), ws_bytes, _stream(dev)))
+    return gw, gb
 
 
 def acc_dtype(dtype):

@@ -308,3 +308,63 @@ extern "C" int td_value_proj(int dtype, const void* memory, const void* weight, 
         return set_error(TD_E_ARG, "null pointer argument");
     return launch_value_proj(dtype, memory, weight, bias, value, M, K, NO, static_cast<hipStream_t>(stream), 0);
 }
+
+extern "C" int td_sample_backward(int dtype, const void* value, const int64_t* spatial_shapes,
+                                  const int64_t* level_start_index, const void* sampling_locations,
+                                  const void* attention_weights, const uint8_t* padding_mask, const void* grad_out,
+                                  void* grad_value_acc, void* grad_value, void* grad_loc, void* grad_attn, int64_t B,
+                                  int64_t Q, int64_t N, int64_t H, int64_t D, int64_t L, int64_t P, void* stream) {
+    int rc = check_geometry(dtype, B, Q, N, H, D, L, P, spatial_shapes, level_start_index, sampling_locations,
+                            attention_weights, grad_loc);
+    if (rc != TD_OK) return rc;
+    if (B * N * H * D > 0 && grad_value_acc == nullptr) return set_error(TD_E_ARG, "null pointer argument");
+    if (B * Q * H * L * P > 0 && (value == nullptr || grad_out == nullptr || grad_attn == nullptr))
+        return set_error(TD_E_ARG, "null pointer argument");
+    if (D > 256) return set_error(TD_E_ARG, "sample backward: head dim must be <= 256");
+    Geom g{spatial_shapes, level_start_index, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N),
+           static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), static_cast<int>(P)};
+    g.mask = padding_mask;
+    set_levels(g, nullptr);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    rc = launch_sample_backward(dtype, value, g, sampling_locations, attention_weights, grad_out, grad_value_acc,
+                                grad_loc, grad_attn, s);
+    if (rc != TD_OK || grad_value == nullptr || grad_value == grad_value_acc) return rc;
+    return launch_convert(dtype, grad_value_acc, grad_value, B * N * H * D, s);
+}
+
+extern "C" int td_input_grad(int dtype, const void* grad_value, const void* value_weight, void* weight_t,
+                             void* grad_memory, int64_t M, int64_t HD, int64_t C, void* stream) {
+    g_last_error.clear();
+    if (!dtype_ok(dtype)) return set_error(TD_E_DTYPE, "unknown dtype code %d", dtype);
+    if (M < 0 || HD < 0 || C < 0) return set_error(TD_E_ARG, "sizes must be non-negative");
+    if (M > kInt32Max || HD > kInt32Max || C > kInt32Max) return set_error(TD_E_ARG, "GEMM size exceeds int32");
+    if (M * C == 0) return TD_OK;
+    if (grad_memory == nullptr || (HD > 0 && (grad_value == nullptr || value_weight == nullptr || weight_t == nullptr)))
+        return set_error(TD_E_ARG, "null pointer argument");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const int rc = launch_transpose(dtype, value_weight, weight_t, HD, C, s);
+    if (rc != TD_OK) return rc;
+    return launch_value_proj(dtype, grad_value, weight_t, nullptr, grad_memory, M, HD, C, s, 0);
+}
+
+extern "C" int64_t td_weight_grad_workspace(int dtype, int64_t M, int64_t HD, int64_t C) {
+    int splits = 1, chunk = 32;
+    int64_t bytes = 0;
+    if (M < 0 || HD < 0 || C < 0) return 0;
+    wgrad_plan(M, HD, C, dtype, &splits, &chunk, &bytes);
+    return bytes;
+}
+
+extern "C" int td_weight_grad(int dtype, const void* grad_value, const void* memory, void* grad_weight,
+                              void* grad_bias, int64_t M, int64_t HD, int64_t C, void* workspace,
+                              int64_t workspace_bytes, void* stream) {
+    g_last_error.clear();
+    if (!dtype_ok(dtype)) return set_error(TD_E_DTYPE, "unknown dtype code %d", dtype);
+    if (M < 0 || HD < 0 || C < 0) return set_error(TD_E_ARG, "sizes must be non-negative");
+    if (M > kInt32Max || HD > kInt32Max || C > kInt32Max) return set_error(TD_E_ARG, "GEMM size exceeds int32");
+    if (HD * C == 0 && (grad_bias == nullptr || HD == 0)) return TD_OK;
+    if (grad_weight == nullptr || (M > 0 && (grad_value == nullptr || memory == nullptr)))
+        return set_error(TD_E_ARG, "null pointer argument");
+    return launch_wgrad(dtype, grad_value, memory, grad_weight, grad_bias, M, HD, C, workspace, workspace_bytes,
+                        static_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,482 @@
+// Backward of value projection + multi-scale deformable attention (training). The reference operator is inference
+// only (README.md:61); the gradients here are those of its reference computation (reference.py:13-40: F.linear, then
+// bilinear grid_sample with zero padding, align_corners=False, weighted by the attention), in project order, which
+// equals fused order up to rounding:
+//
+//   value       = memory . W^T + b                                   [B, N, H*D]
+//   out[r, :]   = sum_s a_s sum_c w_c(fx_s, fy_s) value[t_c, h*D:(h+1)*D]      r = (b, q, h), s = (l, p), c = corner
+//
+//   G = grad_value[t, h*D + d] = sum over (r, s, c) hitting t of a_s w_c g_r[d]         (g_r = grad_out[r, :])
+//   grad_attn[r, s]  = sum_c w_c d_c                 d_c = value[t_c] . g_r (0 for a corner outside the map)
+//   grad_loc[r, s]   = a_s (dV/dfx W_l, dV/dfy H_l)  dV/dfx = (1 - fy)(d_1 - d_0) + fy (d_3 - d_2)
+//                                                    dV/dfy = (1 - fx)(d_2 - d_0) + fx (d_3 - d_1)
+//   grad_memory = G . W,   grad_W = G^T . memory,   grad_b = sum over tokens of G
+//
+// (x = loc_x W_l - 0.5, so dx/dloc_x = W_l; corner k has dx = k & 1, dy = k >> 1.) A location clamped to the map's
+// guard band has all four corners outside, so its gradient is 0, as for grid_sample's zero padding. Discrete
+// sampling (D-FINE) is piecewise constant in the location: its location gradient is 0.
+#include "td_gemm.h"
+
+namespace td {
+namespace {
+
+// The bilinear taps of a sample: tokens (-1 outside the map, outside [0, N) or on a padded token) and the
+// fractional position (fx, fy); the same rule as corners_at (td_common.h), keeping the two factors apart.
+template <typename A>
+struct Taps {
+    int tok[4];
+    A fx, fy;
+};
+
+template <typename A>
+__device__ __forceinline__ Taps<A> taps_at(A lx, A ly, int l, const Geom& g, int64_t row) {
+    Taps<A> t;
+    const int hl = static_cast<int>(g.shapes[2 * l]);
+    const int wl = static_cast<int>(g.shapes[2 * l + 1]);
+    const int64_t st = g.starts[l];
+    const int64_t b = row / (static_cast<int64_t>(g.Q) * g.H);
+    if (g.discrete) {
+        const A fx = fmin(fmax(lx * static_cast<A>(wl) + static_cast<A>(0.5), static_cast<A>(-1)), static_cast<A>(wl));
+        const A fy = fmin(fmax(ly * static_cast<A>(hl) + static_cast<A>(0.5), static_cast<A>(-1)), static_cast<A>(hl));
+        int xi = static_cast<int>(fx), yi = static_cast<int>(fy);
+        xi = xi < 0 ? 0 : xi > wl - 1 ? wl - 1 : xi;
+        yi = yi < 0 ? 0 : yi > hl - 1 ? hl - 1 : yi;
+        const int64_t tk = st + static_cast<int64_t>(yi) * wl + xi;
+        bool in = wl > 0 && hl > 0 && tk >= 0 && tk < g.N;
+        if (in && g.mask != nullptr) in = g.mask[b * g.N + tk] == 0;
+        t.tok[0] = in ? static_cast<int>(tk) : -1;
+        t.tok[1] = t.tok[2] = t.tok[3] = -1;
+        t.fx = t.fy = 0;  // weight 1 on tap 0 (see tap_weight)
+        return t;
+    }
+    A x = lx * static_cast<A>(wl) - static_cast<A>(0.5);
+    A y = ly * static_cast<A>(hl) - static_cast<A>(0.5);
+    x = fmin(fmax(x, static_cast<A>(-2)), static_cast<A>(wl) + static_cast<A>(1));
+    y = fmin(fmax(y, static_cast<A>(-2)), static_cast<A>(hl) + static_cast<A>(1));
+    const A xf = floor(x), yf = floor(y);
+    const int x0 = static_cast<int>(xf), y0 = static_cast<int>(yf);
+    t.fx = x - xf;
+    t.fy = y - yf;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int xi = x0 + (k & 1), yi = y0 + (k >> 1);
+        const int64_t tk = st + static_cast<int64_t>(yi) * wl + xi;
+        bool in = xi >= 0 && xi < wl && yi >= 0 && yi < hl && tk >= 0 && tk < g.N;
+        if (in && g.mask != nullptr) in = g.mask[b * g.N + tk] == 0;
+        t.tok[k] = in ? static_cast<int>(tk) : -1;
+    }
+    return t;
+}
+
+template <typename A>
+__device__ __forceinline__ A tap_weight(const Taps<A>& t, int k) {
+    return ((k & 1) ? t.fx : static_cast<A>(1) - t.fx) * ((k >> 1) ? t.fy : static_cast<A>(1) - t.fy);
+}
+
+__device__ __forceinline__ void atomic_add(float* p, float v) { atomicAdd(p, v); }
+__device__ __forceinline__ void atomic_add(double* p, double v) { atomicAdd(p, v); }
+
+template <typename A>
+__device__ __forceinline__ A xor_sum(A v, int mask) {
+    return v + xor_lane(v, mask);
+}
+
+struct BackParams {
+    const void* value;
+    const void* loc;
+    const void* attn;
+    const void* grad_out;
+    void* grad_value;  // [B, N, H*D] accumulation type, zeroed
+    void* grad_loc;    // [rows, LP, 2] element type (accumulation type with g.loc_acc)
+    void* grad_attn;   // [rows, LP]
+    Geom g;
+    int LG;  // lanes per sample: a power of two, LG * CE >= D
+};
+
+// One wavefront per row (b, q, h); its LP samples go 64 / LG at a time, LG lanes per sample, each lane owning CE
+// consecutive channels of the head. grad_out's channels are read once per row.
+template <typename T, int CE>
+__global__ __launch_bounds__(256) void sample_backward_kernel(BackParams p) {
+    using A = typename AccOf<T>::type;
+    const Geom& g = p.g;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t rows = static_cast<int64_t>(g.B) * g.Q * g.H;
+    if (row >= rows) return;  // uniform across the wavefront
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+    const int LG = p.LG, per = kWave / LG, slot = lane / LG, sub = lane - slot * LG;
+    const int D = g.D, HD = g.H * g.D, LP = g.LP;
+    const int h = static_cast<int>(row % g.H);
+    const int64_t bq = row / g.H, b = bq / g.Q;
+    const int c0 = sub * CE;
+
+    const T* __restrict__ go = static_cast<const T*>(p.grad_out) + bq * HD + h * D;
+    A gr[CE];
+#pragma unroll
+    for (int e = 0; e < CE; ++e) gr[e] = c0 + e < D ? cvt<A>(go[c0 + e]) : static_cast<A>(0);
+
+    const T* __restrict__ vb = static_cast<const T*>(p.value) + b * g.N * HD + h * D;
+    A* __restrict__ gv = static_cast<A*>(p.grad_value) + b * g.N * HD + h * D;
+    for (int j0 = 0; j0 < LP; j0 += per) {
+        const int j = j0 + slot;
+        const bool on = j < LP;  // uniform within a sample's lane group
+        A lx = 0, ly = 0, a = 0;
+        int l = 0;
+        if (on) {
+            const int64_t idx = row * LP + j;
+            if (g.loc_acc) {
+                lx = static_cast<const A*>(p.loc)[2 * idx];
+                ly = static_cast<const A*>(p.loc)[2 * idx + 1];
+                a = static_cast<const A*>(p.attn)[idx];
+            } else {
+                lx = cvt<A>(static_cast<const T*>(p.loc)[2 * idx]);
+                ly = cvt<A>(static_cast<const T*>(p.loc)[2 * idx + 1]);
+                a = cvt<A>(static_cast<const T*>(p.attn)[idx]);
+            }
+            l = level_of(g, j);
+        }
+        Taps<A> t;
+        if (on) {
+            t = taps_at<A>(lx, ly, l, g, row);
+        } else {
+            t.tok[0] = t.tok[1] = t.tok[2] = t.tok[3] = -1;
+            t.fx = t.fy = 0;
+        }
+        A d[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            d[k] = 0;
+            const int tk = t.tok[k];
+            if (tk < 0) continue;
+            const A w = g.discrete ? (k == 0 ? static_cast<A>(1) : static_cast<A>(0)) : tap_weight(t, k);
+            const A aw = a * w;
+            const T* vr = vb + static_cast<int64_t>(tk) * HD;
+            A* gr_row = gv + static_cast<int64_t>(tk) * HD;
+#pragma unroll
+            for (int e = 0; e < CE; ++e) {
+                if (c0 + e < D) {
+                    d[k] += cvt<A>(vr[c0 + e]) * gr[e];
+                    atomic_add(gr_row + c0 + e, aw * gr[e]);
+                }
+            }
+        }
+        // d_k over the sample's LG lanes (xor within the lane group)
+        for (int m = LG >> 1; m > 0; m >>= 1) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) d[k] = xor_sum(d[k], m);
+        }
+        if (on && sub == 0) {
+            const int64_t idx = row * LP + j;
+            A ga, gx = 0, gy = 0;
+            if (g.discrete) {
+                ga = d[0];
+            } else {
+                ga = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) ga += tap_weight(t, k) * d[k];
+                const A one = 1;
+                const A dvx = (one - t.fy) * (d[1] - d[0]) + t.fy * (d[3] - d[2]);
+                const A dvy = (one - t.fx) * (d[2] - d[0]) + t.fx * (d[3] - d[1]);
+                gx = a * dvx * static_cast<A>(g.shapes[2 * l + 1]);
+                gy = a * dvy * static_cast<A>(g.shapes[2 * l]);
+            }
+            if (g.loc_acc) {
+                static_cast<A*>(p.grad_loc)[2 * idx] = gx;
+                static_cast<A*>(p.grad_loc)[2 * idx + 1] = gy;
+                static_cast<A*>(p.grad_attn)[idx] = ga;
+            } else {
+                static_cast<T*>(p.grad_loc)[2 * idx] = static_cast<T>(gx);
+                static_cast<T*>(p.grad_loc)[2 * idx + 1] = static_cast<T>(gy);
+                static_cast<T*>(p.grad_attn)[idx] = static_cast<T>(ga);
+            }
+        }
+    }
+}
+
+template <typename T, typename A>
+__global__ __launch_bounds__(256) void convert_kernel(const A* __restrict__ src, T* __restrict__ dst, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        dst[i] = static_cast<T>(src[i]);
+}
+
+// dst[c, r] = src[r, c] for a [R, Cc] matrix, through 32 x 32 LDS tiles.
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int R, int Cc) {
+    __shared__ T tile[32][33];
+    const int r0 = blockIdx.y * 32, c0 = blockIdx.x * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    for (int i = ty; i < 32; i += 8) {
+        const int r = r0 + i, c = c0 + tx;
+        if (r < R && c < Cc) tile[i][tx] = src[static_cast<int64_t>(r) * Cc + c];
+    }
+    __syncthreads();
+    for (int i = ty; i < 32; i += 8) {
+        const int c = c0 + i, r = r0 + tx;
+        if (r < R && c < Cc) dst[static_cast<int64_t>(c) * R + r] = tile[tx][i];
+    }
+}
+
+// Weight and bias gradients, split over the M tokens: workgroup (n tile, c tile, split s) accumulates
+//   part[s, n, c]  = sum over its tokens m of G[m, n] X[m, c]      (64 x 64 tile, MFMA, float32)
+//   bpart[s, n]    = sum over its tokens m of G[m, n]               (c tile 0 only)
+// G [M, NO] and X [M, K] are token-major, so each K-chunk of tokens is staged in LDS transposed ([n][m], [c][m]):
+// MFMA fragments then hold consecutive tokens. The partials are summed in a fixed order by wgrad_reduce_kernel, so
+// the result does not depend on scheduling.
+struct WgradParams {
+    const void* G;
+    const void* X;
+    float* part;
+    float* bpart;
+    int M, NO, K;
+    int nt, ct, splits, chunk;  // tile counts, splits, tokens per split (a multiple of the MFMA K)
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void wgrad_kernel(WgradParams p) {
+    constexpr int E = 16 / static_cast<int>(sizeof(T));  // elements per 16 bytes
+    constexpr int KB = KBlock<T>::kK;                     // tokens per MFMA step
+    constexpr int LD = KB + E;                            // LDS pitch (elements) of a staged transposed row
+    __shared__ __align__(16) T gs[64 * LD];
+    __shared__ __align__(16) T xs[64 * LD];
+    const int tiles = p.nt * p.ct;
+    const int s = blockIdx.x / tiles, tile = blockIdx.x - s * tiles;
+    const int n0 = (tile / p.ct) * 64, c0 = (tile % p.ct) * 64;
+    const int m_begin = s * p.chunk, m_end = min(p.M, m_begin + p.chunk);
+    const T* __restrict__ G = static_cast<const T*>(p.G);
+    const T* __restrict__ X = static_cast<const T*>(p.X);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r16 = lane & 15, kg = lane >> 4;
+    f32x4 acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float bsum = 0.f;  // thread tid < 64: column n0 + tid of G (c tile 0)
+    const bool do_b = c0 == 0;
+
+    for (int m0 = m_begin; m0 < m_end; m0 += KB) {
+        // stage: KB tokens x 64 columns of each operand, read as rows of E elements, written transposed
+        for (int i = tid; i < KB * (64 / E); i += 256) {
+            const int mm = i / (64 / E), cc = (i % (64 / E)) * E, m = m0 + mm;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const int n = n0 + cc + e, c = c0 + cc + e;
+                gs[(cc + e) * LD + mm] = (m < m_end && n < p.NO) ? G[static_cast<int64_t>(m) * p.NO + n] : T(0);
+                xs[(cc + e) * LD + mm] = (m < m_end && c < p.K) ? X[static_cast<int64_t>(m) * p.K + c] : T(0);
+            }
+        }
+        __syncthreads();
+        if (do_b && tid < 64) {
+            for (int mm = 0; mm < KB; ++mm) bsum += static_cast<float>(gs[tid * LD + mm]);
+        }
+        const u32x4 fa = *reinterpret_cast<const u32x4*>(gs + (wave * 16 + r16) * LD + kg * E);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const u32x4 fb = *reinterpret_cast<const u32x4*>(xs + (t * 16 + r16) * LD + kg * E);
+            acc[t] = KBlock<T>::mma(fa, fb, acc[t]);
+        }
+        __syncthreads();
+    }
+    // acc[t][e]: row n0 + wave*16 + kg*4 + e, column c0 + t*16 + r16
+    float* part = p.part + static_cast<int64_t>(s) * p.NO * p.K;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int c = c0 + t * 16 + r16;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int n = n0 + wave * 16 + kg * 4 + e;
+            if (n < p.NO && c < p.K) part[static_cast<int64_t>(n) * p.K + c] = acc[t][e];
+        }
+    }
+    if (do_b && tid < 64 && n0 + tid < p.NO) p.bpart[static_cast<int64_t>(s) * p.NO + n0 + tid] = bsum;
+}
+
+// float64: the same sums on the vector ALUs, one thread per output of the 64 x 64 tile group
+template <typename T>
+__global__ __launch_bounds__(256) void wgrad_generic_kernel(WgradParams p, double* part, double* bpart) {
+    const int tiles = p.nt * p.ct;
+    const int s = blockIdx.x / tiles, tile = blockIdx.x - s * tiles;
+    const int n0 = (tile / p.ct) * 64, c0 = (tile % p.ct) * 64;
+    const int m_begin = s * p.chunk, m_end = min(p.M, m_begin + p.chunk);
+    const T* __restrict__ G = static_cast<const T*>(p.G);
+    const T* __restrict__ X = static_cast<const T*>(p.X);
+    for (int o = threadIdx.x; o < 64 * 64; o += 256) {
+        const int n = n0 + o / 64, c = c0 + o % 64;
+        if (n >= p.NO || c >= p.K) continue;
+        double acc = 0, bs = 0;
+        for (int m = m_begin; m < m_end; ++m) {
+            const double gv = static_cast<double>(G[static_cast<int64_t>(m) * p.NO + n]);
+            acc += gv * static_cast<double>(X[static_cast<int64_t>(m) * p.K + c]);
+            bs += gv;
+        }
+        part[(static_cast<int64_t>(s) * p.NO + n) * p.K + c] = acc;
+        if (c == 0) bpart[static_cast<int64_t>(s) * p.NO + n] = bs;
+    }
+}
+
+template <typename T, typename P>
+__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const P* __restrict__ part, const P* __restrict__ bpart,
+                                                           int splits, int NO, int K, T* __restrict__ gw,
+                                                           T* __restrict__ gb) {
+    const int64_t n_out = static_cast<int64_t>(NO) * K;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n_out) {
+        P acc = 0;
+        for (int s = 0; s < splits; ++s) acc += part[s * n_out + i];
+        gw[i] = static_cast<T>(acc);
+    }
+    if (gb != nullptr && i < NO) {
+        P acc = 0;
+        for (int s = 0; s < splits; ++s) acc += bpart[static_cast<int64_t>(s) * NO + i];
+        gb[i] = static_cast<T>(acc);
+    }
+}
+
+int launched(const char* what) {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : set_error(-3, "%s launch failed: %s", what, hipGetErrorString(e));
+}
+
+template <typename T>
+int sample_backward_t(const BackParams& p0, hipStream_t stream) {
+    BackParams p = p0;
+    constexpr int CE = 4;
+    int lg = 1;
+    while (lg * CE < p.g.D && lg < kWave) lg <<= 1;
+    p.LG = lg;
+    const int64_t rows = static_cast<int64_t>(p.g.B) * p.g.Q * p.g.H;
+    if (rows == 0) return 0;
+    hipLaunchKernelGGL((sample_backward_kernel<T, CE>), dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0,
+                       stream, p);
+    return launched("sample backward");
+}
+
+}  // namespace
+
+int launch_sample_backward(int dtype, const void* value, const Geom& g, const void* loc, const void* attn,
+                           const void* grad_out, void* grad_value, void* grad_loc, void* grad_attn,
+                           hipStream_t stream) {
+    if (g.D > kWave * 4) return set_error(-1, "sample backward: head dim %d > %d", g.D, kWave * 4);
+    const int acc = dtype == kF64 ? 8 : 4;
+    const int rc = launch_zero(grad_value, static_cast<int64_t>(g.B) * g.N * g.H * g.D * acc, stream);
+    if (rc != 0) return rc;
+    BackParams p{value, loc, attn, grad_out, grad_value, grad_loc, grad_attn, g, 1};
+    switch (dtype) {
+        case kF32: return sample_backward_t<float>(p, stream);
+        case kF16: return sample_backward_t<f16>(p, stream);
+        case kBF16: return sample_backward_t<bf16>(p, stream);
+        case kF64: return sample_backward_t<double>(p, stream);
+        default: return set_error(-2, "unknown dtype code %d", dtype);
+    }
+}
+
+int launch_convert(int dtype, const void* src_acc, void* dst, int64_t n, hipStream_t stream) {
+    if (n <= 0) return 0;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    const dim3 grid(static_cast<unsigned>(blocks));
+    switch (dtype) {
+        case kF32: hipLaunchKernelGGL((convert_kernel<float, float>), grid, dim3(256), 0, stream,
+                                      static_cast<const float*>(src_acc), static_cast<float*>(dst), n); break;
+        case kF16: hipLaunchKernelGGL((convert_kernel<f16, float>), grid, dim3(256), 0, stream,
+                                      static_cast<const float*>(src_acc), static_cast<f16*>(dst), n); break;
+        case kBF16: hipLaunchKernelGGL((convert_kernel<bf16, float>), grid, dim3(256), 0, stream,
+                                       static_cast<const float*>(src_acc), static_cast<bf16*>(dst), n); break;
+        case kF64: hipLaunchKernelGGL((convert_kernel<double, double>), grid, dim3(256), 0, stream,
+                                      static_cast<const double*>(src_acc), static_cast<double*>(dst), n); break;
+        default: return set_error(-2, "unknown dtype code %d", dtype);
+    }
+    return launched("convert");
+}
+
+int launch_transpose(int dtype, const void* src, void* dst, int64_t R, int64_t Cc, hipStream_t stream) {
+    if (R * Cc == 0) return 0;
+    const dim3 grid(static_cast<unsigned>((Cc + 31) / 32), static_cast<unsigned>((R + 31) / 32));
+    const int r = static_cast<int>(R), c = static_cast<int>(Cc);
+    switch (dtype) {
+        case kF32: hipLaunchKernelGGL(transpose_kernel<float>, grid, dim3(256), 0, stream,
+                                      static_cast<const float*>(src), static_cast<float*>(dst), r, c); break;
+        case kF16: hipLaunchKernelGGL(transpose_kernel<f16>, grid, dim3(256), 0, stream,
+                                      static_cast<const f16*>(src), static_cast<f16*>(dst), r, c); break;
+        case kBF16: hipLaunchKernelGGL(transpose_kernel<bf16>, grid, dim3(256), 0, stream,
+                                       static_cast<const bf16*>(src), static_cast<bf16*>(dst), r, c); break;
+        case kF64: hipLaunchKernelGGL(transpose_kernel<double>, grid, dim3(256), 0, stream,
+                                      static_cast<const double*>(src), static_cast<double*>(dst), r, c); break;
+        default: return set_error(-2, "unknown dtype code %d", dtype);
+    }
+    return launched("transpose");
+}
+
+// Split count and workspace of the weight gradient: about 512 workgroups, at least 256 tokens per split.
+void wgrad_plan(int64_t M, int64_t NO, int64_t K, int dtype, int* splits, int* chunk, int64_t* ws_bytes) {
+    const int64_t tiles = ((NO + 63) / 64) * ((K + 63) / 64);
+    int64_t s = (512 + tiles - 1) / tiles;
+    const int64_t max_s = (M + 255) / 256;
+    if (s > max_s) s = max_s;
+    if (s < 1) s = 1;
+    const int kb = dtype == kF32 ? 16 : 32;
+    int64_t c = (M + s - 1) / s;
+    c = (c + kb - 1) / kb * kb;
+    s = c > 0 ? (M + c - 1) / c : 1;
+    if (s < 1) s = 1;
+    *splits = static_cast<int>(s);
+    *chunk = static_cast<int>(c > 0 ? c : kb);
+    const int64_t elem = dtype == kF64 ? 8 : 4;
+    *ws_bytes = s * (NO * K + NO) * elem;
+}
+
+int launch_wgrad(int dtype, const void* G, const void* X, void* gw, void* gb, int64_t M, int64_t NO, int64_t K,
+                 void* workspace, int64_t ws_bytes, hipStream_t stream) {
+    int splits = 1, chunk = 32;
+    int64_t need = 0;
+    wgrad_plan(M, NO, K, dtype, &splits, &chunk, &need);
+    if (workspace == nullptr || ws_bytes < need)
+        return set_error(-4, "weight gradient: workspace of %lld bytes needed, %lld given", static_cast<long long>(need),
+                         static_cast<long long>(ws_bytes));
+    if (NO * K == 0) return 0;
+    WgradParams p{G, X, nullptr, nullptr, static_cast<int>(M), static_cast<int>(NO), static_cast<int>(K),
+                  static_cast<int>((NO + 63) / 64), static_cast<int>((K + 63) / 64), splits, chunk};
+    const int64_t n_out = NO * K;
+    const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(p.nt) * p.ct * splits));
+    const dim3 rgrid(static_cast<unsigned>((n_out + 255) / 256));
+    if (dtype == kF64) {
+        double* part = static_cast<double*>(workspace);
+        double* bpart = part + static_cast<int64_t>(splits) * n_out;
+        if (M == 0) {
+            const int rc = launch_zero(gw, n_out * 8, stream);
+            return rc != 0 || gb == nullptr ? rc : launch_zero(gb, NO * 8, stream);
+        }
+        hipLaunchKernelGGL(wgrad_generic_kernel<double>, grid, dim3(256), 0, stream, p, part, bpart);
+        int rc = launched("weight gradient");
+        if (rc != 0) return rc;
+        hipLaunchKernelGGL((wgrad_reduce_kernel<double, double>), rgrid, dim3(256), 0, stream, part, bpart, splits,
+                           p.NO, p.K, static_cast<double*>(gw), static_cast<double*>(gb));
+        return launched("weight gradient reduce");
+    }
+    p.part = static_cast<float*>(workspace);
+    p.bpart = p.part + static_cast<int64_t>(splits) * n_out;
+    const int es = dtype == kF32 ? 4 : 2;
+    if (M == 0) {
+        const int rc = launch_zero(gw, n_out * es, stream);
+        return rc != 0 || gb == nullptr ? rc : launch_zero(gb, NO * es, stream);
+    }
+    switch (dtype) {
+        case kF32: hipLaunchKernelGGL(wgrad_kernel<float>, grid, dim3(256), 0, stream, p); break;
+        case kF16: hipLaunchKernelGGL(wgrad_kernel<f16>, grid, dim3(256), 0, stream, p); break;
+        case kBF16: hipLaunchKernelGGL(wgrad_kernel<bf16>, grid, dim3(256), 0, stream, p); break;
+        default: return set_error(-2, "unknown dtype code %d", dtype);
+    }
+    int rc = launched("weight gradient");
+    if (rc != 0) return rc;
+    switch (dtype) {
+        case kF32: hipLaunchKernelGGL((wgrad_reduce_kernel<float, float>), rgrid, dim3(256), 0, stream, p.part,
+                                      p.bpart, splits, p.NO, p.K, static_cast<float*>(gw), static_cast<float*>(gb));
+            break;
+        case kF16: hipLaunchKernelGGL((wgrad_reduce_kernel<f16, float>), rgrid, dim3(256), 0, stream, p.part, p.bpart,
+                                      splits, p.NO, p.K, static_cast<f16*>(gw), static_cast<f16*>(gb));
+            break;
+        default: hipLaunchKernelGGL((wgrad_reduce_kernel<bf16, float>), rgrid, dim3(256), 0, stream, p.part,
+                                    p.bpart, splits, p.NO, p.K, static_cast<bf16*>(gw), static_cast<bf16*>(gb));
+            break;
+    }
+    return launched("weight gradient reduce");
+}
+
+}  // namespace td

@@ -58,4 +58,18 @@ int launch_proj_f32(int dtype, const void* a, const void* a2, const void* w, con
 
 int launch_zero(void* out, int64_t bytes, hipStream_t stream);
 
+// Backward (td_backward.hip). grad_value: [B, N, H*D] in the accumulation type, zeroed and accumulated here;
+// grad_loc / grad_attn in the element type (the accumulation type with g.loc_acc).
+int launch_sample_backward(int dtype, const void* value, const Geom& g, const void* loc, const void* attn,
+                           const void* grad_out, void* grad_value, void* grad_loc, void* grad_attn,
+                           hipStream_t stream);
+// dst[i] = src[i] rounded from the accumulation type to dtype
+int launch_convert(int dtype, const void* src_acc, void* dst, int64_t n, hipStream_t stream);
+// dst [Cc, R] = src [R, Cc]^T
+int launch_transpose(int dtype, const void* src, void* dst, int64_t R, int64_t Cc, hipStream_t stream);
+// weight / bias gradient split over tokens: partials in the workspace, summed in a fixed order
+void wgrad_plan(int64_t M, int64_t NO, int64_t K, int dtype, int* splits, int* chunk, int64_t* ws_bytes);
+int launch_wgrad(int dtype, const void* G, const void* X, void* gw, void* gb, int64_t M, int64_t NO, int64_t K,
+                 void* workspace, int64_t ws_bytes, hipStream_t stream);
+
 }  // namespace td

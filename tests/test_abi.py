@@ -32,10 +32,11 @@ def lib():
 
 
 def test_header_declares_the_entry_points():
-    assert header_functions() == ['td_fused_forward', 'td_fused_forward_masked', 'td_last_error',
+    assert header_functions() == ['td_fused_forward', 'td_fused_forward_masked', 'td_input_grad', 'td_last_error',
                                   'td_layer_fused_forward', 'td_layer_prologue', 'td_layer_sample_forward',
-                                  'td_sample_forward', 'td_sample_forward_masked', 'td_sample_forward_v2',
-                                  'td_value_proj', 'td_version']
+                                  'td_sample_backward', 'td_sample_forward', 'td_sample_forward_masked',
+                                  'td_sample_forward_v2', 'td_value_proj', 'td_version', 'td_weight_grad',
+                                  'td_weight_grad_workspace']
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -129,3 +130,43 @@ def test_empty_work_returns_ok_without_launching(lib):
     assert sample(lib, Q=0) == 0
     assert lib.td_value_proj(1, 16, 16, None, 16, 0, 4, 4, None) == 0
     assert lib.td_last_error().decode() == ''
+
+
+def sample_backward(lib, dtype=1, B=1, Q=4, N=100, H=8, D=32, L=3, P=4, ptr=16):
+    p = ptr
+    return lib.td_sample_backward(dtype, p, p, p, p, p, None, p, p, p, p, p, B, Q, N, H, D, L, P, None)
+
+
+def test_backward_entries_reject_on_host(lib):
+    E = header_defines()
+    assert sample_backward(lib, L=8, P=9) == E['TD_E_ARG']
+    assert 'levels x points' in lib.td_last_error().decode()
+    assert sample_backward(lib, ptr=None) == E['TD_E_ARG']
+    assert sample_backward(lib, D=300) == E['TD_E_ARG']
+    assert 'head dim' in lib.td_last_error().decode()
+    assert sample_backward(lib, dtype=5) == E['TD_E_DTYPE']
+    assert lib.td_input_grad(1, None, None, None, None, 4, 4, 4, None) == E['TD_E_ARG']
+    assert lib.td_input_grad(1, 16, 16, 16, 16, -1, 4, 4, None) == E['TD_E_ARG']
+    assert lib.td_input_grad(1, 16, 16, 16, 16, 0, 4, 4, None) == 0  # nothing to compute
+    # the weight gradient checks its workspace against td_weight_grad_workspace before launching anything
+    need = lib.td_weight_grad_workspace(1, 8400, 256, 256)
+    assert need > 0
+    assert lib.td_weight_grad(1, 16, 16, 16, 16, 8400, 256, 256, 16, need - 1, None) == E['TD_E_WORKSPACE']
+    assert 'workspace' in lib.td_last_error().decode()
+    assert lib.td_weight_grad(1, None, None, None, None, 8400, 256, 256, 16, need, None) == E['TD_E_ARG']
+    assert lib.td_weight_grad(1, 16, 16, 16, None, 8400, 0, 256, 16, need, None) == 0  # nothing to compute
+
+
+@pytest.mark.parametrize('dtype,M,NO,K', [(1, 8400, 256, 256), (2, 43520, 1024, 1024), (0, 100, 48, 40),
+                                          (3, 5, 16, 8), (1, 0, 64, 64)])
+def test_weight_grad_workspace_plan(lib, dtype, M, NO, K):
+    # split-K plan: about 512 workgroups of 64 x 64 outputs, splits of at least 256 tokens rounded up to the
+    # MFMA K (16 tokens for float32, 32 otherwise), float32 partials (float64 for float64) plus bias partials
+    tiles = -(-NO // 64) * -(-K // 64)
+    s = max(1, min(-(-512 // tiles), -(-M // 256)))
+    kb = 16 if dtype == 0 else 32
+    chunk = -(-M // s) if M else 0
+    chunk = -(-chunk // kb) * kb
+    s = -(-M // chunk) if chunk else 1
+    elem = 8 if dtype == 3 else 4
+    assert lib.td_weight_grad_workspace(dtype, M, NO, K) == s * (NO * K + NO) * elem

@@ -1,0 +1,179 @@
+"""The backward on the GPU: gradients of ma_deform_attn_train / ma_deform_sample_train (td_sample_backward,
+td_input_grad, td_weight_grad) against the float64 gradient oracle (oracle.gridsample.deform_attn_grads, pinned in
+tests/test_backward.py against finite differences of the brute force).
+
+Tolerance: the largest elementwise difference relative to the largest oracle entry of that gradient: float64
+1e-10, float32 2e-4, float16 1e-2, bfloat16 3e-2. The 16-bit inputs carry their own rounding into every gradient
+(the value gradient is accumulated in float32 and rounded once to the input type before the projection GEMMs, as
+the forward rounds the value), and the location gradient is a difference of corner products, so the 16-bit bars
+are looser than the forward's.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import marearts_tinydeform_amd as td
+from marearts_tinydeform_amd import _native
+from oracle import gridsample
+from inputs import CASES, RTDETR_LEVELS, make, to, workload
+
+pytestmark = pytest.mark.gpu
+
+REL = {torch.float64: 1e-10, torch.float32: 2e-4, torch.float16: 1e-2, torch.bfloat16: 3e-2}
+NAMES = ('memory', 'value_weight', 'value_bias', 'sampling_locations', 'attention_weights')
+POS = (0, 1, 2, 5, 6)
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def grad_out_for(args, seed=9):
+    B, Q, H = args[5].shape[:3]
+    HD = args[1].shape[0]
+    return torch.randn(B, Q, HD, generator=torch.Generator().manual_seed(seed))
+
+
+def gpu_grads(args, grad_out, dtype, mask=None):
+    dev = [None if t is None else t.cuda() for t in args]
+    leaves = [t.requires_grad_(True) if (i in POS and t is not None) else t for i, t in enumerate(dev)]
+    out = td.ma_deform_attn_train(*leaves, padding_mask=None if mask is None else mask.cuda())
+    out.backward(grad_out.to(dtype).cuda())
+    torch.cuda.synchronize()
+    return {n: None if leaves[p] is None else leaves[p].grad for n, p in zip(NAMES, POS)}, out
+
+
+def check(name, got, ref, dtype):
+    if ref is None:
+        assert got is None, name
+        return
+    got = got.double().cpu().numpy()
+    assert got.shape == ref.shape, f'{name}: {got.shape} != {ref.shape}'
+    scale = max(float(np.abs(ref).max()), 1e-6)
+    err = float(np.abs(got - ref).max()) / scale
+    assert err <= REL[dtype], f'{name}: max |diff| / max |ref| = {err:.3g} > {REL[dtype]}'
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16, torch.bfloat16, torch.float64])
+@pytest.mark.parametrize('case', CASES, ids=[c[0] for c in CASES])
+def test_gradients_match_oracle(case, dtype):
+    name, B, Q, H, D, C, levels, P = case
+    args = make(B, Q, H, D, C, levels, P, dtype=dtype)
+    go = grad_out_for(args)
+    say(f'  backward {name} {dtype}')
+    grads, _ = gpu_grads(args, go, dtype)
+    ref = gridsample.deform_attn_grads(*args, go.to(dtype))
+    for n in NAMES:
+        check(f'{name} {dtype} d{n}', grads[n], ref[n], dtype)
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16])
+def test_gradients_with_padding_mask_and_no_bias(dtype):
+    args = make(2, 50, 8, 32, 256, [(40, 40), (20, 20), (10, 10)], 4, dtype=dtype, bias=False)
+    N = args[0].shape[1]
+    mask = torch.rand(2, N, generator=torch.Generator().manual_seed(4)) < 0.3
+    go = grad_out_for(args)
+    grads, _ = gpu_grads(args, go, dtype, mask=mask)
+    ref = gridsample.deform_attn_grads(*args, go.to(dtype), padding_mask=mask)
+    for n in NAMES:
+        check(f'masked d{n}', grads[n], ref[n], dtype)
+    # a padded token's memory row gets no gradient
+    assert not grads['memory'][mask.cuda()].any()
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16])
+def test_sample_only_gradients(dtype):
+    # ma_deform_sample_train: the oracle with the identity projection is the sampling alone
+    name, B, Q, H, D, C, levels, P = CASES[2]
+    args = make(B, Q, H, D, C, levels, P, dtype=dtype)
+    value = torch.randn(B, args[0].shape[1], H * D, generator=torch.Generator().manual_seed(2)).to(dtype)
+    go = grad_out_for(args)
+    v = value.cuda().requires_grad_(True)
+    loc = args[5].cuda().requires_grad_(True)
+    attn = args[6].cuda().requires_grad_(True)
+    out = td.ma_deform_sample_train(v, args[3].cuda(), args[4].cuda(), loc, attn)
+    out.backward(go.to(dtype).cuda())
+    eye = torch.eye(H * D, dtype=dtype)
+    ref = gridsample.deform_attn_grads(value, eye, None, args[3], args[4], args[5], args[6], go.to(dtype))
+    check('dvalue', v.grad, ref['memory'], dtype)
+    check('dloc', loc.grad, ref['sampling_locations'], dtype)
+    check('dattn', attn.grad, ref['attention_weights'], dtype)
+
+
+@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16, torch.float32])
+def test_projection_gradients_alone(dtype):
+    # td_input_grad / td_weight_grad on shapes off the tile sizes, split-K included, against float64 matmuls
+    g = torch.Generator().manual_seed(8)
+    for (B, N, C, HD) in ((1, 8400, 256, 256), (2, 77, 40, 48), (1, 1000, 1024, 96), (3, 5, 8, 16)):
+        gv = torch.randn(B, N, HD, generator=g).to(dtype)
+        mem = torch.randn(B, N, C, generator=g).to(dtype)
+        w = (torch.randn(HD, C, generator=g) / C ** 0.5).to(dtype)
+        say(f'  projection grads {dtype} {(B, N, C, HD)}')
+        gm = _native.input_grad(gv.cuda(), w.cuda())
+        gw, gb = _native.weight_grad(gv.cuda(), mem.cuda())
+        torch.cuda.synchronize()
+        G, X = gv.double().reshape(-1, HD), mem.double().reshape(-1, C)
+        check('grad_memory', gm, (G @ w.double()).reshape(B, N, C).numpy(), dtype)
+        check('grad_weight', gw, (G.T @ X).numpy(), dtype)
+        check('grad_bias', gb, G.sum(0).numpy(), dtype)
+
+
+def test_weight_gradient_is_deterministic():
+    g = torch.Generator().manual_seed(1)
+    gv = torch.randn(1, 8400, 256, generator=g).half().cuda()
+    mem = torch.randn(1, 8400, 256, generator=g).half().cuda()
+    first = _native.weight_grad(gv, mem)
+    for _ in range(3):
+        again = _native.weight_grad(gv, mem)
+        assert torch.equal(first[0], again[0]) and torch.equal(first[1], again[1])
+
+
+def test_headline_shape_backward():
+    # RT-DETR 640, B=1, Q=300, float16 (the benchmark's inputs): every gradient against the oracle
+    args = workload(1, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.float16)
+    go = grad_out_for(args)
+    grads, out = gpu_grads(args, go, torch.float16)
+    ref = gridsample.deform_attn_grads(*args, go.half())
+    for n in NAMES:
+        check(f'headline d{n}', grads[n], ref[n], torch.float16)
+    # the forward of the training entry is the operator's project mode
+    with torch.inference_mode():
+        fwd = td.ma_deform_attn(*to(args, 'cuda'), mode='project')
+    assert torch.equal(out.detach(), fwd)
+
+
+def test_module_training_step_matches_cpu():
+    # MSDeformAttnLayer with grad: PyTorch prologue and output_proj, the library's operator; parameter gradients of
+    # one step against the same module on the CPU in float64 (the reference path under autograd)
+    torch.manual_seed(0)
+    m = td.MSDeformAttnLayer(d_model=64, n_levels=2, n_heads=4, n_points=2)
+    with torch.no_grad():  # non-trivial offsets and attention
+        m.sampling_offsets.weight.normal_(0, 0.05)
+        m.attention_weights.weight.normal_(0, 0.1)
+    levels = [(12, 10), (6, 5)]
+    shapes = torch.tensor(levels)
+    sizes = shapes[:, 0] * shapes[:, 1]
+    starts = torch.cat([sizes.new_zeros(1), sizes.cumsum(0)[:-1]])
+    g = torch.Generator().manual_seed(3)
+    hidden = torch.randn(2, 20, 64, generator=g)
+    memory = torch.randn(2, int(sizes.sum()), 64, generator=g)
+    ref_pts = torch.cat([torch.rand(2, 20, 1, 2, generator=g), torch.rand(2, 20, 1, 2, generator=g) * 0.3 + 0.05], -1)
+    pos = torch.randn(2, 20, 64, generator=g) * 0.1
+
+    def step(module, dev, dtype):
+        module = module.to(dev, dtype)
+        module.zero_grad()
+        out, attn = module(hidden.to(dev, dtype), encoder_hidden_states=memory.to(dev, dtype),
+                           position_embeddings=pos.to(dev, dtype), reference_points=ref_pts.to(dev, dtype),
+                           spatial_shapes=shapes.to(dev), level_start_index=starts.to(dev))
+        (out * out).sum().backward()
+        return {n: p.grad.detach().double().cpu() for n, p in module.named_parameters()}
+
+    import copy
+    gpu = step(copy.deepcopy(m), 'cuda', torch.float32)
+    cpu = step(copy.deepcopy(m), 'cpu', torch.float64)
+    for n in cpu:
+        scale = max(float(cpu[n].abs().max()), 1e-6)
+        err = float((gpu[n] - cpu[n]).abs().max()) / scale
+        assert err <= 5e-4, f'{n}: {err:.3g}'
