@@ -128,6 +128,43 @@ def layer_times(B, Q, H, D, C, levels, P, dtype, steps, warmup):
     return out
 
 
+def train_times(cpu_args, steps, warmup):
+    """µs per training step of the operator (forward + backward, gradients for memory, value_weight, value_bias,
+    the locations and the attention weights, for a fixed random grad_out): ma_deform_attn_train on the library's
+    kernels, and the PyTorch reference path (F.linear + grid_sample) under autograd on the same device."""
+    dev = [None if t is None else t.cuda() for t in cpu_args]
+    ref_args = list(dev)
+    ref_args[3], ref_args[4] = cpu_args[3], cpu_args[4]  # the reference reads the level shapes on the host
+    leaves = [t.requires_grad_(True) if (i in (0, 1, 2, 5, 6) and t is not None) else t for i, t in enumerate(dev)]
+    ref_leaves = [leaves[i] if i in (0, 1, 2, 5, 6) else t for i, t in enumerate(ref_args)]
+    B, Q = dev[5].shape[:2]
+    go = torch.randn(B, Q, dev[1].shape[0], generator=torch.Generator().manual_seed(1)).to(dev[0].dtype).cuda()
+
+    def ours():
+        torch.autograd.backward(td.ma_deform_attn_train(*leaves), go)
+
+    def pytorch():
+        torch.autograd.backward(td.ma_deform_attn_reference(*ref_leaves), go)
+
+    out = {}
+    for name, fn, n in (('train_step', ours, steps), ('pytorch_train_step', pytorch, min(steps, 100))):
+        try:
+            out[name] = graph_time_us(fn, n, min(warmup, 10))
+        except RuntimeError as e:  # capture refused: eager steps timed with events
+            log(f'  {name}: graph capture failed ({str(e).splitlines()[0][:80]}); timing eager steps')
+            torch.cuda.synchronize()
+            for _ in range(3):
+                fn()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(n):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            out[name] = a.elapsed_time(b) * 1e3 / n
+    return out
+
+
 def gemm_kernel(M, K, NO, s):
     """Which value-projection kernel td_value_proj launches for an aligned [M, K] x [K, NO] problem (element size
     s), following its size rule: 16-bit deep K (K >= 512, K % 64 == 0) on a grid of >= 256 tiles of 256 x 128
@@ -354,6 +391,11 @@ def main():
             log('  decoder layer (prologue + value_proj + MSDeformAttn + output_proj): ' +
                 ', '.join(f'{k[6:]} {v:.2f}' for k, v in lay.items()) + ' µs/call')
             kern.update(lay)
+            with torch.inference_mode(False), torch.enable_grad():
+                tr = train_times(cpu_args, min(args.steps, 200), args.warmup)
+            log(f'  training step (forward + backward): {tr["train_step"]:.2f} µs, PyTorch reference path '
+                f'{tr["pytorch_train_step"]:.2f} µs')
+            kern.update(tr)
 
     if pick == 'fused':
         dom, bytes_, t = 'fused', alg['fused_bytes'], times['fused']

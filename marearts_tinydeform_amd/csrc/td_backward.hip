@@ -93,8 +93,11 @@ struct BackParams {
     int LG;  // lanes per sample: a power of two, LG * CE >= D
 };
 
-// One wavefront per row (b, q, h); its LP samples go 64 / LG at a time, LG lanes per sample, each lane owning CE
-// consecutive channels of the head. grad_out's channels are read once per row.
+// One wavefront per row (b, q, h); its LP samples go 64 / LG at a time, LG lanes per sample, lane `sub` of a sample
+// owning channels sub, sub + LG, ... (CE of them). The channels are interleaved so that each value-gradient atomic
+// instruction adds, for each sample, LG consecutive floats of one token's row (one 128-byte line at D = 32): the L2
+// merges them, where a lane-contiguous split would spread one instruction over several lines per sample.
+// grad_out's channels are read once per row.
 template <typename T, int CE>
 __global__ __launch_bounds__(256) void sample_backward_kernel(BackParams p) {
     using A = typename AccOf<T>::type;
@@ -107,12 +110,11 @@ __global__ __launch_bounds__(256) void sample_backward_kernel(BackParams p) {
     const int D = g.D, HD = g.H * g.D, LP = g.LP;
     const int h = static_cast<int>(row % g.H);
     const int64_t bq = row / g.H, b = bq / g.Q;
-    const int c0 = sub * CE;
 
     const T* __restrict__ go = static_cast<const T*>(p.grad_out) + bq * HD + h * D;
     A gr[CE];
 #pragma unroll
-    for (int e = 0; e < CE; ++e) gr[e] = c0 + e < D ? cvt<A>(go[c0 + e]) : static_cast<A>(0);
+    for (int e = 0; e < CE; ++e) gr[e] = sub + e * LG < D ? cvt<A>(go[sub + e * LG]) : static_cast<A>(0);
 
     const T* __restrict__ vb = static_cast<const T*>(p.value) + b * g.N * HD + h * D;
     A* __restrict__ gv = static_cast<A*>(p.grad_value) + b * g.N * HD + h * D;
@@ -153,9 +155,10 @@ __global__ __launch_bounds__(256) void sample_backward_kernel(BackParams p) {
             A* gr_row = gv + static_cast<int64_t>(tk) * HD;
 #pragma unroll
             for (int e = 0; e < CE; ++e) {
-                if (c0 + e < D) {
-                    d[k] += cvt<A>(vr[c0 + e]) * gr[e];
-                    atomic_add(gr_row + c0 + e, aw * gr[e]);
+                const int c = sub + e * LG;
+                if (c < D) {
+                    d[k] += cvt<A>(vr[c]) * gr[e];
+                    atomic_add(gr_row + c, aw * gr[e]);
                 }
             }
         }
@@ -217,7 +220,7 @@ __global__ __launch_bounds__(256) void transpose_kernel(const T* __restrict__ sr
 }
 
 // Weight and bias gradients, split over the M tokens: workgroup (n tile, c tile, split s) accumulates
-//   part[s, n, c]  = sum over its tokens m of G[m, n] X[m, c]      (64 x 64 tile, MFMA, float32)
+//   part[s, n, c]  = sum over its tokens m of G[m, n] X[m, c]      (128 x 128 tile, MFMA, float32)
 //   bpart[s, n]    = sum over its tokens m of G[m, n]               (c tile 0 only)
 // G [M, NO] and X [M, K] are token-major, so each K-chunk of tokens is staged in LDS transposed ([n][m], [c][m]):
 // MFMA fragments then hold consecutive tokens. The partials are summed in a fixed order by wgrad_reduce_kernel, so
@@ -231,74 +234,135 @@ struct WgradParams {
     int nt, ct, splits, chunk;  // tile counts, splits, tokens per split (a multiple of the MFMA K)
 };
 
+// Workgroup tile 128 (n) x 128 (c): 2 x 2 wavefronts of 64 x 64 (4 x 4 MFMA tiles), 16 MFMAs per wavefront per
+// token step. Each thread stages two E-element pieces of each operand per step (KB tokens x 128 columns), from two
+// consecutive tokens at the same columns: with VEC (row lengths a multiple of E, 16-byte aligned rows) as 16-byte
+// loads. The pair is written transposed as E stores of two elements each ([column][token, token + 1]). The next
+// step's pieces are loaded into registers while this step's MFMAs run.
+constexpr int kWgTile = 128;
+
+// two consecutive elements, stored with one 4-byte (16-bit types) or 8-byte (float32) LDS write
 template <typename T>
+struct alignas(2 * sizeof(T)) Pair {
+    T v[2];
+};
+
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void wgrad_kernel(WgradParams p) {
     constexpr int E = 16 / static_cast<int>(sizeof(T));  // elements per 16 bytes
     constexpr int KB = KBlock<T>::kK;                     // tokens per MFMA step
     constexpr int LD = KB + E;                            // LDS pitch (elements) of a staged transposed row
-    __shared__ __align__(16) T gs[64 * LD];
-    __shared__ __align__(16) T xs[64 * LD];
+    constexpr int TL = kWgTile, PIECES = KB * (TL / E) / 256;
+    static_assert(PIECES == 2, "two pieces per thread");
+    __shared__ __align__(16) T gs[TL * LD];
+    __shared__ __align__(16) T xs[TL * LD];
     const int tiles = p.nt * p.ct;
     const int s = blockIdx.x / tiles, tile = blockIdx.x - s * tiles;
-    const int n0 = (tile / p.ct) * 64, c0 = (tile % p.ct) * 64;
+    const int n0 = (tile / p.ct) * TL, c0 = (tile % p.ct) * TL;
     const int m_begin = s * p.chunk, m_end = min(p.M, m_begin + p.chunk);
     const T* __restrict__ G = static_cast<const T*>(p.G);
     const T* __restrict__ X = static_cast<const T*>(p.X);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r16 = lane & 15, kg = lane >> 4;
-    f32x4 acc[4];
+    const int wm = wave >> 1, wn = wave & 1;
+    // this thread's pieces: token rows mm[0] = 2 rp and mm[1] = 2 rp + 1, columns cc[u] = cb .. cb + E - 1
+    const int rp = tid / (TL / E), cb = (tid % (TL / E)) * E;
+    const int mm[PIECES] = {2 * rp, 2 * rp + 1};
+    const int cc[PIECES] = {cb, cb};
+    f32x4 acc[4][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float bsum = 0.f;  // thread tid < 64: column n0 + tid of G (c tile 0)
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float bsum = 0.f;  // thread tid < 128: column n0 + tid of G (c tile 0)
     const bool do_b = c0 == 0;
 
-    for (int m0 = m_begin; m0 < m_end; m0 += KB) {
-        // stage: KB tokens x 64 columns of each operand, read as rows of E elements, written transposed
-        for (int i = tid; i < KB * (64 / E); i += 256) {
-            const int mm = i / (64 / E), cc = (i % (64 / E)) * E, m = m0 + mm;
+    T pg[PIECES][E], px[PIECES][E];
+    auto load = [&](int m0) {
 #pragma unroll
-            for (int e = 0; e < E; ++e) {
-                const int n = n0 + cc + e, c = c0 + cc + e;
-                gs[(cc + e) * LD + mm] = (m < m_end && n < p.NO) ? G[static_cast<int64_t>(m) * p.NO + n] : T(0);
-                xs[(cc + e) * LD + mm] = (m < m_end && c < p.K) ? X[static_cast<int64_t>(m) * p.K + c] : T(0);
+        for (int u = 0; u < PIECES; ++u) {
+            const int m = m0 + mm[u];
+            if constexpr (VEC) {
+                const u32x4 zero = {0u, 0u, 0u, 0u};
+                const u32x4 vg = (m < m_end && n0 + cc[u] < p.NO)
+                                     ? *reinterpret_cast<const u32x4*>(G + static_cast<int64_t>(m) * p.NO + n0 + cc[u])
+                                     : zero;
+                const u32x4 vx = (m < m_end && c0 + cc[u] < p.K)
+                                     ? *reinterpret_cast<const u32x4*>(X + static_cast<int64_t>(m) * p.K + c0 + cc[u])
+                                     : zero;
+                const T* eg = reinterpret_cast<const T*>(&vg);
+                const T* ex = reinterpret_cast<const T*>(&vx);
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    pg[u][e] = eg[e];
+                    px[u][e] = ex[e];
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const int n = n0 + cc[u] + e, c = c0 + cc[u] + e;
+                    pg[u][e] = (m < m_end && n < p.NO) ? G[static_cast<int64_t>(m) * p.NO + n] : T(0);
+                    px[u][e] = (m < m_end && c < p.K) ? X[static_cast<int64_t>(m) * p.K + c] : T(0);
+                }
             }
         }
-        __syncthreads();
-        if (do_b && tid < 64) {
-            for (int mm = 0; mm < KB; ++mm) bsum += static_cast<float>(gs[tid * LD + mm]);
-        }
-        const u32x4 fa = *reinterpret_cast<const u32x4*>(gs + (wave * 16 + r16) * LD + kg * E);
+    };
+    load(m_begin);
+    for (int m0 = m_begin; m0 < m_end; m0 += KB) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const u32x4 fb = *reinterpret_cast<const u32x4*>(xs + (t * 16 + r16) * LD + kg * E);
-            acc[t] = KBlock<T>::mma(fa, fb, acc[t]);
+        for (int e = 0; e < E; ++e) {
+            Pair<T> g2, x2;
+            g2.v[0] = pg[0][e];
+            g2.v[1] = pg[1][e];
+            x2.v[0] = px[0][e];
+            x2.v[1] = px[1][e];
+            *reinterpret_cast<Pair<T>*>(gs + (cb + e) * LD + 2 * rp) = g2;
+            *reinterpret_cast<Pair<T>*>(xs + (cb + e) * LD + 2 * rp) = x2;
         }
+        __syncthreads();
+        if (m0 + KB < m_end) load(m0 + KB);  // in flight during this step's MFMAs
+        if (do_b && tid < TL) {
+            for (int k = 0; k < KB; ++k) bsum += static_cast<float>(gs[tid * LD + k]);
+        }
+        u32x4 fa[4], fb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            fa[i] = *reinterpret_cast<const u32x4*>(gs + (wm * 64 + i * 16 + r16) * LD + kg * E);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            fb[t] = *reinterpret_cast<const u32x4*>(xs + (wn * 64 + t * 16 + r16) * LD + kg * E);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[i][t] = KBlock<T>::mma(fa[i], fb[t], acc[i][t]);
         __syncthreads();
     }
-    // acc[t][e]: row n0 + wave*16 + kg*4 + e, column c0 + t*16 + r16
+    // acc[i][t][e]: row n0 + wm*64 + i*16 + kg*4 + e, column c0 + wn*64 + t*16 + r16
     float* part = p.part + static_cast<int64_t>(s) * p.NO * p.K;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const int c = c0 + t * 16 + r16;
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int n = n0 + wave * 16 + kg * 4 + e;
-            if (n < p.NO && c < p.K) part[static_cast<int64_t>(n) * p.K + c] = acc[t][e];
+        for (int t = 0; t < 4; ++t) {
+            const int c = c0 + wn * 64 + t * 16 + r16;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int n = n0 + wm * 64 + i * 16 + kg * 4 + e;
+                if (n < p.NO && c < p.K) part[static_cast<int64_t>(n) * p.K + c] = acc[i][t][e];
+            }
         }
-    }
-    if (do_b && tid < 64 && n0 + tid < p.NO) p.bpart[static_cast<int64_t>(s) * p.NO + n0 + tid] = bsum;
+    if (do_b && tid < TL && n0 + tid < p.NO) p.bpart[static_cast<int64_t>(s) * p.NO + n0 + tid] = bsum;
 }
 
-// float64: the same sums on the vector ALUs, one thread per output of the 64 x 64 tile group
+// float64: the same sums on the vector ALUs, one thread per output of the tile
 template <typename T>
 __global__ __launch_bounds__(256) void wgrad_generic_kernel(WgradParams p, double* part, double* bpart) {
     const int tiles = p.nt * p.ct;
     const int s = blockIdx.x / tiles, tile = blockIdx.x - s * tiles;
-    const int n0 = (tile / p.ct) * 64, c0 = (tile % p.ct) * 64;
+    const int n0 = (tile / p.ct) * kWgTile, c0 = (tile % p.ct) * kWgTile;
     const int m_begin = s * p.chunk, m_end = min(p.M, m_begin + p.chunk);
     const T* __restrict__ G = static_cast<const T*>(p.G);
     const T* __restrict__ X = static_cast<const T*>(p.X);
-    for (int o = threadIdx.x; o < 64 * 64; o += 256) {
-        const int n = n0 + o / 64, c = c0 + o % 64;
+    for (int o = threadIdx.x; o < kWgTile * kWgTile; o += 256) {
+        const int n = n0 + o / kWgTile, c = c0 + o % kWgTile;
         if (n >= p.NO || c >= p.K) continue;
         double acc = 0, bs = 0;
         for (int m = m_begin; m < m_end; ++m) {
@@ -311,21 +375,44 @@ __global__ __launch_bounds__(256) void wgrad_generic_kernel(WgradParams p, doubl
     }
 }
 
+// grad_W[i] = sum over splits s of part[s, i], grad_b likewise: a workgroup takes 64 outputs, its four wavefronts
+// every fourth split each (reads of 64 consecutive outputs per split), and the four partial sums meet in LDS in a
+// fixed order, so the result does not depend on scheduling.
 template <typename T, typename P>
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const P* __restrict__ part, const P* __restrict__ bpart,
                                                            int splits, int NO, int K, T* __restrict__ gw,
                                                            T* __restrict__ gb) {
+    __shared__ P red[4][64];
     const int64_t n_out = static_cast<int64_t>(NO) * K;
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i < n_out) {
+    const int il = static_cast<int>(threadIdx.x) & 63, sg = static_cast<int>(threadIdx.x) >> 6;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 64 + il;
+    const bool bias_block = gb != nullptr && blockIdx.x * 64 < static_cast<unsigned>(NO);
+    for (int pass = 0; pass < (bias_block ? 2 : 1); ++pass) {
+        const P* src = pass == 0 ? part : bpart;
+        const int64_t n = pass == 0 ? n_out : NO;
         P acc = 0;
-        for (int s = 0; s < splits; ++s) acc += part[s * n_out + i];
-        gw[i] = static_cast<T>(acc);
-    }
-    if (gb != nullptr && i < NO) {
-        P acc = 0;
-        for (int s = 0; s < splits; ++s) acc += bpart[static_cast<int64_t>(s) * NO + i];
-        gb[i] = static_cast<T>(acc);
+        if (i < n) {
+            int s = sg;
+            for (; s + 12 < splits; s += 16) {
+                const P a0 = src[s * n + i], a1 = src[(s + 4) * n + i], a2 = src[(s + 8) * n + i],
+                        a3 = src[(s + 12) * n + i];
+                acc += a0;
+                acc += a1;
+                acc += a2;
+                acc += a3;
+            }
+            for (; s < splits; s += 4) acc += src[s * n + i];
+        }
+        red[sg][il] = acc;
+        __syncthreads();
+        if (sg == 0 && i < n) {
+            const P t = (red[0][il] + red[1][il]) + (red[2][il] + red[3][il]);
+            if (pass == 0)
+                gw[i] = static_cast<T>(t);
+            else
+                gb[i] = static_cast<T>(t);
+        }
+        __syncthreads();
     }
 }
 
@@ -334,10 +421,8 @@ int launched(const char* what) {
     return e == hipSuccess ? 0 : set_error(-3, "%s launch failed: %s", what, hipGetErrorString(e));
 }
 
-template <typename T>
-int sample_backward_t(const BackParams& p0, hipStream_t stream) {
-    BackParams p = p0;
-    constexpr int CE = 4;
+template <typename T, int CE>
+int sample_backward_go(BackParams p, hipStream_t stream) {
     int lg = 1;
     while (lg * CE < p.g.D && lg < kWave) lg <<= 1;
     p.LG = lg;
@@ -346,6 +431,14 @@ int sample_backward_t(const BackParams& p0, hipStream_t stream) {
     hipLaunchKernelGGL((sample_backward_kernel<T, CE>), dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0,
                        stream, p);
     return launched("sample backward");
+}
+
+// one channel per lane up to D = 64 (LG = D rounded up to a power of two), then D / 64 per lane
+template <typename T>
+int sample_backward_t(const BackParams& p, hipStream_t stream) {
+    if (p.g.D <= 64) return sample_backward_go<T, 1>(p, stream);
+    if (p.g.D <= 128) return sample_backward_go<T, 2>(p, stream);
+    return sample_backward_go<T, 4>(p, stream);
 }
 
 }  // namespace
@@ -406,7 +499,7 @@ int launch_transpose(int dtype, const void* src, void* dst, int64_t R, int64_t C
 
 // Split count and workspace of the weight gradient: about 512 workgroups, at least 256 tokens per split.
 void wgrad_plan(int64_t M, int64_t NO, int64_t K, int dtype, int* splits, int* chunk, int64_t* ws_bytes) {
-    const int64_t tiles = ((NO + 63) / 64) * ((K + 63) / 64);
+    const int64_t tiles = ((NO + kWgTile - 1) / kWgTile) * ((K + kWgTile - 1) / kWgTile);
     int64_t s = (512 + tiles - 1) / tiles;
     const int64_t max_s = (M + 255) / 256;
     if (s > max_s) s = max_s;
@@ -432,10 +525,11 @@ int launch_wgrad(int dtype, const void* G, const void* X, void* gw, void* gb, in
                          static_cast<long long>(ws_bytes));
     if (NO * K == 0) return 0;
     WgradParams p{G, X, nullptr, nullptr, static_cast<int>(M), static_cast<int>(NO), static_cast<int>(K),
-                  static_cast<int>((NO + 63) / 64), static_cast<int>((K + 63) / 64), splits, chunk};
+                  static_cast<int>((NO + kWgTile - 1) / kWgTile), static_cast<int>((K + kWgTile - 1) / kWgTile), splits,
+                  chunk};
     const int64_t n_out = NO * K;
     const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(p.nt) * p.ct * splits));
-    const dim3 rgrid(static_cast<unsigned>((n_out + 255) / 256));
+    const dim3 rgrid(static_cast<unsigned>((n_out + 63) / 64));
     if (dtype == kF64) {
         double* part = static_cast<double*>(workspace);
         double* bpart = part + static_cast<int64_t>(splits) * n_out;
@@ -457,10 +551,16 @@ int launch_wgrad(int dtype, const void* G, const void* X, void* gw, void* gb, in
         const int rc = launch_zero(gw, n_out * es, stream);
         return rc != 0 || gb == nullptr ? rc : launch_zero(gb, NO * es, stream);
     }
-    switch (dtype) {
-        case kF32: hipLaunchKernelGGL(wgrad_kernel<float>, grid, dim3(256), 0, stream, p); break;
-        case kF16: hipLaunchKernelGGL(wgrad_kernel<f16>, grid, dim3(256), 0, stream, p); break;
-        case kBF16: hipLaunchKernelGGL(wgrad_kernel<bf16>, grid, dim3(256), 0, stream, p); break;
+    const int E = dtype == kF32 ? 4 : 8;
+    const bool vec = NO % E == 0 && K % E == 0 &&
+                     ((reinterpret_cast<uintptr_t>(G) | reinterpret_cast<uintptr_t>(X)) % 16) == 0;
+    switch (dtype * 2 + (vec ? 1 : 0)) {
+        case kF32 * 2: hipLaunchKernelGGL((wgrad_kernel<float, false>), grid, dim3(256), 0, stream, p); break;
+        case kF32 * 2 + 1: hipLaunchKernelGGL((wgrad_kernel<float, true>), grid, dim3(256), 0, stream, p); break;
+        case kF16 * 2: hipLaunchKernelGGL((wgrad_kernel<f16, false>), grid, dim3(256), 0, stream, p); break;
+        case kF16 * 2 + 1: hipLaunchKernelGGL((wgrad_kernel<f16, true>), grid, dim3(256), 0, stream, p); break;
+        case kBF16 * 2: hipLaunchKernelGGL((wgrad_kernel<bf16, false>), grid, dim3(256), 0, stream, p); break;
+        case kBF16 * 2 + 1: hipLaunchKernelGGL((wgrad_kernel<bf16, true>), grid, dim3(256), 0, stream, p); break;
         default: return set_error(-2, "unknown dtype code %d", dtype);
     }
     int rc = launched("weight gradient");
