@@ -57,7 +57,11 @@ def load(path=LIB_PATH):
         load_error = f'cannot load {path}: {e}'
         return None
     for name, (res, args) in SIGNATURES.items():
-        fn = getattr(lib, name)
+        try:
+            fn = getattr(lib, name)
+        except AttributeError:
+            load_error = f'{path} has no {name}: it predates these sources (rebuild it)'
+            return None
         fn.restype = res
         fn.argtypes = args
     return lib
