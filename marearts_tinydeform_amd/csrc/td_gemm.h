@@ -62,4 +62,8 @@ struct KBlock<float> {
 // 16-byte aligned operands, variant 14..18.
 int launch_gemm_dma(int dtype, GemmParams p, hipStream_t stream, int variant);
 
+// The streaming kernel for narrow K (td_gemm_stream.hip): 16-bit, NO = 256, K = 128 or 256, 16-byte aligned a, w, c.
+bool gemm_stream_fits(int dtype, const GemmParams& p);
+int launch_gemm_stream(int dtype, GemmParams p, hipStream_t stream);
+
 }  // namespace td

@@ -408,10 +408,15 @@ int go_mfma(GemmParams p, hipStream_t stream) {
 //   12 256 x 128 A and W through LDS (2 x 2 waves of 128 x 64)
 //   13 128 x 128 A and W through LDS, K chunks of 32/16
 //   14..21 256 x 128 / 256 x 256 tiles fed by direct-to-LDS loads (td_gemm_dma.hip; 16-bit, K % 64 == 0)
+//   22 the streaming kernel: W resident in LDS, token rows streamed into MFMA fragments (td_gemm_stream.hip;
+//      16-bit, NO = 256, K = 128 or 256)
 template <typename T>
 int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
     if (variant <= 0) {
         // measured on MI355X (16-bit):
+        //   256 outputs, K = 128 or 256, from 60000 rows: the streaming kernel (22) (K = 256: M = 67200 21.4 µs
+        //     against 23.2 for 13, M = 88892 23.5 against 28.5, M = 177784 40.8 against 52.4; it loses below about
+        //     55000 rows, where its start, W into every CU's LDS, is not paid back);
         //   deep K (K >= 512, K % 64 == 0) on a grid of at least 256 tiles of 256 x 128: the direct-to-LDS kernel,
         //     256 x 256 tiles (16) from 2.5 rounds of them on 256 CUs, else 256 x 128 (14) (C = 1024: M = 43520
         //     101 µs against 122 µs for 13; M = 21760 57 against 68);
@@ -423,7 +428,9 @@ int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
         const int64_t tiles_128 = ((p.M + 127) / 128) * static_cast<int64_t>((p.NO + 127) / 128);
         const int64_t tiles_256x128 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 127) / 128);
         const int64_t tiles_256 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 255) / 256);
-        if (sizeof(T) == 2) {
+        if (sizeof(T) == 2 && p.M >= 60000 && gemm_stream_fits(std::is_same<T, bf16>::value ? kBF16 : kF16, p)) {
+            variant = 22;
+        } else if (sizeof(T) == 2) {
             if (p.K >= 512 && p.K % 64 == 0 && tiles_256x128 >= 256)
                 variant = tiles_256 >= 640 ? 16 : 14;
             else
@@ -449,6 +456,9 @@ int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
         case 14: case 15: case 16: case 17: case 18: case 19: case 20: case 21:
             return launch_gemm_dma(std::is_same<T, bf16>::value ? kBF16 : std::is_same<T, f16>::value ? kF16 : -1, p,
                                    stream, variant);
+        case 22:
+            return launch_gemm_stream(std::is_same<T, bf16>::value ? kBF16 : std::is_same<T, f16>::value ? kF16 : -1,
+                                      p, stream);
         default: return set_error(-1, "value_proj: unknown tile variant %d", variant);
     }
 }

@@ -1,0 +1,234 @@
+// Streaming value projection for narrow K: value[M, 256] = memory[M, K] . W[256, K]^T + bias, K = 128 or 256,
+// 16-bit operands (the C = 256 projections of RT-DETR, DINO and Deformable-DETR decoders).
+//
+// At K <= 256 the product is bound by HBM: each token row is read once (K * 2 bytes) and its value row written once
+// (512 bytes), 128 flops per byte, below MI355X's ridge. A tiled GEMM spends a tile's short life (K / 32 chunks)
+// on staging W and crossing barriers; this kernel instead keeps W resident and lets every wavefront stream:
+//   * one workgroup per CU (persistent grid), W (64 or 128 KB) and the bias staged into LDS once;
+//   * each wavefront owns a contiguous range of tokens (an equal share of M) and walks it in steps of 32 tokens,
+//     loading the token rows straight from HBM into MFMA fragments two steps ahead of the MFMAs (double buffer,
+//     no barrier inside the loop, no LDS traffic for the tokens);
+//   * the product is formed transposed, D = W . tokens^T on v_mfma_f32_16x16x32, so a lane's 4 accumulators are 4
+//     output channels of one token. The W rows of the 16 x 16 output tiles are permuted so that tiles 2p and 2p + 1
+//     give lane (r, kg) channels 32 p + 8 kg .. + 3 and + 4 .. + 7 of token r: 8 consecutive channels, one 16-byte
+//     store (row 4 a + b of tile 2p + h is channel 32 p + 8 a + 4 h + b).
+// LDS layout of W: [256 rows][K / 8 chunks of 16 bytes], chunk c of row n at slot c ^ key(n) with
+// key(n) = ((n >> 1) & 12) | (n & 3), which differs across the 16 rows of one fragment read (one chunk each), so they
+// fall in 16 distinct 16-byte bank groups.
+#include "td_gemm.h"
+
+namespace td {
+namespace {
+
+constexpr int kStreamNO = 256;   // output columns
+constexpr int kStreamWaves = 4;  // wavefronts per workgroup (one per SIMD)
+constexpr int kStreamTM = 2;     // 16-token halves per step
+
+template <typename T>
+struct Out8 {
+    T v[8];
+};
+
+// LDS slot key of W row n (see the layout above)
+__device__ __forceinline__ int wkey(int n) { return ((n >> 1) & 12) | (n & 3); }
+
+// 16 bytes per lane from global memory straight into LDS: lane i's bytes land at dst + 16 i (dst is the
+// wavefront's base, the same for every lane)
+__device__ __forceinline__ void load_lds16(const void* src, void* dst) {
+    __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+}
+
+template <typename T, int KB>
+__global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_stream_kernel(
+    GemmParams p) {
+    constexpr int NT = kStreamNO / 16;  // output tiles of 16 channels
+    constexpr int CH = KB * 4;          // 16-byte chunks per row (K / 8)
+    constexpr int TM = kStreamTM;
+    static_assert(CH % 16 == 0, "the swizzle needs K a multiple of 128");
+    extern __shared__ __align__(16) unsigned char smem[];
+    u32x4* ws = reinterpret_cast<u32x4*>(smem);        // [256][CH]
+    const T* bs = reinterpret_cast<const T*>(ws + kStreamNO * CH);  // [256] the bias in dtype
+
+    const T* __restrict__ A = static_cast<const T*>(p.a);
+    const T* __restrict__ W = static_cast<const T*>(p.w);
+    const T* __restrict__ bias = static_cast<const T*>(p.bias);
+    T* __restrict__ C = static_cast<T*>(p.c);
+    const int M = p.M, K = p.K;
+    const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+    const int r = lane & 15, kg = lane >> 4;
+
+    // this wavefront's tokens [lo, hi): an equal share of M; steps of 32 tokens from lo, the last one partial
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * kStreamWaves;
+    const int64_t gw = static_cast<int64_t>(blockIdx.x) * kStreamWaves + wave;
+    const int lo = static_cast<int>(gw * M / nw), hi = static_cast<int>((gw + 1) * M / nw);
+    const int last = hi > lo ? lo + (hi - lo - 1) / 32 * 32 : lo;  // first token of the last step
+    const int mmax = hi > lo ? hi - 1 : 0;                          // last row a load may touch
+
+    // token fragments of one step: lane (r, kg) holds token m0 + 16 s + r, k = 32 kb + 8 kg .. + 7. Rows past hi
+    // read row hi - 1 (never stored); a step past the last re-reads the last step (L2 hits), and a wavefront without
+    // tokens reads row 0, so every load is unconditional: the wait counts below and the compiler's stay exact.
+    auto load = [&](u32x4 (&tf)[TM][KB], int m0) {
+        m0 = m0 < last ? m0 : last;
+#pragma unroll
+        for (int s = 0; s < TM; ++s) {
+            int m = m0 + s * 16 + r;
+            m = m < mmax ? m : mmax;
+            const T* row = A + static_cast<size_t>(m) * K + kg * 8;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) tf[s][kb] = *reinterpret_cast<const u32x4*>(row + kb * 32);
+        }
+    };
+
+    // Order of this wavefront's memory operations: the bias (wavefront 0) and W into LDS by direct loads, then the
+    // first two steps' tokens. The workgroup then waits only for the direct loads (the older ones; the tokens stay
+    // in flight and the first MFMAs wait for them one register at a time). Nothing else writes LDS here: after a
+    // direct load the compiler orders any LDS store behind every outstanding load.
+    // W: a wavefront's direct load fills 64 consecutive slots, so the swizzle is applied on the source side: the
+    // lane that fills slot j of row n loads chunk j ^ key(n).
+    static_assert(kStreamNO * sizeof(T) == 32 * 16, "the bias is 32 lanes x 16 bytes");
+    if (bias != nullptr && wave == 0 && lane < 32) load_lds16(bias + lane * 8, const_cast<T*>(bs));
+    __builtin_amdgcn_sched_barrier(0);  // keep the issue order
+    constexpr int WCH = kStreamNO * CH;
+    static_assert(WCH % (kStreamWaves * kWave) == 0, "W staging tiles the workgroup");
+#pragma unroll
+    for (int u = 0; u < WCH / (kStreamWaves * kWave); ++u) {  // a constant trip count, fully unrolled
+        const int i0 = u * kStreamWaves * kWave + wave * kWave;
+        const int i = i0 + lane, n = i / CH, j = i - n * CH;
+        load_lds16(W + static_cast<size_t>(n) * K + (j ^ wkey(n)) * 8, ws + i0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 ta[TM][KB], tb[TM][KB];
+    load(ta, lo);
+    load(tb, lo + 32);
+    // W and the bias landed (at most the 2 TM KB token loads still in flight), then the workgroup meets; no fence,
+    // which would wait for the tokens too
+    constexpr int TOKEN_LOADS = 2 * TM * KB;
+    static_assert(TOKEN_LOADS <= 63, "wait count");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((TOKEN_LOADS & 15) | ((TOKEN_LOADS >> 4) << 14) | (7 << 4));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (hi <= lo) return;
+
+    auto mma = [&](const u32x4 (&tf)[TM][KB], f32x4 (&acc)[TM][NT]) {
+#pragma unroll
+        for (int s = 0; s < TM; ++s)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // W fragment j = (kb, t): lane r reads row n = 32 (t / 2) + 8 (r / 4) + 4 (t % 2) + r % 4, chunk 4 kb + kg.
+        // The fragments pass through a ring of DEPTH registers, each read DEPTH fragments ahead of its MFMAs; the
+        // scheduling groups keep one LDS read between every two MFMAs.
+        constexpr int J = KB * NT, DEPTH = 8;
+        const int rrow = 8 * (r >> 2) + (r & 3), rkey = wkey(rrow);  // wkey(n) is the same for every t
+        auto rd = [&](int j) {
+            const int kb = j / NT, t = j - kb * NT;
+            const int n = 32 * (t >> 1) + 4 * (t & 1) + rrow;
+            return ws[n * CH + ((kb * 4 + kg) ^ rkey)];
+        };
+        u32x4 ring[DEPTH];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < DEPTH; ++j) ring[j] = rd(j);
+        __builtin_amdgcn_sched_group_barrier(0x100, DEPTH, 0);  // the first DEPTH LDS reads
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int kb = j / NT, t = j - kb * NT;
+            const u32x4 wf = ring[j % DEPTH];
+            if (j + DEPTH < J) ring[j % DEPTH] = rd(j + DEPTH);
+#pragma unroll
+            for (int s = 0; s < TM; ++s) acc[s][t] = KBlock<T>::mma(wf, tf[s][kb], acc[s][t]);
+            __builtin_amdgcn_sched_group_barrier(0x008, TM, 0);                  // TM MFMAs
+            if (j + DEPTH < J) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // then one LDS read
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto store = [&](const f32x4 (&acc)[TM][NT], int m0) {
+        // lane (r, kg) holds channels 32 p + 8 kg .. + 7 of token m0 + 16 s + r in tiles 2p (first 4) and 2p + 1
+#pragma unroll
+        for (int s = 0; s < TM; ++s) {
+            const int m = m0 + s * 16 + r;
+            if (m >= hi) continue;
+            T* dst = C + static_cast<size_t>(m) * kStreamNO + 8 * kg;
+#pragma unroll
+            for (int pp = 0; pp < NT / 2; ++pp) {
+                Out8<T> bv = {};
+                if (bias != nullptr) bv = __builtin_bit_cast(Out8<T>, *reinterpret_cast<const u32x4*>(bs + 32 * pp + 8 * kg));
+                Out8<T> o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    o.v[e] = static_cast<T>(acc[s][2 * pp][e] + cvt<float>(bv.v[e]));
+                    o.v[4 + e] = static_cast<T>(acc[s][2 * pp + 1][e] + cvt<float>(bv.v[4 + e]));
+                }
+                *reinterpret_cast<u32x4*>(dst + 32 * pp) = __builtin_bit_cast(u32x4, o);
+            }
+        }
+    };
+
+    // the next-but-one step's tokens are requested as soon as the MFMAs have read this step's, before the stores
+    f32x4 acc[TM][NT];
+    for (int m0 = lo;;) {
+        mma(ta, acc);
+        load(ta, m0 + 64);
+        store(acc, m0);
+        m0 += 32;
+        if (m0 >= hi) break;
+        mma(tb, acc);
+        load(tb, m0 + 64);
+        store(acc, m0);
+        m0 += 32;
+        if (m0 >= hi) break;
+    }
+}
+
+// compute units of the current device, asked once per device
+int cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+template <typename T, int KB>
+int go_stream(GemmParams p, hipStream_t stream) {
+    constexpr size_t lds = static_cast<size_t>(kStreamNO) * KB * 4 * 16 + kStreamNO * sizeof(T);
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_stream_kernel<T, KB>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       static_cast<int>(lds));
+    if (attr != hipSuccess) return set_error(-3, "value_proj: LDS size attribute refused: %s", hipGetErrorString(attr));
+    // one workgroup per CU, but at least 64 tokens per wavefront (W is staged once per workgroup)
+    int64_t grid = (static_cast<int64_t>(p.M) + 64 * kStreamWaves - 1) / (64 * kStreamWaves);
+    const int cus = cu_count();
+    if (grid > cus) grid = cus;
+    if (grid < 1) grid = 1;
+    hipLaunchKernelGGL((gemm_stream_kernel<T, KB>), dim3(static_cast<unsigned>(grid)), dim3(kStreamWaves * kWave), lds,
+                       stream, p);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : set_error(-3, "value_proj launch failed: %s", hipGetErrorString(e));
+}
+
+template <typename T>
+int stream_t(GemmParams p, hipStream_t stream) {
+    if (p.K == 256) return go_stream<T, 8>(p, stream);
+    return go_stream<T, 4>(p, stream);
+}
+
+}  // namespace
+
+bool gemm_stream_fits(int dtype, const GemmParams& p) {
+    const uintptr_t al = reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.w) |
+                         reinterpret_cast<uintptr_t>(p.c);
+    return (dtype == kF16 || dtype == kBF16) && p.NO == kStreamNO && (p.K == 128 || p.K == 256) && p.M > 0 &&
+           al % 16 == 0;
+}
+
+int launch_gemm_stream(int dtype, GemmParams p, hipStream_t stream) {
+    if (!gemm_stream_fits(dtype, p)) return set_error(-1, "value_proj: the streaming kernel does not take this shape");
+    return dtype == kF16 ? stream_t<f16>(p, stream) : stream_t<bf16>(p, stream);
+}
+
+}  // namespace td

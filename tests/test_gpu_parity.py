@@ -209,6 +209,24 @@ def test_value_proj_deep_k_matches_oracle(dtype):
         assert_close(f'value_proj {dtype} {(M, K, NO)}', got[:, rows], ref, eps, eps)
 
 
+@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
+def test_value_proj_streaming_matches_oracle(dtype):
+    # 16-bit, 256 outputs, K = 128 or 256, from 60000 rows: the streaming kernel (W resident in LDS, each wavefront
+    # an equal share of the rows in steps of 32 with a partial last step). Every row is checked: the wavefront
+    # boundaries fall anywhere in M. Odd M, with and without bias.
+    g = torch.Generator().manual_seed(12)
+    for (M, K, bias) in ((60001, 256, True), (67200, 256, True), (70003, 128, False)):
+        say(f'  value_proj streaming {dtype} M={M} K={K} bias={bias}')
+        mem = torch.randn(1, M, K, generator=g).to(dtype)
+        w = (torch.randn(256, K, generator=g) / K ** 0.5).to(dtype)
+        b = (torch.randn(256, generator=g) * 0.1).to(dtype) if bias else None
+        with torch.inference_mode():
+            got = _native.value_proj(mem.cuda(), w.cuda(), None if b is None else b.cuda()).cpu()
+        ref = bruteforce.project(mem, w, b)
+        eps = {torch.float16: 2e-3, torch.bfloat16: 1e-2}[dtype]
+        assert_close(f'value_proj streaming {dtype} {(M, K)}', got, ref, eps, eps)
+
+
 def test_sample_alone_matches_oracle():
     for dtype in (torch.float16, torch.bfloat16, torch.float32):
         for name, B, Q, H, D, C, levels, P in CASES:
