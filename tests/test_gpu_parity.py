@@ -316,7 +316,7 @@ def test_dino_4level_fp16_b4_q900():
                     torch.float16)
 
 
-@pytest.mark.parametrize('Q', [50, 300])
+@pytest.mark.parametrize('Q', [50, 300, 900])
 def test_limit_case_bf16_c1024(Q):
     args = workload(2, Q, 16, 64, 1024, LIMIT_LEVELS, 16, torch.bfloat16, bias=False)
     rows = np.random.default_rng(Q).choice(2 * Q * 16, size=min(1024, 2 * Q * 16), replace=False)
