@@ -18,6 +18,12 @@ __global__ void zero_kernel(unsigned* p, int64_t words) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < words; i += stride) p[i] = 0u;
 }
+// 16 bytes per store
+__global__ void zero16_kernel(u32x4* p, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        p[i] = u32x4{0u, 0u, 0u, 0u};
+}
 __global__ void zero_bytes_kernel(unsigned char* p, int64_t bytes) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < bytes) p[i] = 0;
@@ -36,7 +42,13 @@ int set_error(int code, const char* fmt, ...) {
 
 int launch_zero(void* out, int64_t bytes, hipStream_t stream) {
     if (bytes <= 0) return 0;
-    if (reinterpret_cast<uintptr_t>(out) % 4 == 0 && bytes % 4 == 0) {
+    if (reinterpret_cast<uintptr_t>(out) % 16 == 0 && bytes % 16 == 0) {
+        const int64_t n = bytes / 16;
+        int64_t blocks = (n + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        hipLaunchKernelGGL(zero16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                           static_cast<u32x4*>(out), n);
+    } else if (reinterpret_cast<uintptr_t>(out) % 4 == 0 && bytes % 4 == 0) {
         const int64_t words = bytes / 4;
         int64_t blocks = (words + 255) / 256;
         if (blocks > 4096) blocks = 4096;

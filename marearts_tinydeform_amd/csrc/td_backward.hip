@@ -202,6 +202,27 @@ __global__ __launch_bounds__(256) void convert_kernel(const A* __restrict__ src,
         dst[i] = static_cast<T>(src[i]);
 }
 
+// float32 -> 16-bit, 8 elements per thread: two 16-byte loads, one 16-byte store (n8 groups of 8; 16-byte aligned)
+template <typename T>
+struct Pack8 {
+    T v[8];
+};
+template <typename T>
+__global__ __launch_bounds__(256) void convert8_kernel(const f32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                       int64_t n8) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n8; i += stride) {
+        const f32x4 a = src[2 * i], b = src[2 * i + 1];
+        Pack8<T> o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            o.v[e] = static_cast<T>(a[e]);
+            o.v[4 + e] = static_cast<T>(b[e]);
+        }
+        dst[i] = __builtin_bit_cast(u32x4, o);
+    }
+}
+
 // dst[c, r] = src[r, c] for a [R, Cc] matrix, through 32 x 32 LDS tiles.
 template <typename T>
 __global__ __launch_bounds__(256) void transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int R, int Cc) {
@@ -462,6 +483,20 @@ int launch_sample_backward(int dtype, const void* value, const Geom& g, const vo
 
 int launch_convert(int dtype, const void* src_acc, void* dst, int64_t n, hipStream_t stream) {
     if (n <= 0) return 0;
+    const bool vec = (dtype == kF16 || dtype == kBF16) && n % 8 == 0 &&
+                     (reinterpret_cast<uintptr_t>(src_acc) | reinterpret_cast<uintptr_t>(dst)) % 16 == 0;
+    if (vec) {
+        int64_t blocks = (n / 8 + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        const dim3 grid(static_cast<unsigned>(blocks));
+        if (dtype == kF16)
+            hipLaunchKernelGGL(convert8_kernel<f16>, grid, dim3(256), 0, stream, static_cast<const f32x4*>(src_acc),
+                               static_cast<u32x4*>(dst), n / 8);
+        else
+            hipLaunchKernelGGL(convert8_kernel<bf16>, grid, dim3(256), 0, stream, static_cast<const f32x4*>(src_acc),
+                               static_cast<u32x4*>(dst), n / 8);
+        return launched("convert");
+    }
     int64_t blocks = (n + 255) / 256;
     if (blocks > 8192) blocks = 8192;
     const dim3 grid(static_cast<unsigned>(blocks));
