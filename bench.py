@@ -45,6 +45,8 @@ WORKLOADS = {
     'limit-bf16-c1024-b2-q300': (2, 300, 16, 64, 1024, LIMIT_LEVELS, 16, torch.bfloat16, False, 'uniform'),
     'limit-bf16-c1024-b2-q900': (2, 900, 16, 64, 1024, LIMIT_LEVELS, 16, torch.bfloat16, False, 'uniform'),
     'rtdetr640-fp16-b1-q300-clustered': (1, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.float16, True, 'clustered'),
+    # encoder self-attention: every memory token is a query (Q = N = 22223)
+    'dino4l-encoder-fp16-b2': (2, 22223, 8, 32, 256, DINO_LEVELS, 4, torch.float16, True, 'encoder'),
 }
 
 DTYPE_NAMES = {torch.float16: 'f16', torch.bfloat16: 'bf16', torch.float32: 'f32', torch.float64: 'f64'}

@@ -50,7 +50,9 @@ def make(B, Q, H, D, C, levels, P, dtype=torch.float32, spread=1.0, bias=True, s
 
 def workload(B, Q, H, D, C, levels, P, dtype, bias=True, loc_dist='uniform', seed=0):
     """Benchmark inputs (CPU tensors): loc_dist 'uniform' = U[-0.05, 1.05]; 'outside10' = U[0, 1] with a
-    seeded 10% of samples moved to U[-0.5, 0) or (1, 1.5]; 'clustered' = per-query centre + 0.05 randn."""
+    seeded 10% of samples moved to U[-0.5, 0) or (1, 1.5]; 'clustered' = per-query centre + 0.05 randn;
+    'encoder' = encoder self-attention (Deformable-DETR / DINO): query q is memory token q % N and samples every
+    level around that token's normalized centre, 2 randn pixels of the level away."""
     g = torch.Generator().manual_seed(seed)
     shapes, starts, N = level_index(levels)
     L = len(levels)
@@ -68,11 +70,25 @@ def workload(B, Q, H, D, C, levels, P, dtype, bias=True, loc_dist='uniform', see
         loc = torch.where(moved, outside, loc)
     elif loc_dist == 'clustered':
         loc = torch.rand(B, Q, 1, 1, 1, 2, generator=g) + 0.05 * torch.randn(B, Q, H, L, P, 2, generator=g)
+    elif loc_dist == 'encoder':
+        ref = token_centres(levels)[torch.arange(Q) % N]                          # [Q, 2] (x, y)
+        pix = torch.tensor([[w, h] for h, w in levels], dtype=torch.float32)     # [L, 2] (width, height)
+        off = 2.0 * torch.randn(B, Q, H, L, P, 2, generator=g)
+        loc = ref[None, :, None, None, None, :] + off / pix[None, None, None, :, None, :]
     else:
         raise ValueError(loc_dist)
     attn = torch.randn(B, Q, H, L * P, generator=g).softmax(-1).view(B, Q, H, L, P)
     return [t if t is None or t.dtype == torch.long else t.to(dtype) for t in
             (memory, weight, b, shapes, starts, loc, attn)]
+
+
+def token_centres(levels):
+    """Normalized (x, y) centre of every memory token, level by level: [N, 2]."""
+    out = []
+    for h, w in levels:
+        y, x = torch.meshgrid((torch.arange(h) + 0.5) / h, (torch.arange(w) + 0.5) / w, indexing='ij')
+        out.append(torch.stack([x.flatten(), y.flatten()], -1))
+    return torch.cat(out)
 
 
 def to(args, device):

@@ -316,6 +316,14 @@ def test_dino_4level_fp16_b4_q900():
                     torch.float16)
 
 
+def test_dino_encoder_fp16_b2():
+    # encoder self-attention: every memory token is a query (Q = N = 22223), sampling around its own position;
+    # 2048 sampled rows against the oracle, fused and project compared over the whole output
+    args = workload(2, 22223, 8, 32, 256, DINO_LEVELS, 4, torch.float16, loc_dist='encoder')
+    rows = np.random.default_rng(7).choice(2 * 22223 * 8, size=2048, replace=False)
+    full_size_check('dino encoder fp16 B2 Q=N', args, torch.float16, rows=np.sort(rows))
+
+
 @pytest.mark.parametrize('Q', [50, 300, 900])
 def test_limit_case_bf16_c1024(Q):
     args = workload(2, Q, 16, 64, 1024, LIMIT_LEVELS, 16, torch.bfloat16, bias=False)
