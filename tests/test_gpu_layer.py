@@ -188,3 +188,25 @@ def test_layer_graph_capture_replays_match_eager():
             graph.replay()
             torch.cuda.synchronize()
             assert torch.equal(static_out, eager), f'replay {i}'
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16, torch.bfloat16])
+def test_encoder_layer_self_attention(dtype):
+    """The layer as a Deformable-DETR / DINO encoder calls it: the queries are the memory tokens (hidden states =
+    memory, Q = N), the reference points are every token's centre, repeated per level ([B, N, L, 2]), and each
+    query samples a few pixels around itself; all three modes against the oracle."""
+    from inputs import token_centres
+    levels = [(32, 48), (16, 24), (8, 12)]
+    a = make_layer(2, 1, 8, 32, 256, levels, 4, 2, 'L', dtype=torch.float32)
+    memory = a[1]
+    B, N = memory.shape[:2]
+    ref = token_centres(levels)[None, :, None, :].expand(B, N, len(levels), 2).contiguous()
+    a = [t.to(dtype) if isinstance(t, torch.Tensor) and t.is_floating_point() else t for t in a]
+    a[0], a[2] = memory.to(dtype), ref.to(dtype)  # hidden states = memory; token-centre reference points
+    a[15] = (torch.randn(B, N, memory.shape[2], generator=torch.Generator().manual_seed(4)) * 0.5).to(dtype)
+    ref_out, ref_attn = olayer.layer(*a[:15], position_embeddings=a[15])
+    dev = to(a[:13], 'cuda') + a[13:15] + to(a[15:], 'cuda')
+    for mode in ('fused', 'project', 'auto'):
+        say(f'  encoder layer {dtype} [{mode}] N={N}')
+        out, attn = run_layer(dev, mode)
+        check(f'encoder layer {dtype} [{mode}]', out, ref_out, dtype)
