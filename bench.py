@@ -233,6 +233,22 @@ def measured_traffic(workload_name, kernel):
         return None
 
 
+def head_major(dtype, D):
+    """Whether td_project_forward projects into the head-major layout (a head row of 64 bytes or less, a multiple
+    of 16), so that the kernel legs time the halves the project path runs."""
+    row = D * torch.empty((), dtype=dtype).element_size()
+    return dtype != torch.float64 and row <= 64 and row % 16 == 0
+
+
+def project_halves(dev, H, D, dtype):
+    """(projection, sampling) callables of the project path: the sampling one takes the projection's output."""
+    if head_major(dtype, D):
+        return (lambda: _native.value_proj_heads(dev[0], dev[1], dev[2], H),
+                lambda v: _native.sample_forward_heads(v, *dev[3:]))
+    return (lambda: _native.value_proj(dev[0], dev[1], dev[2]),
+            lambda v: _native.sample_forward(v, H, *dev[3:]))
+
+
 def pmc_run(dev, H, steps):
     src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device='cuda')
     dst = torch.empty_like(src)
@@ -244,11 +260,12 @@ def pmc_run(dev, H, steps):
         for _ in range(steps):
             td.ma_deform_attn(*dev, mode='fused')
         torch.cuda.synchronize()
+        proj, smp = project_halves(dev, H, dev[1].size(0) // H, dev[0].dtype)
         for _ in range(steps):
-            value = _native.value_proj(dev[0], dev[1], dev[2])
+            value = proj()
         torch.cuda.synchronize()
         for _ in range(steps):
-            _native.sample_forward(value, H, *dev[3:])
+            smp(value)
         torch.cuda.synchronize()
     log(f'pmc run done: copy of {COPY_BYTES} bytes, {steps} calls of fused / value_proj / sample')
 
@@ -379,11 +396,11 @@ def main():
         log(f'  auto     {times["auto"]:9.2f} µs/call (picks {pick})')
         kern = {}
         if not args.modes_only:
-            value = _native.value_proj(dev[0], dev[1], dev[2])
-            kern['value_proj'] = graph_time_us(lambda: _native.value_proj(dev[0], dev[1], dev[2]), args.steps,
-                                               args.warmup)
-            kern['sample'] = graph_time_us(lambda: _native.sample_forward(value, H, *dev[3:]), args.steps,
-                                           args.warmup)
+            # the two halves td_project_forward runs (head-major value when a head row is 64 bytes or less)
+            proj, smp = project_halves(dev, H, D, dtype)
+            value = proj()
+            kern['value_proj'] = graph_time_us(proj, args.steps, args.warmup)
+            kern['sample'] = graph_time_us(lambda: smp(value), args.steps, args.warmup)
             kern['fused'] = times['fused']
             log(f'  kernels: value_proj {kern["value_proj"]:.2f} µs, sample {kern["sample"]:.2f} µs')
             # the standard PyTorch path (F.linear + per-level grid_sample) on the same device, same graph timing;

@@ -98,6 +98,36 @@ int td_sample_forward_masked(int dtype, const void* value, const int64_t* spatia
                              int64_t Q, int64_t N, int64_t H, int64_t D, int64_t L, int64_t P, void* stream);
 
 /*
+ * The two halves of td_project_forward with the head-major value layout, for callers that keep the projected values
+ * between calls. td_value_proj_heads: value [B, H, N, D] = memory [B, N, C] @ value_weight[H * D, C]^T + bias, float32
+ * accumulation, one rounding; D * element size must be a multiple of 16 bytes. td_sample_forward_heads: sampling of
+ * such a value into out [B, Q, H, D], arguments as td_project_forward. No counterpart in the reference, whose value
+ * is always [B, N, H * D] (marearts_tinydeform/__init__.py:77): with D = 32 16-bit elements a head row is 64 bytes, and
+ * head-major places the two corners of a bilinear pair (x0, x0 + 1) in one 128-byte run.
+ */
+int td_value_proj_heads(int dtype, const void* memory, const void* value_weight, const void* value_bias, void* value,
+                        int64_t B, int64_t N, int64_t C, int64_t H, int64_t D, void* stream);
+int td_sample_forward_heads(int dtype, const void* value, const int64_t* spatial_shapes,
+                            const int64_t* level_start_index, const void* sampling_locations,
+                            const void* attention_weights, const uint8_t* padding_mask, int loc_acc, void* out,
+                            int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D, int64_t L, int64_t P, void* stream);
+
+/*
+ * Project mode in one call: value_ws = memory @ value_weight^T + value_bias on the library's GEMM, then sampling of
+ * value_ws into out [B, Q, H, D]. value_ws is caller-provided device memory of B * N * H * D elements of dtype that
+ * holds the projected values afterwards in a layout the library picks (head-major [B, H, N, D] when a head row is 64
+ * bytes or less, else [B, N, H * D]), so callers treat it as scratch. loc_acc = 1: sampling_locations and
+ * attention_weights are float32 (float64 for TD_F64), as td_layer_prologue writes them; 0: dtype. padding_mask as in
+ * td_sample_forward_masked. Replaces the reference's F.linear + _C.sample_forward pair of mode='project'
+ * (marearts_tinydeform/__init__.py:77-80, csrc/ma_deform_fused.cu:327-350).
+ */
+int td_project_forward(int dtype, const void* memory, const void* value_weight, const void* value_bias,
+                       const int64_t* spatial_shapes, const int64_t* level_start_index,
+                       const void* sampling_locations, const void* attention_weights, const uint8_t* padding_mask,
+                       int loc_acc, void* value_ws, void* out, int64_t B, int64_t Q, int64_t N, int64_t C, int64_t H,
+                       int64_t D, int64_t L, int64_t P, void* stream);
+
+/*
  * Sampling with per-level point counts and a choice of sampling method (the deformable attention core of D-FINE:
  * transformers models/d_fine/modeling_d_fine.py:150-216, multi_scale_deformable_attention_v2). Level l has
  * points_per_level[l] samples (a host array of L entries, sum <= 64), so sampling_locations is

@@ -123,13 +123,9 @@ def ma_deform_attn(memory, value_weight, value_bias, spatial_shapes, level_start
 
 def _project(memory, value_weight, value_bias, spatial_shapes, level_start_index, sampling_locations,
              attention_weights, padding_mask):
-    H = sampling_locations.shape[2] if sampling_locations.dim() == 6 else 0
-    _native.check_geometry(memory, spatial_shapes, level_start_index, sampling_locations, attention_weights)
-    _native.check_padding_mask(memory, padding_mask)
-    value = _native.value_proj(memory, value_weight, value_bias)
     # padded tokens: the sampler drops their corners, the same as zeroing their value rows
-    return _native.sample_forward(value, H, spatial_shapes, level_start_index, sampling_locations, attention_weights,
-                                  padding_mask)
+    return _native.project_forward(memory, value_weight, value_bias, spatial_shapes, level_start_index,
+                                   sampling_locations, attention_weights, padding_mask)
 
 
 def ma_deform_sample(value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
@@ -220,8 +216,8 @@ def _layer(hidden_states, memory, reference_points, spatial_shapes, level_start_
         _native.check_padding_mask(memory, padding_mask)
         loc, attn = _native.layer_prologue(hidden_states, position, reference_points, ow, ob, aw, ab, spatial_shapes,
                                            H, P)
-        value = _native.value_proj(memory, value_weight, value_bias)
-        core = _native.layer_sample_forward(value, H, spatial_shapes, level_start_index, loc, attn, padding_mask)
+        core = _native.project_forward(memory, value_weight, value_bias, spatial_shapes, level_start_index, loc, attn,
+                                       padding_mask, loc_acc=True)
     out = core if output_weight is None else _native.value_proj(core, output_weight, output_bias)
     if want_attn:
         return out, attn.to(memory.dtype)

@@ -31,6 +31,9 @@ SIGNATURES = {
     'td_sample_forward_masked': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 7 + [_vp]),
     'td_sample_forward_v2': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 6 + [_vp, _int, _vp]),
     'td_value_proj': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    'td_project_forward': (_int, [_int] + [_vp] * 8 + [_int, _vp, _vp] + [_i64] * 8 + [_vp]),
+    'td_value_proj_heads': (_int, [_int, _vp, _vp, _vp, _vp] + [_i64] * 5 + [_vp]),
+    'td_sample_forward_heads': (_int, [_int] + [_vp] * 6 + [_int, _vp] + [_i64] * 7 + [_vp]),
     'td_layer_prologue': (_int, [_int, _vp, _vp, _vp, _i64, _i64] + [_vp] * 7 + [_i64] * 6 + [_vp]),
     'td_layer_fused_forward': (_int, [_int, _vp, _vp, _vp, _i64, _i64] + [_vp] * 13 + [_i64] * 9 + [_vp]),
     'td_layer_sample_forward': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 7 + [_vp]),
@@ -286,6 +289,101 @@ def value_proj(memory, weight, bias):
     _check(lib_.td_value_proj(DTYPE_CODES[memory.dtype], mem.data_ptr(), w.data_ptr(), _ptr(b), value.data_ptr(),
                               B * N, C, HD, _stream(dev)))
     return value
+
+
+def _check_locations(ref, spatial_shapes, level_start_index, loc, attn, loc_acc):
+    """Geometry checks for the project-mode entries; returns B, Q, H, L, P. loc_acc=False: loc / attn in ref's dtype,
+    checked as the reference does (csrc/ma_deform_fused.cu:236-266); True: in float32 (float64 for float64), as
+    layer_prologue writes them."""
+    if not loc_acc:
+        return check_geometry(ref, spatial_shapes, level_start_index, loc, attn)
+    if not ref.is_cuda:
+        raise RuntimeError('inputs must be GPU tensors')
+    if loc.dim() != 6 or loc.size(5) != 2 or attn.shape != loc.shape[:5]:
+        raise RuntimeError('sampling_locations must be [B, Q, H, L, P, 2]')
+    B, Q, H, L, P = loc.shape[:5]
+    acc = acc_dtype(ref.dtype)
+    if loc.dtype != acc or attn.dtype != acc:
+        raise RuntimeError(f'locations and weights must be {acc} for {ref.dtype} values')
+    if ref.size(0) != B:
+        raise RuntimeError('batch size mismatch')
+    if spatial_shapes.dtype != torch.int64 or spatial_shapes.shape != (L, 2):
+        raise RuntimeError('spatial_shapes must be int64 [L, 2]')
+    if level_start_index.dtype != torch.int64 or level_start_index.shape != (L,):
+        raise RuntimeError('level_start_index must be int64 [L]')
+    for t in (loc, attn, spatial_shapes, level_start_index):
+        if t.device != ref.device:
+            raise RuntimeError('all tensors must be on the same device')
+    if ref.dtype not in DTYPE_CODES:
+        raise RuntimeError(f'unsupported dtype {ref.dtype}')
+    return B, Q, H, L, P
+
+
+def project_forward(memory, weight, bias, spatial_shapes, level_start_index, loc, attn, padding_mask=None,
+                    loc_acc=False):
+    """Project mode in one call (td_project_forward): value projection into a scratch buffer, then sampling.
+    loc_acc as in _check_locations."""
+    lib_ = _require()
+    if memory.dim() != 3:
+        raise RuntimeError('memory / value must be [B, N, C]')
+    B, Q, H, L, P = _check_locations(memory, spatial_shapes, level_start_index, loc, attn, loc_acc)
+    HD = check_projection(memory, weight, bias, H)
+    mask = check_padding_mask(memory, padding_mask)
+    N, C = memory.size(1), memory.size(2)
+    dev = memory.device
+    mem, w, b, lc, aw, sh, st = _contig(memory, weight, bias, loc, attn, spatial_shapes, level_start_index)
+    out = torch.empty((B, Q, HD), dtype=memory.dtype, device=dev)
+    if out.numel() == 0:
+        return out
+    ws = torch.empty((B * N * HD,), dtype=memory.dtype, device=dev)
+    _check(lib_.td_project_forward(DTYPE_CODES[memory.dtype], mem.data_ptr(), w.data_ptr(), _ptr(b), sh.data_ptr(),
+                                   st.data_ptr(), lc.data_ptr(), aw.data_ptr(), _ptr(mask), 1 if loc_acc else 0,
+                                   ws.data_ptr(), out.data_ptr(), B, Q, N, C, H, HD // H, L, P, _stream(dev)))
+    return out
+
+
+def value_proj_heads(memory, weight, bias, heads):
+    """Head-major value projection (td_value_proj_heads): [B, N, C] -> [B, H, N, D]."""
+    lib_ = _require()
+    if not memory.is_cuda:
+        raise RuntimeError('inputs must be GPU tensors')
+    if memory.dim() != 3:
+        raise RuntimeError('memory / value must be [B, N, C]')
+    if memory.dtype not in DTYPE_CODES:
+        raise RuntimeError(f'unsupported dtype {memory.dtype}')
+    HD = check_projection(memory, weight, bias, heads)
+    B, N, C = memory.shape
+    D = HD // heads
+    if D * memory.element_size() % 16 != 0:
+        raise RuntimeError('head-major values need a head row of a multiple of 16 bytes')
+    mem, w, b = _contig(memory, weight, bias)
+    value = torch.empty((B, heads, N, D), dtype=memory.dtype, device=memory.device)
+    if value.numel() == 0:
+        return value
+    _check(lib_.td_value_proj_heads(DTYPE_CODES[memory.dtype], mem.data_ptr(), w.data_ptr(), _ptr(b),
+                                    value.data_ptr(), B, N, C, heads, D, _stream(memory.device)))
+    return value
+
+
+def sample_forward_heads(value, spatial_shapes, level_start_index, loc, attn, padding_mask=None, loc_acc=False):
+    """Sampling of a head-major value [B, H, N, D] (td_sample_forward_heads) -> [B, Q, H * D]."""
+    lib_ = _require()
+    if value.dim() != 4:
+        raise RuntimeError('value must be [B, H, N, D]')
+    B_, H_, N, D = value.shape
+    flat = value.view(B_, N, H_ * D) if value.is_contiguous() else value.reshape(B_, N, H_ * D)
+    B, Q, H, L, P = _check_locations(flat, spatial_shapes, level_start_index, loc, attn, loc_acc)
+    if H != H_:
+        raise RuntimeError('value must be [B, H, N, D] with H = sampling_locations.size(2)')
+    mask = check_padding_mask(flat, padding_mask)
+    v, lc, aw, sh, st = _contig(value, loc, attn, spatial_shapes, level_start_index)
+    out = torch.empty((B, Q, H * D), dtype=value.dtype, device=value.device)
+    if out.numel() == 0:
+        return out
+    _check(lib_.td_sample_forward_heads(DTYPE_CODES[value.dtype], v.data_ptr(), sh.data_ptr(), st.data_ptr(),
+                                        lc.data_ptr(), aw.data_ptr(), _ptr(mask), 1 if loc_acc else 0,
+                                        out.data_ptr(), B, Q, N, H, D, L, P, _stream(value.device)))
+    return out
 
 
 def sample_backward(value, heads, spatial_shapes, level_start_index, sampling_locations, attention_weights, grad_out,

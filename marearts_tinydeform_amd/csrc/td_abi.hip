@@ -292,6 +292,97 @@ extern "C" int td_layer_sample_forward(int dtype, const void* value, const int64
     return launch_sample(dtype, value, g, loc, attn, out, s, tune);
 }
 
+namespace {
+// Head-major value when a head row is 64 bytes or less: the sampler's bilinear pairs (x0, x0 + 1) are then one
+// contiguous run instead of two rows H * D apart
+bool head_major_pays(int dtype, int64_t D) {
+    const int64_t row_bytes = D * elem_size(dtype);
+    return dtype != TD_F64 && row_bytes <= 64 && row_bytes % 16 == 0;
+}
+
+int check_proj_sizes(int dtype, int64_t M, int64_t K, int64_t NO) {
+    if (!dtype_ok(dtype)) return set_error(TD_E_DTYPE, "unknown dtype code %d", dtype);
+    if (M < 0 || K < 0 || NO < 0) return set_error(TD_E_ARG, "sizes must be non-negative");
+    if (M > kInt32Max || K > kInt32Max || NO > kInt32Max) return set_error(TD_E_ARG, "GEMM size exceeds int32");
+    return TD_OK;
+}
+
+int sample_heads(int dtype, const void* value, const int64_t* spatial_shapes, const int64_t* level_start_index,
+                 const void* loc, const void* attn, const uint8_t* padding_mask, int loc_acc, void* out, int64_t B,
+                 int64_t Q, int64_t N, int64_t H, int64_t D, int64_t L, int64_t P, hipStream_t s) {
+    Geom g{spatial_shapes, level_start_index, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N),
+           static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), static_cast<int>(P), padding_mask};
+    set_levels(g, nullptr);
+    g.loc_acc = loc_acc;
+    g.value_hm = 1;
+    SampleTune tune;
+    return launch_sample(dtype, value, g, loc, attn, out, s, tune);
+}
+}  // namespace
+
+extern "C" int td_value_proj_heads(int dtype, const void* memory, const void* weight, const void* bias, void* value,
+                                   int64_t B, int64_t N, int64_t C, int64_t H, int64_t D, void* stream) {
+    g_last_error.clear();
+    if (!dtype_ok(dtype)) return set_error(TD_E_DTYPE, "unknown dtype code %d", dtype);
+    if (B < 0 || N < 0 || C < 0 || H <= 0 || D <= 0) return set_error(TD_E_ARG, "need B, N, C >= 0 and H, D >= 1");
+    const int rc = check_proj_sizes(dtype, B * N, C, H * D);
+    if (rc != TD_OK) return rc;
+    if ((D * elem_size(dtype)) % 16 != 0) return set_error(TD_E_ARG, "head row must be a multiple of 16 bytes");
+    if (B * N == 0) return TD_OK;
+    if (value == nullptr || (C > 0 && (memory == nullptr || weight == nullptr)))
+        return set_error(TD_E_ARG, "null pointer argument");
+    return launch_value_proj(dtype, memory, weight, bias, value, B * N, C, H * D, static_cast<hipStream_t>(stream), 0,
+                             static_cast<int>(N), static_cast<int>(H));
+}
+
+extern "C" int td_sample_forward_heads(int dtype, const void* value, const int64_t* spatial_shapes,
+                                       const int64_t* level_start_index, const void* sampling_locations,
+                                       const void* attention_weights, const uint8_t* padding_mask, int loc_acc,
+                                       void* out, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D, int64_t L,
+                                       int64_t P, void* stream) {
+    int rc = check_geometry(dtype, B, Q, N, H, D, L, P, spatial_shapes, level_start_index, sampling_locations,
+                            attention_weights, out);
+    if (rc != TD_OK) return rc;
+    if (loc_acc != 0 && loc_acc != 1) return set_error(TD_E_ARG, "loc_acc must be 0 or 1");
+    if (B * N * H * D > 0 && value == nullptr) return set_error(TD_E_ARG, "null pointer argument");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (B * Q * H * D == 0) return TD_OK;
+    if (N == 0 || L * P == 0) return launch_zero(out, B * Q * H * D * elem_size(dtype), s);
+    return sample_heads(dtype, value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+                        padding_mask, loc_acc, out, B, Q, N, H, D, L, P, s);
+}
+
+extern "C" int td_project_forward(int dtype, const void* memory, const void* value_weight, const void* value_bias,
+                                  const int64_t* spatial_shapes, const int64_t* level_start_index,
+                                  const void* sampling_locations, const void* attention_weights,
+                                  const uint8_t* padding_mask, int loc_acc, void* value_ws, void* out, int64_t B,
+                                  int64_t Q, int64_t N, int64_t C, int64_t H, int64_t D, int64_t L, int64_t P,
+                                  void* stream) {
+    int rc = check_geometry(dtype, B, Q, N, H, D, L, P, spatial_shapes, level_start_index, sampling_locations,
+                            attention_weights, out);
+    if (rc != TD_OK) return rc;
+    if (loc_acc != 0 && loc_acc != 1) return set_error(TD_E_ARG, "loc_acc must be 0 or 1");
+    if (C < 0 || C > kInt32Max || B * N > kInt32Max) return set_error(TD_E_ARG, "GEMM size exceeds int32");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (B * Q * H * D == 0) return TD_OK;
+    if (N == 0 || L * P == 0) return launch_zero(out, B * Q * H * D * elem_size(dtype), s);
+    if (value_ws == nullptr || (C > 0 && (memory == nullptr || value_weight == nullptr)))
+        return set_error(TD_E_ARG, "null pointer argument");
+    const bool hm = head_major_pays(dtype, D);
+    rc = launch_value_proj(dtype, memory, value_weight, value_bias, value_ws, B * N, C, H * D, s, 0,
+                           hm ? static_cast<int>(N) : 0, hm ? static_cast<int>(H) : 0);
+    if (rc != TD_OK) return rc;
+    if (hm)
+        return sample_heads(dtype, value_ws, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+                            padding_mask, loc_acc, out, B, Q, N, H, D, L, P, s);
+    Geom g{spatial_shapes, level_start_index, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N),
+           static_cast<int>(H), static_cast<int>(D), static_cast<int>(L), static_cast<int>(P), padding_mask};
+    set_levels(g, nullptr);
+    g.loc_acc = loc_acc;
+    SampleTune tune;
+    return launch_sample(dtype, value_ws, g, sampling_locations, attention_weights, out, s, tune);
+}
+
 extern "C" int td_fused_forward(int dtype, const void* memory, const void* value_weight, const void* value_bias,
                                 const int64_t* spatial_shapes, const int64_t* level_start_index,
                                 const void* sampling_locations, const void* attention_weights, void* out, int64_t B,

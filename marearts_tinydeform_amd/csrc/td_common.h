@@ -46,6 +46,7 @@ struct Geom {
     int discrete = 0;               // 1: nearest-pixel sampling (D-FINE's "discrete" method) instead of bilinear
     int loc_acc = 0;                // 1: locations and weights are in the accumulation type (float; double for
                                     // float64) instead of the element type (computed by the query prologue)
+    int value_hm = 0;               // sampling: 1 when value is head-major [B, H, N, D] instead of [B, N, H * D]
     uint8_t level_end[kMaxLevelPoints] = {};  // per-level point counts (P == 0): first sample after level l
 
     // true when the general corner rule is needed (padding mask, per-level point counts, discrete sampling or

@@ -6,6 +6,25 @@
 
 namespace td {
 
+// n / d for 0 <= n < 2^31 and 1 <= d < 2^31 by a multiply-high, an add and a shift (Granlund and Montgomery,
+// "Division by invariant integers using multiplication", PLDI 1994, the round-up form): with l = ceil(log2 d) and
+// mul = floor(2^32 (2^l - d) / d) + 1, n / d = (mulhi(n, mul) + n) >> l; mul < 2^32, and the sum stays below 2^32
+// because mulhi(n, mul) < n < 2^31.
+struct FastDiv {
+    uint32_t mul = 1, shift = 0;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t l = 0;
+    while ((uint64_t{1} << l) < d) ++l;
+    FastDiv f;
+    f.mul = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1);
+    f.shift = l;
+    return f;
+}
+__device__ __forceinline__ uint32_t fast_div(const FastDiv& f, uint32_t n) {
+    return (__umulhi(n, f.mul) + n) >> f.shift;
+}
+
 struct GemmParams {
     const void* a;
     const void* w;
@@ -15,7 +34,25 @@ struct GemmParams {
     int mt, nt;  // tile counts
     int per_xcd;
     const void* a2 = nullptr;  // second A operand of the two-operand form (C = A . W^T + A2 . W^T + bias)
+    // head-major output (hm_D > 0): row m = b * hm_N + t and column n = h * hm_D + d go to
+    // C[((b * H + h) * hm_N + t) * hm_D + d] with H = NO / hm_D, i.e. C is [B, H, N, D]; hm_D is a multiple of the
+    // 16-byte vector
+    int hm_N = 0, hm_D = 0;
+    FastDiv hm_ndiv, hm_ddiv;  // division by hm_N and hm_D
 };
+
+// Element offset of output (m, n) = out_row(m) + out_col(n): row-major [M, NO], or head-major (GemmParams::hm_D)
+__device__ __forceinline__ size_t out_row(const GemmParams& p, int m) {
+    if (p.hm_D == 0) return static_cast<size_t>(m) * p.NO;
+    const int b = static_cast<int>(fast_div(p.hm_ndiv, static_cast<uint32_t>(m))), t = m - b * p.hm_N;
+    return static_cast<size_t>(b) * p.hm_N * p.NO + static_cast<size_t>(t) * p.hm_D;
+}
+__device__ __forceinline__ size_t out_col(const GemmParams& p, int n) {
+    if (p.hm_D == 0) return static_cast<size_t>(n);
+    const int h = static_cast<int>(fast_div(p.hm_ddiv, static_cast<uint32_t>(n))), d = n - h * p.hm_D;
+    return static_cast<size_t>(h) * p.hm_N * p.hm_D + d;
+}
+__device__ __forceinline__ size_t out_index(const GemmParams& p, int m, int n) { return out_row(p, m) + out_col(p, n); }
 
 // Linear tile index for this workgroup; -1 when the workgroup has no tile. Workgroups are dealt to the 8 XCDs
 // round-robin, so consecutive tiles (the N tiles of one M tile) land on one XCD and share its L2.
@@ -62,7 +99,8 @@ struct KBlock<float> {
 // 16-byte aligned operands, variant 14..18.
 int launch_gemm_dma(int dtype, GemmParams p, hipStream_t stream, int variant);
 
-// The streaming kernel for narrow K (td_gemm_stream.hip): 16-bit, NO = 256, K = 128 or 256, 16-byte aligned a, w, c.
+// The streaming kernel for narrow K (td_gemm_stream.hip): 16-bit, NO = 256, K = 128 or 256, 16-byte aligned a, w, c;
+// a head-major output needs hm_D a multiple of 8.
 bool gemm_stream_fits(int dtype, const GemmParams& p);
 int launch_gemm_stream(int dtype, GemmParams p, hipStream_t stream);
 

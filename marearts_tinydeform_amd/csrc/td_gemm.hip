@@ -169,7 +169,7 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_mfma_kernel(GemmParams p) 
         const int m = m0 + row, n = n0 + col;
         if (m >= M || n >= NO) continue;
         const O* src = Ct + row * LDC + col;
-        O* dst = Cm + static_cast<size_t>(m) * NO + n;
+        O* dst = Cm + out_index(p, m, n);
         if (vec_ok && n + EO <= NO) {
             *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
         } else {
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_lds_kernel(GemmParams p) {
         const int m = m0 + row, n = n0 + col;
         if (m >= M || n >= NO) continue;
         const T* src = Ct + row * LDC + col;
-        T* dst = Cm + static_cast<size_t>(m) * NO + n;
+        T* dst = Cm + out_index(p, m, n);
         if (vec_ok && n + E <= NO) {
             *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
         } else {
@@ -364,7 +364,7 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmParams p) {
         const A bv = bias != nullptr ? cvt<A>(bias[n]) : static_cast<A>(0);
         for (int i = 0; i < 4; ++i) {
             const int m = m0 + ty + 16 * i;
-            if (m < M) Cm[static_cast<size_t>(m) * NO + n] = static_cast<T>(acc[i][j] + bv);
+            if (m < M) Cm[out_index(p, m, n)] = static_cast<T>(acc[i][j] + bv);
         }
     }
 }
@@ -499,8 +499,14 @@ int launch_proj_f32(int dtype, const void* a, const void* a2, const void* w, con
 }
 
 int launch_value_proj(int dtype, const void* a, const void* w, const void* bias, void* c, int64_t M, int64_t K,
-                      int64_t NO, hipStream_t stream, int variant) {
+                      int64_t NO, hipStream_t stream, int variant, int hm_N, int hm_H) {
     GemmParams p{a, w, bias, c, static_cast<int>(M), static_cast<int>(K), static_cast<int>(NO), 0, 0, 0};
+    if (hm_N > 0) {
+        p.hm_N = hm_N;
+        p.hm_D = static_cast<int>(NO) / hm_H;
+        p.hm_ndiv = make_fastdiv(static_cast<uint32_t>(hm_N));
+        p.hm_ddiv = make_fastdiv(static_cast<uint32_t>(p.hm_D));
+    }
     switch (dtype) {
         case kF32: return launch_t<float>(p, stream, variant);
         case kF16: return launch_t<f16>(p, stream, variant);

@@ -206,7 +206,7 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(TN == 
         const int m = m0 + row, n = n0 + col;
         if (m >= M || n >= NO) continue;
         const T* src = Ct + row * LDC + col;
-        T* dst = Cm + static_cast<size_t>(m) * NO + n;
+        T* dst = Cm + out_index(p, m, n);
         if (vec_ok && n + E <= NO) {
             *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
         } else {

@@ -148,7 +148,7 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
         for (int s = 0; s < TM; ++s) {
             const int m = m0 + s * 16 + r;
             if (m >= hi) continue;
-            T* dst = C + static_cast<size_t>(m) * kStreamNO + 8 * kg;
+            T* const row = C + out_row(p, m);
 #pragma unroll
             for (int pp = 0; pp < NT / 2; ++pp) {
                 Out8<T> bv = {};
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
                     o.v[e] = static_cast<T>(acc[s][2 * pp][e] + cvt<float>(bv.v[e]));
                     o.v[4 + e] = static_cast<T>(acc[s][2 * pp + 1][e] + cvt<float>(bv.v[4 + e]));
                 }
-                *reinterpret_cast<u32x4*>(dst + 32 * pp) = __builtin_bit_cast(u32x4, o);
+                *reinterpret_cast<u32x4*>(row + out_col(p, 32 * pp + 8 * kg)) = __builtin_bit_cast(u32x4, o);
             }
         }
     };
@@ -223,7 +223,7 @@ bool gemm_stream_fits(int dtype, const GemmParams& p) {
     const uintptr_t al = reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.w) |
                          reinterpret_cast<uintptr_t>(p.c);
     return (dtype == kF16 || dtype == kBF16) && p.NO == kStreamNO && (p.K == 128 || p.K == 256) && p.M > 0 &&
-           al % 16 == 0;
+           al % 16 == 0 && p.hm_D % 8 == 0;
 }
 
 int launch_gemm_stream(int dtype, GemmParams p, hipStream_t stream) {

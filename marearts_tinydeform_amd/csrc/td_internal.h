@@ -47,8 +47,10 @@ int launch_sample(int dtype, const void* value, const Geom& g, const void* loc, 
                   hipStream_t stream, const SampleTune& tune);
 
 // variant: 0 picks the tile shape by size, > 0 forces an MFMA tile variant, -1 forces the generic kernel.
+// hm_N > 0: c is head-major [M / hm_N, hm_H, hm_N, NO / hm_H] instead of [M, NO] (rows are b * hm_N + t); the head
+// width NO / hm_H must be a multiple of 16 bytes.
 int launch_value_proj(int dtype, const void* a, const void* w, const void* bias, void* c, int64_t M, int64_t K,
-                      int64_t NO, hipStream_t stream, int variant);
+                      int64_t NO, hipStream_t stream, int variant, int hm_N = 0, int hm_H = 0);
 
 // Projection in float32 for the layer prologue: c[M, NO] = a[M, K] . w[NO, K]^T (+ a2[M, K] . w^T) + bias, float32
 // accumulation, stored unrounded; a2 may be null. 16/32-bit operands with K a multiple of 16 bytes and 16-byte

@@ -62,12 +62,16 @@ __global__ __launch_bounds__(WAVES* kWave) void sample_kernel(SampleParams p) {
         const bool valid = row < p.rows;
         const int64_t b = valid ? row / QH : 0;
         const int h = valid ? static_cast<int>(row % g.H) : 0;
-        const T* base = value + static_cast<size_t>(b) * g.N * HD + static_cast<size_t>(h) * D + ch * V;
+        // token-major value [B, N, H*D]: head rows HD apart; head-major [B, H, N, D]: D apart, so a bilinear pair
+        // (x0, x0 + 1) is one contiguous 2 D-element run
+        const T* base = g.value_hm ? value + (static_cast<size_t>(b) * g.H + h) * g.N * D + ch * V
+                                   : value + static_cast<size_t>(b) * g.N * HD + static_cast<size_t>(h) * D + ch * V;
+        const size_t stride = g.value_hm ? static_cast<size_t>(D) : static_cast<size_t>(HD);
         float acc[V];
 #pragma unroll
         for (int i = 0; i < V; ++i) acc[i] = 0.f;
         float ws = 0.f;
-        gather_sum<T, V, NB>(cw + r * S, S, sg, SG, base, static_cast<size_t>(HD), acc, ws);
+        gather_sum<T, V, NB>(cw + r * S, S, sg, SG, base, stride, acc, ws);
         for (int m = DV; m < GS; m <<= 1) {
 #pragma unroll
             for (int i = 0; i < V; ++i) acc[i] += xor_lane(acc[i], m);
@@ -108,11 +112,13 @@ __global__ __launch_bounds__(WAVES* kWave) void sample_f64_kernel(SampleParams p
         if (row >= p.rows) continue;
         const int64_t b = row / QH;
         const int h = static_cast<int>(row % g.H);
-        const double* base = value + static_cast<size_t>(b) * g.N * HD + static_cast<size_t>(h) * D + d;
+        const double* base = g.value_hm ? value + (static_cast<size_t>(b) * g.H + h) * g.N * D + d
+                                        : value + static_cast<size_t>(b) * g.N * HD + static_cast<size_t>(h) * D + d;
+        const size_t stride = g.value_hm ? static_cast<size_t>(D) : static_cast<size_t>(HD);
         double acc = 0.0;
         for (int s = 0; s < S; ++s) {
             const Corner<double> c = cw[r * S + s];
-            const double v = base[static_cast<size_t>(c.tok < 0 ? 0 : c.tok) * HD];
+            const double v = base[static_cast<size_t>(c.tok < 0 ? 0 : c.tok) * stride];
             acc = fma(c.w, c.tok < 0 ? 0.0 : v, acc);
         }
         out[static_cast<size_t>(row) * D + d] = acc;

@@ -34,8 +34,9 @@ def lib():
 def test_header_declares_the_entry_points():
     assert header_functions() == ['td_fused_forward', 'td_fused_forward_masked', 'td_input_grad', 'td_last_error',
                                   'td_layer_fused_forward', 'td_layer_prologue', 'td_layer_sample_forward',
-                                  'td_sample_backward', 'td_sample_forward', 'td_sample_forward_masked',
-                                  'td_sample_forward_v2', 'td_value_proj', 'td_version', 'td_weight_grad',
+                                  'td_project_forward', 'td_sample_backward', 'td_sample_forward',
+                                  'td_sample_forward_heads', 'td_sample_forward_masked', 'td_sample_forward_v2',
+                                  'td_value_proj', 'td_value_proj_heads', 'td_version', 'td_weight_grad',
                                   'td_weight_grad_workspace']
 
 
@@ -106,6 +107,41 @@ def test_masked_entries_reject_on_host(lib):
         header_defines()['TD_E_ARG']
     assert 'levels x points' in lib.td_last_error().decode()
     assert lib.td_sample_forward_masked(1, p, p, p, p, p, None, p, 1, 0, 100, 8, 32, 3, 4, None) == 0
+
+
+def project(lib, dtype=1, B=1, Q=4, N=100, C=256, H=8, D=32, L=3, P=4, loc_acc=0, ws=16, ptr=16):
+    p = ptr
+    return lib.td_project_forward(dtype, p, p, None, p, p, p, p, None, loc_acc, ws, p, B, Q, N, C, H, D, L, P, None)
+
+
+def test_project_rejects_on_host(lib):
+    E = header_defines()
+    assert project(lib, L=8, P=9) == E['TD_E_ARG']
+    assert 'levels x points' in lib.td_last_error().decode()
+    assert project(lib, loc_acc=2) == E['TD_E_ARG']
+    assert 'loc_acc' in lib.td_last_error().decode()
+    assert project(lib, ws=None) == E['TD_E_ARG']
+    assert 'null pointer' in lib.td_last_error().decode()
+    assert project(lib, dtype=4) == E['TD_E_DTYPE']
+    assert project(lib, Q=0) == 0  # nothing to compute
+    assert project(lib, Q=0, ws=None) == 0
+
+
+def test_head_major_entries_reject_on_host(lib):
+    E = header_defines()
+    p = 16
+    # D = 4 float16 elements is an 8-byte head row: head-major needs a multiple of 16 bytes
+    assert lib.td_value_proj_heads(1, p, p, None, p, 1, 100, 256, 64, 4, None) == E['TD_E_ARG']
+    assert '16 bytes' in lib.td_last_error().decode()
+    assert lib.td_value_proj_heads(1, p, p, None, p, 1, 100, 256, 0, 32, None) == E['TD_E_ARG']
+    assert lib.td_value_proj_heads(1, None, None, None, None, 1, 100, 256, 8, 32, None) == E['TD_E_ARG']
+    assert lib.td_value_proj_heads(6, p, p, None, p, 1, 100, 256, 8, 32, None) == E['TD_E_DTYPE']
+    assert lib.td_value_proj_heads(1, p, p, None, p, 0, 100, 256, 8, 32, None) == 0  # nothing to compute
+    assert lib.td_sample_forward_heads(1, p, p, p, p, p, None, 0, p, 1, 4, 100, 8, 32, 8, 9, None) == E['TD_E_ARG']
+    assert 'levels x points' in lib.td_last_error().decode()
+    assert lib.td_sample_forward_heads(1, p, p, p, p, p, None, 3, p, 1, 4, 100, 8, 32, 3, 4, None) == E['TD_E_ARG']
+    assert lib.td_sample_forward_heads(1, None, p, p, p, p, None, 0, p, 1, 4, 100, 8, 32, 3, 4, None) == E['TD_E_ARG']
+    assert lib.td_sample_forward_heads(1, p, p, p, p, p, None, 0, p, 1, 0, 100, 8, 32, 3, 4, None) == 0
 
 
 def test_sample_v2_rejects_on_host(lib):

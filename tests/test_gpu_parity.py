@@ -227,6 +227,55 @@ def test_value_proj_streaming_matches_oracle(dtype):
         assert_close(f'value_proj streaming {dtype} {(M, K)}', got, ref, eps, eps)
 
 
+def heads_of(value, H):
+    """[B, N, H * D] -> head-major [B, H, N, D] (torch tensor or numpy array)."""
+    B, N, HD = value.shape
+    if isinstance(value, np.ndarray):
+        return np.ascontiguousarray(value.reshape(B, N, H, HD // H).transpose(0, 2, 1, 3))
+    return value.reshape(B, N, H, HD // H).permute(0, 2, 1, 3).contiguous()
+
+
+def test_value_proj_heads_matches_oracle():
+    # the head-major GEMM output: row b * N + t, column h * D + d lands at [b, h, t, d]. Shapes reach every tile
+    # family: 64 x 64 one-chunk (1 x 8400), LDS 128 x 128 (4 x 9000, 2 x 8192 x 1024 outputs), direct-to-LDS
+    # (K = 576), the streaming kernel (16-bit, 256 outputs, K = 256 or 128, from 60000 rows), ragged B, N and heads
+    # of 16 bytes. Every row is checked.
+    g = torch.Generator().manual_seed(21)
+    shapes = {torch.float16: ((1, 8400, 256, 8, 32), (4, 9000, 256, 8, 32), (2, 8192, 128, 32, 32),
+                              (3, 77, 40, 6, 8), (2, 2501, 576, 17, 8), (2, 30001, 256, 8, 32),
+                              (3, 20011, 128, 16, 16)),
+              torch.bfloat16: ((1, 8400, 256, 8, 32), (2, 30001, 256, 8, 32), (5, 131, 96, 3, 24)),
+              torch.float32: ((1, 8400, 256, 8, 16), (2, 77, 40, 5, 4), (3, 1000, 64, 2, 12)),
+              torch.float64: ((2, 77, 40, 4, 2), (1, 300, 256, 8, 8))}
+    for dtype, cases in shapes.items():
+        for (B, N, C, H, D) in cases:
+            say(f'  value_proj_heads {dtype} B={B} N={N} C={C} H={H} D={D}')
+            mem = torch.randn(B, N, C, generator=g).to(dtype)
+            w = (torch.randn(H * D, C, generator=g) / C ** 0.5).to(dtype)
+            b = (torch.randn(H * D, generator=g) * 0.1).to(dtype)
+            with torch.inference_mode():
+                got = _native.value_proj_heads(mem.cuda(), w.cuda(), b.cuda(), H).cpu()
+            assert got.shape == (B, H, N, D)
+            ref = heads_of(bruteforce.project(mem, w, b), H)
+            eps = {torch.float16: 2e-3, torch.bfloat16: 1e-2, torch.float32: 1e-5, torch.float64: 1e-12}[dtype]
+            assert_close(f'value_proj_heads {dtype} {(B, N, C, H, D)}', got, ref, eps, eps)
+
+
+def test_sample_heads_matches_oracle():
+    # the sampler on a head-major value: same results as on [B, N, H * D] (every case, every dtype; any D)
+    for dtype in (torch.float16, torch.bfloat16, torch.float32, torch.float64):
+        for name, B, Q, H, D, C, levels, P in CASES:
+            args = make(B, Q, H, D, C, levels, P, dtype=dtype)
+            g = torch.Generator().manual_seed(6)
+            value = torch.randn(B, args[0].shape[1], H * D, generator=g).to(dtype)
+            ref = bruteforce.sample(value, H, *args[3:])
+            with torch.inference_mode():
+                got = _native.sample_forward_heads(heads_of(value, H).cuda(), *to(args[3:], 'cuda'))
+            torch.cuda.synchronize()
+            atol, rtol = TOL[dtype]
+            assert_close(f'sample_heads {name} {dtype}', got, ref, atol, rtol)
+
+
 def test_sample_alone_matches_oracle():
     for dtype in (torch.float16, torch.bfloat16, torch.float32):
         for name, B, Q, H, D, C, levels, P in CASES:
