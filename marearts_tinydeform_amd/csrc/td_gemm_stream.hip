@@ -89,10 +89,14 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
     if (bias != nullptr && wave == 0 && lane < 32) load_lds16(bias + lane * 8, const_cast<T*>(bs));
     __builtin_amdgcn_sched_barrier(0);  // keep the issue order
     constexpr int WCH = kStreamNO * CH;
-    static_assert(WCH % (kStreamWaves * kWave) == 0, "W staging tiles the workgroup");
+    constexpr int NU = WCH / (kStreamWaves * kWave);  // W pieces per wavefront
+    static_assert(WCH % (kStreamWaves * kWave) == 0 && (NU & (NU - 1)) == 0, "W staging tiles the workgroup");
+    // every workgroup stages the same 64 or 128 KB at the same moment: the CUs of one XCD start at different pieces
+    // (workgroups are dealt to the XCDs round-robin), so their requests spread over the L2 channels
+    const int rot = static_cast<int>(blockIdx.x / kXcds);
 #pragma unroll
-    for (int u = 0; u < WCH / (kStreamWaves * kWave); ++u) {  // a constant trip count, fully unrolled
-        const int i0 = u * kStreamWaves * kWave + wave * kWave;
+    for (int u = 0; u < NU; ++u) {  // a constant trip count, fully unrolled
+        const int i0 = ((u + rot) & (NU - 1)) * kStreamWaves * kWave + wave * kWave;
         const int i = i0 + lane, n = i / CH, j = i - n * CH;
         load_lds16(W + static_cast<size_t>(n) * K + (j ^ wkey(n)) * 8, ws + i0);
     }
