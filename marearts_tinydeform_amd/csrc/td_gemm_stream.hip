@@ -65,8 +65,8 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
     const int mmax = hi > lo ? hi - 1 : 0;                          // last row a load may touch
 
     // token fragments of one step: lane (r, kg) holds token m0 + 16 s + r, k = 32 kb + 8 kg .. + 7. Rows past hi
-    // read row hi - 1 (never stored); a step past the last re-reads the last step (L2 hits), and a wavefront without
-    // tokens reads row 0, so every load is unconditional: the wait counts below and the compiler's stay exact.
+    // read row hi - 1 (never stored) and a step past the last re-reads the last step (L2 hits), so every load is
+    // unconditional and the compiler's wait counts stay exact.
     auto load = [&](u32x4 (&tf)[TM][KB], int m0) {
         m0 = m0 < last ? m0 : last;
 #pragma unroll
@@ -79,10 +79,10 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
         }
     };
 
-    // Order of this wavefront's memory operations: the bias (wavefront 0) and W into LDS by direct loads, then the
-    // first two steps' tokens. The workgroup then waits only for the direct loads (the older ones; the tokens stay
-    // in flight and the first MFMAs wait for them one register at a time). Nothing else writes LDS here: after a
-    // direct load the compiler orders any LDS store behind every outstanding load.
+    // The bias (wavefront 0) and W go into LDS by direct loads; the workgroup waits for them and meets before any
+    // token is requested. Requesting the first steps' tokens ahead of the wait was slower (M = 88892: 24.7 against
+    // 22.4 µs): every wavefront's 32 KB of token rows competed with W for the fabric, and W arrived last. Nothing else
+    // writes LDS here: after a direct load the compiler orders any LDS store behind every outstanding load.
     // W: a wavefront's direct load fills 64 consecutive slots, so the swizzle is applied on the source side: the
     // lane that fills slot j of row n loads chunk j ^ key(n).
     static_assert(kStreamNO * sizeof(T) == 32 * 16, "the bias is 32 lanes x 16 bytes");
@@ -101,18 +101,14 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
         load_lds16(W + static_cast<size_t>(n) * K + (j ^ wkey(n)) * 8, ws + i0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    u32x4 ta[TM][KB], tb[TM][KB];
-    load(ta, lo);
-    load(tb, lo + 32);
-    // W and the bias landed (at most the 2 TM KB token loads still in flight), then the workgroup meets; no fence,
-    // which would wait for the tokens too
-    constexpr int TOKEN_LOADS = 2 * TM * KB;
-    static_assert(TOKEN_LOADS <= 63, "wait count");
     asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt((TOKEN_LOADS & 15) | ((TOKEN_LOADS >> 4) << 14) | (7 << 4));
+    __builtin_amdgcn_s_waitcnt(7 << 4);  // vmcnt(0), lgkmcnt(0): W and the bias landed
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (hi <= lo) return;
+    u32x4 ta[TM][KB], tb[TM][KB];
+    load(ta, lo);
+    load(tb, lo + 32);
 
     auto mma = [&](const u32x4 (&tf)[TM][KB], f32x4 (&acc)[TM][NT]) {
 #pragma unroll
@@ -168,17 +164,20 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
         }
     };
 
-    // the next-but-one step's tokens are requested as soon as the MFMAs have read this step's, before the stores
+    // Each step stores its outputs, then requests the next-but-one step's tokens into the registers its MFMAs have
+    // just read. In the other order (tokens, then stores) the compiler's waits before the next MFMAs covered the
+    // token requests just issued as well, and the two-step prefetch stopped overlapping (M = 88892: 25.0 against
+    // 24.2 µs; 177784: 42.3 against 39.2)
     f32x4 acc[TM][NT];
     for (int m0 = lo;;) {
         mma(ta, acc);
-        load(ta, m0 + 64);
         store(acc, m0);
+        load(ta, m0 + 64);
         m0 += 32;
         if (m0 >= hi) break;
         mma(tb, acc);
-        load(tb, m0 + 64);
         store(acc, m0);
+        load(tb, m0 + 64);
         m0 += 32;
         if (m0 >= hi) break;
     }
