@@ -414,27 +414,29 @@ template <typename T>
 int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
     if (variant <= 0) {
         // measured on MI355X (16-bit):
-        //   256 outputs, K = 128 or 256, from 60000 rows: the streaming kernel (22) (K = 256: M = 67200 21.4 µs
-        //     against 23.2 for 13, M = 88892 23.5 against 28.5, M = 177784 40.8 against 52.4; it loses below about
-        //     55000 rows, where its start, W into every CU's LDS, is not paid back);
+        //   256 outputs, K = 128 or 256, from 36000 rows: the streaming kernel (22) (K = 256: M = 40000 15.4 µs
+        //     against 16.6 for 13, M = 44446 15.7 against 17.1, M = 60000 16.6 against 23.0; K = 128: M = 44446
+        //     11.7 against 12.3; it loses at 30000 rows, 15.0 against 13.1, where its start, W into every CU's LDS,
+        //     is not paid back);
         //   deep K (K >= 512, K % 64 == 0) on a grid of at least 256 tiles of 256 x 128: the direct-to-LDS kernel,
         //     256 x 256 tiles (16) from 2.5 rounds of them on 256 CUs, else 256 x 128 (14) (C = 1024: M = 43520
         //     101 µs against 122 µs for 13; M = 21760 57 against 68);
-        //   other grids under 512 tiles of 128 x 128: 64 x 64 tiles with K in chunks of 256 (5) (M = 600, K = 1024,
-        //     1024 outputs: 10.3 µs against 19-20 µs for 13, 14 or 16);
+        //   other grids under 512 tiles of 128 x 128 (under 256 for K <= 256): 64 x 64 tiles with K in chunks of 256
+        //     (5) (M = 600, K = 1024, 1024 outputs: 10.3 µs against 19-20 µs for 13, 14 or 16; K = NO = 256:
+        //     M = 8400 7.9 against 9.0, M = 16384 10.2 against 10.0, M = 30000 17.5 against 13.3);
         //   else both operands through LDS in 128 x 128 tiles with K chunks of 32 (13).
         // float32: one round trip (5) for K <= 128 on small grids, else A direct in 64 x 128 tiles (2).
         constexpr int one_chunk = 8 * KBlock<T>::kK;
         const int64_t tiles_128 = ((p.M + 127) / 128) * static_cast<int64_t>((p.NO + 127) / 128);
         const int64_t tiles_256x128 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 127) / 128);
         const int64_t tiles_256 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 255) / 256);
-        if (sizeof(T) == 2 && p.M >= 60000 && gemm_stream_fits(std::is_same<T, bf16>::value ? kBF16 : kF16, p)) {
+        if (sizeof(T) == 2 && p.M >= 36000 && gemm_stream_fits(std::is_same<T, bf16>::value ? kBF16 : kF16, p)) {
             variant = 22;
         } else if (sizeof(T) == 2) {
             if (p.K >= 512 && p.K % 64 == 0 && tiles_256x128 >= 256)
                 variant = tiles_256 >= 640 ? 16 : 14;
             else
-                variant = tiles_128 < 512 ? 5 : 13;
+                variant = tiles_128 < (p.K <= 256 ? 256 : 512) ? 5 : 13;
         } else {
             variant = p.K <= one_chunk && tiles_128 < 512 ? 5 : 2;
         }
