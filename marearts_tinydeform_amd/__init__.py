@@ -31,9 +31,9 @@ MODES = ('auto', 'fused', 'project')
 #   fused   = f0 + f1 * gathered_mb
 #   project = p0 + p1 * gemm_mb + p2 * gemm_gflop + p3 * sample_mb
 FUSED_LIMIT = {
-    torch.float32: {'fused': (8.0544, 0.0642), 'project': (18.9109, 0.6264, 0.0000, 0.1113)},
-    torch.float16: {'fused': (6.2928, 0.0675), 'project': (8.9357, 0.3726, 0.8518, 0.0953)},
-    torch.bfloat16: {'fused': (6.2928, 0.0675), 'project': (8.9357, 0.3726, 0.8518, 0.0953)},
+    torch.float32: {'fused': (8.6391, 0.0530), 'project': (19.5112, 0.6407, 0.0000, 0.0867)},
+    torch.float16: {'fused': (6.3135, 0.0618), 'project': (11.8753, 0.1007, 0.8887, 0.0891)},
+    torch.bfloat16: {'fused': (6.3135, 0.0618), 'project': (11.8753, 0.1007, 0.8887, 0.0891)},
 }
 
 # cost tables by GPU architecture (gcnArchName without feature suffixes)
