@@ -425,7 +425,9 @@ int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
         //     (5) (M = 600, K = 1024, 1024 outputs: 10.3 µs against 19-20 µs for 13, 14 or 16; K = NO = 256:
         //     M = 8400 7.9 against 9.0, M = 16384 10.2 against 10.0, M = 30000 17.5 against 13.3);
         //   else both operands through LDS in 128 x 128 tiles with K chunks of 32 (13).
-        // float32: one round trip (5) for K <= 128 on small grids, else A direct in 64 x 128 tiles (2).
+        // float32 (MFMA-bound: v_mfma_f32_16x16x4_f32): 64 x 64 tiles (5) for K <= 128 on grids under 512 tiles and
+        //   for K <= 256 under 1024 (K = NO = 256: M = 8400 20.9 µs against 24.2 for 2, M = 33600 54.4 against
+        //   56.2), else A direct in 64 x 128 tiles (2) (M = 67200: 93.5 against 96.4).
         constexpr int one_chunk = 8 * KBlock<T>::kK;
         const int64_t tiles_128 = ((p.M + 127) / 128) * static_cast<int64_t>((p.NO + 127) / 128);
         const int64_t tiles_256x128 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 127) / 128);
@@ -438,7 +440,7 @@ int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
             else
                 variant = tiles_128 < (p.K <= 256 ? 256 : 512) ? 5 : 13;
         } else {
-            variant = p.K <= one_chunk && tiles_128 < 512 ? 5 : 2;
+            variant = (p.K <= one_chunk && tiles_128 < 512) || (p.K <= 256 && tiles_128 < 1024) ? 5 : 2;
         }
     }
     switch (variant) {
