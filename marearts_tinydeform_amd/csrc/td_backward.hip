@@ -195,6 +195,169 @@ __global__ __launch_bounds__(256) void sample_backward_kernel(BackParams p) {
     }
 }
 
+// The same gradients for D <= 64 (one channel per lane), ordered so that no load waits behind an atomic. A
+// wavefront's vector memory operations retire in order, so a load issued after the value-gradient atomics of earlier
+// corners cannot be consumed before those atomics have completed at the L2; in sample_backward_kernel each corner's
+// value load sits behind the previous corners' atomics. Here the wavefront of row (b, q, h) first computes the taps
+// of all its LP samples (lane j: sample j) into LDS, then works through the samples in chunks of NC iterations of
+// 64 / LG samples: the chunk's value loads are issued together, and the next chunk's loads are issued before this
+// chunk's atomics, so the atomics retire while the next chunk computes.
+template <typename A>
+struct BTap {
+    int tok[4];
+    A fx, fy, a;
+    A wl, hl;  // the sample's level width and height (the location gradient's scale)
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void sample_backward_batched_kernel(BackParams p) {
+    using A = typename AccOf<T>::type;
+    constexpr int NC = 4;  // iterations per chunk
+    __shared__ BTap<A> taps[4][kMaxLevelPoints];
+    const Geom& g = p.g;
+    const int wv = static_cast<int>(threadIdx.x) >> 6;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wv;
+    const int64_t rows = static_cast<int64_t>(g.B) * g.Q * g.H;
+    if (row >= rows) return;  // uniform across the wavefront; no workgroup barrier below
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+    const int LG = p.LG, per = kWave / LG, slot = lane / LG, sub = lane - slot * LG;
+    const int D = g.D, HD = g.H * g.D, LP = g.LP;
+    const int h = static_cast<int>(row % g.H);
+    const int64_t bq = row / g.H, b = bq / g.Q;
+    BTap<A>* tw = taps[wv];
+
+    const T* __restrict__ go = static_cast<const T*>(p.grad_out) + bq * HD + h * D;
+    const A gr = sub < D ? cvt<A>(go[sub]) : static_cast<A>(0);
+
+    // taps of every sample of the row, one sample per lane (LP <= 64)
+    if (lane < LP) {
+        const int64_t idx = row * LP + lane;
+        A lx, ly, a;
+        if (g.loc_acc) {
+            lx = static_cast<const A*>(p.loc)[2 * idx];
+            ly = static_cast<const A*>(p.loc)[2 * idx + 1];
+            a = static_cast<const A*>(p.attn)[idx];
+        } else {
+            lx = cvt<A>(static_cast<const T*>(p.loc)[2 * idx]);
+            ly = cvt<A>(static_cast<const T*>(p.loc)[2 * idx + 1]);
+            a = cvt<A>(static_cast<const T*>(p.attn)[idx]);
+        }
+        const int l = level_of(g, lane);
+        const Taps<A> t = taps_at<A>(lx, ly, l, g, row);
+        BTap<A> bt;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bt.tok[k] = t.tok[k];
+        bt.fx = t.fx;
+        bt.fy = t.fy;
+        bt.a = a;
+        bt.wl = static_cast<A>(g.shapes[2 * l + 1]);
+        bt.hl = static_cast<A>(g.shapes[2 * l]);
+        tw[lane] = bt;
+    }
+    // the wavefront's own LDS writes, read back by other lanes of the same wavefront: LDS operations of one
+    // wavefront complete in order
+    __builtin_amdgcn_wave_barrier();
+
+    const T* __restrict__ vb = static_cast<const T*>(p.value) + b * g.N * HD + h * D + (sub < D ? sub : 0);
+    A* __restrict__ gv = static_cast<A*>(p.grad_value) + b * g.N * HD + h * D + sub;
+    const int nit = (LP + per - 1) / per;
+
+    // value loads of chunk c0 (iterations c0 .. c0 + NC - 1); corners outside the map read token 0 and are dropped
+    auto load = [&](int c0, T (&v)[NC][4]) {
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int j = (c0 + i) * per + slot;
+            const bool on = c0 + i < nit && j < LP;
+            const BTap<A> t = tw[on ? j : 0];  // unconditional: no branch around the loads
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int tk = on ? t.tok[k] : -1;
+                v[i][k] = vb[static_cast<int64_t>(tk < 0 ? 0 : tk) * HD];
+            }
+        }
+    };
+    // gradients of chunk c0 from its loaded values: location and weight gradients, then the value-gradient atomics
+    auto finish = [&](int c0, const T (&v)[NC][4], auto&& between) {
+        A d[NC][4];
+        BTap<A> bt[NC];
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int j = (c0 + i) * per + slot;
+            const bool on = c0 + i < nit && j < LP;
+            bt[i] = tw[on ? j : 0];
+            if (!on) bt[i].tok[0] = bt[i].tok[1] = bt[i].tok[2] = bt[i].tok[3] = -1;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) d[i][k] = bt[i].tok[k] >= 0 ? cvt<A>(v[i][k]) * gr : static_cast<A>(0);
+        }
+        between();  // the next chunk's loads go out before this chunk's atomics
+        for (int m = LG >> 1; m > 0; m >>= 1) {
+#pragma unroll
+            for (int i = 0; i < NC; ++i)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) d[i][k] = xor_sum(d[i][k], m);
+        }
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int j = (c0 + i) * per + slot;
+            if (!(c0 + i < nit && j < LP) || sub != 0) continue;
+            Taps<A> t;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) t.tok[k] = bt[i].tok[k];
+            t.fx = bt[i].fx;
+            t.fy = bt[i].fy;
+            const A a = bt[i].a;
+            const int64_t idx = row * LP + j;
+            A ga, gx = 0, gy = 0;
+            if (g.discrete) {
+                ga = d[i][0];
+            } else {
+                ga = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) ga += tap_weight(t, k) * d[i][k];
+                const A one = 1;
+                const A dvx = (one - t.fy) * (d[i][1] - d[i][0]) + t.fy * (d[i][3] - d[i][2]);
+                const A dvy = (one - t.fx) * (d[i][2] - d[i][0]) + t.fx * (d[i][3] - d[i][1]);
+                gx = a * dvx * bt[i].wl;
+                gy = a * dvy * bt[i].hl;
+            }
+            if (g.loc_acc) {
+                static_cast<A*>(p.grad_loc)[2 * idx] = gx;
+                static_cast<A*>(p.grad_loc)[2 * idx + 1] = gy;
+                static_cast<A*>(p.grad_attn)[idx] = ga;
+            } else {
+                static_cast<T*>(p.grad_loc)[2 * idx] = static_cast<T>(gx);
+                static_cast<T*>(p.grad_loc)[2 * idx + 1] = static_cast<T>(gy);
+                static_cast<T*>(p.grad_attn)[idx] = static_cast<T>(ga);
+            }
+        }
+        if (sub < D) {
+#pragma unroll
+            for (int i = 0; i < NC; ++i) {
+                Taps<A> t;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) t.tok[k] = bt[i].tok[k];
+                t.fx = bt[i].fx;
+                t.fy = bt[i].fy;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int tk = bt[i].tok[k];
+                    if (tk < 0) continue;
+                    const A w = g.discrete ? (k == 0 ? static_cast<A>(1) : static_cast<A>(0)) : tap_weight(t, k);
+                    atomic_add(gv + static_cast<int64_t>(tk) * HD, bt[i].a * w * gr);
+                }
+            }
+        }
+    };
+
+    T va[NC][4], vb2[NC][4];
+    load(0, va);
+    for (int c0 = 0; c0 < nit; c0 += 2 * NC) {
+        finish(c0, va, [&] { if (c0 + NC < nit) load(c0 + NC, vb2); });
+        if (c0 + NC >= nit) break;
+        finish(c0 + NC, vb2, [&] { if (c0 + 2 * NC < nit) load(c0 + 2 * NC, va); });
+    }
+}
+
 template <typename T, typename A>
 __global__ __launch_bounds__(256) void convert_kernel(const A* __restrict__ src, T* __restrict__ dst, int64_t n) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -454,10 +617,22 @@ int sample_backward_go(BackParams p, hipStream_t stream) {
     return launched("sample backward");
 }
 
-// one channel per lane up to D = 64 (LG = D rounded up to a power of two), then D / 64 per lane
+// one channel per lane up to D = 64 (LG = D rounded up to a power of two, the batched form), then D / 64 per lane
+template <typename T>
+int sample_backward_batched_go(BackParams p, hipStream_t stream) {
+    int lg = 1;
+    while (lg < p.g.D) lg <<= 1;
+    p.LG = lg;
+    const int64_t rows = static_cast<int64_t>(p.g.B) * p.g.Q * p.g.H;
+    if (rows == 0) return 0;
+    hipLaunchKernelGGL((sample_backward_batched_kernel<T>), dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0,
+                       stream, p);
+    return launched("sample backward");
+}
+
 template <typename T>
 int sample_backward_t(const BackParams& p, hipStream_t stream) {
-    if (p.g.D <= 64) return sample_backward_go<T, 1>(p, stream);
+    if (p.g.D <= 64) return sample_backward_batched_go<T>(p, stream);
     if (p.g.D <= 128) return sample_backward_go<T, 2>(p, stream);
     return sample_backward_go<T, 4>(p, stream);
 }

@@ -69,6 +69,20 @@ def test_gradients_match_oracle(case, dtype):
 
 
 @pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize('D', [96, 128, 256])
+def test_gradients_wide_heads(D, dtype):
+    # head dims above 64 take the several-channels-per-lane sampling backward (D <= 64 the batched one, covered by
+    # the cases above); 96 is not a power of two
+    args = make(1, 20, 2, D, 64, [(10, 12), (5, 6)], 2, dtype=dtype)
+    go = grad_out_for(args)
+    say(f'  backward wide heads D={D} {dtype}')
+    grads, _ = gpu_grads(args, go, dtype)
+    ref = gridsample.deform_attn_grads(*args, go.to(dtype))
+    for n in NAMES:
+        check(f'D={D} {dtype} d{n}', grads[n], ref[n], dtype)
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16])
 def test_gradients_with_padding_mask_and_no_bias(dtype):
     args = make(2, 50, 8, 32, 256, [(40, 40), (20, 20), (10, 10)], 4, dtype=dtype, bias=False)
     N = args[0].shape[1]
