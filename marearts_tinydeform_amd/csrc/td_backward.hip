@@ -359,6 +359,158 @@ __global__ __launch_bounds__(256) void sample_backward_batched_kernel(BackParams
 }
 
 template <typename T, typename A>
+__device__ __forceinline__ void sample_input(const BackParams& p, int64_t idx, A& lx, A& ly, A& a) {
+    if (p.g.loc_acc) {
+        lx = static_cast<const A*>(p.loc)[2 * idx];
+        ly = static_cast<const A*>(p.loc)[2 * idx + 1];
+        a = static_cast<const A*>(p.attn)[idx];
+    } else {
+        lx = cvt<A>(static_cast<const T*>(p.loc)[2 * idx]);
+        ly = cvt<A>(static_cast<const T*>(p.loc)[2 * idx + 1]);
+        a = cvt<A>(static_cast<const T*>(p.attn)[idx]);
+    }
+}
+
+inline bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+
+// The batched form with 16-byte value loads (16/32-bit types, D * element size a multiple of 16, D <= 64). The
+// corner dot products d_c = value[t_c] . g_r need the value rows; the value-gradient atomics need only g_r and the
+// tap weights. So the two use different lane layouts: for the dots, DV = D / V lanes hold V consecutive channels
+// each and one load instruction fetches 64 / DV corner rows (16 at D = 32 in 16 bits, against 2 with one channel
+// per lane); for the atomics, lane `sub` holds channel sub, so an atomic instruction adds whole 128-byte lines.
+// Per row: taps into LDS (lane j: sample j); every corner's value row loaded at once and dotted with g_r, the dots
+// into LDS; location and weight gradients (lane j: sample j); then the atomics, which no load follows.
+template <typename T, int V>
+__global__ __launch_bounds__(256) void sample_backward_vec_kernel(BackParams p) {
+    using A = float;
+    using IO = VecIO<T, V>;
+    constexpr int MAXB = 4 * kMaxLevelPoints;  // corners per row at most
+    __shared__ BTap<A> taps[4][kMaxLevelPoints];
+    __shared__ A dots[4][MAXB];
+    const Geom& g = p.g;
+    const int wv = static_cast<int>(threadIdx.x) >> 6;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wv;
+    const int64_t rows = static_cast<int64_t>(g.B) * g.Q * g.H;
+    if (row >= rows) return;  // uniform across the wavefront; no workgroup barrier below
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+    const int D = g.D, HD = g.H * g.D, LP = g.LP, S = 4 * LP;
+    const int DV = D / V, CPI = kWave / DV;  // lanes per corner row, corners per load instruction
+    const int h = static_cast<int>(row % g.H);
+    const int64_t bq = row / g.H, b = bq / g.Q;
+    BTap<A>* tw = taps[wv];
+    A* dd = dots[wv];
+    const T* __restrict__ go = static_cast<const T*>(p.grad_out) + bq * HD + h * D;
+
+    if (lane < LP) {
+        const int64_t idx = row * LP + lane;
+        A lx, ly, a;
+        sample_input<T, A>(p, idx, lx, ly, a);
+        const int l = level_of(g, lane);
+        const Taps<A> t = taps_at<A>(lx, ly, l, g, row);
+        BTap<A> bt;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bt.tok[k] = t.tok[k];
+        bt.fx = t.fx;
+        bt.fy = t.fy;
+        bt.a = a;
+        bt.wl = static_cast<A>(g.shapes[2 * l + 1]);
+        bt.hl = static_cast<A>(g.shapes[2 * l]);
+        tw[lane] = bt;
+    }
+    __builtin_amdgcn_wave_barrier();  // LDS operations of one wavefront complete in order
+
+    // dots: lane (corner slot cs, chunk ch) loads V channels of corner i * CPI + cs
+    {
+        const int cs = lane / DV, ch = lane - cs * DV;
+        A gc[V];
+        IO::unpack(IO::load(go + ch * V), gc);
+        const T* __restrict__ vb = static_cast<const T*>(p.value) + b * g.N * HD + h * D + ch * V;
+        constexpr int NB = 16;  // load instructions in flight per lane
+        const int nb = (S + CPI - 1) / CPI;
+        for (int i0 = 0; i0 < nb; i0 += NB) {
+            typename IO::raw_t raw[NB];
+            int tks[NB];
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                const int c = (i0 + u) * CPI + cs;
+                tks[u] = i0 + u < nb && c < S ? tw[c >> 2].tok[c & 3] : -1;
+                raw[u] = IO::load(vb + static_cast<int64_t>(tks[u] < 0 ? 0 : tks[u]) * HD);
+            }
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                const int c = (i0 + u) * CPI + cs;
+                A v[V];
+                IO::unpack(raw[u], v);
+                A d = 0;
+#pragma unroll
+                for (int e = 0; e < V; ++e) d += v[e] * gc[e];
+                for (int m = 1; m < DV; m <<= 1) d = xor_sum(d, m);
+                if (ch == 0 && i0 + u < nb && c < S) dd[c] = tks[u] >= 0 ? d : static_cast<A>(0);
+            }
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+
+    if (lane < LP) {
+        const BTap<A> bt = tw[lane];
+        A d[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) d[k] = dd[4 * lane + k];
+        Taps<A> t;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t.tok[k] = bt.tok[k];
+        t.fx = bt.fx;
+        t.fy = bt.fy;
+        const int64_t idx = row * LP + lane;
+        A ga, gx = 0, gy = 0;
+        if (g.discrete) {
+            ga = d[0];
+        } else {
+            ga = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) ga += tap_weight(t, k) * d[k];
+            const A one = 1;
+            const A dvx = (one - t.fy) * (d[1] - d[0]) + t.fy * (d[3] - d[2]);
+            const A dvy = (one - t.fx) * (d[2] - d[0]) + t.fx * (d[3] - d[1]);
+            gx = bt.a * dvx * bt.wl;
+            gy = bt.a * dvy * bt.hl;
+        }
+        if (g.loc_acc) {
+            static_cast<A*>(p.grad_loc)[2 * idx] = gx;
+            static_cast<A*>(p.grad_loc)[2 * idx + 1] = gy;
+            static_cast<A*>(p.grad_attn)[idx] = ga;
+        } else {
+            static_cast<T*>(p.grad_loc)[2 * idx] = static_cast<T>(gx);
+            static_cast<T*>(p.grad_loc)[2 * idx + 1] = static_cast<T>(gy);
+            static_cast<T*>(p.grad_attn)[idx] = static_cast<T>(ga);
+        }
+    }
+
+    // value-gradient atomics: LG lanes per sample (LG = D rounded up to a power of two), lane sub adds channel sub
+    {
+        const int LG = p.LG, per = kWave / LG, slot = lane / LG, sub = lane - slot * LG;
+        if (sub >= D) return;
+        const A gr = cvt<A>(go[sub]);
+        A* __restrict__ gv = static_cast<A*>(p.grad_value) + b * g.N * HD + h * D + sub;
+        for (int j = slot; j < LP; j += per) {
+            const BTap<A> bt = tw[j];
+            Taps<A> t;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) t.tok[k] = bt.tok[k];
+            t.fx = bt.fx;
+            t.fy = bt.fy;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int tk = bt.tok[k];
+                if (tk < 0) continue;
+                const A w = g.discrete ? (k == 0 ? static_cast<A>(1) : static_cast<A>(0)) : tap_weight(t, k);
+                atomic_add(gv + static_cast<int64_t>(tk) * HD, bt.a * w * gr);
+            }
+        }
+    }
+}
+
+template <typename T, typename A>
 __global__ __launch_bounds__(256) void convert_kernel(const A* __restrict__ src, T* __restrict__ dst, int64_t n) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
@@ -625,13 +777,33 @@ int sample_backward_batched_go(BackParams p, hipStream_t stream) {
     p.LG = lg;
     const int64_t rows = static_cast<int64_t>(p.g.B) * p.g.Q * p.g.H;
     if (rows == 0) return 0;
-    hipLaunchKernelGGL((sample_backward_batched_kernel<T>), dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0,
+    hipLaunchKernelGGL((sample_backward_batched_kernel<T>), dim3(static_cast<unsigned>((rows + 3) / 4)),
+                       dim3(256), 0, stream, p);
+    return launched("sample backward");
+}
+
+template <typename T>
+int sample_backward_vec_go(BackParams p, hipStream_t stream) {
+    constexpr int V = 16 / static_cast<int>(sizeof(T));
+    int lg = 1;
+    while (lg < p.g.D) lg <<= 1;
+    p.LG = lg;
+    const int64_t rows = static_cast<int64_t>(p.g.B) * p.g.Q * p.g.H;
+    if (rows == 0) return 0;
+    hipLaunchKernelGGL((sample_backward_vec_kernel<T, V>), dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0,
                        stream, p);
     return launched("sample backward");
 }
 
 template <typename T>
 int sample_backward_t(const BackParams& p, hipStream_t stream) {
+    constexpr int V = 16 / static_cast<int>(sizeof(T));
+    if constexpr (sizeof(T) <= 4) {
+        // 16-byte value loads need D a multiple of V and 16-byte aligned value rows
+        if (p.g.D <= 64 && p.g.D % V == 0 && is_pow2(p.g.D / V) && reinterpret_cast<uintptr_t>(p.value) % 16 == 0 &&
+            reinterpret_cast<uintptr_t>(p.grad_out) % 16 == 0)
+            return sample_backward_vec_go<T>(p, stream);
+    }
     if (p.g.D <= 64) return sample_backward_batched_go<T>(p, stream);
     if (p.g.D <= 128) return sample_backward_go<T, 2>(p, stream);
     return sample_backward_go<T, 4>(p, stream);
