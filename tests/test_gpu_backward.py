@@ -192,3 +192,23 @@ def test_module_training_step_matches_cpu():
         scale = max(float(cpu[n].abs().max()), 1e-6)
         err = float((gpu[n] - cpu[n]).abs().max()) / scale
         assert err <= 5e-4, f'{n}: {err:.3g}'
+
+
+@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize('with_mask', [False, True])
+def test_encoder_shape_gradients(dtype, with_mask):
+    # self-attention shapes (every token a query, sampling around itself, as encoder layers call the operator):
+    # neighbouring queries add into the same value-gradient rows many times over. Q = N = 4080 on four levels, and
+    # Q = 4077; a padding mask drops tokens as in the other paths
+    levels = [(48, 64), (24, 32), (12, 16), (6, 8)]
+    for Q in (4080, 4077):
+        args = workload(1, Q, 8, 32, 64, levels, 4, dtype, loc_dist='encoder', seed=5)
+        N = args[0].shape[1]
+        mask = (torch.rand(1, N, generator=torch.Generator().manual_seed(6)) < 0.2) if with_mask else None
+        go = grad_out_for(args)
+        say(f'  backward encoder shape Q={Q} {dtype} mask={with_mask}')
+        grads, _ = gpu_grads(args, go, dtype, mask=mask)
+        ref = gridsample.deform_attn_grads(*args, go.to(dtype), padding_mask=mask)
+        for n in NAMES:
+            check(f'encoder Q={Q} {dtype} d{n}', grads[n], ref[n], dtype)
+
