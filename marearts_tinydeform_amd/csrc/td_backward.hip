@@ -202,6 +202,21 @@ __global__ __launch_bounds__(256) void sample_backward_kernel(BackParams p) {
 // of all its LP samples (lane j: sample j) into LDS, then works through the samples in chunks of NC iterations of
 // 64 / LG samples: the chunk's value loads are issued together, and the next chunk's loads are issued before this
 // chunk's atomics, so the atomics retire while the next chunk computes.
+// location and attention weight of sample idx (= row * LP + j), in the element type or, with g.loc_acc, in the
+// accumulation type
+template <typename T, typename A>
+__device__ __forceinline__ void sample_input(const BackParams& p, int64_t idx, A& lx, A& ly, A& a) {
+    if (p.g.loc_acc) {
+        lx = static_cast<const A*>(p.loc)[2 * idx];
+        ly = static_cast<const A*>(p.loc)[2 * idx + 1];
+        a = static_cast<const A*>(p.attn)[idx];
+    } else {
+        lx = cvt<A>(static_cast<const T*>(p.loc)[2 * idx]);
+        ly = cvt<A>(static_cast<const T*>(p.loc)[2 * idx + 1]);
+        a = cvt<A>(static_cast<const T*>(p.attn)[idx]);
+    }
+}
+
 template <typename A>
 struct BTap {
     int tok[4];
@@ -233,15 +248,7 @@ __global__ __launch_bounds__(256) void sample_backward_batched_kernel(BackParams
     if (lane < LP) {
         const int64_t idx = row * LP + lane;
         A lx, ly, a;
-        if (g.loc_acc) {
-            lx = static_cast<const A*>(p.loc)[2 * idx];
-            ly = static_cast<const A*>(p.loc)[2 * idx + 1];
-            a = static_cast<const A*>(p.attn)[idx];
-        } else {
-            lx = cvt<A>(static_cast<const T*>(p.loc)[2 * idx]);
-            ly = cvt<A>(static_cast<const T*>(p.loc)[2 * idx + 1]);
-            a = cvt<A>(static_cast<const T*>(p.attn)[idx]);
-        }
+        sample_input<T, A>(p, idx, lx, ly, a);
         const int l = level_of(g, lane);
         const Taps<A> t = taps_at<A>(lx, ly, l, g, row);
         BTap<A> bt;
@@ -355,19 +362,6 @@ __global__ __launch_bounds__(256) void sample_backward_batched_kernel(BackParams
         finish(c0, va, [&] { if (c0 + NC < nit) load(c0 + NC, vb2); });
         if (c0 + NC >= nit) break;
         finish(c0 + NC, vb2, [&] { if (c0 + 2 * NC < nit) load(c0 + 2 * NC, va); });
-    }
-}
-
-template <typename T, typename A>
-__device__ __forceinline__ void sample_input(const BackParams& p, int64_t idx, A& lx, A& ly, A& a) {
-    if (p.g.loc_acc) {
-        lx = static_cast<const A*>(p.loc)[2 * idx];
-        ly = static_cast<const A*>(p.loc)[2 * idx + 1];
-        a = static_cast<const A*>(p.attn)[idx];
-    } else {
-        lx = cvt<A>(static_cast<const T*>(p.loc)[2 * idx]);
-        ly = cvt<A>(static_cast<const T*>(p.loc)[2 * idx + 1]);
-        a = cvt<A>(static_cast<const T*>(p.attn)[idx]);
     }
 }
 
