@@ -344,6 +344,41 @@ def fit_auto(out_path):
                    'current_within_10pct': within, 'cases': len(rows)}, f, indent=1)
 
 
+def table(args):
+    """The reference's benchmark table (bench/bench.py:64-121): for every dtype, batch and query count, the PyTorch
+    path (F.linear + grid_sample), fused, project and auto, graph-timed µs, with the largest difference of fused and
+    project from the PyTorch path. Inputs as the reference's (clustered locations: a centre per query plus 0.05
+    randn), generated here on the CPU from a fixed seed. The reference's 'official' column (the Deformable-DETR CUDA
+    extension) has no counterpart on this GPU and is left out."""
+    levels = [tuple(int(v) for v in s.split('x')) for s in args.levels.split(',')]
+    C, H, P = args.channels, args.heads, args.points
+    D = C // H
+    N = sum(h * w for h, w in levels)
+    print(f'{torch.cuda.get_device_name()} ({torch.cuda.get_device_properties(0).gcnArchName}), torch '
+          f'{torch.__version__}, tokens {N}, C {C}, heads {H}, levels {len(levels)}, points {P}')
+    print('| dtype | batch | queries | pytorch | fused | project | auto (picks) | auto vs pytorch | '
+          'max abs diff vs pytorch |')
+    print('|---|---:|---:|---:|---:|---:|---:|---:|---:|')
+    for name in args.dtype:
+        dtype = getattr(torch, name)
+        for B in args.batch:
+            for Q in args.queries:
+                cpu = workload(B, Q, H, D, C, levels, P, dtype, loc_dist='clustered')
+                a = [None if t is None else t.cuda() for t in cpu]
+                a_ref = a[:3] + [cpu[3], cpu[4]] + a[5:]  # the PyTorch path reads the level sizes on the host
+                with torch.inference_mode():
+                    ref = td.ma_deform_attn_reference(*a_ref).float()
+                    diff = max((td.ma_deform_attn(*a, mode=m).float() - ref).abs().max().item()
+                               for m in ('fused', 'project'))
+                    t_ref = graph_time_us(lambda: td.ma_deform_attn_reference(*a_ref), 100, 3)
+                    t_fus = graph_time_us(lambda: td.ma_deform_attn(*a, mode='fused'), 100, 3)
+                    t_prj = graph_time_us(lambda: td.ma_deform_attn(*a, mode='project'), 100, 3)
+                pick = td.choose_mode(a[0], a[1], a[5])
+                t_auto = t_fus if pick == 'fused' else t_prj
+                print(f'| {name} | {B} | {Q} | {t_ref:.1f} | {t_fus:.1f} | {t_prj:.1f} | {t_auto:.1f} ({pick}) | '
+                      f'{t_ref / t_auto:.1f}x | {diff:.1e} |', flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -356,6 +391,16 @@ def main():
     ap.add_argument('--fit-auto', metavar='OUT.json', default=None,
                     help='time fused and project over the auto grid, fit the per-dtype cost model of '
                          'marearts_tinydeform_amd.FUSED_LIMIT and report how far auto is from the faster mode')
+    ap.add_argument('--table', action='store_true',
+                    help="the reference's sweep (its bench/bench.py): PyTorch path, fused, project and auto per dtype, "
+                         'batch and query count, as a markdown table on stdout')
+    ap.add_argument('--queries', type=int, nargs='+', default=[50, 100, 300], help='--table: query counts')
+    ap.add_argument('--batch', type=int, nargs='+', default=[1, 4], help='--table: batch sizes')
+    ap.add_argument('--dtype', nargs='+', default=['float32', 'float16'], help='--table: dtypes')
+    ap.add_argument('--levels', default='80x80,40x40,20x20', help='--table: level sizes HxW')
+    ap.add_argument('--channels', type=int, default=256, help='--table: C')
+    ap.add_argument('--heads', type=int, default=8, help='--table: H')
+    ap.add_argument('--points', type=int, default=4, help='--table: P')
     ap.add_argument('--pmc-run', action='store_true',
                     help='for rocprofv3 --pmc: one plain copy of COPY_BYTES (the counter calibration), then '
                          '--steps eager calls of the fused kernel, the value projection and the sampling kernel')
@@ -370,6 +415,9 @@ def main():
     assert torch.cuda.is_available(), 'no HIP device'
     if args.fit_auto:
         fit_auto(args.fit_auto)
+        return
+    if args.table:
+        table(args)
         return
 
     spec = WORKLOADS[args.workload]
