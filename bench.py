@@ -170,17 +170,20 @@ def train_times(cpu_args, steps, warmup):
 def gemm_kernel(M, K, NO, s):
     """Which value-projection kernel td_value_proj launches for an aligned [M, K] x [K, NO] problem (element size
     s), following its size rule: 16-bit with 256 outputs, K = 128 or 256 and at least 36000 rows takes the streaming
-    kernel; 16-bit deep K (K >= 512, K % 64 == 0) on a grid of >= 256 tiles of 256 x 128 the direct-to-LDS kernel;
-    other 16-bit grids under 512 tiles of 128 x 128 (256 for K <= 256) take 64 x 64 tiles, larger ones both operands
-    through LDS;
+    kernel; 16-bit deep K (K >= 512, K % 64 == 0) on a grid of >= 200 tiles of 256 x 128 the direct-to-LDS kernel;
+    other 16-bit grids take register-operand tiles (32 x 32 to 64 x 64) up to 1100 tiles of 64 x 64 for K <= 256 and
+    under 512 for deeper K, larger ones both operands through LDS;
     float32 takes 64 x 64 tiles for K <= 128 on small grids, else 64 x 128 tiles."""
     tiles_128 = -(-M // 128) * -(-NO // 128)
     if s == 2:
         if NO == 256 and K in (128, 256) and M >= 36000:
             return 'gemm_stream_kernel'
-        if K >= 512 and K % 64 == 0 and -(-M // 256) * -(-NO // 128) >= 256:
+        if K >= 512 and K % 64 == 0 and -(-M // 256) * -(-NO // 128) >= 200:
             return 'gemm_dma_kernel'
-        return 'gemm_mfma_kernel' if tiles_128 < (256 if K <= 256 else 512) else 'gemm_lds_kernel'
+        tiles_64 = -(-M // 64) * -(-NO // 64)
+        if K <= 256:
+            return 'gemm_mfma_kernel' if tiles_64 <= 1100 else 'gemm_lds_kernel'
+        return 'gemm_mfma_kernel' if tiles_64 < 512 else 'gemm_lds_kernel'
     return 'gemm_mfma_kernel'
 
 

@@ -410,6 +410,9 @@ int go_mfma(GemmParams p, hipStream_t stream) {
 //   14..21 256 x 128 / 256 x 256 tiles fed by direct-to-LDS loads (td_gemm_dma.hip; 16-bit, K % 64 == 0)
 //   22 the streaming kernel: W resident in LDS, token rows streamed into MFMA fragments (td_gemm_stream.hip;
 //      16-bit, NO = 256, K = 128 or 256)
+//   23 64 x 32   4 waves of 16 x 32, one chunk of 256/128, one stage
+//   24 32 x 32   2 waves of 16 x 32, one chunk of 256/128, one stage
+//   25 64 x 64   4 waves of 16 x 64, K chunks of 128/64, two stages
 template <typename T>
 int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
     if (variant <= 0) {
@@ -418,13 +421,17 @@ int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
         //     against 16.6 for 13, M = 44446 15.7 against 17.1, M = 60000 16.6 against 23.0; K = 128: M = 44446
         //     11.7 against 12.3; it loses at 30000 rows, 15.0 against 13.1, where its start, W into every CU's LDS,
         //     is not paid back);
-        //   deep K (K >= 512, K % 64 == 0) on a grid of at least 256 tiles of 256 x 128: the direct-to-LDS kernel,
+        //   deep K (K >= 512, K % 64 == 0) on a grid of at least 200 tiles of 256 x 128: the direct-to-LDS kernel,
         //     256 x 256 tiles (16) from 2.5 rounds of them on 256 CUs, else 256 x 128 (14) (C = 1024: M = 43520
-        //     101 µs against 122 µs for 13; M = 21760 57 against 68);
-        //   other grids under 512 tiles of 128 x 128 (under 256 for K <= 256): 64 x 64 tiles with K in chunks of 256
-        //     (5) (M = 600, K = 1024, 1024 outputs: 10.3 µs against 19-20 µs for 13, 14 or 16; K = NO = 256:
-        //     M = 8400 7.9 against 9.0, M = 16384 10.2 against 10.0, M = 30000 17.5 against 13.3);
-        //   else both operands through LDS in 128 x 128 tiles with K chunks of 32 (13).
+        //     101 µs against 122 µs for 13; M = 21760 57 against 68; M = 7200 23.6 against 29.2 for 13);
+        //   smaller grids by their count of 64 x 64 tiles (µs, against the former 64 x 64 one-chunk tiles, 5):
+        //     K <= 256: up to 300 tiles 32 x 32 (24) (NO = 256: M = 300 3.3 against 4.5, M = 2400 4.5 against 4.7),
+        //       up to 1100 64 x 64 with two-stage K chunks of 128 (25) (M = 8400 7.2 against 7.8, M = 16384 9.5
+        //       against 10.0), else 13 (M = 30000 12.9);
+        //     K >= 512: under 64 tiles 32 x 32 (24) (M = 100, K = NO = 1024: 6.5 against 10.2), under 128 64 x 32
+        //       (23) (M = 300: 8.0 against 10.2), under 512 two-stage 64 x 64 (25) (M = 600: 10.0 against 10.4,
+        //       M = 1800: 13.2 against 14.2), then both operands through LDS with K chunks of 128 (9) while under
+        //       512 tiles of 128 x 128 (M = 3600: 19.4 against 25.9), else 13.
         // float32 (MFMA-bound: v_mfma_f32_16x16x4_f32): 64 x 64 tiles (5) for K <= 128 on grids under 512 tiles and
         //   for K <= 256 under 1024 (K = NO = 256: M = 8400 20.9 µs against 24.2 for 2, M = 33600 54.4 against
         //   56.2), else A direct in 64 x 128 tiles (2) (M = 67200: 93.5 against 96.4).
@@ -435,10 +442,13 @@ int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
         if (sizeof(T) == 2 && p.M >= 36000 && gemm_stream_fits(std::is_same<T, bf16>::value ? kBF16 : kF16, p)) {
             variant = 22;
         } else if (sizeof(T) == 2) {
-            if (p.K >= 512 && p.K % 64 == 0 && tiles_256x128 >= 256)
+            const int64_t tiles_64 = ((p.M + 63) / 64) * static_cast<int64_t>((p.NO + 63) / 64);
+            if (p.K >= 512 && p.K % 64 == 0 && tiles_256x128 >= 200)
                 variant = tiles_256 >= 640 ? 16 : 14;
+            else if (p.K <= 256)
+                variant = tiles_64 <= 300 ? 24 : tiles_64 <= 1100 ? 25 : 13;
             else
-                variant = tiles_128 < (p.K <= 256 ? 256 : 512) ? 5 : 13;
+                variant = tiles_64 < 64 ? 24 : tiles_64 < 128 ? 23 : tiles_64 < 512 ? 25 : tiles_128 < 512 ? 9 : 13;
         } else {
             variant = (p.K <= one_chunk && tiles_128 < 512) || (p.K <= 256 && tiles_128 < 1024) ? 5 : 2;
         }
@@ -450,6 +460,9 @@ int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
         case 4: return go_mfma<T, 4, 1, 2, 4, 2, 2>(p, stream);
         case 5: return go_mfma<T, 4, 1, 1, 4, 8, 1>(p, stream);
         case 6: return go_mfma<T, 4, 1, 1, 8, 8, 1>(p, stream);
+        case 23: return go_mfma<T, 4, 1, 1, 2, 8, 1>(p, stream);
+        case 24: return go_mfma<T, 2, 1, 1, 2, 8, 1>(p, stream);
+        case 25: return go_mfma<T, 4, 1, 1, 4, 4, 2>(p, stream);
         case 7: return go_lds<T, 2, 2, 4, 4, 2>(p, stream);
         case 8: return go_lds<T, 4, 2, 4, 4, 2>(p, stream);
         case 9: return go_lds<T, 2, 2, 4, 4, 4>(p, stream);
