@@ -432,10 +432,12 @@ int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
         //       (23) (M = 300: 8.0 against 10.2), under 512 two-stage 64 x 64 (25) (M = 600: 10.0 against 10.4,
         //       M = 1800: 13.2 against 14.2), then both operands through LDS with K chunks of 128 (9) while under
         //       512 tiles of 128 x 128 (M = 3600: 19.4 against 25.9), else 13.
-        // float32 (MFMA-bound: v_mfma_f32_16x16x4_f32): 64 x 64 tiles (5) for K <= 128 on grids under 512 tiles and
-        //   for K <= 256 under 1024 (K = NO = 256: M = 8400 20.9 µs against 24.2 for 2, M = 33600 54.4 against
-        //   56.2), else A direct in 64 x 128 tiles (2) (M = 67200: 93.5 against 96.4).
-        constexpr int one_chunk = 8 * KBlock<T>::kK;
+        // float32 (MFMA-bound: v_mfma_f32_16x16x4_f32), by the count of 64 x 64 tiles: K <= 256: up to 40 tiles
+        //   32 x 32 (24) (K = NO = 256: M = 300 6.0 µs against 9.4 for 5), up to 100 64 x 32 (23) (M = 1200 6.8
+        //   against 9.5), up to 1100 two-stage 64 x 64 (25) (M = 2400 9.2 against 9.7, M = 8400 19.8 against
+        //   20.9), then 64 x 64 one-chunk tiles (5) under 1024 tiles of 128 x 128 (M = 33600 54.4 against 56.2),
+        //   else A direct in 64 x 128 tiles (2) (M = 67200: 93.5 against 96.4); K >= 512: two-stage 64 x 64 (25)
+        //   under 512 tiles (M = 600, K = NO = 1024: 27.2 against 48.8 for 2), else 2.
         const int64_t tiles_128 = ((p.M + 127) / 128) * static_cast<int64_t>((p.NO + 127) / 128);
         const int64_t tiles_256x128 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 127) / 128);
         const int64_t tiles_256 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 255) / 256);
@@ -450,7 +452,11 @@ int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
             else
                 variant = tiles_64 < 64 ? 24 : tiles_64 < 128 ? 23 : tiles_64 < 512 ? 25 : tiles_128 < 512 ? 9 : 13;
         } else {
-            variant = (p.K <= one_chunk && tiles_128 < 512) || (p.K <= 256 && tiles_128 < 1024) ? 5 : 2;
+            const int64_t tiles_64 = ((p.M + 63) / 64) * static_cast<int64_t>((p.NO + 63) / 64);
+            if (p.K <= 256)
+                variant = tiles_64 <= 40 ? 24 : tiles_64 <= 100 ? 23 : tiles_64 <= 1100 ? 25 : tiles_128 < 1024 ? 5 : 2;
+            else
+                variant = tiles_64 < 512 ? 25 : 2;
         }
     }
     switch (variant) {
