@@ -417,10 +417,10 @@ template <typename T>
 int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
     if (variant <= 0) {
         // measured on MI355X (16-bit):
-        //   256 outputs, K = 128 or 256, from 36000 rows: the streaming kernel (22) (K = 256: M = 40000 15.4 µs
-        //     against 16.6 for 13, M = 44446 15.7 against 17.1, M = 60000 16.6 against 23.0; K = 128: M = 44446
-        //     11.7 against 12.3; it loses at 30000 rows, 15.0 against 13.1, where its start, W into every CU's LDS,
-        //     is not paid back);
+        //   256 outputs, K = 128 or 256, from 16500 rows: the streaming kernel (22) (K = 256: M = 16800 10.5 µs
+        //     against 11.2 for 13 and 12.2 for 25, M = 20000 10.9 against 11.8, M = 33600 12.8 against 15.4,
+        //     M = 67200 19.5 against 23.5; K = 128: M = 16800 7.4 against 8.5; it loses at 16384 rows, 10.8 against
+        //     9.9 for 25, where its start, W into every CU's LDS, is not paid back);
         //   deep K (K >= 512, K % 64 == 0) on a grid of at least 200 tiles of 256 x 128: the direct-to-LDS kernel,
         //     256 x 256 tiles (16) from 2.5 rounds of them on 256 CUs, else 256 x 128 (14) (C = 1024: M = 43520
         //     101 µs against 122 µs for 13; M = 21760 57 against 68; M = 7200 23.6 against 29.2 for 13);
@@ -441,7 +441,7 @@ int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
         const int64_t tiles_128 = ((p.M + 127) / 128) * static_cast<int64_t>((p.NO + 127) / 128);
         const int64_t tiles_256x128 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 127) / 128);
         const int64_t tiles_256 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 255) / 256);
-        if (sizeof(T) == 2 && p.M >= 36000 && gemm_stream_fits(std::is_same<T, bf16>::value ? kBF16 : kF16, p)) {
+        if (sizeof(T) == 2 && p.M >= 16500 && gemm_stream_fits(std::is_same<T, bf16>::value ? kBF16 : kF16, p)) {
             variant = 22;
         } else if (sizeof(T) == 2) {
             const int64_t tiles_64 = ((p.M + 63) / 64) * static_cast<int64_t>((p.NO + 63) / 64);

@@ -5,9 +5,12 @@
 // (512 bytes), 128 flops per byte, below MI355X's ridge. A tiled GEMM spends a tile's short life (K / 32 chunks)
 // on staging W and crossing barriers; this kernel instead keeps W resident and lets every wavefront stream:
 //   * one workgroup per CU (persistent grid), W (64 or 128 KB) and the bias staged into LDS once;
-//   * each wavefront owns a contiguous range of tokens (an equal share of M) and walks it in steps of 32 tokens,
-//     loading the token rows straight from HBM into MFMA fragments two steps ahead of the MFMAs (double buffer,
-//     no barrier inside the loop, no LDS traffic for the tokens);
+//   * each workgroup owns an equal share of M and walks it in rounds of 4 x 32 tokens, one 32-token step per
+//     wavefront, loading the token rows straight from HBM into MFMA fragments two steps ahead of the MFMAs (double
+//     buffer, no barrier inside the loop, no LDS traffic for the tokens). A short remainder (at most 64 tokens at
+//     K = 256, 32 at K = 128) goes through in steps that all four wavefronts take together, each computing a
+//     quarter of the 256 channels, so it costs a quarter step per 32 tokens instead of a whole step; a longer one
+//     is spread evenly, every wavefront walking a quarter of the share;
 //   * the product is formed transposed, D = W . tokens^T on v_mfma_f32_16x16x32, so a lane's 4 accumulators are 4
 //     output channels of one token. The W rows of the 16 x 16 output tiles are permuted so that tiles 2p and 2p + 1
 //     give lane (r, kg) channels 32 p + 8 kg .. + 3 and + 4 .. + 7 of token r: 8 consecutive channels, one 16-byte
@@ -15,6 +18,8 @@
 // LDS layout of W: [256 rows][K / 8 chunks of 16 bytes], chunk c of row n at slot c ^ key(n) with
 // key(n) = ((n >> 1) & 12) | (n & 3), which differs across the 16 rows of one fragment read (one chunk each), so they
 // fall in 16 distinct 16-byte bank groups.
+#include <type_traits>
+
 #include "td_gemm.h"
 
 namespace td {
@@ -38,7 +43,7 @@ __device__ __forceinline__ void load_lds16(const void* src, void* dst) {
     __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
 }
 
-template <typename T, int KB>
+template <typename T, int KB, bool SPLIT>
 __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_stream_kernel(
     GemmParams p) {
     constexpr int NT = kStreamNO / 16;  // output tiles of 16 channels
@@ -54,21 +59,44 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
     const T* __restrict__ bias = static_cast<const T*>(p.bias);
     T* __restrict__ C = static_cast<T*>(p.c);
     const int M = p.M, K = p.K;
-    const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int r = lane & 15, kg = lane >> 4;
 
-    // this wavefront's tokens [lo, hi): an equal share of M; steps of 32 tokens from lo, the last one partial
+    // this workgroup's tokens [lo, hi): an equal share of M, taken one of two ways.
+    //  * Rounds (SPLIT, and the share is whole rounds of 4 x 32 tokens plus a short remainder): step i < R is tokens
+    //    lo + 128 i + 32 wave .. + 31, all 256 channels; each remainder step i >= R is tokens lo + 128 R + 32 (i - R)
+    //    .. + 31 for every wavefront, channels 64 wave .. + 63 (tiles 4 wave .. + 3). Remainder steps pay a step's
+    //    latency each for a quarter of its MFMAs: at K = 256 two of them beat a round, at K = 128 (half the MFMAs
+    //    per step) only one does (80000 x 128: 16.1 against 14.7 µs with two).
+    //  * Otherwise every wavefront walks an equal quarter [wlo, whi) of the share in steps of 32, all channels. A
+    //    last round that only some wavefronts fill would leave the others idle and the first ones with more stores
+    //    (80000 x 128: 16.3 against 14.7 µs).
+    //  Without SPLIT the quarters are taken over the whole of M (the same split up to rounding).
+    const int lo = static_cast<int>(static_cast<int64_t>(blockIdx.x) * M / gridDim.x);
+    const int hi = static_cast<int>(static_cast<int64_t>(blockIdx.x + 1) * M / gridDim.x);
+    constexpr int kRound = 32 * kStreamWaves, kRemMax = KB == 8 ? 2 * 32 : 32;
+    const int rem = (hi - lo) % kRound;
+    const bool rounds = SPLIT && rem <= kRemMax;  // the same for the whole workgroup
     const int64_t nw = static_cast<int64_t>(gridDim.x) * kStreamWaves;
     const int64_t gw = static_cast<int64_t>(blockIdx.x) * kStreamWaves + wave;
-    const int lo = static_cast<int>(gw * M / nw), hi = static_cast<int>((gw + 1) * M / nw);
-    const int last = hi > lo ? lo + (hi - lo - 1) / 32 * 32 : lo;  // first token of the last step
-    const int mmax = hi > lo ? hi - 1 : 0;                          // last row a load may touch
+    const int wlo = !SPLIT ? static_cast<int>(gw * M / nw) : rounds ? lo : lo + (hi - lo) * wave / kStreamWaves;
+    const int whi = !SPLIT ? static_cast<int>((gw + 1) * M / nw)
+                           : rounds ? hi : lo + (hi - lo) * (wave + 1) / kStreamWaves;
+    const int R = rounds ? (hi - lo) / kRound : (whi - wlo + 31) / 32;  // steps over all 256 channels
+    const int ns = rounds ? R + (rem + 31) / 32 : R;                  // steps of this wavefront
+    const int mmax = whi > wlo ? whi - 1 : 0;                         // last row a load may touch
+    auto tok = [&](int i) {
+        i = i < ns ? i : ns - 1;
+        if (!rounds) return wlo + 32 * i;
+        return i < R ? lo + 32 * (kStreamWaves * i + wave) : lo + 32 * (kStreamWaves * R + i - R);
+    };
 
-    // token fragments of one step: lane (r, kg) holds token m0 + 16 s + r, k = 32 kb + 8 kg .. + 7. Rows past hi
-    // read row hi - 1 (never stored) and a step past the last re-reads the last step (L2 hits), so every load is
+    // token fragments of step i: lane (r, kg) holds token tok(i) + 16 s + r, k = 32 kb + 8 kg .. + 7. Rows past whi
+    // read row whi - 1 (never stored) and a step past the last re-reads the last step (L2 hits), so every load is
     // unconditional and the compiler's wait counts stay exact.
-    auto load = [&](u32x4 (&tf)[TM][KB], int m0) {
-        m0 = m0 < last ? m0 : last;
+    auto load = [&](u32x4 (&tf)[TM][KB], int i) {
+        const int m0 = tok(i);
 #pragma unroll
         for (int s = 0; s < TM; ++s) {
             int m = m0 + s * 16 + r;
@@ -105,23 +133,23 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
     __builtin_amdgcn_s_waitcnt(7 << 4);  // vmcnt(0), lgkmcnt(0): W and the bias landed
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (hi <= lo) return;
+    if (whi <= wlo) return;
     u32x4 ta[TM][KB], tb[TM][KB];
-    load(ta, lo);
-    load(tb, lo + 32);
 
-    auto mma = [&](const u32x4 (&tf)[TM][KB], f32x4 (&acc)[TM][NT]) {
+    // the MFMAs of one step over NTW output tiles from tile t0 (all 16, or a wavefront's quarter)
+    auto mma = [&](auto ntw, const u32x4 (&tf)[TM][KB], f32x4 (&acc)[TM][decltype(ntw)::value], int t0) {
+        constexpr int NTW = decltype(ntw)::value;
 #pragma unroll
         for (int s = 0; s < TM; ++s)
 #pragma unroll
-            for (int t = 0; t < NT; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int t = 0; t < NTW; ++t) acc[s][t] = f32x4{0.f, 0.f, 0.f, 0.f};
         // W fragment j = (kb, t): lane r reads row n = 32 (t / 2) + 8 (r / 4) + 4 (t % 2) + r % 4, chunk 4 kb + kg.
         // The fragments pass through a ring of DEPTH registers, each read DEPTH fragments ahead of its MFMAs; the
         // scheduling groups keep one LDS read between every two MFMAs.
-        constexpr int J = KB * NT, DEPTH = 8;
+        constexpr int J = KB * NTW, DEPTH = 8;
         const int rrow = 8 * (r >> 2) + (r & 3), rkey = wkey(rrow);  // wkey(n) is the same for every t
         auto rd = [&](int j) {
-            const int kb = j / NT, t = j - kb * NT;
+            const int kb = j / NTW, t = t0 + j - kb * NTW;
             const int n = 32 * (t >> 1) + 4 * (t & 1) + rrow;
             return ws[n * CH + ((kb * 4 + kg) ^ rkey)];
         };
@@ -132,7 +160,7 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
         __builtin_amdgcn_sched_group_barrier(0x100, DEPTH, 0);  // the first DEPTH LDS reads
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const int kb = j / NT, t = j - kb * NT;
+            const int kb = j / NTW, t = j - kb * NTW;
             const u32x4 wf = ring[j % DEPTH];
             if (j + DEPTH < J) ring[j % DEPTH] = rd(j + DEPTH);
 #pragma unroll
@@ -142,24 +170,26 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    auto store = [&](const f32x4 (&acc)[TM][NT], int m0) {
+    auto store = [&](auto ntw, const f32x4 (&acc)[TM][decltype(ntw)::value], int m0, int t0) {
         // lane (r, kg) holds channels 32 p + 8 kg .. + 7 of token m0 + 16 s + r in tiles 2p (first 4) and 2p + 1
+        constexpr int NTW = decltype(ntw)::value;
 #pragma unroll
         for (int s = 0; s < TM; ++s) {
             const int m = m0 + s * 16 + r;
-            if (m >= hi) continue;
+            if (m >= whi) continue;
             T* const row = C + out_row(p, m);
 #pragma unroll
-            for (int pp = 0; pp < NT / 2; ++pp) {
+            for (int pp = 0; pp < NTW / 2; ++pp) {
+                const int ch = 16 * t0 + 32 * pp + 8 * kg;
                 Out8<T> bv = {};
-                if (bias != nullptr) bv = __builtin_bit_cast(Out8<T>, *reinterpret_cast<const u32x4*>(bs + 32 * pp + 8 * kg));
+                if (bias != nullptr) bv = __builtin_bit_cast(Out8<T>, *reinterpret_cast<const u32x4*>(bs + ch));
                 Out8<T> o;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     o.v[e] = static_cast<T>(acc[s][2 * pp][e] + cvt<float>(bv.v[e]));
                     o.v[4 + e] = static_cast<T>(acc[s][2 * pp + 1][e] + cvt<float>(bv.v[4 + e]));
                 }
-                *reinterpret_cast<u32x4*>(row + out_col(p, 32 * pp + 8 * kg)) = __builtin_bit_cast(u32x4, o);
+                *reinterpret_cast<u32x4*>(row + out_col(p, ch)) = __builtin_bit_cast(u32x4, o);
             }
         }
     };
@@ -167,19 +197,63 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
     // Each step stores its outputs, then requests the next-but-one step's tokens into the registers its MFMAs have
     // just read. In the other order (tokens, then stores) the compiler's waits before the next MFMAs covered the
     // token requests just issued as well, and the two-step prefetch stopped overlapping (M = 88892: 25.0 against
-    // 24.2 µs; 177784: 42.3 against 39.2)
-    f32x4 acc[TM][NT];
-    for (int m0 = lo;;) {
-        mma(ta, acc);
-        store(acc, m0);
-        load(ta, m0 + 64);
-        m0 += 32;
-        if (m0 >= hi) break;
-        mma(tb, acc);
-        store(acc, m0);
-        load(tb, m0 + 64);
-        m0 += 32;
-        if (m0 >= hi) break;
+    // 24.2 µs; 177784: 42.3 against 39.2). A step is a round step or a remainder step by a uniform branch inside
+    // the one loop: a remainder loop of its own after this one made the compiler's waits at this loop's head cover
+    // the loads just issued.
+    using Full = std::integral_constant<int, NT>;
+    using Quarter = std::integral_constant<int, NT / kStreamWaves>;
+    auto step = [&](u32x4 (&x)[TM][KB], int i) {
+        if (!SPLIT || i < R) {
+            f32x4 acc[TM][NT];
+            mma(Full{}, x, acc, 0);
+            store(Full{}, acc, tok(i), 0);
+        } else {
+            f32x4 acc[TM][Quarter::value];
+            mma(Quarter{}, x, acc, wave * Quarter::value);
+            store(Quarter{}, acc, tok(i), wave * Quarter::value);
+        }
+        load(x, i + 2);
+    };
+    if constexpr (SPLIT) {
+        load(ta, 0);
+        load(tb, 1);
+        for (int i = 0;;) {
+            step(ta, i);
+            if (++i >= ns) break;
+            step(tb, i);
+            if (++i >= ns) break;
+        }
+    } else {
+        // the same walk by token offsets, the form the compiler schedules best when every step is whole (its one
+        // full wait per two steps lands before the next tokens are requested, not after the stores: M = 88892
+        // 23.3 against 24.3 µs)
+        const int last = wlo + (whi - wlo - 1) / 32 * 32;  // first token of the last step
+        auto load_at = [&](u32x4 (&tf)[TM][KB], int m0) {
+            m0 = m0 < last ? m0 : last;
+#pragma unroll
+            for (int s = 0; s < TM; ++s) {
+                int m = m0 + s * 16 + r;
+                m = m < mmax ? m : mmax;
+                const T* row = A + static_cast<size_t>(m) * K + kg * 8;
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb) tf[s][kb] = *reinterpret_cast<const u32x4*>(row + kb * 32);
+            }
+        };
+        load_at(ta, wlo);
+        load_at(tb, wlo + 32);
+        f32x4 acc[TM][NT];
+        for (int m0 = wlo;;) {
+            mma(Full{}, ta, acc, 0);
+            store(Full{}, acc, m0, 0);
+            load_at(ta, m0 + 64);
+            m0 += 32;
+            if (m0 >= whi) break;
+            mma(Full{}, tb, acc, 0);
+            store(Full{}, acc, m0, 0);
+            load_at(tb, m0 + 64);
+            m0 += 32;
+            if (m0 >= whi) break;
+        }
     }
 }
 
@@ -196,28 +270,31 @@ int cu_count() {
     return cached[dev];
 }
 
-template <typename T, int KB>
-int go_stream(GemmParams p, hipStream_t stream) {
+template <typename T, int KB, bool SPLIT>
+int go_stream(GemmParams p, int64_t grid, hipStream_t stream) {
     constexpr size_t lds = static_cast<size_t>(kStreamNO) * KB * 4 * 16 + kStreamNO * sizeof(T);
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_stream_kernel<T, KB>),
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_stream_kernel<T, KB, SPLIT>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                                        static_cast<int>(lds));
     if (attr != hipSuccess) return set_error(-3, "value_proj: LDS size attribute refused: %s", hipGetErrorString(attr));
-    // one workgroup per CU, but at least 64 tokens per wavefront (W is staged once per workgroup)
-    int64_t grid = (static_cast<int64_t>(p.M) + 64 * kStreamWaves - 1) / (64 * kStreamWaves);
-    const int cus = cu_count();
-    if (grid > cus) grid = cus;
-    if (grid < 1) grid = 1;
-    hipLaunchKernelGGL((gemm_stream_kernel<T, KB>), dim3(static_cast<unsigned>(grid)), dim3(kStreamWaves * kWave), lds,
-                       stream, p);
+    hipLaunchKernelGGL((gemm_stream_kernel<T, KB, SPLIT>), dim3(static_cast<unsigned>(grid)), dim3(kStreamWaves * kWave),
+                       lds, stream, p);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : set_error(-3, "value_proj launch failed: %s", hipGetErrorString(e));
 }
 
+// One workgroup per CU, but at least one round of 4 x 32 tokens per workgroup (W is staged once per workgroup). The
+// workgroups' shares differ by at most one token; the kernel with the remainder path (SPLIT) runs only when a share
+// ends in a short remainder, since that path's code slows the other steps down (M = 88892: 24.0 against 23.3 µs).
 template <typename T>
 int stream_t(GemmParams p, hipStream_t stream) {
-    if (p.K == 256) return go_stream<T, 8>(p, stream);
-    return go_stream<T, 4>(p, stream);
+    int64_t grid = (static_cast<int64_t>(p.M) + 32 * kStreamWaves - 1) / (32 * kStreamWaves);
+    const int cus = cu_count();
+    if (grid > cus) grid = cus;
+    if (grid < 1) grid = 1;
+    const int64_t rem = (p.M / grid) % (32 * kStreamWaves);
+    if (p.K == 256) return rem < 2 * 32 ? go_stream<T, 8, true>(p, grid, stream) : go_stream<T, 8, false>(p, grid, stream);
+    return rem < 32 ? go_stream<T, 4, true>(p, grid, stream) : go_stream<T, 4, false>(p, grid, stream);
 }
 
 }  // namespace

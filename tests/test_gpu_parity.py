@@ -211,11 +211,16 @@ def test_value_proj_deep_k_matches_oracle(dtype):
 
 @pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
 def test_value_proj_streaming_matches_oracle(dtype):
-    # 16-bit, 256 outputs, K = 128 or 256, from 36000 rows: the streaming kernel (W resident in LDS, each wavefront
-    # an equal share of the rows in steps of 32 with a partial last step). Every row is checked: the wavefront
-    # boundaries fall anywhere in M. Odd M, with and without bias.
+    # 16-bit, 256 outputs, K = 128 or 256, from 16500 rows: the streaming kernel (W resident in LDS; each workgroup
+    # an equal share of the rows). Shares that end in a short remainder go in rounds of 4 x 32 tokens and then
+    # remainder steps in which every wavefront computes a quarter of the channels: one such step (36001, 33600,
+    # 67200 at K = 256; 70003 at K = 128), two (44447 at K = 256), none (131072). Other shares are split evenly over
+    # the wavefronts in steps of 32 with a partial last step (16800, 20011, 44447 at K = 128, 88892). Every row is
+    # checked: the boundaries fall anywhere in M. Odd M, with and without bias.
     g = torch.Generator().manual_seed(12)
-    for (M, K, bias) in ((36001, 256, True), (67200, 256, True), (44447, 128, False), (70003, 128, True)):
+    for (M, K, bias) in ((36001, 256, True), (33600, 256, False), (67200, 256, True), (44447, 256, False),
+                         (131072, 256, True), (16800, 256, True), (88892, 256, True), (70003, 128, True),
+                         (44447, 128, False), (20011, 128, True)):
         say(f'  value_proj streaming {dtype} M={M} K={K} bias={bias}')
         mem = torch.randn(1, M, K, generator=g).to(dtype)
         w = (torch.randn(256, K, generator=g) / K ** 0.5).to(dtype)
@@ -238,7 +243,7 @@ def heads_of(value, H):
 def test_value_proj_heads_matches_oracle():
     # the head-major GEMM output: row b * N + t, column h * D + d lands at [b, h, t, d]. Shapes reach every tile
     # family: 64 x 64 one-chunk (1 x 8400), LDS 128 x 128 (4 x 9000, 2 x 8192 x 1024 outputs), direct-to-LDS
-    # (K = 576), the streaming kernel (16-bit, 256 outputs, K = 256 or 128, from 36000 rows), ragged B, N and heads
+    # (K = 576), the streaming kernel (16-bit, 256 outputs, K = 256 or 128, from 16500 rows), ragged B, N and heads
     # of 16 bytes. Every row is checked.
     g = torch.Generator().manual_seed(21)
     shapes = {torch.float16: ((1, 8400, 256, 8, 32), (4, 9000, 256, 8, 32), (2, 8192, 128, 32, 32),
