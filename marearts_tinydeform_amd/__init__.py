@@ -31,9 +31,9 @@ MODES = ('auto', 'fused', 'project')
 #   fused   = f0 + f1 * gathered_mb
 #   project = p0 + p1 * gemm_mb + p2 * gemm_gflop + p3 * sample_mb
 FUSED_LIMIT = {
-    torch.float32: {'fused': (8.6391, 0.0530), 'project': (19.5112, 0.6407, 0.0000, 0.0867)},
-    torch.float16: {'fused': (6.3135, 0.0618), 'project': (11.8753, 0.1007, 0.8887, 0.0891)},
-    torch.bfloat16: {'fused': (6.3135, 0.0618), 'project': (11.8753, 0.1007, 0.8887, 0.0891)},
+    torch.float32: {'fused': (8.6944, 0.0528), 'project': (15.1746, 0.6783, 0.0000, 0.0830)},
+    torch.float16: {'fused': (6.3746, 0.0618), 'project': (11.4986, 0.0872, 0.8761, 0.0911)},
+    torch.bfloat16: {'fused': (6.3746, 0.0618), 'project': (11.4986, 0.0872, 0.8761, 0.0911)},
 }
 
 # cost tables by GPU architecture (gcnArchName without feature suffixes)
