@@ -243,13 +243,14 @@ def heads_of(value, H):
 def test_value_proj_heads_matches_oracle():
     # the head-major GEMM output: row b * N + t, column h * D + d lands at [b, h, t, d]. Shapes reach every tile
     # family: 64 x 64 one-chunk (1 x 8400), LDS 128 x 128 (4 x 9000, 2 x 8192 x 1024 outputs), direct-to-LDS
-    # (K = 576), the streaming kernel (16-bit, 256 outputs, K = 256 or 128, from 16500 rows), ragged B, N and heads
-    # of 16 bytes. Every row is checked.
+    # (K = 576), the streaming kernel (16-bit, 256 outputs, K = 256 or 128, from 16500 rows; its even split at
+    # 2 x 30001 and 3 x 20011, rounds with a quarter-channel remainder step at 4 x 8400 and 8 x 8400), ragged B, N
+    # and heads of 16 bytes. Every row is checked.
     g = torch.Generator().manual_seed(21)
     shapes = {torch.float16: ((1, 8400, 256, 8, 32), (4, 9000, 256, 8, 32), (2, 8192, 128, 32, 32),
                               (3, 77, 40, 6, 8), (2, 2501, 576, 17, 8), (2, 30001, 256, 8, 32),
-                              (3, 20011, 128, 16, 16)),
-              torch.bfloat16: ((1, 8400, 256, 8, 32), (2, 30001, 256, 8, 32), (5, 131, 96, 3, 24)),
+                              (3, 20011, 128, 16, 16), (4, 8400, 256, 8, 32)),
+              torch.bfloat16: ((1, 8400, 256, 8, 32), (2, 30001, 256, 8, 32), (5, 131, 96, 3, 24), (8, 8400, 256, 8, 32)),
               torch.float32: ((1, 8400, 256, 8, 16), (2, 77, 40, 5, 4), (3, 1000, 64, 2, 12)),
               torch.float64: ((2, 77, 40, 4, 2), (1, 300, 256, 8, 8))}
     for dtype, cases in shapes.items():
