@@ -201,6 +201,16 @@ int td_value_proj(int dtype, const void* memory, const void* weight, const void*
                   int64_t K, int64_t NO, void* stream);
 
 /*
+ * Which value-projection kernel td_value_proj (head_major_N = 0) or td_value_proj_heads (head_major_N = N, with H
+ * heads) launches for these operands: the tile variant number, 0 for the generic VALU kernel, or a negative TD_E*
+ * code. The pointers are only inspected for their alignment, never read, so any address of the right alignment will
+ * do. No counterpart in the reference (it calls F.linear); for tests and tuning, which check that every kernel the
+ * size rule can pick has a parity case.
+ */
+int td_value_proj_plan(int dtype, const void* memory, const void* weight, const void* bias, const void* value,
+                       int64_t M, int64_t K, int64_t NO, int64_t head_major_N, int64_t H);
+
+/*
  * Backward (training). No counterpart in the reference, whose operator is inference only (README.md:61); these are
  * the gradients of its reference computation (reference.py:13-40: value = memory . W^T + b, then bilinear
  * grid_sample with zero padding, align_corners=False, weighted by the attention), for callers that train through

@@ -41,6 +41,7 @@ SIGNATURES = {
     'td_input_grad': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     'td_weight_grad_workspace': (_i64, [_int, _i64, _i64, _i64]),
     'td_weight_grad': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
+    'td_value_proj_plan': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64]),
 }
 
 TD_E_WORKSPACE = -4  # td_layer_fused_forward: the problem needs loc_out / attn_out
@@ -289,6 +290,23 @@ def value_proj(memory, weight, bias):
     _check(lib_.td_value_proj(DTYPE_CODES[memory.dtype], mem.data_ptr(), w.data_ptr(), _ptr(b), value.data_ptr(),
                               B * N, C, HD, _stream(dev)))
     return value
+
+
+def value_proj_plan(dtype, M, K, NO, bias=True, offsets=None, heads=None, N=None):
+    """The tile variant td_value_proj (or, with heads and N, td_value_proj_heads) launches for an [M, K] x [NO, K]^T
+    problem (0: the generic VALU kernel). offsets: byte offsets from a 256-byte boundary of the memory, weight, bias
+    and value pointers, as a dict with any of those keys (default 0); bias=False: no bias. No memory is touched."""
+    lib_ = _require()
+    off = {'memory': 0, 'weight': 0, 'bias': 0, 'value': 0}
+    off.update(offsets or {})
+    base = 1 << 20
+    ptrs = [base * (i + 1) + off[k] for i, k in enumerate(('memory', 'weight', 'bias', 'value'))]
+    if not bias:
+        ptrs[2] = None
+    rc = lib_.td_value_proj_plan(DTYPE_CODES[dtype], *ptrs, M, K, NO, N or 0, heads or 0)
+    if rc < 0:
+        _check(rc)
+    return rc
 
 
 def _check_locations(ref, spatial_shapes, level_start_index, loc, attn, loc_acc):

@@ -331,7 +331,7 @@ extern "C" int td_value_proj_heads(int dtype, const void* memory, const void* we
     if (B * N == 0) return TD_OK;
     if (value == nullptr || (C > 0 && (memory == nullptr || weight == nullptr)))
         return set_error(TD_E_ARG, "null pointer argument");
-    return launch_value_proj(dtype, memory, weight, bias, value, B * N, C, H * D, static_cast<hipStream_t>(stream), 0,
+    return launch_value_proj(dtype, memory, weight, bias, value, B * N, C, H * D, static_cast<hipStream_t>(stream),
                              static_cast<int>(N), static_cast<int>(H));
 }
 
@@ -369,7 +369,7 @@ extern "C" int td_project_forward(int dtype, const void* memory, const void* val
     if (value_ws == nullptr || (C > 0 && (memory == nullptr || value_weight == nullptr)))
         return set_error(TD_E_ARG, "null pointer argument");
     const bool hm = head_major_pays(dtype, D);
-    rc = launch_value_proj(dtype, memory, value_weight, value_bias, value_ws, B * N, C, H * D, s, 0,
+    rc = launch_value_proj(dtype, memory, value_weight, value_bias, value_ws, B * N, C, H * D, s,
                            hm ? static_cast<int>(N) : 0, hm ? static_cast<int>(H) : 0);
     if (rc != TD_OK) return rc;
     if (hm)
@@ -409,7 +409,20 @@ extern "C" int td_value_proj(int dtype, const void* memory, const void* weight, 
     if (M * NO == 0) return TD_OK;
     if (value == nullptr || (K > 0 && (memory == nullptr || weight == nullptr)))
         return set_error(TD_E_ARG, "null pointer argument");
-    return launch_value_proj(dtype, memory, weight, bias, value, M, K, NO, static_cast<hipStream_t>(stream), 0);
+    return launch_value_proj(dtype, memory, weight, bias, value, M, K, NO, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int td_value_proj_plan(int dtype, const void* memory, const void* weight, const void* bias,
+                                  const void* value, int64_t M, int64_t K, int64_t NO, int64_t head_major_N,
+                                  int64_t H) {
+    g_last_error.clear();
+    if (!dtype_ok(dtype)) return set_error(TD_E_DTYPE, "unknown dtype code %d", dtype);
+    if (M < 0 || K < 0 || NO < 0 || head_major_N < 0) return set_error(TD_E_ARG, "sizes must be non-negative");
+    if (M > kInt32Max || K > kInt32Max || NO > kInt32Max) return set_error(TD_E_ARG, "GEMM size exceeds int32");
+    if (head_major_N > 0 && (H <= 0 || NO % H != 0 || M % head_major_N != 0))
+        return set_error(TD_E_ARG, "head-major output needs H dividing NO and N dividing M");
+    return value_proj_plan(dtype, memory, weight, bias, value, M, K, NO, static_cast<int>(head_major_N),
+                           static_cast<int>(head_major_N > 0 ? H : 0));
 }
 
 extern "C" int td_sample_backward(int dtype, const void* value, const int64_t* spatial_shapes,
@@ -447,7 +460,7 @@ extern "C" int td_input_grad(int dtype, const void* grad_value, const void* valu
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const int rc = launch_transpose(dtype, value_weight, weight_t, HD, C, s);
     if (rc != TD_OK) return rc;
-    return launch_value_proj(dtype, grad_value, weight_t, nullptr, grad_memory, M, HD, C, s, 0);
+    return launch_value_proj(dtype, grad_value, weight_t, nullptr, grad_memory, M, HD, C, s);
 }
 
 extern "C" int64_t td_weight_grad_workspace(int dtype, int64_t M, int64_t HD, int64_t C) {

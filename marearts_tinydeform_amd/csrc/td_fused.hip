@@ -74,7 +74,8 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     Corner<float>* cw = reinterpret_cast<Corner<float>*>(smem);  // [QT][S]
     float* gs = reinterpret_cast<float*>(cw + QT * S);           // [QT][GP]
     float* wsum = gs + QT * GP;                                   // [16]
-    float* part = wsum + 16;                                      // [KS][16][PW]
+    unsigned* gmax = reinterpret_cast<unsigned*>(wsum + 16);      // [1] float16: largest |g| above 2^15 (bits)
+    float* part = wsum + 20;                                      // [KS][16][PW]
     float* pro = part + p.KS * 16 * PW;                           // layer: [16][PP] query projections
     float* rstat = pro + 16 * PP;                                 // layer: [16][2] softmax max, 1 / sum
 
@@ -102,6 +103,7 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     }
 
     // phase 1: corner table
+    if (tid == 0) *gmax = 0u;
     for (int i = tid; i < QT * LP; i += NTH) {
         const int r = i / LP, j = i - r * LP, q = q0 + r;
         Corner<float>* c4 = cw + r * S + 4 * j;
@@ -142,6 +144,12 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
             for (int i = 0; i < V; i += 4)
                 *reinterpret_cast<f32x4*>(dst + i) = f32x4{acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
             if (ch == 0) wsum[r] = ws;
+            if constexpr (std::is_same<T, f16>::value) {
+                float m = 0.f;
+#pragma unroll
+                for (int i = 0; i < V; ++i) m = fmaxf(m, fabsf(acc[i]));
+                if (m > 32768.f) atomicMax(gmax, __float_as_uint(m));  // rare: un-normalised weights, huge memory
+            }
         }
     }
     __syncthreads();
@@ -151,6 +159,19 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     const int n16 = lane & 15, kg = lane >> 4;
     const bool av = n16 < QT;
     const float* ga = gs + (av ? n16 : 0) * GP;
+    // float16 splits g into hi + lo halves of 16 bits, and hi overflows past 65504. When some |g| of the workgroup
+    // exceeds 2^15, g is scaled by a power of two sc that brings the largest below 2^14 and the products by 1 / sc
+    // (both exact), so the output stays what float32 accumulation gives, as in the reference.
+    float sc = 1.f, inv_sc = 1.f;
+    if constexpr (std::is_same<T, f16>::value) {
+        const float mx = __uint_as_float(*gmax);
+        if (mx > 32768.f && mx <= 3.4e38f) {
+            int e;
+            frexpf(mx, &e);  // mx < 2^e
+            sc = ldexpf(1.f, 14 - e);
+            inv_sc = ldexpf(1.f, e - 14);
+        }
+    }
     if constexpr (sizeof(T) == 2) {
         using M = MfmaOp<T>;
         using frag = typename M::frag;
@@ -170,8 +191,8 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
                 if (dv && kv) braw = *reinterpret_cast<const u32x4*>(wr + k);
                 f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
                 if (av && kv) {
-                    a0 = *reinterpret_cast<const f32x4*>(ga + k);
-                    a1 = *reinterpret_cast<const f32x4*>(ga + k + 4);
+                    a0 = *reinterpret_cast<const f32x4*>(ga + k) * sc;
+                    a1 = *reinterpret_cast<const f32x4*>(ga + k + 4) * sc;
                 }
                 frag hi, lo;
 #pragma unroll
@@ -222,6 +243,7 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
         if (q >= g.Q) continue;
         float v = part[r * PW + d];
         for (int ks = 1; ks < p.KS; ++ks) v += part[(ks * 16 + r) * PW + d];
+        v *= inv_sc;
         if (bias != nullptr) v = fmaf(cvt<float>(bias[static_cast<size_t>(br.h) * D + d]), wsum[r], v);
         out[((static_cast<size_t>(br.b) * g.Q + q) * g.H + br.h) * D + d] = static_cast<T>(v);
     }
@@ -392,7 +414,7 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
             const int PP = ((3 * LP + 15) & ~15) + 4;
             auto lds = [&](int q) {
                 return static_cast<size_t>(q) * S * sizeof(Corner<float>) + static_cast<size_t>(q) * GP * 4 +
-                       16 * 4 + static_cast<size_t>(ks) * 16 * NTILE * 16 * 4 +
+                       20 * 4 + static_cast<size_t>(ks) * 16 * NTILE * 16 * 4 +
                        (layer ? static_cast<size_t>(16 * PP + 32) * 4 : 0);
             };
             while (qt > 1 && lds(qt) > kLdsBudget) --qt;
@@ -410,11 +432,9 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
                     }
                 }
                 switch (waves) {
-                    case 1: return go_vec<T, 1, false>(p, lds(qt), stream);
-                    case 2: return go_vec<T, 2, false>(p, lds(qt), stream);
                     case 4: return go_vec<T, 4, false>(p, lds(qt), stream);
                     case 8: return go_vec<T, 8, false>(p, lds(qt), stream);
-                    default: return set_error(-1, "fused: waves must be 1, 2, 4 or 8 (got %d)", waves);
+                    default: return set_error(-1, "fused: waves must be 4 or 8 (got %d)", waves);
                 }
             }
         }

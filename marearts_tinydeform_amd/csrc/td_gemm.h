@@ -96,11 +96,11 @@ struct KBlock<float> {
 };
 
 // The direct-to-LDS kernel for large 16-bit problems (td_gemm_dma.hip): dtype kF16 or kBF16, K % 64 == 0,
-// 16-byte aligned operands, variant 14..18.
+// 16-byte aligned a and w; variant 14 (256 x 128 tiles) or 16 (256 x 256 tiles).
 int launch_gemm_dma(int dtype, GemmParams p, hipStream_t stream, int variant);
 
-// The streaming kernel for narrow K (td_gemm_stream.hip): 16-bit, NO = 256, K = 128 or 256, 16-byte aligned a, w, c;
-// a head-major output needs hm_D a multiple of 8.
+// The streaming kernel for narrow K (td_gemm_stream.hip): 16-bit, NO = 256, K = 128 or 256, 16-byte aligned a, w, c
+// and bias (or no bias); a head-major output needs hm_D a multiple of 8.
 bool gemm_stream_fits(int dtype, const GemmParams& p);
 int launch_gemm_stream(int dtype, GemmParams p, hipStream_t stream);
 

@@ -305,23 +305,7 @@ __global__ __launch_bounds__(WM* WN* kWave) void gemm_lds_kernel(GemmParams p) {
     }
 }
 
-// MFMA GEMM for large 16-bit problems with K a multiple of 64: 256 x BN tiles (BN = 256 or 128), four wavefronts
-// in a 2 x 2 grid, each owning 128 x BN/2 (8 x BN/32 tiles of 16 x 16: up to 256 accumulator registers per lane, one
-// wavefront per SIMD). The L2 → CU traffic per flop halves against 128 x 128 tiles, which is what lets the MFMAs
-// rather than the L2 set the pace.
-//
-// K streams through a ring of STAGES LDS buffers, STAGES - 1 chunks of 32 ahead of the MFMAs, by direct
-// global-to-LDS loads (global_load_lds_dwordx4: lane i's 16 bytes land at the wavefront's LDS base + 16 i), so the
-// staging costs no registers and no LDS store instructions. The compiler does not track these loads, so the
-// kernel orders them itself: `s_waitcnt vmcnt(n)` lets exactly the chunks after the one about to be read stay in
-// flight (8 loads per chunk per wavefront), and a plain `s_barrier` (no fence, which would drain every
-// outstanding load) then publishes the chunk (meet()); the same barrier tells every wavefront that the buffer refilled next
-// (the one read in the previous step) is no longer read.
-//
-// LDS layout of a staged operand: [rows][4 slots of 16 bytes]; row r's K piece kc (8 elements) sits in slot
-// kc ^ ((r >> 2) & 3), so each 16-lane phase of a fragment read (16 rows, one kc) touches 16 distinct 16-byte
-// bank groups. The swizzle is applied on the source side: the lane whose LDS slot is s loads piece s ^ f(row).
-// Rows past M or NO load the last valid row (their results are never stored), so no load is predicated.
+// VALU GEMM for float64, odd K and unaligned operands: 64 x 64 tiles, K in blocks of 16 through LDS.
 template <typename T>
 __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmParams p) {
     using A = typename AccOf<T>::type;
@@ -392,106 +376,85 @@ int go_mfma(GemmParams p, hipStream_t stream) {
               stream);
 }
 
-// Tile shape by problem size (variant > 0 forces one, for tuning). K per chunk = NKB 16-byte blocks
-// (32 elements each for 16-bit types, 16 for float32).
-//   1  64 x 64   4 waves of 16 x 64,  K chunks of 64/32, two stages
-//   2  64 x 128  4 waves of 16 x 128, K chunks of 64/32, two stages
-//   3  128 x 128 2 x 2 waves of 64 x 64, two stages
-//   4  128 x 64  4 waves of 32 x 64, two stages
-//   5  64 x 64   one chunk of 256/128 (K <= 256 for 16-bit: a single round trip), one stage
-//   6  64 x 128  one chunk of 256/128, one stage
-//   7  128 x 128 A and W both through LDS (2 x 2 waves of 64 x 64), K chunks of 64/32
-//   8  256 x 128 A and W through LDS (4 x 2 waves of 64 x 64)
-//   9  128 x 128 A and W through LDS, K chunks of 128/64
-//   10 128 x 256 A and W through LDS (2 x 4 waves of 64 x 64)
-//   11 128 x 256 A and W through LDS (2 x 2 waves of 64 x 128)
-//   12 256 x 128 A and W through LDS (2 x 2 waves of 128 x 64)
+// Kernel by problem size: the tile variants the size rule picks (K per chunk = NKB 16-byte blocks, 32 elements each
+// for 16-bit types, 16 for float32).
+//   2  64 x 128  4 waves of 16 x 128, A fragments from memory, W through LDS, K chunks of 64/32, two stages
+//   5  64 x 64   4 waves of 16 x 64, one chunk of 256/128 (K <= 256 for 16-bit: a single round trip), one stage
+//   9  128 x 128 A and W through LDS (2 x 2 waves of 64 x 64), K chunks of 128/64
 //   13 128 x 128 A and W through LDS, K chunks of 32/16
-//   14..21 256 x 128 / 256 x 256 tiles fed by direct-to-LDS loads (td_gemm_dma.hip; 16-bit, K % 64 == 0)
+//   14 256 x 128 tiles fed by direct-to-LDS loads (td_gemm_dma.hip; 16-bit, K % 64 == 0)
+//   16 256 x 256 tiles fed by direct-to-LDS loads (td_gemm_dma.hip; 16-bit, K % 64 == 0)
 //   22 the streaming kernel: W resident in LDS, token rows streamed into MFMA fragments (td_gemm_stream.hip;
 //      16-bit, NO = 256, K = 128 or 256)
 //   23 64 x 32   4 waves of 16 x 32, one chunk of 256/128, one stage
 //   24 32 x 32   2 waves of 16 x 32, one chunk of 256/128, one stage
 //   25 64 x 64   4 waves of 16 x 64, K chunks of 128/64, two stages
-template <typename T>
-int launch_mfma(GemmParams p, hipStream_t stream, int variant) {
-    if (variant <= 0) {
-        // measured on MI355X (16-bit):
-        //   256 outputs, K = 128 or 256, from 16500 rows: the streaming kernel (22) (K = 256: M = 16800 10.5 µs
-        //     against 11.2 for 13 and 12.2 for 25, M = 20000 10.9 against 11.8, M = 33600 12.8 against 15.4,
-        //     M = 67200 19.5 against 23.5; K = 128: M = 16800 7.4 against 8.5; it loses at 16384 rows, 10.8 against
-        //     9.9 for 25, where its start, W into every CU's LDS, is not paid back);
-        //   deep K (K >= 512, K % 64 == 0) on a grid of at least 200 tiles of 256 x 128: the direct-to-LDS kernel,
-        //     256 x 256 tiles (16) from 2.5 rounds of them on 256 CUs, else 256 x 128 (14) (C = 1024: M = 43520
-        //     101 µs against 122 µs for 13; M = 21760 57 against 68; M = 7200 23.6 against 29.2 for 13);
-        //   smaller grids by their count of 64 x 64 tiles (µs, against the former 64 x 64 one-chunk tiles, 5):
-        //     K <= 256: up to 300 tiles 32 x 32 (24) (NO = 256: M = 300 3.3 against 4.5, M = 2400 4.5 against 4.7),
-        //       up to 1100 64 x 64 with two-stage K chunks of 128 (25) (M = 8400 7.2 against 7.8, M = 16384 9.5
-        //       against 10.0), else 13 (M = 30000 12.9);
-        //     K >= 512: under 64 tiles 32 x 32 (24) (M = 100, K = NO = 1024: 6.5 against 10.2), under 128 64 x 32
-        //       (23) (M = 300: 8.0 against 10.2), under 512 two-stage 64 x 64 (25) (M = 600: 10.0 against 10.4,
-        //       M = 1800: 13.2 against 14.2), then both operands through LDS with K chunks of 128 (9) while under
-        //       512 tiles of 128 x 128 (M = 3600: 19.4 against 25.9), else 13.
-        // float32 (MFMA-bound: v_mfma_f32_16x16x4_f32), by the count of 64 x 64 tiles: K <= 256: up to 40 tiles
-        //   32 x 32 (24) (K = NO = 256: M = 300 6.0 µs against 9.4 for 5), up to 100 64 x 32 (23) (M = 1200 6.8
-        //   against 9.5), up to 1100 two-stage 64 x 64 (25) (M = 2400 9.2 against 9.7, M = 8400 19.8 against
-        //   20.9), then 64 x 64 one-chunk tiles (5) under 1024 tiles of 128 x 128 (M = 33600 54.4 against 56.2),
-        //   else A direct in 64 x 128 tiles (2) (M = 67200: 93.5 against 96.4); K >= 512: two-stage 64 x 64 (25)
-        //   under 512 tiles (M = 600, K = NO = 1024: 27.2 against 48.8 for 2), else 2.
-        const int64_t tiles_128 = ((p.M + 127) / 128) * static_cast<int64_t>((p.NO + 127) / 128);
-        const int64_t tiles_256x128 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 127) / 128);
-        const int64_t tiles_256 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 255) / 256);
-        if (sizeof(T) == 2 && p.M >= 16500 && gemm_stream_fits(std::is_same<T, bf16>::value ? kBF16 : kF16, p)) {
-            variant = 22;
-        } else if (sizeof(T) == 2) {
-            const int64_t tiles_64 = ((p.M + 63) / 64) * static_cast<int64_t>((p.NO + 63) / 64);
-            if (p.K >= 512 && p.K % 64 == 0 && tiles_256x128 >= 200)
-                variant = tiles_256 >= 640 ? 16 : 14;
-            else if (p.K <= 256)
-                variant = tiles_64 <= 300 ? 24 : tiles_64 <= 1100 ? 25 : 13;
-            else
-                variant = tiles_64 < 64 ? 24 : tiles_64 < 128 ? 23 : tiles_64 < 512 ? 25 : tiles_128 < 512 ? 9 : 13;
-        } else {
-            const int64_t tiles_64 = ((p.M + 63) / 64) * static_cast<int64_t>((p.NO + 63) / 64);
-            if (p.K <= 256)
-                variant = tiles_64 <= 40 ? 24 : tiles_64 <= 100 ? 23 : tiles_64 <= 1100 ? 25 : tiles_128 < 1024 ? 5 : 2;
-            else
-                variant = tiles_64 < 512 ? 25 : 2;
-        }
+//   0  gemm_generic_kernel (float64, odd K, A or W not 16-byte aligned)
+//
+// Measured on MI355X (16-bit):
+//   256 outputs, K = 128 or 256, from 16500 rows: the streaming kernel (22) (K = 256: M = 16800 10.5 µs against 11.2
+//     for 13 and 12.2 for 25, M = 20000 10.9 against 11.8, M = 33600 12.8 against 15.4, M = 67200 19.5 against 23.5;
+//     K = 128: M = 16800 7.4 against 8.5; it loses at 16384 rows, 10.8 against 9.9 for 25, where its start, W into
+//     every CU's LDS, is not paid back);
+//   deep K (K >= 512, K % 64 == 0) on a grid of at least 200 tiles of 256 x 128: the direct-to-LDS kernel, 256 x 256
+//     tiles (16) from 2.5 rounds of them on 256 CUs, else 256 x 128 (14) (C = 1024: M = 43520 101 µs against 122 µs
+//     for 13; M = 21760 57 against 68; M = 7200 23.6 against 29.2 for 13);
+//   smaller grids by their count of 64 x 64 tiles:
+//     K <= 256: up to 300 tiles 32 x 32 (24) (NO = 256: M = 300 3.3 against 4.5 for 64 x 64 one-chunk tiles, M = 2400
+//       4.5 against 4.7), up to 1100 64 x 64 with two-stage K chunks of 128 (25) (M = 8400 7.2 against 7.8,
+//       M = 16384 9.5 against 10.0), else 13 (M = 30000 12.9);
+//     K >= 512: under 64 tiles 32 x 32 (24) (M = 100, K = NO = 1024: 6.5 against 10.2), under 128 64 x 32 (23)
+//       (M = 300: 8.0 against 10.2), under 512 two-stage 64 x 64 (25) (M = 600: 10.0 against 10.4, M = 1800: 13.2
+//       against 14.2), then both operands through LDS with K chunks of 128 (9) while under 512 tiles of 128 x 128
+//       (M = 3600: 19.4 against 25.9), else 13.
+// float32 (MFMA-bound: v_mfma_f32_16x16x4_f32), by the count of 64 x 64 tiles: K <= 256: up to 40 tiles 32 x 32 (24)
+//   (K = NO = 256: M = 300 6.0 µs against 9.4 for 5), up to 100 64 x 32 (23) (M = 1200 6.8 against 9.5), up to 1100
+//   two-stage 64 x 64 (25) (M = 2400 9.2 against 9.7, M = 8400 19.8 against 20.9), then 64 x 64 one-chunk tiles (5)
+//   under 1024 tiles of 128 x 128 (M = 33600 54.4 against 56.2), else A direct in 64 x 128 tiles (2) (M = 67200: 93.5
+//   against 96.4); K >= 512: two-stage 64 x 64 (25) under 512 tiles (M = 600, K = NO = 1024: 27.2 against 48.8 for
+//   2), else 2.
+int pick_variant(int dtype, const GemmParams& p) {
+    if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return 0;
+    const int E = dtype == kF32 ? 4 : 8;
+    const uintptr_t al = reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.w);
+    if (p.K % E != 0 || al % 16 != 0) return 0;
+    const int64_t tiles_64 = ((p.M + 63) / 64) * static_cast<int64_t>((p.NO + 63) / 64);
+    const int64_t tiles_128 = ((p.M + 127) / 128) * static_cast<int64_t>((p.NO + 127) / 128);
+    if (dtype == kF32) {
+        if (p.K <= 256) return tiles_64 <= 40 ? 24 : tiles_64 <= 100 ? 23 : tiles_64 <= 1100 ? 25 : tiles_128 < 1024 ? 5 : 2;
+        return tiles_64 < 512 ? 25 : 2;
     }
-    switch (variant) {
-        case 1: return go_mfma<T, 4, 1, 1, 4, 2, 2>(p, stream);
-        case 2: return go_mfma<T, 4, 1, 1, 8, 2, 2>(p, stream);
-        case 3: return go_mfma<T, 2, 2, 4, 4, 2, 2>(p, stream);
-        case 4: return go_mfma<T, 4, 1, 2, 4, 2, 2>(p, stream);
-        case 5: return go_mfma<T, 4, 1, 1, 4, 8, 1>(p, stream);
-        case 6: return go_mfma<T, 4, 1, 1, 8, 8, 1>(p, stream);
-        case 23: return go_mfma<T, 4, 1, 1, 2, 8, 1>(p, stream);
-        case 24: return go_mfma<T, 2, 1, 1, 2, 8, 1>(p, stream);
-        case 25: return go_mfma<T, 4, 1, 1, 4, 4, 2>(p, stream);
-        case 7: return go_lds<T, 2, 2, 4, 4, 2>(p, stream);
-        case 8: return go_lds<T, 4, 2, 4, 4, 2>(p, stream);
-        case 9: return go_lds<T, 2, 2, 4, 4, 4>(p, stream);
-        case 10: return go_lds<T, 2, 4, 4, 4, 2>(p, stream);
-        case 11: return go_lds<T, 2, 2, 4, 8, 2>(p, stream);
-        case 12: return go_lds<T, 2, 2, 8, 4, 2>(p, stream);
-        case 13: return go_lds<T, 2, 2, 4, 4, 1>(p, stream);
-        case 14: case 15: case 16: case 17: case 18: case 19: case 20: case 21:
-            return launch_gemm_dma(std::is_same<T, bf16>::value ? kBF16 : std::is_same<T, f16>::value ? kF16 : -1, p,
-                                   stream, variant);
-        case 22:
-            return launch_gemm_stream(std::is_same<T, bf16>::value ? kBF16 : std::is_same<T, f16>::value ? kF16 : -1,
-                                      p, stream);
-        default: return set_error(-1, "value_proj: unknown tile variant %d", variant);
-    }
+    if (p.M >= 16500 && gemm_stream_fits(dtype, p)) return 22;
+    const int64_t tiles_256x128 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 127) / 128);
+    const int64_t tiles_256 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 255) / 256);
+    if (p.K >= 512 && p.K % 64 == 0 && tiles_256x128 >= 200) return tiles_256 >= 640 ? 16 : 14;
+    if (p.K <= 256) return tiles_64 <= 300 ? 24 : tiles_64 <= 1100 ? 25 : 13;
+    return tiles_64 < 64 ? 24 : tiles_64 < 128 ? 23 : tiles_64 < 512 ? 25 : tiles_128 < 512 ? 9 : 13;
 }
 
 template <typename T>
 int launch_t(GemmParams p, hipStream_t stream, int variant) {
+    constexpr int dt = std::is_same<T, float>::value ? kF32 : std::is_same<T, f16>::value ? kF16
+                       : std::is_same<T, bf16>::value ? kBF16 : kF64;
     if constexpr (!std::is_same<T, double>::value) {
-        constexpr int E = 16 / static_cast<int>(sizeof(T));
-        const uintptr_t al = reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.w);
-        if (variant >= 0 && p.K % E == 0 && al % 16 == 0) return launch_mfma<T>(p, stream, variant);
+        switch (variant) {
+            case 0: break;
+            case 2: return go_mfma<T, 4, 1, 1, 8, 2, 2>(p, stream);
+            case 5: return go_mfma<T, 4, 1, 1, 4, 8, 1>(p, stream);
+            case 23: return go_mfma<T, 4, 1, 1, 2, 8, 1>(p, stream);
+            case 24: return go_mfma<T, 2, 1, 1, 2, 8, 1>(p, stream);
+            case 25: return go_mfma<T, 4, 1, 1, 4, 4, 2>(p, stream);
+            case 9:
+                if constexpr (sizeof(T) == 2) return go_lds<T, 2, 2, 4, 4, 4>(p, stream);
+                break;
+            case 13:
+                if constexpr (sizeof(T) == 2) return go_lds<T, 2, 2, 4, 4, 1>(p, stream);
+                break;
+            case 14: case 16: return launch_gemm_dma(dt, p, stream, variant);
+            case 22: return launch_gemm_stream(dt, p, stream);
+            default: break;
+        }
+        if (variant != 0) return set_error(-1, "value_proj: no tile variant %d for this dtype", variant);
     }
     return go(gemm_generic_kernel<T>, p, 64, 64, 256, stream);
 }
@@ -522,7 +485,7 @@ int launch_proj_f32(int dtype, const void* a, const void* a2, const void* w, con
 }
 
 int launch_value_proj(int dtype, const void* a, const void* w, const void* bias, void* c, int64_t M, int64_t K,
-                      int64_t NO, hipStream_t stream, int variant, int hm_N, int hm_H) {
+                      int64_t NO, hipStream_t stream, int hm_N, int hm_H) {
     GemmParams p{a, w, bias, c, static_cast<int>(M), static_cast<int>(K), static_cast<int>(NO), 0, 0, 0};
     if (hm_N > 0) {
         p.hm_N = hm_N;
@@ -530,6 +493,7 @@ int launch_value_proj(int dtype, const void* a, const void* w, const void* bias,
         p.hm_ndiv = make_fastdiv(static_cast<uint32_t>(hm_N));
         p.hm_ddiv = make_fastdiv(static_cast<uint32_t>(p.hm_D));
     }
+    const int variant = pick_variant(dtype, p);
     switch (dtype) {
         case kF32: return launch_t<float>(p, stream, variant);
         case kF16: return launch_t<f16>(p, stream, variant);
@@ -537,6 +501,17 @@ int launch_value_proj(int dtype, const void* a, const void* w, const void* bias,
         case kF64: return launch_t<double>(p, stream, variant);
         default: return set_error(-2, "unknown dtype code %d", dtype);
     }
+}
+
+int value_proj_plan(int dtype, const void* a, const void* w, const void* bias, const void* c, int64_t M, int64_t K,
+                    int64_t NO, int hm_N, int hm_H) {
+    GemmParams p{a, w, bias, const_cast<void*>(c), static_cast<int>(M), static_cast<int>(K), static_cast<int>(NO),
+                 0, 0, 0};
+    if (hm_N > 0) {
+        p.hm_N = hm_N;
+        p.hm_D = static_cast<int>(NO) / hm_H;
+    }
+    return pick_variant(dtype, p);
 }
 
 }  // namespace td

@@ -15,19 +15,6 @@ __device__ __forceinline__ void load_lds16(const void* src, void* dst) {
     __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
 }
 
-// acc += a . b on one 16x16x32 MFMA with the accumulator tied in accumulation registers (AGPRs). Used by the
-// 128 x 128 wavefront tile, whose 256 accumulators fit only there; through the builtin the compiler picks the untied
-// form and copies each accumulator through a temporary. The compiler does not look inside the asm for hazards:
-// fragments reach it behind an explicit LDS wait (meet()), each accumulator's MFMAs are a full step apart, and
-// the kernel waits out the MFMA pipeline before it reads the accumulators.
-template <typename T>
-__device__ __forceinline__ void mfma_agpr(f32x4& acc, const u32x4& a, const u32x4& b) {
-    if constexpr (std::is_same<T, bf16>::value)
-        asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
-    else
-        asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
-}
-
 // Slot swizzle g of a staged row, from the row's index within its 16-row group.
 __device__ __forceinline__ int swz(int r) { return ((r >> 1 ^ r >> 3) & 1) | (r & 4) >> 1; }
 
@@ -47,11 +34,9 @@ __device__ __forceinline__ void meet() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// 256 x BN tiles (BN = 16 * TN * WN), 2 x WN wavefronts, each owning 128 x 16 TN of the tile (8 x TN MFMA tiles of
-// 16 x 16). Against 128 x 128 tiles this halves (BN = 128) or quarters (BN = 256) the L2 -> CU operand traffic per
-// flop. TN = 4: 128 accumulators in VGPRs, two wavefronts per SIMD. TN = 8: 256 accumulators in AGPRs, one
-// wavefront per SIMD, and a third fewer LDS fragment reads per flop (the LDS, not the MFMAs, bounds TN = 4 at
-// C = 1024).
+// 256 x BN tiles (BN = 64 * WN), 2 x WN wavefronts, each owning 128 x 64 of the tile (8 x 4 MFMA tiles of 16 x 16:
+// 128 accumulators in VGPRs, two wavefronts per SIMD). Against 128 x 128 tiles this halves (BN = 128) or quarters
+// (BN = 256) the L2 -> CU operand traffic per flop.
 //
 // K streams through a ring of STAGES LDS buffers, STAGES - 1 chunks of 32 ahead of the MFMAs, by direct
 // global-to-LDS loads (global_load_lds_dwordx4: lane i's 16 bytes land at the wavefront's LDS base + 16 i), so the
@@ -64,9 +49,9 @@ __device__ __forceinline__ void meet() {
 // distinct groups of a 128-byte window, so the read is conflict-free whether the LDS serves 16 or 8 lanes of a
 // 16-byte read per cycle. The swizzle is applied on the source side: the lane whose LDS slot is s loads piece
 // s ^ g(row). Rows past M or NO load the last valid row (their results are never stored), so no load is predicated.
-template <typename T, int WN, int TN, int STAGES>
-__global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(TN == 8 ? 1 : 2))) void gemm_dma_kernel(
-    GemmParams p) {
+template <typename T, int WN, int STAGES>
+__global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(2))) void gemm_dma_kernel(GemmParams p) {
+    constexpr int TN = 4;
     constexpr int NTH = 128 * WN, WAVES = 2 * WN;
     constexpr int BM = 256, BN = 16 * TN * WN, KC = 32;  // elements; one 16x16x32 MFMA step per chunk
     constexpr int TM = 8, WTN = 16 * TN;                 // 16 x 16 tiles per wavefront; wavefront tile width
@@ -150,12 +135,7 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(TN == 
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int t = 0; t < TN; ++t) {
-                if constexpr (TN == 8)
-                    mfma_agpr<T>(acc[i][t], xa[i], xb[t]);
-                else
-                    acc[i][t] = KBlock<T>::mma(xa[i], xb[t], acc[i][t]);
-            }
+            for (int t = 0; t < TN; ++t) acc[i][t] = KBlock<T>::mma(xa[i], xb[t], acc[i][t]);
         // The next chunk's fragment reads and loads are not needed before the next step: spread them over the
         // MFMA stream (one read after each of the first MFMAs, one load after every second MFMA after that), so
         // their issue hides in the MFMA pipeline's shadow instead of delaying the first MFMA.
@@ -184,7 +164,6 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(TN == 
     // epilogue: bias, one rounding, the tile transposed through LDS (once every wavefront's tail loads have landed
     // and its fragment reads are done), then 16-byte stores along rows
     meet<0>();
-    if constexpr (TN == 8) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");  // MFMA results land
     constexpr int E = 8, LDC = BN + E;
     T* Ct = reinterpret_cast<T*>(lds);
     const T* __restrict__ bias = static_cast<const T*>(p.bias);
@@ -215,14 +194,14 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(TN == 
     }
 }
 
-template <typename T, int WN, int TN, int STAGES>
+template <typename T, int WN, int STAGES>
 int go_dma(GemmParams p, hipStream_t stream) {
-    constexpr int BN = 16 * TN * WN;
+    constexpr int BN = 64 * WN;
     constexpr size_t stages = static_cast<size_t>(STAGES) * (256 + BN) * 64;
     constexpr size_t out = static_cast<size_t>(256) * (BN + 8) * sizeof(T);
     constexpr size_t lds = stages > out ? stages : out;
     static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(gemm_dma_kernel<T, WN, TN, STAGES>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        reinterpret_cast<const void*>(gemm_dma_kernel<T, WN, STAGES>), hipFuncAttributeMaxDynamicSharedMemorySize,
         static_cast<int>(lds));
     if (attr != hipSuccess) return set_error(-3, "value_proj: LDS size attribute refused: %s", hipGetErrorString(attr));
     p.mt = (p.M + 255) / 256;
@@ -230,27 +209,18 @@ int go_dma(GemmParams p, hipStream_t stream) {
     const int64_t tiles = static_cast<int64_t>(p.mt) * p.nt;
     p.per_xcd = static_cast<int>((tiles + kXcds - 1) / kXcds);
     const unsigned grid = static_cast<unsigned>(static_cast<int64_t>(p.per_xcd) * kXcds);
-    hipLaunchKernelGGL((gemm_dma_kernel<T, WN, TN, STAGES>), dim3(grid), dim3(128 * WN), lds, stream, p);
+    hipLaunchKernelGGL((gemm_dma_kernel<T, WN, STAGES>), dim3(grid), dim3(128 * WN), lds, stream, p);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : set_error(-3, "value_proj launch failed: %s", hipGetErrorString(e));
 }
 
-// variants (td_gemm.hip lists them with the others): tile, wavefronts x wavefront tile, LDS ring depth
-//   14  256 x 128, 4 x (128 x 64), 3      15  256 x 128, 4 x (128 x 64), 4
-//   16  256 x 256, 8 x (128 x 64), 3      17  256 x 256, 8 x (128 x 64), 2
-//   18  256 x 256, 4 x (128 x 128), 3     19  256 x 256, 4 x (128 x 128), 2
-//   20  256 x 128, 2 x (128 x 128), 3     21  256 x 256, 4 x (128 x 128), 4
+// variants (td_gemm.hip lists them with the others): 14 = 256 x 128 tiles of 4 wavefronts, 16 = 256 x 256 tiles of
+// 8 wavefronts; three LDS stages
 template <typename T>
 int launch_dma_t(GemmParams p, hipStream_t stream, int variant) {
     switch (variant) {
-        case 14: return go_dma<T, 2, 4, 3>(p, stream);
-        case 15: return go_dma<T, 2, 4, 4>(p, stream);
-        case 16: return go_dma<T, 4, 4, 3>(p, stream);
-        case 17: return go_dma<T, 4, 4, 2>(p, stream);
-        case 18: return go_dma<T, 2, 8, 3>(p, stream);
-        case 19: return go_dma<T, 2, 8, 2>(p, stream);
-        case 20: return go_dma<T, 1, 8, 3>(p, stream);
-        case 21: return go_dma<T, 2, 8, 4>(p, stream);
+        case 14: return go_dma<T, 2, 3>(p, stream);
+        case 16: return go_dma<T, 4, 3>(p, stream);
         default: return set_error(-1, "value_proj: unknown tile variant %d", variant);
     }
 }

@@ -299,9 +299,10 @@ int stream_t(GemmParams p, hipStream_t stream) {
 
 }  // namespace
 
+// The bias is staged in LDS by a 16-byte direct load, so it must be 16-byte aligned like the other operands.
 bool gemm_stream_fits(int dtype, const GemmParams& p) {
     const uintptr_t al = reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.w) |
-                         reinterpret_cast<uintptr_t>(p.c);
+                         reinterpret_cast<uintptr_t>(p.c) | reinterpret_cast<uintptr_t>(p.bias);
     return (dtype == kF16 || dtype == kBF16) && p.NO == kStreamNO && (p.K == 128 || p.K == 256) && p.M > 0 &&
            al % 16 == 0 && p.hm_D % 8 == 0;
 }

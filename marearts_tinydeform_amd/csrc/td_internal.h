@@ -17,7 +17,7 @@ inline int elem_size(int dtype) { return dtype == kF64 ? 8 : dtype == kF32 ? 4 :
 struct FusedTune {
     int qt = 0;     // query rows per workgroup (1..16)
     int sg = 0;     // corner split per row (power of two)
-    int waves = 0;  // wavefronts per workgroup (1, 2, 4 or 8)
+    int waves = 0;  // wavefronts per workgroup (4 or 8)
     int generic = 0;  // 1 forces the generic kernel
 };
 
@@ -46,11 +46,14 @@ int launch_prologue(int dtype, const LayerArgs& layer, const Geom& g, hipStream_
 int launch_sample(int dtype, const void* value, const Geom& g, const void* loc, const void* attn, void* out,
                   hipStream_t stream, const SampleTune& tune);
 
-// variant: 0 picks the tile shape by size, > 0 forces an MFMA tile variant, -1 forces the generic kernel.
-// hm_N > 0: c is head-major [M / hm_N, hm_H, hm_N, NO / hm_H] instead of [M, NO] (rows are b * hm_N + t); the head
-// width NO / hm_H must be a multiple of 16 bytes.
+// The kernel is picked by size and operand alignment (value_proj_plan). hm_N > 0: c is head-major
+// [M / hm_N, hm_H, hm_N, NO / hm_H] instead of [M, NO] (rows are b * hm_N + t); the head width NO / hm_H must be a
+// multiple of 16 bytes.
 int launch_value_proj(int dtype, const void* a, const void* w, const void* bias, void* c, int64_t M, int64_t K,
-                      int64_t NO, hipStream_t stream, int variant, int hm_N = 0, int hm_H = 0);
+                      int64_t NO, hipStream_t stream, int hm_N = 0, int hm_H = 0);
+// The tile variant launch_value_proj runs for these operands (0: the generic kernel); reads no memory.
+int value_proj_plan(int dtype, const void* a, const void* w, const void* bias, const void* c, int64_t M, int64_t K,
+                    int64_t NO, int hm_N = 0, int hm_H = 0);
 
 // Projection in float32 for the layer prologue: c[M, NO] = a[M, K] . w[NO, K]^T (+ a2[M, K] . w^T) + bias, float32
 // accumulation, stored unrounded; a2 may be null. 16/32-bit operands with K a multiple of 16 bytes and 16-byte

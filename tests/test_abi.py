@@ -36,7 +36,8 @@ def test_header_declares_the_entry_points():
                                   'td_layer_fused_forward', 'td_layer_prologue', 'td_layer_sample_forward',
                                   'td_project_forward', 'td_sample_backward', 'td_sample_forward',
                                   'td_sample_forward_heads', 'td_sample_forward_masked', 'td_sample_forward_v2',
-                                  'td_value_proj', 'td_value_proj_heads', 'td_version', 'td_weight_grad',
+                                  'td_value_proj', 'td_value_proj_heads', 'td_value_proj_plan', 'td_version',
+                                  'td_weight_grad',
                                   'td_weight_grad_workspace']
 
 

@@ -1,0 +1,71 @@
+"""The value projection's size rule, evaluated on the CPU through td_value_proj_plan (no kernel is launched).
+
+Every case of tests/gemm_cases.py must get the kernel it is tagged with, and every kernel the rule can pick for any
+shape (a sweep over M, K and NO in every dtype, plus the alignment cases) must be one that some GPU parity case runs.
+"""
+
+import itertools
+
+import pytest
+
+from marearts_tinydeform_amd import _native
+from gemm_cases import BF16, F16, F32, F64, all_cases
+
+pytestmark = pytest.mark.skipif(_native.lib is None, reason='libtinydeform.so is not built')
+
+
+def test_every_parity_case_gets_its_kernel():
+    for dt, M, K, NO, bias, offsets, heads, N, kern in all_cases():
+        got = _native.value_proj_plan(dt, M, K, NO, bias=bias, offsets=offsets, heads=heads, N=N)
+        assert got == kern, f'{dt} M={M} K={K} NO={NO} bias={bias} offsets={offsets} heads={heads}: kernel {got}, ' \
+                            f'tagged {kern}'
+
+
+def covered():
+    cov = {}
+    for dt, *_, kern in all_cases():
+        cov.setdefault(dt, set()).add(kern)
+    return cov
+
+
+def test_every_reachable_kernel_has_a_parity_case():
+    cov = covered()
+    Ms = sorted({int(1.37 ** i) for i in range(40)} | {300, 600, 3600, 8400, 16499, 16500, 21760, 43520, 67200,
+                                                       88892, 177784, 300000})
+    Ks = (8, 40, 64, 96, 128, 256, 512, 520, 576, 1024, 2048)
+    NOs = (16, 48, 64, 136, 200, 256, 512, 1000, 1024, 2048)
+    reach = {}
+    for dt in (F16, BF16, F32, F64):
+        for M, K, NO in itertools.product(Ms, Ks, NOs):
+            for bias, offsets in ((True, None), (False, None), (True, {'bias': 2}), (True, {'memory': 2}),
+                                  (True, {'weight': 4})):
+                reach.setdefault(dt, set()).add(_native.value_proj_plan(dt, M, K, NO, bias=bias, offsets=offsets))
+            if NO % 8 == 0 and K % 8 == 0:
+                D = 32 if NO % 32 == 0 else 8
+                reach[dt].add(_native.value_proj_plan(dt, M, K, NO, heads=NO // D, N=M))
+    for dt in reach:
+        missing = reach[dt] - cov.get(dt, set())
+        assert not missing, f'{dt}: kernels {sorted(missing)} are reachable but no GPU parity case runs them'
+    # the sweep reaches every kernel of the rule (a guard against the sweep itself going stale)
+    assert reach[F16] == reach[BF16] == {0, 9, 13, 14, 16, 22, 23, 24, 25}
+    assert reach[F32] == {0, 2, 5, 23, 24, 25}
+    assert reach[F64] == {0}
+
+
+def test_streaming_kernel_needs_an_aligned_bias():
+    # the streaming kernel loads the bias with 16-byte direct loads: any bias offset leaves it
+    assert _native.value_proj_plan(F16, 67200, 256, 256) == 22
+    assert _native.value_proj_plan(F16, 67200, 256, 256, bias=False) == 22
+    for off in (2, 4, 8):
+        assert _native.value_proj_plan(F16, 67200, 256, 256, offsets={'bias': off}) != 22
+    assert _native.value_proj_plan(F16, 67200, 256, 256, offsets={'bias': 16}) == 22
+    # so must memory, weight and value
+    for k in ('memory', 'weight', 'value'):
+        assert _native.value_proj_plan(BF16, 67200, 256, 256, offsets={k: 8}) != 22
+
+
+def test_plan_rejects_bad_sizes():
+    with pytest.raises(RuntimeError):
+        _native.value_proj_plan(F16, -1, 256, 256)
+    with pytest.raises(RuntimeError):
+        _native.value_proj_plan(F16, 100, 256, 256, heads=3, N=100)

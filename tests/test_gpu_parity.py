@@ -3,7 +3,8 @@
 
 Tolerances: float32 atol 2e-5 / rtol 1e-4 and float16 3e-3 / bfloat16 2e-2 (atol = rtol) against float64, as the
 reference's tests use (tests/test_correctness.py:70,76); float64 1e-10. At the benchmark configurations the
-relative error max|got - ref| / max|ref| must also stay within 1e-4 (float32) / 2e-2 (float16, bfloat16).
+operator's accuracy bar holds as well, literally: max |got - ref| <= 1e-4 in float32, and
+max |got - ref| / max |ref| <= 2e-2 in float16 and bfloat16 (float32 also <= 1e-4 relative).
 """
 
 import os
@@ -16,6 +17,7 @@ import torch
 import marearts_tinydeform_amd as td
 from marearts_tinydeform_amd import _native
 from oracle import bruteforce
+import gemm_cases
 from inputs import CASES, DINO_LEVELS, LIMIT_LEVELS, RTDETR_LEVELS, as_f64, make, to, workload
 
 pytestmark = pytest.mark.gpu
@@ -23,6 +25,7 @@ pytestmark = pytest.mark.gpu
 TOL = {torch.float32: (2e-5, 1e-4), torch.float16: (3e-3, 3e-3), torch.bfloat16: (2e-2, 2e-2),
        torch.float64: (1e-10, 1e-10)}
 REL = {torch.float32: 1e-4, torch.float16: 2e-2, torch.bfloat16: 2e-2, torch.float64: 1e-10}
+ABS_MAX = {torch.float32: 1e-4, torch.float64: 1e-10}  # max abs error at the benchmark configurations
 MODES = ('fused', 'project', 'auto')
 
 
@@ -136,6 +139,28 @@ def test_nonfinite_locations_sample_nothing():
             assert_close(f'nonfinite {dtype} [{mode}]', run(dev, mode), ref, atol, rtol)
 
 
+def test_float16_sums_beyond_the_half_range():
+    # un-normalised attention (about 8 per sample instead of 1 / (L P)) on memory values of about 1e4: the gathered
+    # sums g pass the float16 range (65504), while the projected outputs, with a weight scaled by 1/32, stay inside
+    # it. float32 accumulation, as in the reference, gives finite outputs; so must the float16 kernels.
+    args = make(1, 64, 8, 32, 256, [(20, 20), (10, 10)], 4, dtype=torch.float32, spread=0.3)
+    args[0] = (args[0] * 1e4).clamp(-6e4, 6e4)
+    args[1] = args[1] / 32
+    args[6] = args[6] * 8
+    args = [t if t is None or t.dtype == torch.long else t.half() for t in args]
+    ref = bruteforce.deform_attn(*args)
+    g = bruteforce.deform_attn(args[0], torch.eye(256).half(), None, *args[3:])  # W = I: g itself (per head)
+    assert np.abs(g).max() > 65504 and np.abs(ref).max() < 3e4
+    dev = to(args, 'cuda')
+    for mode in MODES:
+        out = run(dev, mode)
+        assert torch.isfinite(out).all(), mode
+        # tolerances scaled with the values (project mode rounds its ~300-sized values to float16 on the way)
+        scale = np.abs(ref).max()
+        err = assert_close(f'float16 large sums [{mode}]', out, ref, 3e-3 * scale, 3e-3)
+        assert err / scale <= 2e-2
+
+
 def test_rejects_bad_input():
     # reference tests/test_correctness.py:109-146 (project mode checks the weight too here: our GEMM, not F.linear)
     args = to(make(1, 8, 2, 8, 16, [(6, 7), (3, 4)], 2), 'cuda')
@@ -170,66 +195,84 @@ def test_rejects_bad_input():
             td.ma_deform_attn(*big, mode='fused')
 
 
-def test_value_proj_matches_oracle():
-    # the GEMM alone, with M, N, K off the tile sizes
-    g = torch.Generator().manual_seed(3)
-    for dtype in (torch.float16, torch.bfloat16, torch.float32, torch.float64):
-        # tile variants by size: small (1 x 8400), medium (4 x 9000), large (2 x 8192 x 1024 outputs), ragged edges
-        for (B, N, C, HD) in ((1, 8400, 256, 256), (4, 9000, 256, 256), (2, 8192, 128, 1024), (2, 77, 40, 48),
-                              (1, 130, 96, 72), (3, 5, 8, 16), (1, 33, 1024, 64)):
-            mem = torch.randn(B, N, C, generator=g).to(dtype)
-            w = (torch.randn(HD, C, generator=g) / C ** 0.5).to(dtype)
-            b = (torch.randn(HD, generator=g) * 0.1).to(dtype)
-            ref = bruteforce.project(mem, w, b)
-            with torch.inference_mode():
-                got = _native.value_proj(mem.cuda(), w.cuda(), b.cuda())
-            torch.cuda.synchronize()
-            # one rounding to dtype after float32 accumulation
-            eps = {torch.float16: 2e-3, torch.bfloat16: 1e-2, torch.float32: 1e-5, torch.float64: 1e-12}[dtype]
-            assert_close(f'value_proj {dtype} {(B, N, C, HD)}', got, ref, eps, eps)
+GEMM_EPS = {torch.float16: 2e-3, torch.bfloat16: 1e-2, torch.float32: 1e-5, torch.float64: 1e-12}
+
+
+def shifted(t, offset_bytes):
+    """A contiguous copy of t on the device whose data pointer lies offset_bytes past a 256-byte boundary."""
+    e = t.element_size()
+    assert offset_bytes % e == 0
+    buf = torch.empty(t.numel() + 256 // e, dtype=t.dtype, device='cuda')
+    v = buf[offset_bytes // e:offset_bytes // e + t.numel()].view(t.shape)
+    v.copy_(t)
+    assert v.data_ptr() % 256 == offset_bytes
+    return v
+
+
+def gemm_case(dt, M, K, NO, bias, offsets, kern, seed, rows=None):
+    """value_proj on an [M, K] x [NO, K]^T problem whose operands sit at the given byte offsets; checks that the
+    library picks kernel `kern`, then the result against the float64 oracle (on `rows`, or every row)."""
+    g = torch.Generator().manual_seed(seed)
+    mem = torch.randn(1, M, K, generator=g).to(dt)
+    w = (torch.randn(NO, K, generator=g) / K ** 0.5).to(dt)
+    b = (torch.randn(NO, generator=g) * 0.1).to(dt) if bias else None
+    offsets = offsets or {}
+    assert _native.value_proj_plan(dt, M, K, NO, bias=bias, offsets=offsets) == kern
+    say(f'  value_proj {dt} M={M} K={K} NO={NO} bias={bias} offsets={offsets} kernel {kern}')
+    dm = shifted(mem.cuda(), offsets.get('memory', 0))
+    dw = shifted(w.cuda(), offsets.get('weight', 0))
+    db = None if b is None else shifted(b.cuda(), offsets.get('bias', 0))
+    with torch.inference_mode():
+        got = _native.value_proj(dm, dw, db).cpu()
+    if rows is None:
+        ref = bruteforce.project(mem, w, b)
+    else:
+        ref = bruteforce.project(mem[:, rows], w, b)
+        got = got[:, rows]
+    assert_close(f'value_proj {dt} {(M, K, NO)} kernel {kern}', got, ref, GEMM_EPS[dt], GEMM_EPS[dt])
+
+
+def sample_rows(M, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.cat([torch.arange(0, min(M, 300)), torch.randint(0, M, (700,), generator=g),
+                      torch.arange(max(M - 300, 0), M)]).unique()
+
+
+@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16, torch.float32, torch.float64])
+def test_value_proj_matches_oracle(dtype):
+    # the GEMM alone, with M, N, K off the tile sizes; every row
+    for (B, N, C, HD), kern in gemm_cases.SMALL:
+        gemm_case(dtype, B * N, C, HD, True, None, kern[dtype], 3)
 
 
 @pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
 def test_value_proj_deep_k_matches_oracle(dtype):
-    # 16-bit, K >= 512 and K % 64 == 0: the direct-to-LDS kernel, 256 x 128 tiles for the small grids and 256 x 256
-    # tiles for >= 640 of them (the C=1024 limit shape, here with M and the output width off the tile sizes). Rows
-    # are checked on a sample that includes the last, partial M tile.
-    g = torch.Generator().manual_seed(11)
-    for (M, K, NO) in ((1037, 512, 200), (5000, 576, 136), (43557, 1024, 1000)):
-        say(f'  value_proj {dtype} M={M} K={K} NO={NO}')
-        mem = torch.randn(1, M, K, generator=g).to(dtype)
-        w = (torch.randn(NO, K, generator=g) / K ** 0.5).to(dtype)
-        b = (torch.randn(NO, generator=g) * 0.1).to(dtype)
-        with torch.inference_mode():
-            got = _native.value_proj(mem.cuda(), w.cuda(), b.cuda()).cpu()
-        rows = torch.cat([torch.arange(0, min(M, 300)), torch.randint(0, M, (700,), generator=g),
-                          torch.arange(max(M - 300, 0), M)]).unique()
-        ref = bruteforce.project(mem[:, rows], w, b)
-        eps = {torch.float16: 2e-3, torch.bfloat16: 1e-2}[dtype]
-        assert_close(f'value_proj {dtype} {(M, K, NO)}', got[:, rows], ref, eps, eps)
+    # 16-bit, K >= 512: register tiles for the small grids, both operands through LDS (9) in the middle, the
+    # direct-to-LDS kernel, 256 x 128 tiles (14) and 256 x 256 tiles (16) for >= 640 of them, with M and the output
+    # width off the tile sizes. Rows are checked on a sample that includes the first and the last, partial, M tile.
+    for M, K, NO, kern in gemm_cases.DEEP_K:
+        gemm_case(dtype, M, K, NO, True, None, kern, 11, rows=sample_rows(M, 11))
 
 
 @pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
 def test_value_proj_streaming_matches_oracle(dtype):
     # 16-bit, 256 outputs, K = 128 or 256, from 16500 rows: the streaming kernel (W resident in LDS; each workgroup
-    # an equal share of the rows). Shares that end in a short remainder go in rounds of 4 x 32 tokens and then
-    # remainder steps in which every wavefront computes a quarter of the channels: one such step (36001, 33600,
-    # 67200 at K = 256; 70003 at K = 128), two (44447 at K = 256), none (131072). Other shares are split evenly over
-    # the wavefronts in steps of 32 with a partial last step (16800, 20011, 44447 at K = 128, 88892). Every row is
-    # checked: the boundaries fall anywhere in M. Odd M, with and without bias.
-    g = torch.Generator().manual_seed(12)
-    for (M, K, bias) in ((36001, 256, True), (33600, 256, False), (67200, 256, True), (44447, 256, False),
-                         (131072, 256, True), (16800, 256, True), (88892, 256, True), (70003, 128, True),
-                         (44447, 128, False), (20011, 128, True)):
-        say(f'  value_proj streaming {dtype} M={M} K={K} bias={bias}')
-        mem = torch.randn(1, M, K, generator=g).to(dtype)
-        w = (torch.randn(256, K, generator=g) / K ** 0.5).to(dtype)
-        b = (torch.randn(256, generator=g) * 0.1).to(dtype) if bias else None
-        with torch.inference_mode():
-            got = _native.value_proj(mem.cuda(), w.cuda(), None if b is None else b.cuda()).cpu()
-        ref = bruteforce.project(mem, w, b)
-        eps = {torch.float16: 2e-3, torch.bfloat16: 1e-2}[dtype]
-        assert_close(f'value_proj streaming {dtype} {(M, K)}', got, ref, eps, eps)
+    # an equal share of the rows); see tests/gemm_cases.py for which remainder path each M takes. Every row is
+    # checked: the share boundaries fall anywhere in M. Odd M, with and without bias.
+    for M, K, bias, kern in gemm_cases.STREAM:
+        gemm_case(dtype, M, K, 256, bias, None, kern, 12)
+
+
+def test_value_proj_unaligned_bias_falls_back():
+    # a bias view 2 bytes off a 16-byte boundary (buf[1:] in float16) at sizes the streaming kernel would take
+    for M, K, NO, kern in gemm_cases.BIAS_OFFSET:
+        gemm_case(torch.float16, M, K, NO, True, {'bias': 2}, kern, 13)
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16, torch.bfloat16])
+def test_value_proj_unaligned_operands_use_generic_kernel(dtype):
+    for M, K, NO, offsets, kern in gemm_cases.UNALIGNED:
+        gemm_case(dtype, M, K, NO, True, offsets, kern, 14)
 
 
 def heads_of(value, H):
@@ -241,21 +284,13 @@ def heads_of(value, H):
 
 
 def test_value_proj_heads_matches_oracle():
-    # the head-major GEMM output: row b * N + t, column h * D + d lands at [b, h, t, d]. Shapes reach every tile
-    # family: 64 x 64 one-chunk (1 x 8400), LDS 128 x 128 (4 x 9000, 2 x 8192 x 1024 outputs), direct-to-LDS
-    # (K = 576), the streaming kernel (16-bit, 256 outputs, K = 256 or 128, from 16500 rows; its even split at
-    # 2 x 30001 and 3 x 20011, rounds with a quarter-channel remainder step at 4 x 8400 and 8 x 8400), ragged B, N
-    # and heads of 16 bytes. Every row is checked.
+    # the head-major GEMM output: row b * N + t, column h * D + d lands at [b, h, t, d]. The shapes reach every tile
+    # family (tests/gemm_cases.py), with ragged B, N and heads of 16 bytes. Every row is checked.
     g = torch.Generator().manual_seed(21)
-    shapes = {torch.float16: ((1, 8400, 256, 8, 32), (4, 9000, 256, 8, 32), (2, 8192, 128, 32, 32),
-                              (3, 77, 40, 6, 8), (2, 2501, 576, 17, 8), (2, 30001, 256, 8, 32),
-                              (3, 20011, 128, 16, 16), (4, 8400, 256, 8, 32)),
-              torch.bfloat16: ((1, 8400, 256, 8, 32), (2, 30001, 256, 8, 32), (5, 131, 96, 3, 24), (8, 8400, 256, 8, 32)),
-              torch.float32: ((1, 8400, 256, 8, 16), (2, 77, 40, 5, 4), (3, 1000, 64, 2, 12)),
-              torch.float64: ((2, 77, 40, 4, 2), (1, 300, 256, 8, 8))}
-    for dtype, cases in shapes.items():
-        for (B, N, C, H, D) in cases:
-            say(f'  value_proj_heads {dtype} B={B} N={N} C={C} H={H} D={D}')
+    for dtype, cases in gemm_cases.HEADS.items():
+        for (B, N, C, H, D), kern in cases:
+            say(f'  value_proj_heads {dtype} B={B} N={N} C={C} H={H} D={D} kernel {kern}')
+            assert _native.value_proj_plan(dtype, B * N, C, H * D, heads=H, N=N) == kern
             mem = torch.randn(B, N, C, generator=g).to(dtype)
             w = (torch.randn(H * D, C, generator=g) / C ** 0.5).to(dtype)
             b = (torch.randn(H * D, generator=g) * 0.1).to(dtype)
@@ -263,8 +298,7 @@ def test_value_proj_heads_matches_oracle():
                 got = _native.value_proj_heads(mem.cuda(), w.cuda(), b.cuda(), H).cpu()
             assert got.shape == (B, H, N, D)
             ref = heads_of(bruteforce.project(mem, w, b), H)
-            eps = {torch.float16: 2e-3, torch.bfloat16: 1e-2, torch.float32: 1e-5, torch.float64: 1e-12}[dtype]
-            assert_close(f'value_proj_heads {dtype} {(B, N, C, H, D)}', got, ref, eps, eps)
+            assert_close(f'value_proj_heads {dtype} {(B, N, C, H, D)}', got, ref, GEMM_EPS[dtype], GEMM_EPS[dtype])
 
 
 def test_sample_heads_matches_oracle():
@@ -343,7 +377,10 @@ def full_size_check(name, args, dtype, rows=None, modes=('fused', 'project')):
             got = got.reshape(-1, D)[rows]
         err = assert_close(f'{name} [{mode}]', got, ref, atol, rtol)
         rel = err / max(np.abs(ref).max(), 1e-30)
+        say(f'    max |diff| {err:.3g}, relative {rel:.3g}')
         assert rel <= REL[dtype], f'{name} [{mode}]: relative error {rel:.3g}'
+        if dtype in ABS_MAX:
+            assert err <= ABS_MAX[dtype], f'{name} [{mode}]: max abs error {err:.3g}'
     if len(outs) == 2:  # linear reordering: both orders agree over the whole output
         a, b = (o.double() for o in outs.values())
         assert torch.allclose(a, b, atol=2 * atol, rtol=2 * rtol), f'{name}: fused and project disagree'
@@ -384,6 +421,15 @@ def test_limit_case_bf16_c1024(Q):
     args = workload(2, Q, 16, 64, 1024, LIMIT_LEVELS, 16, torch.bfloat16, bias=False)
     rows = np.random.default_rng(Q).choice(2 * Q * 16, size=min(1024, 2 * Q * 16), replace=False)
     full_size_check(f'limit bf16 C1024 B2 Q{Q}', args, torch.bfloat16, rows=np.sort(rows))
+
+
+def test_limit_case_bf16_c1024_b1_project():
+    # the C = 1024 limit shape at batch 1 (21760 tokens: the 256 x 128 direct-to-LDS value GEMM), project mode end to
+    # end, 1024 sampled rows against the oracle
+    args = workload(1, 300, 16, 64, 1024, LIMIT_LEVELS, 16, torch.bfloat16, bias=False)
+    assert _native.value_proj_plan(torch.bfloat16, 21760, 1024, 1024, bias=False) == 14
+    rows = np.random.default_rng(1).choice(300 * 16, size=1024, replace=False)
+    full_size_check('limit bf16 C1024 B1 Q300', args, torch.bfloat16, rows=np.sort(rows), modes=('project',))
 
 
 # ---- value padding mask ---------------------------------------------------------------------------------------

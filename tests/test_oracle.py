@@ -326,6 +326,22 @@ def test_sample_v2_matches_dfine_restatement(points, method):
     assert np.abs(got - ref).max() <= 1e-12
 
 
+@pytest.mark.parametrize('points', [[3, 6, 3], [4, 4, 4], [2, 1, 5, 3], [8]])
+@pytest.mark.parametrize('method', ['default', 'discrete'])
+def test_sample_v2_matches_transformers(points, method):
+    # the library routine itself: transformers' D-FINE core (models/d_fine/modeling_d_fine.py:150-216, installed in
+    # this image), run in float64 on the CPU, with locations that reach past every edge of the maps
+    dfine = pytest.importorskip('transformers.models.d_fine.modeling_d_fine')
+    levels = [(12, 9), (6, 5), (3, 3), (2, 2)][:len(points)]
+    value, shapes, starts, loc, attn = dfine_inputs(2, 7, 3, 4, levels, points, seed=41, spread=0.6)
+    assert (loc < 0).any() and (loc > 1).any()
+    ref = dfine.multi_scale_deformable_attention_v2(value, [tuple(int(v) for v in s) for s in shapes], loc, attn,
+                                                    points, method).numpy()
+    got = bruteforce.sample_v2(value, shapes, starts, loc, attn, points, method)
+    assert got.shape == ref.shape
+    assert np.abs(got - ref).max() <= 1e-12
+
+
 def test_sample_v2_uniform_points_equals_sample():
     levels = [(12, 9), (6, 5), (3, 3)]
     value, shapes, starts, loc, attn = dfine_inputs(2, 5, 3, 4, levels, [4, 4, 4], seed=32)
