@@ -128,6 +128,22 @@ int td_project_forward(int dtype, const void* memory, const void* value_weight, 
                        int64_t D, int64_t L, int64_t P, void* stream);
 
 /*
+ * td_project_forward without the value_ws workspace: the projected values go to a static device array of
+ * TD_NOALLOC_SCRATCH_BYTES per GPU instead, so the call allocates nothing (no hipMalloc, no allocating library
+ * routine). No counterpart in the reference; for callers that cannot allocate: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc. A problem whose projected values (B*N*H*D elements of dtype) exceed
+ * the array is refused with TD_E_ARG (td_project_forward with a workspace takes it). Every call on one GPU shares
+ * that GPU's array, so calls that overlap on one GPU (other streams, other host threads) race; the stream's device
+ * must be the current device. Same results as td_project_forward, bit for bit.
+ */
+#define TD_NOALLOC_SCRATCH_BYTES 67108864 /* 64 MiB per GPU */
+int td_project_forward_noalloc(int dtype, const void* memory, const void* value_weight, const void* value_bias,
+                               const int64_t* spatial_shapes, const int64_t* level_start_index,
+                               const void* sampling_locations, const void* attention_weights,
+                               const uint8_t* padding_mask, int loc_acc, void* out, int64_t B, int64_t Q, int64_t N,
+                               int64_t C, int64_t H, int64_t D, int64_t L, int64_t P, void* stream);
+
+/*
  * Sampling with per-level point counts and a choice of sampling method (the deformable attention core of D-FINE:
  * transformers models/d_fine/modeling_d_fine.py:150-216, multi_scale_deformable_attention_v2). Level l has
  * points_per_level[l] samples (a host array of L entries, sum <= 64), so sampling_locations is

@@ -42,6 +42,7 @@ SIGNATURES = {
     'td_weight_grad_workspace': (_i64, [_int, _i64, _i64, _i64]),
     'td_weight_grad': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     'td_value_proj_plan': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64]),
+    'td_project_forward_noalloc': (_int, [_int] + [_vp] * 8 + [_int, _vp] + [_i64] * 8 + [_vp]),
 }
 
 TD_E_WORKSPACE = -4  # td_layer_fused_forward: the problem needs loc_out / attn_out
@@ -357,6 +358,36 @@ def project_forward(memory, weight, bias, spatial_shapes, level_start_index, loc
     _check(lib_.td_project_forward(DTYPE_CODES[memory.dtype], mem.data_ptr(), w.data_ptr(), _ptr(b), sh.data_ptr(),
                                    st.data_ptr(), lc.data_ptr(), aw.data_ptr(), _ptr(mask), 1 if loc_acc else 0,
                                    ws.data_ptr(), out.data_ptr(), B, Q, N, C, H, HD // H, L, P, _stream(dev)))
+    return out
+
+
+NOALLOC_SCRATCH_BYTES = 64 << 20  # TD_NOALLOC_SCRATCH_BYTES
+
+
+def project_forward_noalloc(memory, weight, bias, spatial_shapes, level_start_index, loc, attn, padding_mask=None,
+                            loc_acc=False, out=None):
+    """Project mode without a workspace (td_project_forward_noalloc): the projected values go to the library's
+    static per-GPU scratch array (NOALLOC_SCRATCH_BYTES), so the library allocates nothing; out (optional) is the
+    caller's [B, Q, H*D] output. Calls that overlap on one GPU race on the scratch array."""
+    lib_ = _require()
+    if memory.dim() != 3:
+        raise RuntimeError('memory / value must be [B, N, C]')
+    B, Q, H, L, P = _check_locations(memory, spatial_shapes, level_start_index, loc, attn, loc_acc)
+    HD = check_projection(memory, weight, bias, H)
+    mask = check_padding_mask(memory, padding_mask)
+    N, C = memory.size(1), memory.size(2)
+    dev = memory.device
+    mem, w, b, lc, aw, sh, st = _contig(memory, weight, bias, loc, attn, spatial_shapes, level_start_index)
+    if out is None:
+        out = torch.empty((B, Q, HD), dtype=memory.dtype, device=dev)
+    elif out.shape != (B, Q, HD) or out.dtype != memory.dtype or out.device != dev or not out.is_contiguous():
+        raise RuntimeError('out must be a contiguous [B, Q, H*D] tensor of the memory dtype on its device')
+    if out.numel() == 0:
+        return out
+    _check(lib_.td_project_forward_noalloc(DTYPE_CODES[memory.dtype], mem.data_ptr(), w.data_ptr(), _ptr(b),
+                                           sh.data_ptr(), st.data_ptr(), lc.data_ptr(), aw.data_ptr(), _ptr(mask),
+                                           1 if loc_acc else 0, out.data_ptr(), B, Q, N, C, H, HD // H, L, P,
+                                           _stream(dev)))
     return out
 
 

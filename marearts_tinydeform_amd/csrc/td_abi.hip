@@ -352,12 +352,13 @@ extern "C" int td_sample_forward_heads(int dtype, const void* value, const int64
                         padding_mask, loc_acc, out, B, Q, N, H, D, L, P, s);
 }
 
-extern "C" int td_project_forward(int dtype, const void* memory, const void* value_weight, const void* value_bias,
-                                  const int64_t* spatial_shapes, const int64_t* level_start_index,
-                                  const void* sampling_locations, const void* attention_weights,
-                                  const uint8_t* padding_mask, int loc_acc, void* value_ws, void* out, int64_t B,
-                                  int64_t Q, int64_t N, int64_t C, int64_t H, int64_t D, int64_t L, int64_t P,
-                                  void* stream) {
+namespace td {
+
+int project_forward(int dtype, const void* memory, const void* value_weight, const void* value_bias,
+                    const int64_t* spatial_shapes, const int64_t* level_start_index, const void* sampling_locations,
+                    const void* attention_weights, const uint8_t* padding_mask, int loc_acc, void* value_ws,
+                    int64_t value_ws_bytes, void* out, int64_t B, int64_t Q, int64_t N, int64_t C, int64_t H,
+                    int64_t D, int64_t L, int64_t P, void* stream) {
     int rc = check_geometry(dtype, B, Q, N, H, D, L, P, spatial_shapes, level_start_index, sampling_locations,
                             attention_weights, out);
     if (rc != TD_OK) return rc;
@@ -366,6 +367,10 @@ extern "C" int td_project_forward(int dtype, const void* memory, const void* val
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (B * Q * H * D == 0) return TD_OK;
     if (N == 0 || L * P == 0) return launch_zero(out, B * Q * H * D * elem_size(dtype), s);
+    if (value_ws_bytes >= 0 && B * N * H * D * elem_size(dtype) > value_ws_bytes)
+        return set_error(TD_E_ARG, "project: the projected values need %lld bytes, more than the %lld available",
+                         static_cast<long long>(B * N * H * D * elem_size(dtype)),
+                         static_cast<long long>(value_ws_bytes));
     if (value_ws == nullptr || (C > 0 && (memory == nullptr || value_weight == nullptr)))
         return set_error(TD_E_ARG, "null pointer argument");
     const bool hm = head_major_pays(dtype, D);
@@ -381,6 +386,19 @@ extern "C" int td_project_forward(int dtype, const void* memory, const void* val
     g.loc_acc = loc_acc;
     SampleTune tune;
     return launch_sample(dtype, value_ws, g, sampling_locations, attention_weights, out, s, tune);
+}
+
+}  // namespace td
+
+extern "C" int td_project_forward(int dtype, const void* memory, const void* value_weight, const void* value_bias,
+                                  const int64_t* spatial_shapes, const int64_t* level_start_index,
+                                  const void* sampling_locations, const void* attention_weights,
+                                  const uint8_t* padding_mask, int loc_acc, void* value_ws, void* out, int64_t B,
+                                  int64_t Q, int64_t N, int64_t C, int64_t H, int64_t D, int64_t L, int64_t P,
+                                  void* stream) {
+    return project_forward(dtype, memory, value_weight, value_bias, spatial_shapes, level_start_index,
+                           sampling_locations, attention_weights, padding_mask, loc_acc, value_ws, -1, out, B, Q, N, C,
+                           H, D, L, P, stream);
 }
 
 extern "C" int td_fused_forward(int dtype, const void* memory, const void* value_weight, const void* value_bias,

@@ -63,6 +63,14 @@ int launch_proj_f32(int dtype, const void* a, const void* a2, const void* w, con
 
 int launch_zero(void* out, int64_t bytes, hipStream_t stream);
 
+// Project mode (td_project_forward) with the projected values in value_ws; value_ws_bytes >= 0 bounds the bytes
+// they may take (an error beyond it), -1 leaves the size to the caller.
+int project_forward(int dtype, const void* memory, const void* value_weight, const void* value_bias,
+                    const int64_t* spatial_shapes, const int64_t* level_start_index, const void* sampling_locations,
+                    const void* attention_weights, const uint8_t* padding_mask, int loc_acc, void* value_ws,
+                    int64_t value_ws_bytes, void* out, int64_t B, int64_t Q, int64_t N, int64_t C, int64_t H,
+                    int64_t D, int64_t L, int64_t P, void* stream);
+
 // Backward (td_backward.hip). grad_value: [B, N, H*D] in the accumulation type, zeroed and accumulated here;
 // grad_loc / grad_attn in the element type (the accumulation type with g.loc_acc).
 int launch_sample_backward(int dtype, const void* value, const Geom& g, const void* loc, const void* attn,

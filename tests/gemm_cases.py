@@ -53,10 +53,10 @@ BIAS_OFFSET = [
     (67200, 256, 256, 13),
 ]
 
-# (M, K, NO, offsets, kernel) in float32, float16 and bfloat16: memory 2 bytes off a 16-byte boundary, or K not a
+# (M, K, NO, offsets, kernel) in float32, float16 and bfloat16: memory 4 bytes off a 16-byte boundary, or K not a
 # multiple of 16 bytes: the generic VALU kernel
 UNALIGNED = [
-    (1000, 256, 256, {'memory': 2}, 0),
+    (1000, 256, 256, {'memory': 4}, 0),
     (333, 38, 72, None, 0),
 ]
 

@@ -34,7 +34,8 @@ def lib():
 def test_header_declares_the_entry_points():
     assert header_functions() == ['td_fused_forward', 'td_fused_forward_masked', 'td_input_grad', 'td_last_error',
                                   'td_layer_fused_forward', 'td_layer_prologue', 'td_layer_sample_forward',
-                                  'td_project_forward', 'td_sample_backward', 'td_sample_forward',
+                                  'td_project_forward', 'td_project_forward_noalloc', 'td_sample_backward',
+                                  'td_sample_forward',
                                   'td_sample_forward_heads', 'td_sample_forward_masked', 'td_sample_forward_v2',
                                   'td_value_proj', 'td_value_proj_heads', 'td_value_proj_plan', 'td_version',
                                   'td_weight_grad',
@@ -52,6 +53,7 @@ def test_header_constants_match_python(lib):
     d = header_defines()
     assert d['TD_MAX_LEVEL_POINTS'] == _native.MAX_LEVEL_POINTS
     assert d['TD_MAX_CHANNELS'] == _native.MAX_CHANNELS
+    assert d['TD_NOALLOC_SCRATCH_BYTES'] == _native.NOALLOC_SCRATCH_BYTES
     assert {d['TD_F32'], d['TD_F16'], d['TD_BF16'], d['TD_F64']} == set(_native.DTYPE_CODES.values())
     import torch
     assert _native.DTYPE_CODES[torch.float32] == d['TD_F32']
