@@ -40,6 +40,18 @@ int set_error(int code, const char* fmt, ...) {
     return code;
 }
 
+int cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 int launch_zero(void* out, int64_t bytes, hipStream_t stream) {
     if (bytes <= 0) return 0;
     if (reinterpret_cast<uintptr_t>(out) % 16 == 0 && bytes % 16 == 0) {

@@ -104,11 +104,21 @@ struct Corner {
 // GENERAL = false compiles the reference's case only (P points on every level, bilinear, no mask); kernels are
 // instantiated both ways and the launchers pick GENERAL = true only when a mask, per-level point counts, the
 // discrete method or accumulation-type locations are in use, so the common path carries none of their cost.
+struct LevelGeom {
+    int hl, wl;   // height, width
+    int64_t st;   // first token
+};
+__device__ __forceinline__ LevelGeom level_geom(const Geom& g, int l) {
+    return LevelGeom{static_cast<int>(g.shapes[2 * l]), static_cast<int>(g.shapes[2 * l + 1]), g.starts[l]};
+}
+
+// The corner rule with the level's geometry already loaded (kernels that sample one level per lane across many rows
+// load it once).
 template <typename A, bool GENERAL>
-__device__ __forceinline__ void corners_at(A lx, A ly, A w, int l, const Geom& g, int64_t row, Corner<A>* out) {
-    const int hl = static_cast<int>(g.shapes[2 * l]);
-    const int wl = static_cast<int>(g.shapes[2 * l + 1]);
-    const int64_t st = g.starts[l];
+__device__ __forceinline__ void corners_lv(A lx, A ly, A w, const LevelGeom& lg, const Geom& g, int64_t row,
+                                           Corner<A>* out) {
+    const int hl = lg.hl, wl = lg.wl;
+    const int64_t st = lg.st;
     if (GENERAL && g.discrete) {
         const A fx = fmin(fmax(lx * static_cast<A>(wl) + static_cast<A>(0.5), static_cast<A>(-1)), static_cast<A>(wl));
         const A fy = fmin(fmax(ly * static_cast<A>(hl) + static_cast<A>(0.5), static_cast<A>(-1)), static_cast<A>(hl));
@@ -142,6 +152,11 @@ __device__ __forceinline__ void corners_at(A lx, A ly, A w, int l, const Geom& g
         out[k].w = in ? w * (dx ? fx : static_cast<A>(1) - fx) * (dy ? fy : static_cast<A>(1) - fy)
                       : static_cast<A>(0);
     }
+}
+
+template <typename A, bool GENERAL>
+__device__ __forceinline__ void corners_at(A lx, A ly, A w, int l, const Geom& g, int64_t row, Corner<A>* out) {
+    corners_lv<A, GENERAL>(lx, ly, w, level_geom(g, l), g, row, out);
 }
 
 // The corners of sample j (j = l * P + p, or the running index over per-level point counts) of row `row`, with the

@@ -7,7 +7,8 @@
 // are linear (reference csrc/ma_deform_fused.cu:6-14, README.md:16-22).
 //
 // fused_vec_kernel (float / half / bfloat16, C a multiple of 16 bytes, 16-byte aligned memory and weight):
-//   workgroup = (b, tile of QT queries, h); heads vary fastest across workgroups.
+//   workgroup = (b, tile of QT queries, h), or for small problems (h, balanced slice of the B * Q rows of head h:
+//            every CU then holds the same number of rows to within one); heads vary fastest across workgroups.
 //   phase 1  corner table of the QT rows into LDS.
 //   phase 2  gather: CV*SG lanes per row, lane = (corner group sg, 16-byte channel chunk ch); each lane sums
 //            every SG-th corner of its row with float32 FMAs, the SG partial sums meet by cross-lane adds,
@@ -36,6 +37,8 @@ struct FusedParams {
     int C, QT, SG, KS, qtiles;
     int per_xcd, units;  // work-unit mapping (decode_block)
     LayerArgs lay;       // query prologue (layer kernels only)
+    // balanced slices (slices > 0): B * Q = slices * slice_rows + slice_extra rows per head
+    int slices = 0, slice_rows = 0, slice_extra = 0;
 };
 
 // Workgroup index -> work unit (b, query tile, h) with heads fastest. Workgroups are dealt to the 8 XCDs
@@ -87,16 +90,34 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     T* __restrict__ out = static_cast<T*>(p.out);
 
     const int tid = threadIdx.x;
-    const BlockRow br = decode_block(blockIdx.x, g.H, p.qtiles, p.per_xcd, p.units);
-    if (!br.valid) return;
-    const int q0 = br.qt * QT;
+    // the workgroup's rows: nrows consecutive (batch, query) rows from rbase (row index b * Q + q) of head h. Tiles
+    // (p.slices = 0): QT queries of one image. Balanced slices (p.slices > 0, not the layer kernel): slice s of the
+    // B * Q rows, slice_rows + (s < slice_extra) of them, so that every workgroup holds the same number of rows to
+    // within one.
+    int h, rbase, nrows, q0 = 0, bimg = 0;
+    if (!LAYER && p.slices > 0) {
+        const int unit = (blockIdx.x % kXcds) * p.per_xcd + blockIdx.x / kXcds;
+        if (unit >= p.units) return;
+        h = unit % g.H;
+        const int slice = unit / g.H;
+        rbase = slice * p.slice_rows + (slice < p.slice_extra ? slice : p.slice_extra);
+        nrows = p.slice_rows + (slice < p.slice_extra ? 1 : 0);
+    } else {
+        const BlockRow br = decode_block(blockIdx.x, g.H, p.qtiles, p.per_xcd, p.units);
+        if (!br.valid) return;
+        h = br.h;
+        bimg = br.b;
+        q0 = br.qt * QT;
+        rbase = br.b * g.Q + q0;
+        nrows = g.Q - q0 < QT ? g.Q - q0 : QT;
+    }
 
     if constexpr (LAYER) {
         // phase 0 (layer): sampling offsets and attention logits of the tile's queries for head h, on MFMA; the
         // query rows are staged in the g rows' LDS, which phase 2 overwrites only after the corner table is built
-        stage_queries<T, float, true, NTH>(p.lay, br.b, q0, QT, g.Q, gs, GP);
+        stage_queries<T, float, true, NTH>(p.lay, bimg, q0, QT, g.Q, gs, GP);
         __syncthreads();
-        prologue_mfma<T, WAVES>(p.lay, br.h, LP, QT, gs, GP, pro, PP);
+        prologue_mfma<T, WAVES>(p.lay, h, LP, QT, gs, GP, pro, PP);
         __syncthreads();
         prologue_stats<float, NTH>(LP, QT, pro, PP, rstat);
         __syncthreads();
@@ -105,13 +126,13 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     // phase 1: corner table
     if (tid == 0) *gmax = 0u;
     for (int i = tid; i < QT * LP; i += NTH) {
-        const int r = i / LP, j = i - r * LP, q = q0 + r;
+        const int r = i / LP, j = i - r * LP;
         Corner<float>* c4 = cw + r * S + 4 * j;
-        if (q < g.Q) {
-            const int64_t row = (static_cast<int64_t>(br.b) * g.Q + q) * g.H + br.h;
+        if (r < nrows) {
+            const int64_t row = static_cast<int64_t>(rbase + r) * g.H + h;
             if constexpr (LAYER) {
                 float lx, ly, a;
-                prologue_sample<T, float>(p.lay, g, br.b, q, br.h, r, j, pro, PP, rstat, lx, ly, a);
+                prologue_sample<T, float>(p.lay, g, bimg, q0 + r, h, r, j, pro, PP, rstat, lx, ly, a);
                 corners_at<float, GENERAL>(lx, ly, a, j / g.P, g, row, c4);
             } else {
                 corner4<T, float, GENERAL>(loc, attn, g, row, j, c4);
@@ -124,10 +145,10 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     __syncthreads();
 
     // phase 2: gather C-wide rows, float32 accumulation
-    const T* mb = mem + static_cast<size_t>(br.b) * g.N * C;
     const int GS = CV * SG;
     for (int it = tid; it < QT * GS; it += NTH) {
         const int r = it / GS, rem = it - r * GS, sg = rem / CV, ch = rem - sg * CV;
+        const T* mb = mem + static_cast<size_t>(r < nrows ? (rbase + r) / g.Q : 0) * g.N * C;
         float acc[V];
 #pragma unroll
         for (int i = 0; i < V; ++i) acc[i] = 0.f;
@@ -181,7 +202,7 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
             const int kb = ks * nk / p.KS, ke = (ks + 1) * nk / p.KS;
             const int d = nt * 16 + n16;
             const bool dv = d < D;
-            const T* wr = w + (static_cast<size_t>(br.h) * D + (dv ? d : 0)) * C;
+            const T* wr = w + (static_cast<size_t>(h) * D + (dv ? d : 0)) * C;
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 2
             for (int kk = kb; kk < ke; ++kk) {
@@ -218,7 +239,7 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
             const int kb = ks * nk / p.KS, ke = (ks + 1) * nk / p.KS;
             const int d = nt * 16 + n16;
             const bool dv = d < D;
-            const T* wr = w + (static_cast<size_t>(br.h) * D + (dv ? d : 0)) * C;
+            const T* wr = w + (static_cast<size_t>(h) * D + (dv ? d : 0)) * C;
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 2
             for (int kk = kb; kk < ke; ++kk) {
@@ -239,13 +260,13 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
 
     // epilogue: sum the K slices, add bias * sum of in-map weights, round once
     for (int o = tid; o < QT * D; o += NTH) {
-        const int r = o / D, d = o - r * D, q = q0 + r;
-        if (q >= g.Q) continue;
+        const int r = o / D, d = o - r * D;
+        if (r >= nrows) continue;
         float v = part[r * PW + d];
         for (int ks = 1; ks < p.KS; ++ks) v += part[(ks * 16 + r) * PW + d];
         v *= inv_sc;
-        if (bias != nullptr) v = fmaf(cvt<float>(bias[static_cast<size_t>(br.h) * D + d]), wsum[r], v);
-        out[((static_cast<size_t>(br.b) * g.Q + q) * g.H + br.h) * D + d] = static_cast<T>(v);
+        if (bias != nullptr) v = fmaf(cvt<float>(bias[static_cast<size_t>(h) * D + d]), wsum[r], v);
+        out[(static_cast<size_t>(rbase + r) * g.H + h) * D + d] = static_cast<T>(v);
     }
 }
 
@@ -327,7 +348,8 @@ inline bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
 // Sets the work-unit mapping and returns the grid size (a multiple of the XCD count).
 inline int64_t map_units(FusedParams& p) {
-    const int64_t units = static_cast<int64_t>(p.g.B) * p.g.H * p.qtiles;
+    const int64_t units = p.slices > 0 ? static_cast<int64_t>(p.slices) * p.g.H
+                                       : static_cast<int64_t>(p.g.B) * p.g.H * p.qtiles;
     p.units = static_cast<int>(units);
     p.per_xcd = static_cast<int>((units + kXcds - 1) / kXcds);
     return static_cast<int64_t>(p.per_xcd) * kXcds;
@@ -385,7 +407,7 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
             // workgroup (more workgroups in flight); large ones 8-wave workgroups of 16 rows.
             const int64_t rows = static_cast<int64_t>(g.B) * g.Q * g.H;
             const bool big = rows >= 8192;
-            const int waves = tune.waves ? tune.waves : big ? 8 : 4;
+            int waves = tune.waves ? tune.waves : big ? 8 : 4;
             const int nth = waves * kWave;
             int sg = tune.sg;
             if (sg <= 0) {
@@ -405,6 +427,31 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
             }
             if (qt > qmax) qt = qmax;
             if (qt < 1) qt = 1;
+            // Small problems with one row per wavefront take balanced slices instead of query tiles: k workgroups
+            // per CU for the smallest k whose slices fit 8 rows, each slice holding the same number of (batch,
+            // query) rows of its head to within one, in 8-wavefront workgroups. A grid of fixed 4-row tiles left
+            // some CUs a third tile: 600 tiles on 256 CUs at the headline, 8.94 µs against 8.66 with two slices of
+            // 4-5 rows per CU; one workgroup per CU is best where it fits (100 queries: 6.65 against 7.60 µs, and
+            // 7.54 with two per CU; 50 queries: 6.30 against 6.62); float32 300 queries: 13.21 against 14.02.
+            int64_t slices = 0;
+            const int64_t BQ = static_cast<int64_t>(g.B) * g.Q;
+            if (!layer && !big && GS == kWave && tune.qt <= 0 && tune.waves <= 0) {
+                const int cus = cu_count();
+                int64_t per = 0;
+                for (int k = 1; k <= 4; ++k) {
+                    slices = static_cast<int64_t>(k) * cus / g.H;
+                    if (slices < 1) slices = 1;
+                    if (slices > BQ) slices = BQ;
+                    per = (BQ + slices - 1) / slices;
+                    if (per <= 8) break;
+                }
+                if (per <= 8) {
+                    qt = static_cast<int>(per);
+                    waves = 8;
+                } else {
+                    slices = 0;
+                }
+            }
             const int NTILE = (D + 15) / 16;
             const int nk = sizeof(T) == 2 ? (C + 31) / 32 : (C + 15) / 16;
             int ks = waves / NTILE;
@@ -417,12 +464,18 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
                        20 * 4 + static_cast<size_t>(ks) * 16 * NTILE * 16 * 4 +
                        (layer ? static_cast<size_t>(16 * PP + 32) * 4 : 0);
             };
+            if (slices > 0 && lds(qt) > kLdsBudget) slices = 0;  // a slice's rows must all fit the tile: use tiles
             while (qt > 1 && lds(qt) > kLdsBudget) --qt;
             if (lds(qt) <= kLdsBudget) {
                 p.QT = qt;
                 p.SG = sg;
                 p.KS = ks;
                 p.qtiles = (g.Q + qt - 1) / qt;
+                if (slices > 0) {
+                    p.slices = static_cast<int>(slices);
+                    p.slice_rows = static_cast<int>(BQ / slices);
+                    p.slice_extra = static_cast<int>(BQ % slices);
+                }
                 // 8 corner loads in flight per lane: measured best on MI355X at every benchmark shape
                 if (layer) {
                     switch (waves) {

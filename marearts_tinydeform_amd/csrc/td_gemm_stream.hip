@@ -258,18 +258,6 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
 }
 
 // compute units of the current device, asked once per device
-int cu_count() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
-    }
-    return cached[dev];
-}
-
 template <typename T, int KB, bool SPLIT>
 int go_stream(GemmParams p, int64_t grid, hipStream_t stream) {
     constexpr size_t lds = static_cast<size_t>(kStreamNO) * KB * 4 * 16 + kStreamNO * sizeof(T);

@@ -28,6 +28,9 @@ struct SampleTune {
     int vec = 0;  // elements per load
 };
 
+// Compute units of the current device (256 on MI355X), cached per device.
+int cu_count();
+
 // Every launcher returns 0, or a negative TD_E* code after recording a message with set_error.
 int set_error(int code, const char* fmt, ...);
 
