@@ -6,7 +6,9 @@ A step is one ma_deform_attn call (mode='auto', the default) on one batch of syn
 in HBM. Like the reference's bench (bench/bench.py:40-61) the calls are captured in a HIP graph, so Python launch
 overhead is excluded: W warm-up steps (one graph replay), then a graph of EXACTLY K steps replayed 7 times, each
 replay bracketed by torch.cuda.synchronize() and timed with events on the replay stream; the best replay gives
-the µs per call, as the reference takes the best of 7 replays of its 100-call graph.
+the µs per call, as the reference takes the best of 7 replays of its 100-call graph. A replay's fixed cost (about
+10 µs: the graph launch and the timing events) is inside the timed region, so a short graph reads higher per call
+than a long one (0.5 µs per call at 20 calls).
 
 Prints diagnostics on stderr and ONE JSON line on stdout: value = µs per layer call (auto mode), with per-mode
 times, the roofline of the dominant kernel (algorithmic bytes per launch / its average launch duration, measured
@@ -65,7 +67,9 @@ def log(*a):
 def graph_time_us(fn, steps, warmup, replays=7):
     """µs per call: W warm-up calls (eager on a side stream, then one replay of a W-call graph), then the best of
     `replays` timed replays of a graph of exactly `steps` calls, events recorded on the replay stream (the
-    reference's method, bench/bench.py:40-61)."""
+    reference's method, bench/bench.py:40-61). Each timed replay carries a fixed cost of about 10 µs on MI355X
+    (two timing events with nothing between them read 4.2 µs; a one-call graph 18.9 µs against 8.6 µs per further
+    call at the headline), which a short graph spreads over few calls: 0.5 µs per call at 20 calls, 0.1 at 100."""
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
@@ -308,26 +312,69 @@ def cost_features(B, Q, H, D, C, N, L, P, s):
             [1.0, B * N * (C + HD) * s / 1e6, 2 * B * N * C * HD / 1e9, samples * D * s / 1e6])
 
 
-def fit_auto(out_path):
-    """Measure both modes over auto_grid(), fit FUSED_LIMIT's linear cost model per dtype family by non-negative
-    least squares on relative error, and report every case's loss of the fitted and the current selector."""
-    import numpy as np
-    from scipy.optimize import nnls
+def measure_grid(cases):
+    """Graph-timed µs of both modes for every case, with the mode the current table picks."""
     rows = []
     with torch.inference_mode():
-        for name, B, Q, H, D, C, levels, P, dt, bias, ld in auto_grid():
+        for name, B, Q, H, D, C, levels, P, dt, bias, ld in cases:
             dev = [None if t is None else t.cuda() for t in workload(B, Q, H, D, C, levels, P, dt, bias=bias,
                                                                       loc_dist=ld)]
             N, L = dev[0].shape[1], len(levels)
             steps = 100 if B * Q * C < 2_000_000 else 20
             t = {m: graph_time_us(lambda m=m: td.ma_deform_attn(*dev, mode=m), steps, 5) for m in ('fused', 'project')}
             cur = td.choose_mode(dev[0], dev[1], dev[5])
-            rows.append(dict(case=name, dtype=DTYPE_NAMES[dt], B=B, Q=Q, H=H, D=D, C=C, N=N, L=L, P=P,
-                             s=dev[0].element_size(), fused=t['fused'], project=t['project'], current_pick=cur))
-            log(f'{name:9s} {DTYPE_NAMES[dt]:4s} B={B} Q={Q:3d} fused {t["fused"]:8.2f} project {t["project"]:8.2f}'
-                f' auto now picks {cur}')
+            best = min(t.values())
+            rows.append(dict(case=name, dtype=DTYPE_NAMES[dt], B=B, Q=Q, H=H, D=D, C=C, N=N, L=L, P=P, loc=ld,
+                             s=dev[0].element_size(), fused=t['fused'], project=t['project'], current_pick=cur,
+                             current_loss=round(t[cur] / best, 3)))
+            log(f'{name:9s} {DTYPE_NAMES[dt]:4s} B={B} Q={Q:3d} {ld:9s} fused {t["fused"]:8.2f} project '
+                f'{t["project"]:8.2f} auto picks {cur} ({t[cur] / best:.3f} of the faster)')
             del dev
             torch.cuda.empty_cache()
+    return rows
+
+
+def holdout_grid():
+    """Shapes the auto selector was not fitted on: query counts, batch sizes, a channel width, a level count and a
+    location distribution outside auto_grid()."""
+    five = [(100, 100), (50, 50), (25, 25), (13, 13), (7, 7)]
+    cases = []
+    for dt in (torch.float32, torch.float16, torch.bfloat16):
+        for B in (2, 3, 6):
+            for Q in (150, 450, 750):
+                for ld in ('uniform', 'clustered'):
+                    cases.append(('rtdetr640', B, Q, 8, 32, 256, RTDETR_LEVELS, 4, dt, True, ld))
+    for dt in (torch.float16, torch.bfloat16):
+        for B in (1, 2, 3, 6):
+            for Q in (150, 450, 750):
+                cases.append(('c512', B, Q, 8, 64, 512, RTDETR_LEVELS, 4, dt, True, 'uniform'))
+    for dt in (torch.float32, torch.float16):
+        for B in (1, 3):
+            for Q in (150, 450, 750):
+                cases.append(('five-level', B, Q, 8, 32, 256, five, 4, dt, True, 'uniform'))
+    return cases
+
+
+def holdout(out_path):
+    """Measure both modes over holdout_grid() and report how far the current selector's pick is from the faster
+    mode in each case (no refit)."""
+    rows = measure_grid(holdout_grid())
+    worst = max(r['current_loss'] for r in rows)
+    within = sum(r['current_loss'] <= 1.10 for r in rows)
+    right = sum(r['current_loss'] <= 1.0 for r in rows)
+    log(f'held-out grid: {len(rows)} cases, auto picked the faster mode in {right}, within 10% in {within}; '
+        f'worst auto/best {worst:.3f}')
+    with open(out_path, 'w') as f:
+        json.dump({'rows': rows, 'worst_current': worst, 'current_within_10pct': within, 'faster_picked': right,
+                   'cases': len(rows)}, f, indent=1)
+
+
+def fit_auto(out_path):
+    """Measure both modes over auto_grid(), fit FUSED_LIMIT's linear cost model per dtype family by non-negative
+    least squares on relative error, and report every case's loss of the fitted and the current selector."""
+    import numpy as np
+    from scipy.optimize import nnls
+    rows = measure_grid(auto_grid())
     table = {}
     for fam in (('f32',), ('f16', 'bf16')):
         xs = [r for r in rows if r['dtype'] in fam]
@@ -345,7 +392,6 @@ def fit_auto(out_path):
     for r in rows:
         best = min(r['fused'], r['project'])
         r['fitted_loss'] = round(r[r['fitted_pick']] / best, 3)
-        r['current_loss'] = round(r[r['current_pick']] / best, 3)
     worst_fit = max(r['fitted_loss'] for r in rows)
     worst_cur = max(r['current_loss'] for r in rows)
     within = sum(r['current_loss'] <= 1.10 for r in rows)
@@ -404,6 +450,9 @@ def main():
     ap.add_argument('--fit-auto', metavar='OUT.json', default=None,
                     help='time fused and project over the auto grid, fit the per-dtype cost model of '
                          'marearts_tinydeform_amd.FUSED_LIMIT and report how far auto is from the faster mode')
+    ap.add_argument('--holdout', metavar='OUT.json', default=None,
+                    help='time fused and project over shapes the selector was not fitted on and report how far '
+                         'auto is from the faster mode in each')
     ap.add_argument('--table', action='store_true',
                     help="the reference's sweep (its bench/bench.py): PyTorch path, fused, project and auto per dtype, "
                          'batch and query count, as a markdown table on stdout')
@@ -428,6 +477,9 @@ def main():
     assert torch.cuda.is_available(), 'no HIP device'
     if args.fit_auto:
         fit_auto(args.fit_auto)
+        return
+    if args.holdout:
+        holdout(args.holdout)
         return
     if args.table:
         table(args)
@@ -536,6 +588,8 @@ def main():
         'config': {'workload': args.workload, 'B': B, 'Q': Q, 'N': N, 'C': C, 'H': H, 'D': D, 'L': L, 'P': P,
                    'mode': 'auto'},
         'modes_us': {k: round(v, 2) for k, v in times.items()},
+        'timing': f'best of 7 replays of a {args.steps}-call graph; each replay also carries about 10 µs of fixed '
+                  f'cost (graph launch and the two timing events), {10.0 / args.steps:.2f} µs per call here',
         'auto_pick': pick,
         'kernels_us': {k: round(v, 2) for k, v in kern.items()},
         'queries_per_s': round(B * Q / (times['auto'] * 1e-6)),
