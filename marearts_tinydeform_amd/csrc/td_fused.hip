@@ -75,10 +75,14 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
 
     extern __shared__ __align__(16) unsigned char smem[];
     Corner<float>* cw = reinterpret_cast<Corner<float>*>(smem);  // [QT][S]
-    float* gs = reinterpret_cast<float*>(cw + QT * S);           // [QT][GP]
-    float* wsum = gs + QT * GP;                                   // [16]
-    unsigned* gmax = reinterpret_cast<unsigned*>(wsum + 16);      // [1] float16: largest |g| above 2^15 (bits)
-    float* part = wsum + 20;                                      // [KS][16][PW]
+    // rows whose corner groups span two wavefronts (SG > 1, CV * SG = 128 lanes) keep the two halves' sums apart:
+    // g = gs + gs2. (With SG = 1 a row wider than a wavefront is split by channels and needs no second half.)
+    const bool two = SG > 1 && CV * SG > kWave;
+    float* gs = reinterpret_cast<float*>(cw + QT * S);            // [QT][GP]
+    float* gs2 = gs + QT * GP;                                     // [QT][GP] (two wavefronts per row)
+    float* wsum = gs2 + (two ? QT * GP : 0);                       // [2][16]
+    unsigned* gmax = reinterpret_cast<unsigned*>(wsum + 32);      // [1] float16: largest |g| above 2^15 (bits)
+    float* part = wsum + 36;                                      // [KS][16][PW]
     float* pro = part + p.KS * 16 * PW;                           // layer: [16][PP] query projections
     float* rstat = pro + 16 * PP;                                 // layer: [16][2] softmax max, 1 / sum
 
@@ -154,21 +158,23 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
         for (int i = 0; i < V; ++i) acc[i] = 0.f;
         float ws = 0.f;
         gather_sum<T, V, NB>(cw + r * S, S, sg, SG, mb + ch * V, static_cast<size_t>(C), acc, ws);
-        for (int m = CV; m < GS; m <<= 1) {
+        for (int m = CV; m < GS && m < kWave; m <<= 1) {
 #pragma unroll
             for (int i = 0; i < V; ++i) acc[i] += xor_lane(acc[i], m);
             ws += xor_lane(ws, m);
         }
-        if (sg == 0) {
-            float* dst = gs + r * GP + ch * V;
+        if ((rem & (kWave - 1)) < CV) {  // the first corner group of each wavefront holds its wavefront's sums
+            const int half = two && rem >= kWave;
+            float* dst = (half ? gs2 : gs) + r * GP + ch * V;
 #pragma unroll
             for (int i = 0; i < V; i += 4)
                 *reinterpret_cast<f32x4*>(dst + i) = f32x4{acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
-            if (ch == 0) wsum[r] = ws;
+            if (ch == 0) wsum[16 * half + r] = ws;
             if constexpr (std::is_same<T, f16>::value) {
                 float m = 0.f;
 #pragma unroll
                 for (int i = 0; i < V; ++i) m = fmaxf(m, fabsf(acc[i]));
+                if (two) m *= 2.f;  // bounds the sum of the two halves
                 if (m > 32768.f) atomicMax(gmax, __float_as_uint(m));  // rare: un-normalised weights, huge memory
             }
         }
@@ -212,8 +218,14 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
                 if (dv && kv) braw = *reinterpret_cast<const u32x4*>(wr + k);
                 f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
                 if (av && kv) {
-                    a0 = *reinterpret_cast<const f32x4*>(ga + k) * sc;
-                    a1 = *reinterpret_cast<const f32x4*>(ga + k + 4) * sc;
+                    a0 = *reinterpret_cast<const f32x4*>(ga + k);
+                    a1 = *reinterpret_cast<const f32x4*>(ga + k + 4);
+                    if (two) {
+                        a0 += *reinterpret_cast<const f32x4*>(ga + QT * GP + k);
+                        a1 += *reinterpret_cast<const f32x4*>(ga + QT * GP + k + 4);
+                    }
+                    a0 *= sc;
+                    a1 *= sc;
                 }
                 frag hi, lo;
 #pragma unroll
@@ -247,7 +259,10 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
                 const bool kv = k < C;
                 f32x4 bq = {0.f, 0.f, 0.f, 0.f}, aq = bq;
                 if (dv && kv) bq = *reinterpret_cast<const f32x4*>(wr + k);
-                if (av && kv) aq = *reinterpret_cast<const f32x4*>(ga + k);
+                if (av && kv) {
+                    aq = *reinterpret_cast<const f32x4*>(ga + k);
+                    if (two) aq += *reinterpret_cast<const f32x4*>(ga + QT * GP + k);
+                }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[j], bq[j], acc, 0, 0, 0);
             }
@@ -265,7 +280,8 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
         float v = part[r * PW + d];
         for (int ks = 1; ks < p.KS; ++ks) v += part[(ks * 16 + r) * PW + d];
         v *= inv_sc;
-        if (bias != nullptr) v = fmaf(cvt<float>(bias[static_cast<size_t>(h) * D + d]), wsum[r], v);
+        if (bias != nullptr)
+            v = fmaf(cvt<float>(bias[static_cast<size_t>(h) * D + d]), two ? wsum[r] + wsum[16 + r] : wsum[r], v);
         out[(static_cast<size_t>(rbase + r) * g.H + h) * D + d] = static_cast<T>(v);
     }
 }
@@ -355,17 +371,26 @@ inline int64_t map_units(FusedParams& p) {
     return static_cast<int64_t>(p.per_xcd) * kXcds;
 }
 
-template <typename T, int WAVES, bool LAYER>
-int go_vec(FusedParams p, size_t lds, hipStream_t stream) {
+template <typename T, int WAVES, bool LAYER, int NB>
+int go_vec_nb(FusedParams p, size_t lds, hipStream_t stream) {
     const int64_t blocks = map_units(p);
     if (p.g.general())
         hipLaunchKernelGGL((fused_vec_kernel<T, WAVES, 8, true, LAYER>), dim3(static_cast<unsigned>(blocks)),
                            dim3(WAVES * kWave), lds, stream, p);
     else
-        hipLaunchKernelGGL((fused_vec_kernel<T, WAVES, 8, false, LAYER>), dim3(static_cast<unsigned>(blocks)),
+        hipLaunchKernelGGL((fused_vec_kernel<T, WAVES, NB, false, LAYER>), dim3(static_cast<unsigned>(blocks)),
                            dim3(WAVES * kWave), lds, stream, p);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : set_error(-3, "fused_vec launch failed: %s", hipGetErrorString(e));
+}
+
+// nb: corner loads in flight per lane, 8 or 6 (the plain kernel only; 6 keeps it at 64 VGPRs, 8 wavefronts per SIMD)
+template <typename T, int WAVES, bool LAYER>
+int go_vec(FusedParams p, size_t lds, hipStream_t stream, int nb = 8) {
+    if constexpr (!LAYER) {
+        if (nb == 6) return go_vec_nb<T, WAVES, LAYER, 6>(p, lds, stream);
+    }
+    return go_vec_nb<T, WAVES, LAYER, 8>(p, lds, stream);
 }
 
 template <typename T, int WAVES>
@@ -417,7 +442,9 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
                     while (sg > 1 && S / sg < 4) sg >>= 1;
                 }
             }
-            if (sg > 1 && !(is_pow2(CV) && is_pow2(sg) && CV * sg <= kWave)) sg = 1;
+            // corner groups of one row span at most two wavefronts, and more than one only in whole wavefronts
+            if (sg > 1 && !(is_pow2(CV) && is_pow2(sg) && (CV * sg <= kWave || (CV * sg == 2 * kWave && CV <= kWave))))
+                sg = 1;
             const int GS = CV * sg;
             const int rows_per_pass = nth / GS > 0 ? nth / GS : 1;
             int qt = tune.qt;
@@ -427,44 +454,76 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
             }
             if (qt > qmax) qt = qmax;
             if (qt < 1) qt = 1;
-            // Small problems with one row per wavefront take balanced slices instead of query tiles: k workgroups
-            // per CU for the smallest k whose slices fit 8 rows, each slice holding the same number of (batch,
-            // query) rows of its head to within one, in 8-wavefront workgroups. A grid of fixed 4-row tiles left
-            // some CUs a third tile: 600 tiles on 256 CUs at the headline, 8.94 µs against 8.66 with two slices of
-            // 4-5 rows per CU; one workgroup per CU is best where it fits (100 queries: 6.65 against 7.60 µs, and
-            // 7.54 with two per CU; 50 queries: 6.30 against 6.62); float32 300 queries: 13.21 against 14.02.
+            // Small problems take balanced slices instead of query tiles: slice s of head h holds (batch, query)
+            // rows s * slice_rows + min(s, slice_extra) onward, slice_rows + (s < slice_extra) of them, so every CU
+            // holds the same number of rows to within one. Shapes measured on MI355X (graph-timed µs, fixed 4-row
+            // tiles -> chosen shape):
+            //  * when one workgroup per CU takes at most 6 rows, 16-bit rows are gathered by two wavefronts each
+            //    (corner groups over 128 lanes, 6 loads in flight per lane): RT-DETR fp16 B1 Q50 6.28 -> 5.74,
+            //    Q100 6.73 -> 5.87, Q150 7.03 -> 6.68;
+            //  * otherwise one wavefront per row, with k workgroups per CU for the smallest k whose slices fit 12
+            //    rows (k <= 2; 12-wavefront workgroups) or 8 rows (8 wavefronts): fp16 B1 Q300 8.94 (tiles) ->
+            //    8.66 (two 8-wavefront slices of 4-5 rows per CU) -> 8.18 (one 12-wavefront slice of 9-10 rows),
+            //    fp32 B1 Q300 14.02 -> 12.37, fp16 B2 Q300 12.20 -> 11.93, fp16 B3 Q300 (four 8-row slices per CU,
+            //    6 loads in flight so that 32 wavefronts fit) 16.50 -> 15.25.
+            const int NTILE = (D + 15) / 16;
+            const int nk = sizeof(T) == 2 ? (C + 31) / 32 : (C + 15) / 16;
+            const int GP = (layer && p.lay.Cq > C ? p.lay.Cq : C) + 4;
+            const int PP = ((3 * LP + 15) & ~15) + 4;
+            auto k_slices = [&](int w) {
+                int ks = w / NTILE;
+                return ks < 1 ? 1 : ks > nk ? nk : ks;
+            };
+            // LDS bytes of a workgroup of q rows, w wavefronts, gathered by corner groups sgx
+            auto lds_of = [&](int q, int w, int sgx) {
+                const size_t halves = sgx > 1 && CV * sgx > kWave ? 2 : 1;
+                return static_cast<size_t>(q) * S * sizeof(Corner<float>) + halves * q * GP * 4 + 36 * 4 +
+                       static_cast<size_t>(k_slices(w)) * 16 * NTILE * 16 * 4 +
+                       (layer ? static_cast<size_t>(16 * PP + 32) * 4 : 0);
+            };
             int64_t slices = 0;
+            int nb = 8;
             const int64_t BQ = static_cast<int64_t>(g.B) * g.Q;
-            if (!layer && !big && GS == kWave && tune.qt <= 0 && tune.waves <= 0) {
+            if (!layer && !big && GS == kWave && tune.qt <= 0 && tune.waves <= 0 && tune.sg <= 0) {
                 const int cus = cu_count();
-                int64_t per = 0;
-                for (int k = 1; k <= 4; ++k) {
-                    slices = static_cast<int64_t>(k) * cus / g.H;
-                    if (slices < 1) slices = 1;
-                    if (slices > BQ) slices = BQ;
-                    per = (BQ + slices - 1) / slices;
-                    if (per <= 8) break;
+                auto slices_for = [&](int k) {
+                    int64_t sl = static_cast<int64_t>(k) * cus / g.H;
+                    return sl < 1 ? int64_t{1} : sl > BQ ? BQ : sl;
+                };
+                const int64_t s1 = slices_for(1), per1 = (BQ + s1 - 1) / s1;
+                int s_qt = 0, s_waves = 0, s_sg = sg, s_nb = 8;
+                if (sizeof(T) == 2 && S / (2 * sg) >= 4 && per1 <= 6) {
+                    s_sg = 2 * sg;  // CV * s_sg = 128: two whole wavefronts per row
+                    slices = s1;
+                    s_qt = static_cast<int>(per1);
+                    s_waves = 2 * s_qt <= 8 ? 8 : 12;
+                    s_nb = 6;
+                } else {
+                    for (int k = 1; k <= 4 && slices == 0; ++k) {
+                        const int64_t sl = slices_for(k), per = (BQ + sl - 1) / sl;
+                        if (per <= 8 || (k <= 2 && per <= 12)) {
+                            slices = sl;
+                            s_qt = static_cast<int>(per);
+                            s_waves = per <= 8 ? 8 : 12;
+                            // 6 loads in flight where 8 (80 VGPRs: 24 wavefronts per CU) do not fit, and for 16-bit
+                            // rows in one 12-wavefront slice per CU (fp16 B1 Q300 8.25 -> 8.18 µs, bf16 8.47 ->
+                            // 8.38; two slices per CU or float32 measured faster with 8)
+                            s_nb = k * s_waves > 24 || (sizeof(T) == 2 && k == 1 && s_waves == 12) ? 6 : 8;
+                        }
+                    }
                 }
-                if (per <= 8) {
-                    qt = static_cast<int>(per);
-                    waves = 8;
+                // a slice's rows must all fit one workgroup's LDS; otherwise query tiles
+                if (slices > 0 && lds_of(s_qt, s_waves, s_sg) <= kLdsBudget) {
+                    qt = s_qt;
+                    waves = s_waves;
+                    sg = s_sg;
+                    nb = s_nb;
                 } else {
                     slices = 0;
                 }
             }
-            const int NTILE = (D + 15) / 16;
-            const int nk = sizeof(T) == 2 ? (C + 31) / 32 : (C + 15) / 16;
-            int ks = waves / NTILE;
-            if (ks < 1) ks = 1;
-            if (ks > nk) ks = nk;
-            const int GP = (layer && p.lay.Cq > C ? p.lay.Cq : C) + 4;
-            const int PP = ((3 * LP + 15) & ~15) + 4;
-            auto lds = [&](int q) {
-                return static_cast<size_t>(q) * S * sizeof(Corner<float>) + static_cast<size_t>(q) * GP * 4 +
-                       20 * 4 + static_cast<size_t>(ks) * 16 * NTILE * 16 * 4 +
-                       (layer ? static_cast<size_t>(16 * PP + 32) * 4 : 0);
-            };
-            if (slices > 0 && lds(qt) > kLdsBudget) slices = 0;  // a slice's rows must all fit the tile: use tiles
+            const int ks = k_slices(waves);
+            auto lds = [&](int q) { return lds_of(q, waves, sg); };
             while (qt > 1 && lds(qt) > kLdsBudget) --qt;
             if (lds(qt) <= kLdsBudget) {
                 p.QT = qt;
@@ -476,7 +535,7 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
                     p.slice_rows = static_cast<int>(BQ / slices);
                     p.slice_extra = static_cast<int>(BQ % slices);
                 }
-                // 8 corner loads in flight per lane: measured best on MI355X at every benchmark shape
+                // corner loads in flight per lane: 8 (6 for the slice shapes above that need it)
                 if (layer) {
                     switch (waves) {
                         case 4: return go_vec<T, 4, true>(p, lds(qt), stream);
@@ -485,9 +544,10 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
                     }
                 }
                 switch (waves) {
-                    case 4: return go_vec<T, 4, false>(p, lds(qt), stream);
-                    case 8: return go_vec<T, 8, false>(p, lds(qt), stream);
-                    default: return set_error(-1, "fused: waves must be 4 or 8 (got %d)", waves);
+                    case 4: return go_vec<T, 4, false>(p, lds(qt), stream, nb);
+                    case 8: return go_vec<T, 8, false>(p, lds(qt), stream, nb);
+                    case 12: return go_vec<T, 12, false>(p, lds(qt), stream, nb);
+                    default: return set_error(-1, "fused: waves must be 4, 8 or 12 (got %d)", waves);
                 }
             }
         }

@@ -392,6 +392,23 @@ def test_rtdetr640_fp16_b1(Q):
                     torch.float16)
 
 
+@pytest.mark.parametrize('dtype,B,Q', [
+    (torch.float16, 1, 150),    # rows gathered by two wavefronts, one 12-wavefront slice per CU
+    (torch.bfloat16, 1, 150),
+    (torch.float16, 2, 300),    # one wavefront per row, two 12-wavefront slices per CU
+    (torch.float32, 2, 300),
+    (torch.float16, 3, 300),    # four 8-wavefront slices per CU, 6 loads in flight per lane
+    (torch.bfloat16, 3, 300),
+    (torch.float16, 4, 50),     # one 8-wavefront slice of 7 rows per CU
+])
+def test_rtdetr640_slice_shapes(dtype, B, Q):
+    # the fused kernel's balanced-slice launch shapes beyond the benchmark configurations (sampled rows against the
+    # oracle, fused and project over the whole output)
+    rows = np.sort(np.random.default_rng(B * Q).choice(B * Q * 8, size=min(B * Q * 8, 1536), replace=False))
+    full_size_check(f'rtdetr640 {dtype} B{B} Q{Q}', workload(B, Q, 8, 32, 256, RTDETR_LEVELS, 4, dtype), dtype,
+                    rows=rows)
+
+
 def test_rtdetr640_fp32_b1_q300():
     full_size_check('rtdetr640 fp32 B1 Q300', workload(1, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.float32),
                     torch.float32)
