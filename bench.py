@@ -183,14 +183,14 @@ def train_times(cpu_args, steps, warmup):
 
 def gemm_kernel(M, K, NO, s):
     """Which value-projection kernel td_value_proj launches for an aligned [M, K] x [K, NO] problem (element size
-    s), following its size rule: 16-bit with 256 outputs, K = 128 or 256 and at least 16500 rows takes the streaming
+    s), following its size rule: 16-bit with 256 outputs, K = 256 and at least 14000 rows (K = 128: 8000) takes the streaming
     kernel; 16-bit deep K (K >= 512, K % 64 == 0) on a grid of >= 200 tiles of 256 x 128 the direct-to-LDS kernel;
     other 16-bit grids take register-operand tiles (32 x 32 to 64 x 64) up to 1100 tiles of 64 x 64 for K <= 256 and
     under 512 for deeper K, larger ones both operands through LDS;
     float32 takes register-operand tiles of 32 x 32 to 64 x 128."""
     tiles_128 = -(-M // 128) * -(-NO // 128)
     if s == 2:
-        if NO == 256 and K in (128, 256) and M >= 16500:
+        if NO == 256 and K in (128, 256) and M >= (14000 if K == 256 else 8000):
             return 'gemm_stream_kernel'
         if K >= 512 and K % 64 == 0 and -(-M // 256) * -(-NO // 128) >= 200:
             return 'gemm_dma_kernel'

@@ -384,18 +384,18 @@ int go_mfma(GemmParams p, hipStream_t stream) {
 //   13 128 x 128 A and W through LDS, K chunks of 32/16
 //   14 256 x 128 tiles fed by direct-to-LDS loads (td_gemm_dma.hip; 16-bit, K % 64 == 0)
 //   16 256 x 256 tiles fed by direct-to-LDS loads (td_gemm_dma.hip; 16-bit, K % 64 == 0)
-//   22 the streaming kernel: W resident in LDS, token rows streamed into MFMA fragments (td_gemm_stream.hip;
-//      16-bit, NO = 256, K = 128 or 256)
+//   22 the streaming kernel: a quarter of W in each wavefront's registers, token rows streamed through LDS
+//      (td_gemm_stream.hip; 16-bit, NO = 256, K = 128 or 256)
 //   23 64 x 32   4 waves of 16 x 32, one chunk of 256/128, one stage
 //   24 32 x 32   2 waves of 16 x 32, one chunk of 256/128, one stage
 //   25 64 x 64   4 waves of 16 x 64, K chunks of 128/64, two stages
 //   0  gemm_generic_kernel (float64, odd K, A or W not 16-byte aligned)
 //
 // Measured on MI355X (16-bit):
-//   256 outputs, K = 128 or 256, from 16500 rows: the streaming kernel (22) (K = 256: M = 16800 10.5 µs against 11.2
-//     for 13 and 12.2 for 25, M = 20000 10.9 against 11.8, M = 33600 12.8 against 15.4, M = 67200 19.5 against 23.5;
-//     K = 128: M = 16800 7.4 against 8.5; it loses at 16384 rows, 10.8 against 9.9 for 25, where its start, W into
-//     every CU's LDS, is not paid back);
+//   256 outputs: the streaming kernel (22) from 14000 rows at K = 256 (M = 16384 8.3 µs against 9.1 for 25, M = 16800
+//     9.1 against 11.2 for 13 and 12.2 for 25, M = 33600 12.2 against 15.4, M = 67200 17.6 against 23.5; it loses at
+//     12000 rows, 7.8 against 7.4 for 25, and at 8400, 7.5 against 7.1), from 8000 rows at K = 128 (M = 8400 5.4
+//     against 5.6 for 25, M = 16384 6.1 against 7.0);
 //   deep K (K >= 512, K % 64 == 0) on a grid of at least 200 tiles of 256 x 128: the direct-to-LDS kernel, 256 x 256
 //     tiles (16) from 2.5 rounds of them on 256 CUs, else 256 x 128 (14) (C = 1024: M = 43520 101 µs against 122 µs
 //     for 13; M = 21760 57 against 68; M = 7200 23.6 against 29.2 for 13);
@@ -424,7 +424,7 @@ int pick_variant(int dtype, const GemmParams& p) {
         if (p.K <= 256) return tiles_64 <= 40 ? 24 : tiles_64 <= 100 ? 23 : tiles_64 <= 1100 ? 25 : tiles_128 < 1024 ? 5 : 2;
         return tiles_64 < 512 ? 25 : 2;
     }
-    if (p.M >= 16500 && gemm_stream_fits(dtype, p)) return 22;
+    if (gemm_stream_fits(dtype, p) && p.M >= (p.K == 256 ? 14000 : 8000)) return 22;
     const int64_t tiles_256x128 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 127) / 128);
     const int64_t tiles_256 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 255) / 256);
     if (p.K >= 512 && p.K % 64 == 0 && tiles_256x128 >= 200) return tiles_256 >= 640 ? 16 : 14;

@@ -3,7 +3,8 @@
 kernel the rule can pick for any shape has at least one of these cases; the GPU tests run them against the oracle.
 
 Kernel numbers (csrc/td_gemm.hip): 0 generic VALU; 2, 5, 23, 24, 25 A-in-registers MFMA tiles; 9, 13 both operands
-through LDS; 14, 16 direct-to-LDS 256 x 128 / 256 x 256 tiles; 22 the streaming kernel (W resident in LDS).
+through LDS; 14, 16 direct-to-LDS 256 x 128 / 256 x 256 tiles; 22 the streaming kernel (W resident in registers,
+tokens streamed through LDS).
 """
 
 import torch
@@ -34,19 +35,20 @@ DEEP_K = [
     (9000, 520, 256, 9),       # K >= 512 but not a multiple of 64
 ]
 
-# 16-bit (M, K, bias, kernel) with NO = 256, every row checked: the streaming kernel from 16500 rows. Shares that
-# end in a short remainder go in rounds of 4 x 32 tokens and then remainder steps in which every wavefront computes a
-# quarter of the channels: one such step (36001, 33600, 67200 at K = 256; 70003 at K = 128), two (44447 at K = 256),
-# none (131072). Other shares are split evenly over the wavefronts in steps of 32 with a partial last step (16800,
-# 20011, 44447 at K = 128, 88892).
+# 16-bit (M, K, bias, kernel) with NO = 256, every row checked: the streaming kernel from 14000 rows at K = 256 and
+# 8000 at K = 128. Each CU takes an equal share of M (shares differ by one row) in steps of 32 tokens, the last one
+# partial: one step per CU (8000, 8100 at K = 128, where fewer than 256 workgroups run), two (16384), shares off the
+# step size (14000, 36001, 44447, 20011, 70003), whole steps (131072 = 256 x 16 x 32), with and without bias.
 STREAM = [
-    (36001, 256, True, 22), (33600, 256, False, 22), (67200, 256, True, 22), (44447, 256, False, 22),
-    (131072, 256, True, 22), (16800, 256, True, 22), (88892, 256, True, 22), (70003, 128, True, 22),
-    (44447, 128, False, 22), (20011, 128, True, 22),
-    (16384, 256, True, 25),    # one tile short of the streaming kernel's range
+    (14000, 256, True, 22), (16384, 256, True, 22), (16800, 256, False, 22), (33600, 256, False, 22),
+    (36001, 256, True, 22), (44447, 256, False, 22), (67200, 256, True, 22), (88892, 256, True, 22),
+    (131072, 256, True, 22), (8000, 128, True, 22), (8100, 128, False, 22), (20011, 128, True, 22),
+    (44447, 128, False, 22), (70003, 128, True, 22),
+    (13999, 256, True, 25),    # one row short of the streaming kernel's range
+    (7999, 128, True, 25),
 ]
 
-# 16-bit (M, K, NO, kernel): a bias view 2 bytes off a 16-byte boundary. The streaming kernel stages the bias with
+# 16-bit (M, K, NO, kernel): a bias view 2 bytes off a 16-byte boundary. The streaming kernel reads the bias with
 # 16-byte loads, so such a bias must fall back to the tiled kernels.
 BIAS_OFFSET = [
     (16800, 256, 256, 25),

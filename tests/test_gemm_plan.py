@@ -30,7 +30,7 @@ def covered():
 
 def test_every_reachable_kernel_has_a_parity_case():
     cov = covered()
-    Ms = sorted({int(1.37 ** i) for i in range(40)} | {300, 600, 3600, 8400, 16499, 16500, 21760, 43520, 67200,
+    Ms = sorted({int(1.37 ** i) for i in range(40)} | {300, 600, 3600, 7999, 8000, 8400, 13999, 14000, 21760, 43520, 67200,
                                                        88892, 177784, 300000})
     Ks = (8, 40, 64, 96, 128, 256, 512, 520, 576, 1024, 2048)
     NOs = (16, 48, 64, 136, 200, 256, 512, 1000, 1024, 2048)
@@ -53,7 +53,7 @@ def test_every_reachable_kernel_has_a_parity_case():
 
 
 def test_streaming_kernel_needs_an_aligned_bias():
-    # the streaming kernel loads the bias with 16-byte direct loads: any bias offset leaves it
+    # the streaming kernel reads the bias with 16-byte loads: any bias offset leaves it
     assert _native.value_proj_plan(F16, 67200, 256, 256) == 22
     assert _native.value_proj_plan(F16, 67200, 256, 256, bias=False) == 22
     for off in (2, 4, 8):

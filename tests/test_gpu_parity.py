@@ -256,9 +256,10 @@ def test_value_proj_deep_k_matches_oracle(dtype):
 
 @pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
 def test_value_proj_streaming_matches_oracle(dtype):
-    # 16-bit, 256 outputs, K = 128 or 256, from 16500 rows: the streaming kernel (W resident in LDS; each workgroup
-    # an equal share of the rows); see tests/gemm_cases.py for which remainder path each M takes. Every row is
-    # checked: the share boundaries fall anywhere in M. Odd M, with and without bias.
+    # 16-bit, 256 outputs, K = 128 or 256, from 14000 / 8000 rows: the streaming kernel (W resident in registers,
+    # tokens streamed through LDS; each workgroup an equal share of the rows); see tests/gemm_cases.py for the step
+    # structure each M takes. Every row is checked: the share boundaries fall anywhere in M. Odd M, with and without
+    # bias.
     for M, K, bias, kern in gemm_cases.STREAM:
         gemm_case(dtype, M, K, 256, bias, None, kern, 12)
 
