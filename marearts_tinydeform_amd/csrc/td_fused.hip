@@ -359,6 +359,7 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_generic_kernel(FusedParams
 }
 
 constexpr size_t kLdsBudget = 65536;
+constexpr size_t kGenericLdsBudget = 160 * 1024;  // MI355X: 160 KB of LDS per CU
 
 inline bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
@@ -393,9 +394,23 @@ int go_vec(FusedParams p, size_t lds, hipStream_t stream, int nb = 8) {
     return go_vec_nb<T, WAVES, LAYER, 8>(p, lds, stream);
 }
 
+// The generic kernel may take up to the CU's whole LDS (wide float64 rows: C = 8192 needs 68 KB at one row per
+// workgroup); launches above 64 KB need the attribute, set once per instantiation.
+template <auto Kernel>
+int allow_lds(size_t lds) {
+    if (lds <= 65536) return 0;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(Kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       static_cast<int>(kGenericLdsBudget));
+    return attr == hipSuccess ? 0 : set_error(-3, "fused_generic: LDS size attribute refused: %s", hipGetErrorString(attr));
+}
+
 template <typename T, int WAVES>
 int go_generic(FusedParams p, size_t lds, hipStream_t stream) {
     const int64_t blocks = map_units(p);
+    const int rc = p.g.general() ? allow_lds<fused_generic_kernel<T, WAVES, true>>(lds)
+                                 : allow_lds<fused_generic_kernel<T, WAVES, false>>(lds);
+    if (rc != 0) return rc;
     if (p.g.general())
         hipLaunchKernelGGL((fused_generic_kernel<T, WAVES, true>), dim3(static_cast<unsigned>(blocks)),
                            dim3(WAVES * kWave), lds, stream, p);
@@ -562,7 +577,7 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
     if (qt > qmax) qt = qmax;
     if (qt < 1) qt = 1;
     while (qt > 1 && lds(qt) > kLdsBudget) --qt;
-    if (lds(qt) > kLdsBudget)
+    if (lds(qt) > kGenericLdsBudget)
         return set_error(-1, "channels (%d) too large for the %s fused kernel", C, sizeof(T) == 8 ? "float64" : "scalar");
     p.QT = qt;
     p.SG = 1;

@@ -83,6 +83,13 @@ def test_float64_cases():
         check_modes(f'{name} fp64', make(*shape, dtype=torch.float64), torch.float64)
 
 
+def test_float64_fused_c8192():
+    # the widest rows fused mode accepts (C <= 8192, reference csrc/ma_deform_fused.cu:301): in float64 one row of
+    # accumulators takes 64 KB of LDS, beyond the default budget of a launch
+    args = make(1, 6, 2, 8, 8192, [(4, 5), (2, 3)], 2, dtype=torch.float64)
+    check_modes('fp64 C8192', args, torch.float64, modes=('fused', 'auto'))
+
+
 def test_unaligned_memory_uses_generic_kernel():
     # reference tests/test_correctness.py:83-95: memory 2 or 4 bytes off a 16-byte boundary
     for dtype in (torch.float32, torch.float16, torch.bfloat16):
