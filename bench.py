@@ -184,7 +184,8 @@ def train_times(cpu_args, steps, warmup):
 def gemm_kernel(M, K, NO, s):
     """Which value-projection kernel td_value_proj launches for an aligned [M, K] x [K, NO] problem (element size
     s), following its size rule: 16-bit with 256 outputs, K = 256 and at least 14000 rows (K = 128: 8000) takes the streaming
-    kernel; 16-bit deep K (K >= 512, K % 64 == 0) on a grid of >= 200 tiles of 256 x 128 the direct-to-LDS kernel;
+    kernel; 16-bit deep K (K >= 512, K % 64 == 0) on a grid of >= 200 tiles of 256 x 128, more than 256 of 128 x 128 or
+    from 8000 rows the direct-to-LDS kernel;
     other 16-bit grids take register-operand tiles (32 x 32 to 64 x 64) up to 1100 tiles of 64 x 64 for K <= 256 and
     under 512 for deeper K, larger ones both operands through LDS;
     float32 takes register-operand tiles of 32 x 32 to 64 x 128."""
@@ -192,7 +193,7 @@ def gemm_kernel(M, K, NO, s):
     if s == 2:
         if NO == 256 and K in (128, 256) and M >= (14000 if K == 256 else 8000):
             return 'gemm_stream_kernel'
-        if K >= 512 and K % 64 == 0 and -(-M // 256) * -(-NO // 128) >= 200:
+        if K >= 512 and K % 64 == 0 and (-(-M // 256) * -(-NO // 128) >= 200 or tiles_128 > 256 or M >= 8000):
             return 'gemm_dma_kernel'
         tiles_64 = -(-M // 64) * -(-NO // 64)
         if K <= 256:
@@ -290,13 +291,19 @@ def pmc_run(dev, H, steps):
 
 def auto_grid():
     """The shapes the auto selector is fitted on: RT-DETR 640 (the reference's bench grid: 3 dtypes x batch 1/4/8
-    x 50..900 queries), DINO 4-level and the C=1024 / 64-sample limit shape."""
+    x 50..900 queries, and batch 2 in 16 bits), a C=512 model (batch 1/2/4), DINO 4-level and the C=1024 / 64-sample
+    limit shape."""
     cases = []
     for dt in (torch.float32, torch.float16, torch.bfloat16):
         for B in (1, 4, 8):
             for Q in (50, 100, 200, 300, 600, 900):
                 cases.append(('rtdetr640', B, Q, 8, 32, 256, RTDETR_LEVELS, 4, dt, True, 'uniform'))
     for dt in (torch.float16, torch.bfloat16):
+        for Q in (100, 300, 600, 900):
+            cases.append(('rtdetr640', 2, Q, 8, 32, 256, RTDETR_LEVELS, 4, dt, True, 'uniform'))
+        for B in (1, 2, 4):
+            for Q in (100, 300, 600, 900):
+                cases.append(('c512', B, Q, 8, 64, 512, RTDETR_LEVELS, 4, dt, True, 'uniform'))
         for B, Q in ((1, 300), (4, 300), (4, 900), (8, 900)):
             cases.append(('dino4l', B, Q, 8, 32, 256, DINO_LEVELS, 4, dt, True, 'outside10'))
     for Q in (50, 300, 900):
@@ -305,11 +312,7 @@ def auto_grid():
     return cases
 
 
-def cost_features(B, Q, H, D, C, N, L, P, s):
-    samples = B * Q * H * L * P * 4
-    HD = H * D
-    return ([1.0, samples * C * s / 1e6],
-            [1.0, B * N * (C + HD) * s / 1e6, 2 * B * N * C * HD / 1e9, samples * D * s / 1e6])
+cost_features = td.cost_features
 
 
 def measure_grid(cases):
@@ -335,8 +338,9 @@ def measure_grid(cases):
 
 
 def holdout_grid():
-    """Shapes the auto selector was not fitted on: query counts, batch sizes, a channel width, a level count and a
-    location distribution outside auto_grid()."""
+    """Shapes the auto selector was not fitted on: query counts (150/450/750), batch sizes (2/3/6 for RT-DETR), a
+    channel width never fitted (C=768, 12 heads), a level count (5) and a location distribution (clustered) outside
+    auto_grid()."""
     five = [(100, 100), (50, 50), (25, 25), (13, 13), (7, 7)]
     cases = []
     for dt in (torch.float32, torch.float16, torch.bfloat16):
@@ -352,6 +356,10 @@ def holdout_grid():
         for B in (1, 3):
             for Q in (150, 450, 750):
                 cases.append(('five-level', B, Q, 8, 32, 256, five, 4, dt, True, 'uniform'))
+    for dt in (torch.float16, torch.bfloat16):
+        for B in (1, 2, 5):
+            for Q in (150, 450, 750):
+                cases.append(('c768', B, Q, 12, 64, 768, RTDETR_LEVELS, 4, dt, True, 'uniform'))
     return cases
 
 

@@ -13,7 +13,7 @@ from . import _native
 from .reference import layer_locations_reference, ma_deform_attn_layer_reference, ma_deform_attn_reference
 
 __all__ = ['ma_deform_attn', 'ma_deform_attn_reference', 'choose_mode', 'ma_deform_sample', 'ma_deform_sample_v2',
-           'predict_us', 'ma_deform_attn_layer', 'ma_deform_attn_layer_reference', 'layer_locations_reference',
+           'predict_us', 'cost_features', 'ma_deform_attn_layer', 'ma_deform_attn_layer_reference', 'layer_locations_reference',
            'MSDeformAttnLayer', 'ma_deform_attn_train', 'ma_deform_sample_train']
 __version__ = '0.1.0'
 
@@ -22,19 +22,36 @@ MODES = ('auto', 'fused', 'project')
 # 'auto' compares predicted times of the two orders (reference marearts_tinydeform/__init__.py:21-46 uses one
 # threshold on queries * levels * points * 4 / (tokens * head_dim); on MI355X the value GEMM is cheap next to
 # gathering C-wide rows, so the crossover also moves with C and one threshold cannot place it). Per dtype, each
-# mode's time in µs is a linear function, fitted to MI355X (gfx950) measurements of both modes
-# (bench.py --fit-auto: RT-DETR 640 shapes at batch 1/4/8 and 50..900 queries, DINO 4-level and C=1024 shapes), of
-#   gathered_mb  B*Q*H*L*P*4*C*s / 1e6   C-wide corner rows read by 'fused'          (s = element bytes)
-#   gemm_mb      B*N*(C + H*D)*s / 1e6   value GEMM traffic of 'project'
-#   gemm_gflop   2*B*N*C*H*D / 1e9       value GEMM work of 'project'
-#   sample_mb    B*Q*H*L*P*4*D*s / 1e6   D-wide corner rows read by 'project'
+# mode's time in µs is a linear function of the work it does (cost_features), fitted to MI355X (gfx950)
+# measurements of both modes (bench.py --fit-auto: RT-DETR 640 shapes at batch 1/2/4/8 and 50..900 queries, C = 512
+# at batch 1/2/4, DINO 4-level and C = 1024 shapes; checked on shapes outside that grid with bench.py --holdout):
 #   fused   = f0 + f1 * gathered_mb
-#   project = p0 + p1 * gemm_mb + p2 * gemm_gflop + p3 * sample_mb
+#   project = p0 + p1 * gemm_mb + p2 * gemm_gflop + p3 * gemm_rounds_k + p4 * sample_mb
 FUSED_LIMIT = {
-    torch.float32: {'fused': (8.6944, 0.0528), 'project': (15.1746, 0.6783, 0.0000, 0.0830)},
-    torch.float16: {'fused': (6.3746, 0.0618), 'project': (11.4986, 0.0872, 0.8761, 0.0911)},
-    torch.bfloat16: {'fused': (6.3746, 0.0618), 'project': (11.4986, 0.0872, 0.8761, 0.0911)},
+    torch.float32: {'fused': (7.4791, 0.0478), 'project': (13.9906, 0.6181, 0.0000, 0.0000, 0.0877)},
+    torch.float16: {'fused': (5.7032, 0.0582), 'project': (11.5020, 0.1554, 0.0000, 10.1974, 0.0925)},
+    torch.bfloat16: {'fused': (5.7032, 0.0582), 'project': (11.5020, 0.1554, 0.0000, 10.1974, 0.0925)},
 }
+
+
+def cost_features(B, Q, H, D, C, N, L, P, s):
+    """The work each mode does, the terms of its cost line: ([1, gathered_mb], [1, gemm_mb, gemm_gflop,
+    gemm_rounds_k, sample_mb]) with s the element size in bytes:
+      gathered_mb    B*Q*H*L*P*4*C*s / 1e6   C-wide corner rows read by 'fused'
+      gemm_mb        B*N*(C + H*D)*s / 1e6   value GEMM traffic of 'project'
+      gemm_gflop     2*B*N*C*H*D / 1e9       value GEMM work of 'project' for C < 512 (the bandwidth-bound kernels)
+      gemm_rounds_k  rounds of 256 x 128 output tiles over MI355X's 256 CUs, times C / 1e3, for C >= 512 (the tiled
+                     kernels, whose time goes by whole rounds of tiles, each as long as K)
+      sample_mb      B*Q*H*L*P*4*D*s / 1e6   D-wide corner rows read by 'project'"""
+    samples = B * Q * H * L * P * 4
+    HD, M = H * D, B * N
+    if C >= 512:
+        tiles = -(-M // 256) * -(-HD // 128)
+        narrow, deep = 0.0, -(-tiles // 256) * C / 1e3
+    else:
+        narrow, deep = 2 * M * C * HD / 1e9, 0.0
+    return ([1.0, samples * C * s / 1e6], [1.0, M * (C + HD) * s / 1e6, narrow, deep, samples * D * s / 1e6])
+
 
 # cost tables by GPU architecture (gcnArchName without feature suffixes)
 ARCH_LIMITS = {'gfx950': FUSED_LIMIT}
@@ -63,12 +80,9 @@ def _predict(memory, value_weight, Q, H, L, P, table=None):
     if table is None:
         table = _limits(memory.get_device()) if memory.is_cuda else FUSED_LIMIT
     coef = table.get(memory.dtype, table[torch.float16])
-    samples = B * Q * H * L * P * 4
-    f0, f1 = coef['fused']
-    p0, p1, p2, p3 = coef['project']
-    fused = f0 + f1 * samples * C * s / 1e6
-    project = p0 + p1 * B * N * (C + HD) * s / 1e6 + p2 * 2 * B * N * C * HD / 1e9 + p3 * samples * D * s / 1e6
-    return {'fused': fused, 'project': project}
+    ff, fp = cost_features(B, Q, H, D, C, N, L, P, s)
+    return {'fused': sum(c * x for c, x in zip(coef['fused'], ff)),
+            'project': sum(c * x for c, x in zip(coef['project'], fp))}
 
 
 def choose_mode(memory, value_weight, sampling_locations):

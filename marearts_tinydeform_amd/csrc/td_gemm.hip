@@ -396,9 +396,11 @@ int go_mfma(GemmParams p, hipStream_t stream) {
 //     9.1 against 11.2 for 13 and 12.2 for 25, M = 33600 12.2 against 15.4, M = 67200 17.6 against 23.5; it loses at
 //     12000 rows, 7.8 against 7.4 for 25, and at 8400, 7.5 against 7.1), from 8000 rows at K = 128 (M = 8400 5.4
 //     against 5.6 for 25, M = 16384 6.1 against 7.0);
-//   deep K (K >= 512, K % 64 == 0) on a grid of at least 200 tiles of 256 x 128: the direct-to-LDS kernel, 256 x 256
-//     tiles (16) from 2.5 rounds of them on 256 CUs, else 256 x 128 (14) (C = 1024: M = 43520 101 µs against 122 µs
-//     for 13; M = 21760 57 against 68; M = 7200 23.6 against 29.2 for 13);
+//   deep K (K >= 512, K % 64 == 0) on a grid of at least 200 tiles of 256 x 128, or more than one round (256) of
+//     128 x 128 tiles, or from 8000 rows: the direct-to-LDS kernel, 256 x 256 tiles (16) from 2.5 rounds of them on
+//     256 CUs, else 256 x 128 (14) (C = 1024: M = 43520 101 µs against 122 µs for 13; M = 21760 57 against 68;
+//     M = 7200 23.6 against 29.2 for 13; M = 6000 23.2 against 35.3 for 9; K = NO = 512: M = 8400 15.0 against 22.2
+//     for 9; K = 512, NO = 256: M = 8400 14.4 against 22.1; K = NO = 768: M = 8400 19.3 against 28.8);
 //   smaller grids by their count of 64 x 64 tiles:
 //     K <= 256: up to 300 tiles 32 x 32 (24) (NO = 256: M = 300 3.3 against 4.5 for 64 x 64 one-chunk tiles, M = 2400
 //       4.5 against 4.7), up to 1100 64 x 64 with two-stage K chunks of 128 (25) (M = 8400 7.2 against 7.8,
@@ -406,7 +408,8 @@ int go_mfma(GemmParams p, hipStream_t stream) {
 //     K >= 512: under 64 tiles 32 x 32 (24) (M = 100, K = NO = 1024: 6.5 against 10.2), under 128 64 x 32 (23)
 //       (M = 300: 8.0 against 10.2), under 512 two-stage 64 x 64 (25) (M = 600: 10.0 against 10.4, M = 1800: 13.2
 //       against 14.2), then both operands through LDS with K chunks of 128 (9) while under 512 tiles of 128 x 128
-//       (M = 3600: 19.4 against 25.9), else 13.
+//       (M = 3600: 19.4 against 25.9; against the direct-to-LDS kernel, K = NO = 512: M = 2400 8.1 against 13.1,
+//       M = 4800 11.5 against 13.6; K = NO = 1024: M = 1800 12.8 against 20.0, M = 3600 18.9 against 21.9), else 13.
 // float32 (MFMA-bound: v_mfma_f32_16x16x4_f32), by the count of 64 x 64 tiles: K <= 256: up to 40 tiles 32 x 32 (24)
 //   (K = NO = 256: M = 300 6.0 µs against 9.4 for 5), up to 100 64 x 32 (23) (M = 1200 6.8 against 9.5), up to 1100
 //   two-stage 64 x 64 (25) (M = 2400 9.2 against 9.7, M = 8400 19.8 against 20.9), then 64 x 64 one-chunk tiles (5)
@@ -427,7 +430,8 @@ int pick_variant(int dtype, const GemmParams& p) {
     if (gemm_stream_fits(dtype, p) && p.M >= (p.K == 256 ? 14000 : 8000)) return 22;
     const int64_t tiles_256x128 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 127) / 128);
     const int64_t tiles_256 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 255) / 256);
-    if (p.K >= 512 && p.K % 64 == 0 && tiles_256x128 >= 200) return tiles_256 >= 640 ? 16 : 14;
+    if (p.K >= 512 && p.K % 64 == 0 && (tiles_256x128 >= 200 || tiles_128 > 256 || p.M >= 8000))
+        return tiles_256 >= 640 ? 16 : 14;
     if (p.K <= 256) return tiles_64 <= 300 ? 24 : tiles_64 <= 1100 ? 25 : 13;
     return tiles_64 < 64 ? 24 : tiles_64 < 128 ? 23 : tiles_64 < 512 ? 25 : tiles_128 < 512 ? 9 : 13;
 }

@@ -33,6 +33,8 @@ DEEP_K = [
     (21760, 512, 512, 14),     # a C = 512 model at batch 1
     (43557, 1024, 1000, 16),   # 256 x 256 direct-to-LDS tiles, M and NO off the tile sizes
     (9000, 520, 256, 9),       # K >= 512 but not a multiple of 64
+    (8400, 512, 256, 14),      # direct-to-LDS from 8000 rows even on a small grid (66 tiles of 256 x 128)
+    (6000, 1024, 1024, 14),    # more than one round of 128 x 128 tiles
 ]
 
 # 16-bit (M, K, bias, kernel) with NO = 256, every row checked: the streaming kernel from 14000 rows at K = 256 and
