@@ -24,7 +24,10 @@ MODES = ('auto', 'fused', 'project')
 # gathering C-wide rows, so the crossover also moves with C and one threshold cannot place it). Per dtype, each
 # mode's time in µs is a linear function of the work it does (cost_features), fitted to MI355X (gfx950)
 # measurements of both modes (bench.py --fit-auto: RT-DETR 640 shapes at batch 1/2/4/8 and 50..900 queries, C = 512
-# at batch 1/2/4, DINO 4-level and C = 1024 shapes; checked on shapes outside that grid with bench.py --holdout):
+# at batch 1/2/4, DINO 4-level and C = 1024 shapes; checked on shapes outside that grid with bench.py --holdout).
+# The coefficients were kept when the deep-K GEMM became persistent 256 x 256 tiles (and gemm_rounds_k began counting
+# them): a refit on the new measurements matched them on the fit grid (worst auto/best 1.044) and did worse on the
+# held-out grid (1.36 against 1.07).
 #   fused   = f0 + f1 * gathered_mb
 #   project = p0 + p1 * gemm_mb + p2 * gemm_gflop + p3 * gemm_rounds_k + p4 * sample_mb
 FUSED_LIMIT = {
@@ -40,13 +43,13 @@ def cost_features(B, Q, H, D, C, N, L, P, s):
       gathered_mb    B*Q*H*L*P*4*C*s / 1e6   C-wide corner rows read by 'fused'
       gemm_mb        B*N*(C + H*D)*s / 1e6   value GEMM traffic of 'project'
       gemm_gflop     2*B*N*C*H*D / 1e9       value GEMM work of 'project' for C < 512 (the bandwidth-bound kernels)
-      gemm_rounds_k  rounds of 256 x 128 output tiles over MI355X's 256 CUs, times C / 1e3, for C >= 512 (the tiled
-                     kernels, whose time goes by whole rounds of tiles, each as long as K)
+      gemm_rounds_k  rounds of 256 x 256 output tiles over MI355X's 256 CUs, times C / 1e3, for C >= 512 (the
+                     direct-to-LDS kernels, whose time goes by the busiest CU's count of tiles, each as long as K)
       sample_mb      B*Q*H*L*P*4*D*s / 1e6   D-wide corner rows read by 'project'"""
     samples = B * Q * H * L * P * 4
     HD, M = H * D, B * N
     if C >= 512:
-        tiles = -(-M // 256) * -(-HD // 128)
+        tiles = -(-M // 256) * -(-HD // 256)
         narrow, deep = 0.0, -(-tiles // 256) * C / 1e3
     else:
         narrow, deep = 2 * M * C * HD / 1e9, 0.0

@@ -448,7 +448,6 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
             const int64_t rows = static_cast<int64_t>(g.B) * g.Q * g.H;
             const bool big = rows >= 8192;
             int waves = tune.waves ? tune.waves : big ? 8 : 4;
-            const int nth = waves * kWave;
             int sg = tune.sg;
             if (sg <= 0) {
                 sg = 1;
@@ -461,6 +460,14 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
             if (sg > 1 && !(is_pow2(CV) && is_pow2(sg) && (CV * sg <= kWave || (CV * sg == 2 * kWave && CV <= kWave))))
                 sg = 1;
             const int GS = CV * sg;
+            // small problems whose rows are wider than a wavefront but do not tile four wavefronts (16-bit C = 768:
+            // two rows of 96 lanes leave a quarter of them idle) take 12 wavefronts when whole rows fill them:
+            // C = 768, 12 heads, fp16 B1 Q450 60.0 -> 36.9 µs, bf16 B2 Q150 42.9 -> 26.3, fp32 B1 Q300 118 -> 62
+            // (large problems keep 8 wavefronts: fp16 B5 Q150 55.4 against 57.0; the layer kernel has 4 or 8)
+            if (tune.waves <= 0 && !big && !layer && GS > kWave && (waves * kWave) % GS != 0 &&
+                (12 * kWave) % GS == 0)
+                waves = 12;
+            const int nth = waves * kWave;
             const int rows_per_pass = nth / GS > 0 ? nth / GS : 1;
             int qt = tune.qt;
             if (qt <= 0) {

@@ -95,8 +95,11 @@ struct KBlock<float> {
     }
 };
 
-// The direct-to-LDS kernel for large 16-bit problems (td_gemm_dma.hip): dtype kF16 or kBF16, K % 64 == 0,
-// 16-byte aligned a and w; variant 14 (256 x 128 tiles) or 16 (256 x 256 tiles).
+// The direct-to-LDS kernels for large 16-bit problems (td_gemm_dma.hip): dtype kF16 or kBF16, K % 64 == 0,
+// 16-byte aligned a and w; variant 14 (256 x 128 tiles, one per workgroup) or 18 (persistent 256 x 256 tiles, one
+// workgroup per CU, for shapes gemm_persistent_fits accepts: M, NO >= 256, NO % 16 == 0 and NO <= 8192, 16-byte
+// aligned c and bias, a head-major D a multiple of 16, M * K, NO * K and M * NO below 2^31).
+bool gemm_persistent_fits(int dtype, const GemmParams& p);
 int launch_gemm_dma(int dtype, GemmParams p, hipStream_t stream, int variant);
 
 // The streaming kernel for narrow K (td_gemm_stream.hip): 16-bit, NO = 256, K = 128 or 256, 16-byte aligned a, w, c

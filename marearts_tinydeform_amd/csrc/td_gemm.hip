@@ -383,7 +383,8 @@ int go_mfma(GemmParams p, hipStream_t stream) {
 //   9  128 x 128 A and W through LDS (2 x 2 waves of 64 x 64), K chunks of 128/64
 //   13 128 x 128 A and W through LDS, K chunks of 32/16
 //   14 256 x 128 tiles fed by direct-to-LDS loads (td_gemm_dma.hip; 16-bit, K % 64 == 0)
-//   16 256 x 256 tiles fed by direct-to-LDS loads (td_gemm_dma.hip; 16-bit, K % 64 == 0)
+//   18 persistent 256 x 256 tiles fed by direct-to-LDS loads, one workgroup per CU (td_gemm_dma.hip; 16-bit,
+//      K % 64 == 0, gemm_persistent_fits)
 //   22 the streaming kernel: a quarter of W in each wavefront's registers, token rows streamed through LDS
 //      (td_gemm_stream.hip; 16-bit, NO = 256, K = 128 or 256)
 //   23 64 x 32   4 waves of 16 x 32, one chunk of 256/128, one stage
@@ -397,10 +398,12 @@ int go_mfma(GemmParams p, hipStream_t stream) {
 //     12000 rows, 7.8 against 7.4 for 25, and at 8400, 7.5 against 7.1), from 8000 rows at K = 128 (M = 8400 5.4
 //     against 5.6 for 25, M = 16384 6.1 against 7.0);
 //   deep K (K >= 512, K % 64 == 0) on a grid of at least 200 tiles of 256 x 128, or more than one round (256) of
-//     128 x 128 tiles, or from 8000 rows: the direct-to-LDS kernel, 256 x 256 tiles (16) from 2.5 rounds of them on
-//     256 CUs, else 256 x 128 (14) (C = 1024: M = 43520 101 µs against 122 µs for 13; M = 21760 57 against 68;
-//     M = 7200 23.6 against 29.2 for 13; M = 6000 23.2 against 35.3 for 9; K = NO = 512: M = 8400 15.0 against 22.2
-//     for 9; K = 512, NO = 256: M = 8400 14.4 against 22.1; K = NO = 768: M = 8400 19.3 against 28.8);
+//     128 x 128 tiles, or from 8000 rows: the direct-to-LDS kernels, persistent 256 x 256 tiles (18) from 120 of
+//     them, else 256 x 128 (14) (C = 1024: M = 43520 87-89 µs for 18 against 97-100 for the same tiles one per
+//     workgroup and 122 for 13; M = 8400 28.5 against 32.7 for 14; K = NO = 512: M = 50400 35.8 against 42.9, M = 16800 18.9 against
+//     21.7; below 120 tiles 14 wins, M = 8400 14.2 against 16.6; M = 21760, K = NO = 1024 54-55 for both;
+//     M = 7200 23.6 for 14 against 29.2 for 13; M = 6000 23.2 against 35.3 for 9; K = 512, NO = 256: M = 8400 14.4
+//     against 22.1; K = NO = 768: M = 8400 19.3 against 28.8);
 //   smaller grids by their count of 64 x 64 tiles:
 //     K <= 256: up to 300 tiles 32 x 32 (24) (NO = 256: M = 300 3.3 against 4.5 for 64 x 64 one-chunk tiles, M = 2400
 //       4.5 against 4.7), up to 1100 64 x 64 with two-stage K chunks of 128 (25) (M = 8400 7.2 against 7.8,
@@ -431,7 +434,7 @@ int pick_variant(int dtype, const GemmParams& p) {
     const int64_t tiles_256x128 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 127) / 128);
     const int64_t tiles_256 = ((p.M + 255) / 256) * static_cast<int64_t>((p.NO + 255) / 256);
     if (p.K >= 512 && p.K % 64 == 0 && (tiles_256x128 >= 200 || tiles_128 > 256 || p.M >= 8000))
-        return tiles_256 >= 640 ? 16 : 14;
+        return tiles_256 >= 120 && gemm_persistent_fits(dtype, p) ? 18 : 14;
     if (p.K <= 256) return tiles_64 <= 300 ? 24 : tiles_64 <= 1100 ? 25 : 13;
     return tiles_64 < 64 ? 24 : tiles_64 < 128 ? 23 : tiles_64 < 512 ? 25 : tiles_128 < 512 ? 9 : 13;
 }
@@ -454,7 +457,7 @@ int launch_t(GemmParams p, hipStream_t stream, int variant) {
             case 13:
                 if constexpr (sizeof(T) == 2) return go_lds<T, 2, 2, 4, 4, 1>(p, stream);
                 break;
-            case 14: case 16: return launch_gemm_dma(dt, p, stream, variant);
+            case 14: case 18: return launch_gemm_dma(dt, p, stream, variant);
             case 22: return launch_gemm_stream(dt, p, stream);
             default: break;
         }

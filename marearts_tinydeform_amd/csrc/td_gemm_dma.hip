@@ -15,6 +15,18 @@ __device__ __forceinline__ void load_lds16(const void* src, void* dst) {
     __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
 }
 
+// The 8-element vector of a 16-bit type.
+template <typename T>
+struct Vec8;
+template <>
+struct Vec8<f16> {
+    using type = f16x8;
+};
+template <>
+struct Vec8<bf16> {
+    using type = bf16x8;
+};
+
 // Slot swizzle g of a staged row, from the row's index within its 16-row group.
 __device__ __forceinline__ int swz(int r) { return ((r >> 1 ^ r >> 3) & 1) | (r & 4) >> 1; }
 
@@ -214,21 +226,223 @@ int go_dma(GemmParams p, hipStream_t stream) {
     return e == hipSuccess ? 0 : set_error(-3, "value_proj launch failed: %s", hipGetErrorString(e));
 }
 
-// variants (td_gemm.hip lists them with the others): 14 = 256 x 128 tiles of 4 wavefronts, 16 = 256 x 256 tiles of
-// 8 wavefronts; three LDS stages
+// Persistent form for many 256 x 256 tiles: the grid holds one workgroup per CU, and each workgroup walks its own
+// tiles with one K-chunk pipeline across them, so the next tile's first chunks load while the current tile's last
+// MFMAs run and its results are stored. 8 wavefronts as 2 (tokens) x 4 (channels), each owning 128 x 64 of the tile.
+//
+// The product is computed transposed (channels as the MFMA's rows, tokens as its columns): W stage position
+// 64 wn + 16 t + r holds channel 64 wn + 16 (r >> 2) + 4 t + (r & 3) of the tile, so MFMA block t's output row
+// 4 kg + e is channel 64 wn + 16 kg + 4 t + e and lane group kg ends with 16 consecutive channels of each of its
+// tokens, which it stores from its accumulators as two 16-byte vectors: the epilogue needs no LDS, and the ring keeps
+// streaming. Tiles are dealt per XCD (consecutive tiles share its L2); the G workgroups of an XCD take them
+// round-robin with G a multiple of the channel-tile count, so each workgroup keeps one channel tile (and its bias) to
+// the end. A last tile that would pass M (or NO) is moved back to end there: the rows it shares with its neighbour
+// are computed twice, identically, and every load address is a per-lane constant plus a tile base in scalar
+// registers. A tile's stores count in vmcnt too; the step after them still waits for exactly enough: loads complete in
+// the order they were sent, so while any load of the awaited chunk is pending, every load sent after it is as well
+// and the count stays above the wait's threshold, whether or not the stores have completed.
+template <typename T, int STAGES>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void gemm_dma_persistent_kernel(GemmParams p) {
+    constexpr int KC = 32, ROW_BYTES = 64, BM = 256, BN = 256, WAVES = 8;
+    constexpr int TM = 8, TN = 4;  // 16-token blocks, 16-channel blocks per wavefront
+    constexpr int A_BYTES = BM * ROW_BYTES, STAGE_BYTES = (BM + BN) * ROW_BYTES;
+    constexpr int A_LOADS = BM / 16 / WAVES, B_LOADS = BN / 16 / WAVES, LOADS = A_LOADS + B_LOADS;
+    static_assert(LOADS * (STAGES - 1) <= 63 && STAGES >= 3 && A_LOADS == 2 && B_LOADS == 2, "tiling");
+    extern __shared__ __align__(16) unsigned char lds[];
+
+    const int M = p.M, K = p.K, NO = p.NO, nt = p.nt, ntiles = p.mt * p.nt;
+    const int xcd = blockIdx.x % kXcds, G = gridDim.x / kXcds;
+    const int first = xcd * p.per_xcd + static_cast<int>(blockIdx.x / kXcds);
+    const int end = min((xcd + 1) * p.per_xcd, ntiles);
+    if (first >= end) return;
+    const int my_tiles = (end - first + G - 1) / G;
+    const int n0 = min((first % nt) * BN, NO - BN), nc = K / KC;
+    auto m0_of = [&](int k) { return min(((first + k * G) / nt) * BM, M - BM); };
+    const T* __restrict__ A = static_cast<const T*>(p.a);
+    const T* __restrict__ W = static_cast<const T*>(p.w);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / 4, wn = wave % 4, r16 = lane & 15, kg = lane >> 4;
+
+    // bias of this lane's 16 channels, loaded first (the first wait below covers it)
+    const int nb = n0 + wn * 64 + kg * 16;
+    u32x4 bias_raw[2] = {u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}};
+    const T* __restrict__ bias = static_cast<const T*>(p.bias);
+    if (bias != nullptr) {
+        bias_raw[0] = *reinterpret_cast<const u32x4*>(bias + nb);
+        bias_raw[1] = *reinterpret_cast<const u32x4*>(bias + nb + 8);
+    }
+
+    // Load sources (element offsets; the host keeps M * K and NO * K below 2^31): wavefront w's load i of an operand
+    // fills stage rows (2 w + i) * 16 .. + 16, lane = 4 * (row % 16) + slot, slot s holding K piece s ^ g(row % 16).
+    // Load i = 1 is load 0 sixteen token rows on, or four channels on (the next 16-position block of the stage).
+    const int piece = ((lane & 3) ^ swz(lane >> 2)) * 8;
+    const uint32_t a_lane = static_cast<uint32_t>((wave * 32 + (lane >> 2)) * K + piece);
+    const int pos = wave * 32 + (lane >> 2), r = pos & 15;
+    const uint32_t b_lane =
+        static_cast<uint32_t>((n0 + (pos & ~63) + (r >> 2) * 16 + ((pos >> 4) & 3) * 4 + (r & 3)) * K + piece);
+    const int a_step = 16 * K, b_step = 4 * K;
+    // The load stream runs STAGES chunks ahead of the MFMAs through the workgroup's tiles; past the last chunk it
+    // re-loads that chunk (an L2 hit) into a stage that is never read for the product, so every step sends one group.
+    int is_k = 0, is_c = 0, stage_in = 0;
+    const T* a_tile = A + static_cast<size_t>(m0_of(0)) * K;
+    auto issue = [&]() {
+        unsigned char* st = lds + stage_in * STAGE_BYTES;
+        const T* ab = a_tile + is_c * KC;
+        const T* wb = W + is_c * KC;
+        load_lds16(ab + a_lane, st + wave * 2048);
+        load_lds16(ab + a_step + a_lane, st + wave * 2048 + 1024);
+        load_lds16(wb + b_lane, st + A_BYTES + wave * 2048);
+        load_lds16(wb + b_step + b_lane, st + A_BYTES + wave * 2048 + 1024);
+        stage_in = stage_in + 1 == STAGES ? 0 : stage_in + 1;
+        if (++is_c == nc) {
+            if (is_k + 1 < my_tiles) {
+                is_c = 0;
+                a_tile = A + static_cast<size_t>(m0_of(++is_k)) * K;
+            } else {
+                is_c = nc - 1;
+            }
+        }
+    };
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int t = 0; t < TN; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int frag = r16 * ROW_BYTES + ((kg ^ swz(r16)) << 4);
+    const int a_off = wm * 128 * ROW_BYTES + frag;
+    const int b_off = A_BYTES + wn * 64 * ROW_BYTES + frag;
+    int stage_out = 0;  // stage of the chunk whose fragments are read next
+    auto read_frags = [&](u32x4 (&xa)[TM], u32x4 (&xb)[TN]) {
+        const unsigned char* st = lds + stage_out * STAGE_BYTES;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) xa[i] = *reinterpret_cast<const u32x4*>(st + a_off + i * 16 * ROW_BYTES);
+#pragma unroll
+        for (int t = 0; t < TN; ++t) xb[t] = *reinterpret_cast<const u32x4*>(st + b_off + t * 16 * ROW_BYTES);
+        stage_out = stage_out + 1 == STAGES ? 0 : stage_out + 1;
+    };
+
+    // epilogue of tile k: bias, one rounding, two 16-byte stores per token (output offsets in 32 bits: the host keeps
+    // M * NO below 2^31; channels nb + 8 follow nb in the output, NO and a head-major D being multiples of 16)
+    T* __restrict__ Cm = static_cast<T*>(p.c);
+    const uint32_t col = static_cast<uint32_t>(out_col(p, nb));
+    auto epilogue = [&](int k) {
+        using V8 = typename Vec8<T>::type;
+        const V8 b0 = __builtin_bit_cast(V8, bias_raw[0]), b1 = __builtin_bit_cast(V8, bias_raw[1]);
+        const int m0 = m0_of(k) + wm * 128 + r16;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const uint32_t o = static_cast<uint32_t>(out_row(p, m0 + i * 16)) + col;
+            V8 v0, v1;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v0[e] = static_cast<T>(acc[i][0][e] + static_cast<float>(b0[e]));
+                v0[4 + e] = static_cast<T>(acc[i][1][e] + static_cast<float>(b0[4 + e]));
+                v1[e] = static_cast<T>(acc[i][2][e] + static_cast<float>(b1[e]));
+                v1[4 + e] = static_cast<T>(acc[i][3][e] + static_cast<float>(b1[4 + e]));
+            }
+            *reinterpret_cast<u32x4*>(Cm + o) = __builtin_bit_cast(u32x4, v0);
+            *reinterpret_cast<u32x4*>(Cm + o + 8) = __builtin_bit_cast(u32x4, v1);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int t = 0; t < TN; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+
+    // Step: wait for the next chunk (the STAGES - 2 groups sent after it stay in flight) and for this wavefront's
+    // fragment reads, meet the others (after which nobody reads the current chunk's stage), refill that stage STAGES
+    // chunks ahead, read the next chunk's fragments, then run the current chunk's MFMAs on the fragments read one
+    // step earlier; after a tile's last chunk, its epilogue.
+    int c = 0, tk = 0;
+    auto step = [&](const u32x4 (&xa)[TM], const u32x4 (&xb)[TN], u32x4 (&ya)[TM], u32x4 (&yb)[TN]) {
+        meet<LOADS * (STAGES - 2)>();
+        issue();
+        read_frags(ya, yb);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int t = 0; t < TN; ++t) acc[i][t] = KBlock<T>::mma(xb[t], xa[i], acc[i][t]);
+#pragma unroll
+        for (int q = 0; q < TM + TN; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+        }
+#pragma unroll
+        for (int q = 0; q < LOADS; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // vector memory read (the LDS load)
+        }
+        sched_fence();
+        if (++c == nc) {
+            epilogue(tk++);
+            c = 0;
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s) issue();
+    meet<LOADS * (STAGES - 1)>();
+    u32x4 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+    read_frags(fa0, fb0);
+    const int steps = my_tiles * nc;  // even: nc is
+    for (int g = 0; g < steps; g += 2) {
+        step(fa0, fb0, fa1, fb1);
+        step(fa1, fb1, fa0, fb0);
+    }
+    // every wavefront's direct-to-LDS loads land before the workgroup's LDS is released
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+}
+
+template <typename T, int STAGES>
+int go_dma_persistent(GemmParams p, hipStream_t stream) {
+    constexpr size_t lds = static_cast<size_t>(STAGES) * 512 * 64;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(gemm_dma_persistent_kernel<T, STAGES>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (attr != hipSuccess) return set_error(-3, "value_proj: LDS size attribute refused: %s", hipGetErrorString(attr));
+    p.mt = (p.M + 255) / 256;
+    p.nt = (p.NO + 255) / 256;
+    const int64_t tiles = static_cast<int64_t>(p.mt) * p.nt;
+    p.per_xcd = static_cast<int>((tiles + kXcds - 1) / kXcds);
+    // workgroups per XCD: one per CU, a multiple of the channel-tile count, no more than the XCD has tiles for
+    int g = (cu_count() / kXcds) / p.nt * p.nt;
+    const int need = (p.per_xcd + p.nt - 1) / p.nt * p.nt;
+    g = g < need ? g : need;
+    if (g <= 0) return go_dma<T, 2, 3>(p, stream);  // more channel tiles than an XCD has CUs
+    hipLaunchKernelGGL((gemm_dma_persistent_kernel<T, STAGES>), dim3(g * kXcds), dim3(512), lds, stream, p);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : set_error(-3, "value_proj launch failed: %s", hipGetErrorString(e));
+}
+
+// variants (td_gemm.hip lists them with the others): 14 = 256 x 128 tiles of 4 wavefronts, one tile per workgroup;
+// 18 = the persistent 256 x 256 form; three LDS stages
 template <typename T>
 int launch_dma_t(GemmParams p, hipStream_t stream, int variant) {
     switch (variant) {
         case 14: return go_dma<T, 2, 3>(p, stream);
-        case 16: return go_dma<T, 4, 3>(p, stream);
+        case 18: return go_dma_persistent<T, 3>(p, stream);
         default: return set_error(-1, "value_proj: unknown tile variant %d", variant);
     }
 }
 
 }  // namespace
 
+bool gemm_persistent_fits(int dtype, const GemmParams& p) {
+    const uintptr_t al = reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.w) |
+                         reinterpret_cast<uintptr_t>(p.c) | reinterpret_cast<uintptr_t>(p.bias);
+    const int64_t lim = int64_t{1} << 31;
+    return (dtype == kF16 || dtype == kBF16) && p.K % 64 == 0 && p.K > 0 && p.M >= 256 && p.NO >= 256 &&
+           p.NO % 16 == 0 && p.NO <= 256 * 32 && al % 16 == 0 && p.hm_D % 16 == 0 &&
+           static_cast<int64_t>(p.M) * p.K < lim && static_cast<int64_t>(p.NO) * p.K < lim &&
+           static_cast<int64_t>(p.M) * p.NO < lim;
+}
+
 int launch_gemm_dma(int dtype, GemmParams p, hipStream_t stream, int variant) {
     if (p.K % 64 != 0 || p.K == 0) return set_error(-1, "value_proj: tile variant %d needs K %% 64 == 0", variant);
+    if (variant == 18 && !gemm_persistent_fits(dtype, p))
+        return set_error(-1, "value_proj: the persistent tiles do not take this shape");
     switch (dtype) {
         case kF16: return launch_dma_t<f16>(p, stream, variant);
         case kBF16: return launch_dma_t<bf16>(p, stream, variant);

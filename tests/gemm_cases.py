@@ -3,8 +3,9 @@
 kernel the rule can pick for any shape has at least one of these cases; the GPU tests run them against the oracle.
 
 Kernel numbers (csrc/td_gemm.hip): 0 generic VALU; 2, 5, 23, 24, 25 A-in-registers MFMA tiles; 9, 13 both operands
-through LDS; 14, 16 direct-to-LDS 256 x 128 / 256 x 256 tiles; 22 the streaming kernel (W resident in registers,
-tokens streamed through LDS).
+through LDS; 14 direct-to-LDS 256 x 128 tiles, one per workgroup; 18 persistent direct-to-LDS 256 x 256 tiles (one
+workgroup per CU walking its tiles; last tiles moved back to end at M and NO); 22 the streaming kernel (W resident in
+registers, tokens streamed through LDS).
 """
 
 import torch
@@ -29,9 +30,14 @@ DEEP_K = [
     (5000, 576, 136, 25),
     (300, 1024, 1024, 23),     # the decoder layer's output projection at C = 1024, 300 queries
     (3600, 1024, 1024, 9),     # both operands through LDS, K chunks of 128
-    (21760, 1024, 1024, 14),   # C = 1024 limit shape at batch 1: 256 x 128 direct-to-LDS tiles
-    (21760, 512, 512, 14),     # a C = 512 model at batch 1
-    (43557, 1024, 1000, 16),   # 256 x 256 direct-to-LDS tiles, M and NO off the tile sizes
+    (21760, 1024, 1024, 18),   # C = 1024 limit shape at batch 1: persistent 256 x 256 tiles, about 1.3 per workgroup
+    (21760, 512, 512, 18),     # a C = 512 model at batch 1
+    (43557, 1024, 1008, 18),   # M and NO off the tile sizes: the last token and channel tiles moved back, overlapping
+    (43557, 1024, 1000, 14),   # NO not a multiple of 16: the 256 x 128 tiles
+    (30001, 768, 768, 18),     # three channel tiles: 30 workgroups per XCD, each keeping its channel tile
+    (60000, 512, 320, 18),     # two channel tiles overlapping by 192 channels, two tiles per workgroup
+    (131072, 512, 512, 18),    # four tiles per workgroup
+    (12000, 1024, 1024, 18),   # 188 tiles: fewer workgroups than CUs, one tile each
     (9000, 520, 256, 9),       # K >= 512 but not a multiple of 64
     (8400, 512, 256, 14),      # direct-to-LDS from 8000 rows even on a small grid (66 tiles of 256 x 128)
     (6000, 1024, 1024, 14),    # more than one round of 128 x 128 tiles
@@ -55,6 +61,7 @@ STREAM = [
 BIAS_OFFSET = [
     (16800, 256, 256, 25),
     (67200, 256, 256, 13),
+    (21760, 1024, 1024, 14),   # the persistent tiles read the bias with 16-byte loads too
 ]
 
 # (M, K, NO, offsets, kernel) in float32, float16 and bfloat16: memory 4 bytes off a 16-byte boundary, or K not a
@@ -68,7 +75,8 @@ UNALIGNED = [
 HEADS = {
     F16: [((1, 8400, 256, 8, 32), 25), ((4, 9000, 256, 8, 32), 22), ((2, 8192, 128, 32, 32), 13),
           ((3, 77, 40, 6, 8), 24), ((2, 2501, 576, 17, 8), 25), ((2, 30001, 256, 8, 32), 22),
-          ((3, 20011, 128, 16, 16), 22), ((4, 8400, 256, 8, 32), 22), ((1, 21760, 1024, 32, 32), 14)],
+          ((3, 20011, 128, 16, 16), 22), ((4, 8400, 256, 8, 32), 22), ((1, 21760, 1024, 32, 32), 18),
+          ((2, 21760, 512, 32, 16), 18), ((1, 21760, 1024, 128, 8), 14)],
     BF16: [((1, 8400, 256, 8, 32), 25), ((2, 30001, 256, 8, 32), 22), ((5, 131, 96, 3, 24), 24),
            ((8, 8400, 256, 8, 32), 22), ((1, 3600, 1024, 32, 32), 9)],
     F32: [((1, 8400, 256, 8, 16), 25), ((2, 77, 40, 5, 4), 24), ((3, 1000, 64, 2, 12), 23)],

@@ -75,12 +75,12 @@ def test_cost_tables_are_sane():
 
 
 def test_cost_features_split_the_gemm_by_depth():
-    # narrow K: the GEMM's flops; deep K (C >= 512): whole rounds of 256 x 128 tiles over 256 CUs, times K
+    # narrow K: the GEMM's flops; deep K (C >= 512): whole rounds of 256 x 256 tiles over 256 CUs, times K
     ff, fp = td.cost_features(1, 300, 8, 32, 256, 8400, 3, 4, 2)
     assert fp[2] == pytest.approx(2 * 8400 * 256 * 256 / 1e9) and fp[3] == 0.0
     assert ff[1] == pytest.approx(300 * 8 * 12 * 4 * 256 * 2 / 1e6)
     _, fp = td.cost_features(2, 300, 16, 64, 1024, 21760, 4, 16, 2)
-    tiles = (43520 // 256) * (1024 // 128)  # 170 x 8 = 1360 tiles: 6 rounds on 256 CUs
+    tiles = (43520 // 256) * (1024 // 256)  # 170 x 4 = 680 tiles: 3 rounds on 256 CUs
     assert fp[2] == 0.0 and fp[3] == pytest.approx(-(-tiles // 256) * 1024 / 1e3)
 
 

@@ -47,7 +47,7 @@ def test_every_reachable_kernel_has_a_parity_case():
         missing = reach[dt] - cov.get(dt, set())
         assert not missing, f'{dt}: kernels {sorted(missing)} are reachable but no GPU parity case runs them'
     # the sweep reaches every kernel of the rule (a guard against the sweep itself going stale)
-    assert reach[F16] == reach[BF16] == {0, 9, 13, 14, 16, 22, 23, 24, 25}
+    assert reach[F16] == reach[BF16] == {0, 9, 13, 14, 18, 22, 23, 24, 25}
     assert reach[F32] == {0, 2, 5, 23, 24, 25}
     assert reach[F64] == {0}
 
@@ -62,6 +62,18 @@ def test_streaming_kernel_needs_an_aligned_bias():
     # so must memory, weight and value
     for k in ('memory', 'weight', 'value'):
         assert _native.value_proj_plan(BF16, 67200, 256, 256, offsets={k: 8}) != 22
+
+
+def test_persistent_tiles_need_their_alignments():
+    # the persistent 256 x 256 tiles store 16 channels per lane as two 16-byte vectors and read the bias the same way
+    assert _native.value_proj_plan(F16, 43520, 1024, 1024) == 18
+    assert _native.value_proj_plan(F16, 43520, 1024, 1024, bias=False) == 18
+    for k in ('bias', 'value'):
+        assert _native.value_proj_plan(BF16, 43520, 1024, 1024, offsets={k: 8}) == 14
+    assert _native.value_proj_plan(F16, 43520, 1024, 1000) == 14          # NO % 16 != 0
+    assert _native.value_proj_plan(F16, 43520, 1024, 1024, heads=128, N=43520) == 14  # D = 8
+    assert _native.value_proj_plan(F16, 43520, 1024, 1024, heads=64, N=43520) == 18   # D = 16
+    assert _native.value_proj_plan(F16, 8400, 512, 512) == 14             # 66 tiles of 256 x 256
 
 
 def test_plan_rejects_bad_sizes():

@@ -255,8 +255,9 @@ def test_value_proj_matches_oracle(dtype):
 @pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
 def test_value_proj_deep_k_matches_oracle(dtype):
     # 16-bit, K >= 512: register tiles for the small grids, both operands through LDS (9) in the middle, the
-    # direct-to-LDS kernel, 256 x 128 tiles (14) and 256 x 256 tiles (16) for >= 640 of them, with M and the output
-    # width off the tile sizes. Rows are checked on a sample that includes the first and the last, partial, M tile.
+    # direct-to-LDS kernels, 256 x 128 tiles (14) and persistent 256 x 256 tiles (18) from 120 of them (one to four
+    # tiles per workgroup, the last token and channel tiles moved back to overlap their neighbours), with M and the
+    # output width off the tile sizes. Rows are checked on a sample that includes the first and the last M tile.
     for M, K, NO, kern in gemm_cases.DEEP_K:
         gemm_case(dtype, M, K, NO, True, None, kern, 11, rows=sample_rows(M, 11))
 
@@ -417,6 +418,16 @@ def test_rtdetr640_slice_shapes(dtype, B, Q):
                     rows=rows)
 
 
+@pytest.mark.parametrize('dtype,B,Q', [(torch.float16, 1, 450), (torch.bfloat16, 2, 150), (torch.float32, 1, 300),
+                                        (torch.float16, 5, 150)])
+def test_wide_rows_c768(dtype, B, Q):
+    # C = 768 (12 heads of 64): rows wider than a wavefront (96 lanes in 16 bits, 192 in float32) that do not tile
+    # four wavefronts, gathered by 12-wavefront workgroups for small problems and 8-wavefront ones from 8192 rows;
+    # sampled rows against the oracle, fused and project over the whole output
+    rows = np.sort(np.random.default_rng(B * Q + 1).choice(B * Q * 12, size=min(B * Q * 12, 1536), replace=False))
+    full_size_check(f'c768 {dtype} B{B} Q{Q}', workload(B, Q, 12, 64, 768, RTDETR_LEVELS, 4, dtype), dtype, rows=rows)
+
+
 def test_rtdetr640_fp32_b1_q300():
     full_size_check('rtdetr640 fp32 B1 Q300', workload(1, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.float32),
                     torch.float32)
@@ -449,10 +460,10 @@ def test_limit_case_bf16_c1024(Q):
 
 
 def test_limit_case_bf16_c1024_b1_project():
-    # the C = 1024 limit shape at batch 1 (21760 tokens: the 256 x 128 direct-to-LDS value GEMM), project mode end to
-    # end, 1024 sampled rows against the oracle
+    # the C = 1024 limit shape at batch 1 (21760 tokens: the persistent 256 x 256 direct-to-LDS value GEMM, 340 tiles
+    # on 256 workgroups), project mode end to end, 1024 sampled rows against the oracle
     args = workload(1, 300, 16, 64, 1024, LIMIT_LEVELS, 16, torch.bfloat16, bias=False)
-    assert _native.value_proj_plan(torch.bfloat16, 21760, 1024, 1024, bias=False) == 14
+    assert _native.value_proj_plan(torch.bfloat16, 21760, 1024, 1024, bias=False, heads=16, N=21760) == 18
     rows = np.random.default_rng(1).choice(300 * 16, size=1024, replace=False)
     full_size_check('limit bf16 C1024 B1 Q300', args, torch.bfloat16, rows=np.sort(rows), modes=('project',))
 
