@@ -185,7 +185,8 @@ def gemm_kernel(M, K, NO, s):
     """Which value-projection kernel td_value_proj launches for an aligned [M, K] x [K, NO] problem (element size
     s), following its size rule: 16-bit with 256 outputs, K = 256 and at least 14000 rows (K = 128: 8000) takes the streaming
     kernel; 16-bit deep K (K >= 512, K % 64 == 0) on a grid of >= 200 tiles of 256 x 128, more than 256 of 128 x 128 or
-    from 8000 rows the direct-to-LDS kernel;
+    from 8000 rows the direct-to-LDS kernels (persistent 256 x 256 tiles from 120 of them when NO % 16 == 0 and the
+    sizes stay below 2^31 elements, else 256 x 128 tiles);
     other 16-bit grids take register-operand tiles (32 x 32 to 64 x 64) up to 1100 tiles of 64 x 64 for K <= 256 and
     under 512 for deeper K, larger ones both operands through LDS;
     float32 takes register-operand tiles of 32 x 32 to 64 x 128."""
@@ -194,6 +195,10 @@ def gemm_kernel(M, K, NO, s):
         if NO == 256 and K in (128, 256) and M >= (14000 if K == 256 else 8000):
             return 'gemm_stream_kernel'
         if K >= 512 and K % 64 == 0 and (-(-M // 256) * -(-NO // 128) >= 200 or tiles_128 > 256 or M >= 8000):
+            lim = 1 << 31
+            if (-(-M // 256) * -(-NO // 256) >= 120 and NO % 16 == 0 and M >= 256 and 256 <= NO <= 8192 and
+                    max(M * K, NO * K, M * NO) < lim):
+                return 'gemm_dma_persistent_kernel'
             return 'gemm_dma_kernel'
         tiles_64 = -(-M // 64) * -(-NO // 64)
         if K <= 256:

@@ -81,3 +81,18 @@ def test_plan_rejects_bad_sizes():
         _native.value_proj_plan(F16, -1, 256, 256)
     with pytest.raises(RuntimeError):
         _native.value_proj_plan(F16, 100, 256, 256, heads=3, N=100)
+
+
+def test_bench_names_the_kernel_the_rule_picks():
+    # bench.py attributes measured time and traffic to the value GEMM's kernel by name (gemm_kernel); it must name
+    # the family td_value_proj_plan picks, for aligned row-major problems with a bias
+    import bench
+    family = {0: 'gemm_generic_kernel', 2: 'gemm_mfma_kernel', 5: 'gemm_mfma_kernel', 23: 'gemm_mfma_kernel',
+              24: 'gemm_mfma_kernel', 25: 'gemm_mfma_kernel', 9: 'gemm_lds_kernel', 13: 'gemm_lds_kernel',
+              14: 'gemm_dma_kernel', 18: 'gemm_dma_persistent_kernel', 22: 'gemm_stream_kernel'}
+    Ms = (300, 2400, 7999, 8000, 8400, 14000, 21760, 30001, 43520, 67200, 177784)
+    for dt, s in ((F16, 2), (BF16, 2)):
+        for M, K, NO in itertools.product(Ms, (128, 256, 512, 768, 1024), (256, 320, 512, 768, 1000, 1024)):
+            got = bench.gemm_kernel(M, K, NO, s)
+            want = family[_native.value_proj_plan(dt, M, K, NO)]
+            assert got == want, f'M={M} K={K} NO={NO}: bench names {got}, the rule picks {want}'
