@@ -187,9 +187,11 @@ int td_layer_prologue(int dtype, const void* query, const void* position, const 
  * Fused layer: the query prologue inside the fused-mode kernel (td_fused_forward_masked with the locations and
  * weights computed in-kernel). out [B, Q, H*D] as td_fused_forward; padding_mask as td_fused_forward_masked.
  * loc_out / attn_out (float32, float64 for TD_F64; NULL for none) receive the locations and weights when given.
- * Problems the in-kernel prologue cannot take (TD_F64; C or Cq not a multiple of 16 bytes; rows not 16-byte
- * aligned) run the standalone prologue into loc_out / attn_out and then the fused kernel: for those both buffers
- * are required, and without them the call returns TD_E_WORKSPACE having launched nothing.
+ * Problems the in-kernel prologue does not take run the standalone prologue into loc_out / attn_out and then the
+ * fused kernel: for those both buffers are required, and without them the call returns TD_E_WORKSPACE having
+ * launched nothing. They are: TD_F64; C or Cq not a multiple of 16 bytes; rows not 16-byte aligned; query
+ * projections of B * Q * H * 3 * L * P * Cq >= 8e8 multiply-adds (they run on the GEMM); and projection weights of
+ * more than 256 KB per head (3 * L * P * Cq elements), or more than 64 KB per head with B * Q >= 200.
  */
 int td_layer_fused_forward(int dtype, const void* query, const void* position, const void* reference_points,
                            int64_t ref_levels, int64_t ref_dim, const void* offsets_weight, const void* offsets_bias,

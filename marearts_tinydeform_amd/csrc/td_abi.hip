@@ -235,6 +235,19 @@ extern "C" int td_layer_prologue(int dtype, const void* query, const void* posit
     return launch_prologue(dtype, la, g, static_cast<hipStream_t>(stream));
 }
 
+// Whether the fused layer kernel computes the query prologue itself. It streams a head's projection weights
+// (3 L P Cq elements) once per 16 queries, so large weights per head, and projections big enough for the GEMM
+// route, go to the standalone prologue and then the fused kernel. Measured on MI355X (layer, fused mode, µs):
+// C = 1024, 16 heads x 4 levels x 16 points (393 KB per head), 100 query rows 120.7 -> 99.0; C = 512, 16 x 4 x 16
+// (196 KB), 300 rows 114.0 -> 98.9 but 100 rows 57.6 against 61.7; C = 1024, 16 x 3 x 4 (74 KB), 300 rows
+// 97.2 -> 83.9; up to 37 KB per head (RT-DETR, DINO, C = 512 with 12 samples) either way alike.
+static bool layer_prologue_in_kernel(int dtype, const Geom& g, int64_t Cq) {
+    if (prologue_wants_gemm(dtype, g, Cq)) return false;
+    const double per_head = 3.0 * g.LP * static_cast<double>(Cq) * elem_size(dtype);
+    const int64_t rows = static_cast<int64_t>(g.B) * g.Q;
+    return !(per_head > 256 * 1024 || (per_head > 64 * 1024 && rows >= 200));
+}
+
 extern "C" int td_layer_fused_forward(int dtype, const void* query, const void* position,
                                       const void* reference_points, int64_t ref_levels, int64_t ref_dim,
                                       const void* offsets_weight, const void* offsets_bias, const void* attn_weight,
@@ -271,14 +284,16 @@ extern "C" int td_layer_fused_forward(int dtype, const void* query, const void* 
         return launch_zero(out, B * Q * H * D * elem_size(dtype), s);
     }
     FusedTune tune;
-    rc = launch_fused(dtype, memory, value_weight, value_bias, g, static_cast<int>(C), nullptr, nullptr, out, s, tune,
-                      &la);
-    if (rc != 1) return rc;
-    // the in-kernel prologue cannot take this problem: standalone prologue, then the fused kernel on its output
+    if (layer_prologue_in_kernel(dtype, g, Cq)) {
+        rc = launch_fused(dtype, memory, value_weight, value_bias, g, static_cast<int>(C), nullptr, nullptr, out, s,
+                          tune, &la);
+        if (rc != 1) return rc;
+    }
+    // the in-kernel prologue does not take this problem: standalone prologue, then the fused kernel on its output
     if (loc_out == nullptr || attn_out == nullptr)
         return set_error(TD_E_WORKSPACE,
-                         "layer: float64, or rows that are not 16-byte multiples or not 16-byte aligned, need "
-                         "loc_out and attn_out");
+                         "layer: float64, rows that are not 16-byte multiples or not 16-byte aligned, or large query "
+                         "projections need loc_out and attn_out");
     rc = launch_prologue(dtype, la, g, s);
     if (rc != TD_OK) return rc;
     g.loc_acc = 1;

@@ -46,6 +46,11 @@ int launch_fused(int dtype, const void* mem, const void* w, const void* bias, co
 // in-place finalize; falls back to the single kernel for float64 or unaligned operands).
 int launch_prologue(int dtype, const LayerArgs& layer, const Geom& g, hipStream_t stream, int route = 0);
 
+// Whether the query projections are large enough for the GEMM route (8e8 multiply-adds; not float64). The fused
+// layer kernel streams a head's projection weights once per 16 queries, so such problems run the standalone
+// prologue and then the fused kernel instead.
+bool prologue_wants_gemm(int dtype, const Geom& g, int64_t Cq);
+
 int launch_sample(int dtype, const void* value, const Geom& g, const void* loc, const void* attn, void* out,
                   hipStream_t stream, const SampleTune& tune);
 

@@ -155,14 +155,18 @@ int launch_prologue_t(PrologueParams p, hipStream_t stream) {
 
 }  // namespace
 
+bool prologue_wants_gemm(int dtype, const Geom& g, int64_t Cq) {
+    const double macs = static_cast<double>(g.B) * g.Q * g.H * 3 * g.LP * Cq;
+    return dtype != kF64 && macs >= 8e8;
+}
+
 int launch_prologue(int dtype, const LayerArgs& layer, const Geom& g, hipStream_t stream, int route) {
     if (layer.loc_out == nullptr || layer.attn_out == nullptr)
         return set_error(-1, "layer prologue: locations and weights need output buffers");
     // route 0: by the projections' multiply-adds. Measured on MI355X: the single kernel up to DINO-sized problems
     // (3600 queries, Cq 256, 8 heads x 16 samples, 3.5e8: 14-17 µs against 25 µs for the GEMM route), the GEMM route
     // for the C = 1024 shape (600 queries, 16 heads x 64 samples, 1.9e9: 45 µs against 72 µs).
-    const double macs = static_cast<double>(g.B) * g.Q * g.H * 3 * g.LP * layer.Cq;
-    if (dtype != kF64 && (route == 2 || (route == 0 && macs >= 8e8))) {
+    if (dtype != kF64 && (route == 2 || (route == 0 && prologue_wants_gemm(dtype, g, layer.Cq)))) {
         int rc = 1;
         switch (dtype) {
             case kF32: rc = launch_prologue_gemm<float>(layer, g, stream); break;

@@ -104,6 +104,49 @@ def test_large_prologue_takes_the_gemm_route(dtype):
         assert np.abs(attn.double().cpu().numpy() - ref_attn).max() <= lt, f'{name}: attention weights'
         out, got_attn = run_layer(dev, 'project')
         check(f'{name} {dtype} [project]', out, ref, dtype)
+        # fused mode takes the same prologue, then the fused kernel on its float32 locations
+        say(f'  gemm route {name} {dtype} [fused]')
+        out, got_attn = run_layer(dev, 'fused')
+        check(f'{name} {dtype} [fused]', out, ref, dtype)
+        np.testing.assert_allclose(got_attn.double().cpu().numpy(), ref_attn, rtol=0, atol=max(lt, 2e-2))
+        # through the C ABI, without location buffers the fused entry asks for them, launching nothing
+        hidden, memory, rp, shapes, starts, ow, ob, aw, ab, vw, vb = dev[:11]
+        N, Cq = memory.shape[1], hidden.shape[2]
+        out = torch.empty(B, Q, H * D, dtype=dtype, device='cuda')
+        args = [_native.DTYPE_CODES[dtype], hidden.data_ptr(), dev[15].data_ptr(), rp.data_ptr(), rp.shape[2],
+                rp.shape[3], ow.data_ptr(), _native._ptr(ob), aw.data_ptr(), _native._ptr(ab), memory.data_ptr(),
+                vw.data_ptr(), _native._ptr(vb), shapes.data_ptr(), starts.data_ptr(), None, out.data_ptr()]
+        sizes = [B, Q, N, Cq, C, H, D, len(levels), P, None]
+        assert _native.lib.td_layer_fused_forward(*args, None, None, *sizes) == _native.TD_E_WORKSPACE
+
+
+@pytest.mark.parametrize('Q,in_kernel', [(200, False), (50, True)])
+def test_wide_projection_weights(Q, in_kernel):
+    # 8 heads x 4 levels x 16 points over C = 512: 196 KB of projection weights per head, under the GEMM route's
+    # 8e8 multiply-adds. From 200 query rows the fused layer runs the standalone prologue and then the fused kernel
+    # (and through the C ABI asks for location buffers); with 50 it keeps the prologue inside the fused kernel.
+    dtype = torch.bfloat16
+    B, H, D, C, levels, P = 1, 8, 64, 512, [(40, 40), (20, 20), (10, 10), (5, 5)], 16
+    a = make_layer(B, Q, H, D, C, levels, P, 4, '1', dtype=dtype)
+    ref, ref_attn = olayer.layer(*a[:15], position_embeddings=a[15])
+    dev = to(a[:13], 'cuda') + a[13:15] + to(a[15:], 'cuda')
+    say(f'  wide weights Q{Q} [fused]')
+    out, got_attn = run_layer(dev, 'fused')
+    check(f'wide weights Q{Q} [fused]', out, ref, dtype)
+    hidden, memory, rp, shapes, starts, ow, ob, aw, ab, vw, vb = dev[:11]
+    out = torch.empty(B, Q, H * D, dtype=dtype, device='cuda')
+    args = [_native.DTYPE_CODES[dtype], hidden.data_ptr(), dev[15].data_ptr(), rp.data_ptr(), rp.shape[2], rp.shape[3],
+            ow.data_ptr(), ob.data_ptr(), aw.data_ptr(), ab.data_ptr(), memory.data_ptr(), vw.data_ptr(),
+            vb.data_ptr(), shapes.data_ptr(), starts.data_ptr(), None, out.data_ptr(), None, None,
+            B, Q, memory.shape[1], hidden.shape[2], C, H, D, len(levels), P, None]
+    rc = _native.lib.td_layer_fused_forward(*args)
+    torch.cuda.synchronize()
+    if in_kernel:
+        assert rc == 0  # the core, before output_proj: apply it in float64 to compare with the layer
+        o_w, o_b = dev[11].double(), dev[12].double()
+        check(f'wide weights Q{Q} [C ABI]', out.double() @ o_w.T + o_b, ref, dtype)
+    else:
+        assert rc == _native.TD_E_WORKSPACE
 
 
 def test_float64_layer_takes_the_standalone_prologue():
