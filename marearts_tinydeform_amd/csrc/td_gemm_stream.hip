@@ -6,7 +6,12 @@
 // on staging W and crossing barriers; this kernel keeps W resident and streams the tokens:
 //   * one workgroup of four wavefronts per CU (persistent grid), each workgroup an equal share of M;
 //   * every wavefront holds a quarter of W (64 output channels x K, 128 VGPRs at K = 256) in registers for the whole
-//     kernel, requested at kernel start K block by K block, the order its first MFMAs use them;
+//     kernel. W reaches them through LDS: at kernel start the workgroup's direct global-to-LDS loads bring W in
+//     whole 1 KB runs (8 full 128-byte lines per load; a register load of a fragment would touch 16 half lines), into
+//     an LDS copy whose 16-byte chunk c of row ch sits at slot ch * (K / 8) + (c ^ key(ch)), key(ch) = the row's
+//     position in its 16 x 16 output tile (bits 3-4 and 0-1 of ch), so that each fragment read (16 rows, one chunk
+//     each) hits 16 distinct 16-byte bank groups; each wavefront then reads its quarter into registers. With W
+//     (128 KB at K = 256) and the two token stages the workgroup holds the CU's whole 160 KB of LDS;
 //   * the token rows stream through LDS in steps of 32 tokens: two stages, the next step's rows requested by direct
 //     global-to-LDS loads while this step's MFMAs run, and the four wavefronts share each staged row (each computing
 //     its 64 channels of it), so a token row is read from memory once per CU;
@@ -21,7 +26,11 @@
 // registers, graph-timed µs): RT-DETR B2 (16800 x 256) 10.3 -> 9.1, B8 bf16 (67200) 18.7 -> 17.6, DINO B4 (88892)
 // 22.5 -> 20.6, DINO encoder B2 (44446) 14.8 -> 14.0, 80000 x 128 14.1 -> 13.6, 177784 x 256 36.3 -> 34.1. Deeper
 // rings measured slower at every size (three stages: B8 18.6, four 19.0, six 20.5): more token rows in flight per CU
-// did not raise the memory rate, they delayed the first stage.
+// did not raise the memory rate, they delayed the first stage. Timestamps per workgroup then showed the start
+// dominating: W's register loads (16 half lines each) took 3.8 µs before the first step and held up the second;
+// staging W through LDS in whole lines, with the second stage requested at kernel start too: 16800 x 256
+// 9.0 -> 7.6, 33600 12.2 -> 10.3, 44446 14.0 -> 12.0, B8 bf16 17.8 -> 15.9, DINO B4 21.3 -> 18.8, 177784 33.7 ->
+// 32.8, 44446 x 128 9.9 -> 8.9. Stores that bypass or write through L2 (nontemporal, sc1) measured no faster.
 #include "td_gemm.h"
 
 namespace td {
@@ -71,12 +80,11 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
     constexpr int NST = SHN * (NTQ / 2);                // stores per wavefront per step
     static_assert(DL >= 1 && CHR >= 16 && CHR % 16 == 0, "stage layout");
     // Waits, in vector-memory operations that may stay in flight (they complete in issue order):
-    //  * step 0 waits for its stage only: W (NTQ * KB loads) and the bias (NTQ / 2) were requested after it, and the
-    //    compiler's own waits before the MFMAs cover W block by block;
-    //  * step 1's stage is requested after step 0's stores, so step 1 waits for everything;
-    //  * later steps: step i's stage was requested after step i - 2's stores, followed by step i - 1's stores.
-    constexpr int VM_FIRST = NTQ * KB + NTQ / 2, VM_STEADY = NST;
-    static_assert(VM_FIRST <= 63, "vmcnt range");
+    //  * before step 0 everything requested at kernel start has landed: stages 0 and 1, W and the bias;
+    //  * step i >= 1: its stage was requested before step i - 1's stores (at kernel start for step 1, after the
+    //    meeting of step i - 1 otherwise), so those stores may stay in flight.
+    constexpr int VM_STEADY = NST;
+    static_assert(VM_STEADY <= 63, "vmcnt range");
     extern __shared__ __align__(16) unsigned char smem[];
 
     const T* __restrict__ A = static_cast<const T*>(p.a);
@@ -109,19 +117,25 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
             load_lds16(A + static_cast<size_t>(m) * K + (c ^ (row & 15)) * 8, st + (wave * DL + j) * 1024);
         }
     };
-    // the first stage goes out ahead of W, so the first 32 tokens do not queue behind it
+    // the first two stages go out ahead of W, so the first 64 tokens do not queue behind it
     issue(0);
+    issue(1);
 
     // this wavefront's W quarter: tile t, K block kb; lane row r of tile t is channel
     // qc + 32 (t / 2) + 8 (r / 4) + 4 (t % 2) + r % 4
     u32x4 wf[NTQ][KB];
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int t = 0; t < NTQ; ++t) {
-            const int ch = qc + 32 * (t >> 1) + 8 * (r >> 2) + 4 * (t & 1) + (r & 3);
-            wf[t][kb] = *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(ch) * K + kg * 8 + kb * 32);
+    unsigned char* const wl = smem + 2 * STAGE;  // the LDS copy of W
+    auto wkey = [](int ch) { return (((ch >> 3) & 3) << 2) | (ch & 3); };
+    {
+        constexpr int WDL = kStreamNO * CHR / kWave / kStreamWaves;  // 1 KB direct loads per wavefront: CHR
+        const int rot = static_cast<int>(blockIdx.x / kXcds) % WDL;
+#pragma unroll 4
+        for (int jj = 0; jj < WDL; ++jj) {
+            const int j = wave * WDL + (jj + rot) % WDL;  // the CUs of an XCD start on different runs
+            const int sl = j * kWave + lane, ch = sl / CHR, c = (sl % CHR) ^ wkey(ch);
+            load_lds16(W + static_cast<size_t>(ch) * K + c * 8, wl + j * 1024);
         }
+    }
     // the bias is loaded unconditionally (W's first row stands in for a missing one) so that the count of loads in
     // flight is the same with and without it
     Out8<T> bv[NTQ / 2];
@@ -174,14 +188,17 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
     // left for the compiler to wait on (with step 0 inside, its merged count put a full wait after every step's
     // direct loads). A stage is refilled only after every wavefront has passed the barrier of the step that follows
     // its reads.
-    meet<VM_FIRST>();
+    meet<0>();  // stages 0 and 1, W and the bias have landed
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int t = 0; t < NTQ; ++t) {
+            const int ch = qc + 32 * (t >> 1) + 8 * (r >> 2) + 4 * (t & 1) + (r & 3);
+            wf[t][kb] = *reinterpret_cast<const u32x4*>(wl + (ch * CHR + ((kb * 4 + kg) ^ wkey(ch))) * 16);
+        }
     step(0);
-    issue(1);
     for (int i = 1; i < ns; ++i) {
-        if (i == 1)
-            meet<0>();
-        else
-            meet<VM_STEADY>();
+        meet<VM_STEADY>();
         issue(i + 1);
         step(i);
     }
@@ -192,7 +209,15 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
 
 template <typename T, int KB>
 int go_stream(GemmParams p, int64_t grid, hipStream_t stream) {
-    constexpr size_t lds = static_cast<size_t>(2) * kStreamStep * KB * 64;
+    // two token stages and W: 160 KB at K = 256, 80 KB at K = 128
+    constexpr size_t lds = static_cast<size_t>(2) * kStreamStep * KB * 64 + static_cast<size_t>(kStreamNO) * KB * 64;
+    if constexpr (lds > 65536) {
+        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_stream_kernel<T, KB>),
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                           static_cast<int>(lds));
+        if (attr != hipSuccess)
+            return set_error(-3, "value_proj: LDS size attribute refused: %s", hipGetErrorString(attr));
+    }
     hipLaunchKernelGGL((gemm_stream_kernel<T, KB>), dim3(static_cast<unsigned>(grid)), dim3(kStreamWaves * kWave), lds,
                        stream, p);
     const hipError_t e = hipGetLastError();
