@@ -20,7 +20,18 @@ struct SampleParams {
     int RB, SG;
     int64_t rows;
     int per_xcd, blocks;  // workgroup -> row-block mapping: XCD x takes a contiguous range of row blocks
+    int hq = 0;           // rows taken in (b, h, q) order instead of the (b, q, h) of the output
 };
+
+// Row (b, q, h) of the i-th row in the order the workgroups take them: the output's own order, or with hq (b, h, q),
+// so that the workgroups of an XCD work through one head's values at a time
+__device__ __forceinline__ int64_t sample_row(const SampleParams& p, int64_t i) {
+    if (!p.hq) return i;
+    const int64_t HQ = static_cast<int64_t>(p.g.H) * p.g.Q;
+    const int64_t b = i / HQ, rem = i - b * HQ;
+    const int64_t h = rem / p.g.Q, q = rem - h * p.g.Q;
+    return (b * p.g.Q + q) * p.g.H + h;
+}
 
 template <typename T, int V, int WAVES, int NB, bool GENERAL>
 __global__ __launch_bounds__(WAVES* kWave) void sample_kernel(SampleParams p) {
@@ -44,10 +55,9 @@ __global__ __launch_bounds__(WAVES* kWave) void sample_kernel(SampleParams p) {
 
     for (int i = tid; i < RB * LP; i += NTH) {
         const int r = i / LP, j = i - r * LP;
-        const int64_t row = row0 + r;
         Corner<float>* c4 = cw + r * S + 4 * j;
-        if (row < p.rows) {
-            corner4<T, float, GENERAL>(loc, attn, g, row, j, c4);
+        if (row0 + r < p.rows) {
+            corner4<T, float, GENERAL>(loc, attn, g, sample_row(p, row0 + r), j, c4);
         } else {
 #pragma unroll
             for (int k = 0; k < 4; ++k) c4[k] = Corner<float>{-1, 0.f};
@@ -58,8 +68,8 @@ __global__ __launch_bounds__(WAVES* kWave) void sample_kernel(SampleParams p) {
     const int64_t QH = static_cast<int64_t>(g.Q) * g.H;
     for (int it = tid; it < RB * GS; it += NTH) {
         const int r = it / GS, rem = it - r * GS, sg = rem / DV, ch = rem - sg * DV;
-        const int64_t row = row0 + r;
-        const bool valid = row < p.rows;
+        const bool valid = row0 + r < p.rows;
+        const int64_t row = valid ? sample_row(p, row0 + r) : 0;
         const int64_t b = valid ? row / QH : 0;
         const int h = valid ? static_cast<int>(row % g.H) : 0;
         // token-major value [B, N, H*D]: head rows HD apart; head-major [B, H, N, D]: D apart, so a bilinear pair
@@ -193,6 +203,15 @@ int launch_sample_t(SampleParams p, hipStream_t stream, const SampleTune& tune) 
     while (rb > 1 && lds(rb) > kLdsBudget) --rb;
     p.RB = rb;
     p.SG = sg;
+    // Rows in (b, h, q) order when one image's values far exceed an XCD's 4 MB L2: taking the rows of all heads of a
+    // few queries, an XCD's workgroups then touch one head's values (N * D elements) at a time instead of the whole
+    // image's. Measured on MI355X (sampler alone, graph-timed µs, (b, q, h) -> (b, h, q)): C = 1024 (44.6 MB per image)
+    // B2 Q300 30.7 -> 23.7, Q900 75.6 -> 56.7, B1 Q300 17.3 -> 13.4; DINO float32 (22.8 MB) B4 Q900 20.7 -> 19.8. At
+    // 8-11 MB per image it won or lost a few percent by shape (DINO fp16 B4 Q900 13.5 -> 12.6, B1 Q300 4.3 -> 4.8;
+    // C = 512 B4 Q900 20.3 -> 22.9), and at 4.3 MB (RT-DETR) or for self-attention it lost (bf16 B8 9.0 -> 9.6,
+    // DINO encoder 85 -> 91).
+    const int64_t image_bytes = static_cast<int64_t>(g.N) * g.H * D * static_cast<int64_t>(sizeof(T));
+    p.hq = !self_attn && image_bytes >= (int64_t{16} << 20) ? 1 : 0;
     switch (V) {
         case 1: return go_waves<T, 1>(p, waves, lds(rb), stream);
         case 2: return go_waves<T, 2>(p, waves, lds(rb), stream);

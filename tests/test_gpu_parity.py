@@ -339,6 +339,31 @@ def test_sample_alone_matches_oracle():
             assert_close(f'sample {name} {dtype}', got, ref, atol, rtol)
 
 
+@pytest.mark.parametrize('dtype', [torch.float16, torch.float32])
+def test_sample_head_order_on_large_values(dtype):
+    # values of 44.6 MB (fp16) / 89 MB (fp32) per image: the sampler takes its rows head by head ((b, h, q) order)
+    # instead of in the output's (b, q, h) order; two images, a query count that tiles nothing, a padding mask on the
+    # second call. Token-major and head-major values.
+    B, Q, H, D, P = 2, 37, 16, 64, 4
+    args = make(B, Q, H, D, H * D, LIMIT_LEVELS, P, dtype=dtype)
+    N = args[0].shape[1]
+    g = torch.Generator().manual_seed(9)
+    value = torch.randn(B, N, H * D, generator=g).to(dtype)
+    mask = torch.rand(B, N, generator=g) < 0.2
+    ref = bruteforce.sample(value, H, *args[3:])
+    ref_m = bruteforce.sample(value, H, *args[3:], padding_mask=mask)
+    dev = to(args[3:], 'cuda')
+    with torch.inference_mode():
+        got = td.ma_deform_sample(value.cuda(), *dev)
+        got_m = td.ma_deform_sample(value.cuda(), *dev, padding_mask=mask.cuda())
+        got_h = _native.sample_forward_heads(heads_of(value, H).cuda(), *dev)
+    torch.cuda.synchronize()
+    atol, rtol = TOL[dtype]
+    assert_close(f'sample (b, h, q) order {dtype}', got, ref, atol, rtol)
+    assert_close(f'sample (b, h, q) order, mask {dtype}', got_m, ref_m, atol, rtol)
+    assert_close(f'sample_heads (b, h, q) order {dtype}', got_h, ref, atol, rtol)
+
+
 def test_graph_capture_replays_match_eager():
     args = to(workload(1, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.float16), 'cuda')
     for mode in MODES:
