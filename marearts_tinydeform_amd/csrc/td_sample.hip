@@ -203,15 +203,21 @@ int launch_sample_t(SampleParams p, hipStream_t stream, const SampleTune& tune) 
     while (rb > 1 && lds(rb) > kLdsBudget) --rb;
     p.RB = rb;
     p.SG = sg;
-    // Rows in (b, h, q) order when one image's values far exceed an XCD's 4 MB L2: taking the rows of all heads of a
-    // few queries, an XCD's workgroups then touch one head's values (N * D elements) at a time instead of the whole
-    // image's. Measured on MI355X (sampler alone, graph-timed µs, (b, q, h) -> (b, h, q)): C = 1024 (44.6 MB per image)
-    // B2 Q300 30.7 -> 23.7, Q900 75.6 -> 56.7, B1 Q300 17.3 -> 13.4; DINO float32 (22.8 MB) B4 Q900 20.7 -> 19.8. At
-    // 8-11 MB per image it won or lost a few percent by shape (DINO fp16 B4 Q900 13.5 -> 12.6, B1 Q300 4.3 -> 4.8;
-    // C = 512 B4 Q900 20.3 -> 22.9), and at 4.3 MB (RT-DETR) or for self-attention it lost (bf16 B8 9.0 -> 9.6,
-    // DINO encoder 85 -> 91).
+    // Rows in (b, h, q) order when one image's values exceed an XCD's 4 MB L2 well and each head's rows are read
+    // again and again: taking the rows of all heads of a few queries, an XCD's workgroups touch the whole image's
+    // values (N * H * D elements), while head by head they touch one head's (N * D) at a time, which then stays in
+    // L2 for the Q * L * P * 4 corner reads of that head. Measured on MI355X (sampler alone, graph-timed µs,
+    // (b, q, h) -> (b, h, q)), with image = N * H * D * s and reads per row = 4 Q L P / N:
+    //  * C = 1024 (44.6 MB; 3.5 and 10.6 reads per row): B2 Q300 30.7 -> 23.7, Q900 75.6 -> 56.7, B1 Q300 17.3 -> 13.4;
+    //    at Q50 (0.6 reads per row) 7.77 -> 7.84;
+    //  * DINO 4-level (11.4 MB in 16 bits, 22.8 MB in float32): at Q900 (2.6 reads per row) fp16 B2 7.90 -> 7.70, B4
+    //    13.5 -> 12.6, B8 23.6 -> 23.0, B16 42.4 -> 40.2, bf16 B4 13.9 -> 13.8, fp32 B4 20.7 -> 19.8; at Q300 (0.9)
+    //    fp16 B1 4.2 -> 4.7, B4 6.6 -> 6.9, B8 9.6 -> 10.5;
+    //  * 8.6 MB (C = 512 in 16 bits, RT-DETR float32): slower at 1.7 and 5.1 reads per row (C = 512 B4 Q900 20.3 ->
+    //    22.9, fp32 B8 Q300 12.7 -> 14.2); 4.3 MB (RT-DETR 16-bit) slower (bf16 B8 9.0 -> 9.6); self-attention
+    //    slower (DINO encoder 85 -> 91).
     const int64_t image_bytes = static_cast<int64_t>(g.N) * g.H * D * static_cast<int64_t>(sizeof(T));
-    p.hq = !self_attn && image_bytes >= (int64_t{16} << 20) ? 1 : 0;
+    p.hq = !self_attn && image_bytes >= (int64_t{10} << 20) && 2 * static_cast<int64_t>(g.Q) * LP >= g.N ? 1 : 0;
     switch (V) {
         case 1: return go_waves<T, 1>(p, waves, lds(rb), stream);
         case 2: return go_waves<T, 2>(p, waves, lds(rb), stream);

@@ -341,10 +341,10 @@ def test_sample_alone_matches_oracle():
 
 @pytest.mark.parametrize('dtype', [torch.float16, torch.float32])
 def test_sample_head_order_on_large_values(dtype):
-    # values of 44.6 MB (fp16) / 89 MB (fp32) per image: the sampler takes its rows head by head ((b, h, q) order)
-    # instead of in the output's (b, q, h) order; two images, a query count that tiles nothing, a padding mask on the
-    # second call. Token-major and head-major values.
-    B, Q, H, D, P = 2, 37, 16, 64, 4
+    # values of 44.6 MB (fp16) / 89 MB (fp32) per image, each head's rows read about twice (4 Q L P / N = 2.01): the
+    # sampler takes its rows head by head ((b, h, q) order) instead of in the output's (b, q, h) order; two images, a
+    # query count that tiles nothing, a padding mask on the second call. Token-major and head-major values.
+    B, Q, H, D, P = 2, 171, 16, 64, 16
     args = make(B, Q, H, D, H * D, LIMIT_LEVELS, P, dtype=dtype)
     N = args[0].shape[1]
     g = torch.Generator().manual_seed(9)
