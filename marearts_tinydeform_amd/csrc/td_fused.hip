@@ -13,8 +13,8 @@
 //   phase 2  gather: CV*SG lanes per row, lane = (corner group sg, 16-byte channel chunk ch); each lane sums
 //            every SG-th corner of its row with float32 FMAs, the SG partial sums meet by cross-lane adds,
 //            and g lands in LDS as float32.
-//   phase 3  projection on MFMA: out[16 x D] = g[16 x C] . W_h^T, split over (N tile, K slice) jobs, one per
-//            wavefront. 16-bit types use v_mfma_f32_16x16x32_{f16,bf16} with g split as hi + lo (two
+//   phase 3  projection on MFMA: out[16 x D] = g[16 x C] . W_h^T, split over jobs of one K slice and every N tile
+//            (D <= 32) or of one (N tile, K slice) pair, one job per wavefront. 16-bit types use v_mfma_f32_16x16x32_{f16,bf16} with g split as hi + lo (two
 //            16-bit values whose sum carries 22 / 16 significant bits), so rounding g to the MFMA input type
 //            costs no accuracy; float32 uses v_mfma_f32_16x16x4_f32.
 // fused_generic_kernel: any C, any alignment, float64 (float64 accumulation); scalar loads, VALU projection.
@@ -25,6 +25,8 @@
 
 namespace td {
 namespace {
+
+constexpr int kAllN = 2;  // N tiles a projection job takes at once when it takes them all (D <= 32)
 
 struct FusedParams {
     const void* mem;
@@ -39,6 +41,7 @@ struct FusedParams {
     LayerArgs lay;       // query prologue (layer kernels only)
     // balanced slices (slices > 0): B * Q = slices * slice_rows + slice_extra rows per head
     int slices = 0, slice_rows = 0, slice_extra = 0;
+    int alln = 0;  // projection jobs take every N tile (D <= 64), one K slice each
 };
 
 // Workgroup index -> work unit (b, query tile, h) with heads fastest. Workgroups are dealt to the 8 XCDs
@@ -181,7 +184,7 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     }
     __syncthreads();
 
-    // phase 3: out[16 x D] = g[16 x C] . W_h^T on MFMA; job = (N tile, K slice)
+    // phase 3: out[16 x D] = g[16 x C] . W_h^T on MFMA; job = K slice with every N tile (p.alln), else (N tile, K slice)
     const int wave = tid / kWave, lane = tid & (kWave - 1);
     const int n16 = lane & 15, kg = lane >> 4;
     const bool av = n16 < QT;
@@ -199,7 +202,86 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
             inv_sc = ldexpf(1.f, e - 14);
         }
     }
-    if constexpr (sizeof(T) == 2) {
+    if (p.alln) {
+        // every N tile in each job (D <= 16 kAllN): job = K slice, and g's chunk is read (and, in 16 bits, split into
+        // hi + lo) once for all N tiles
+        constexpr int KCH = sizeof(T) == 2 ? 32 : 16;  // K per MFMA chunk
+        const int nk = (C + KCH - 1) / KCH;
+        for (int ks = wave; ks < p.KS; ks += WAVES) {
+            const int kb = ks * nk / p.KS, ke = (ks + 1) * nk / p.KS;
+            f32x4 acc[kAllN];
+            bool dv[kAllN];
+#pragma unroll
+            for (int nt = 0; nt < kAllN; ++nt) {
+                acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                dv[nt] = nt < NTILE && nt * 16 + n16 < D;
+            }
+            // row n16 of N tile nt is W_h row nt * 16 + n16
+            const T* wr0 = w + (static_cast<size_t>(h) * D + n16) * C;
+            for (int kk = kb; kk < ke; ++kk) {
+                const int k = kk * KCH + kg * (KCH / 4);
+                const bool kv = k < C;
+                u32x4 braw[kAllN];
+#pragma unroll
+                for (int nt = 0; nt < kAllN; ++nt) {
+                    braw[nt] = u32x4{0u, 0u, 0u, 0u};
+                    if (dv[nt] && kv) braw[nt] = *reinterpret_cast<const u32x4*>(wr0 + static_cast<size_t>(nt) * 16 * C + k);
+                }
+                if constexpr (sizeof(T) == 2) {
+                    using M = MfmaOp<T>;
+                    using frag = typename M::frag;
+                    f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
+                    if (av && kv) {
+                        a0 = *reinterpret_cast<const f32x4*>(ga + k);
+                        a1 = *reinterpret_cast<const f32x4*>(ga + k + 4);
+                        if (two) {
+                            a0 += *reinterpret_cast<const f32x4*>(ga + QT * GP + k);
+                            a1 += *reinterpret_cast<const f32x4*>(ga + QT * GP + k + 4);
+                        }
+                        a0 *= sc;
+                        a1 *= sc;
+                    }
+                    frag hi, lo;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const T x0 = static_cast<T>(a0[i]), x1 = static_cast<T>(a1[i]);
+                        hi[i] = x0;
+                        hi[4 + i] = x1;
+                        lo[i] = static_cast<T>(a0[i] - static_cast<float>(x0));
+                        lo[4 + i] = static_cast<T>(a1[i] - static_cast<float>(x1));
+                    }
+#pragma unroll
+                    for (int nt = 0; nt < kAllN; ++nt) {
+                        if (nt >= NTILE) break;
+                        const frag bf = __builtin_bit_cast(frag, braw[nt]);
+                        acc[nt] = M::mma(hi, bf, acc[nt]);
+                        acc[nt] = M::mma(lo, bf, acc[nt]);
+                    }
+                } else {
+                    f32x4 aq = {0.f, 0.f, 0.f, 0.f};
+                    if (av && kv) {
+                        aq = *reinterpret_cast<const f32x4*>(ga + k);
+                        if (two) aq += *reinterpret_cast<const f32x4*>(ga + QT * GP + k);
+                    }
+#pragma unroll
+                    for (int nt = 0; nt < kAllN; ++nt) {
+                        if (nt >= NTILE) break;
+                        const f32x4 bq = __builtin_bit_cast(f32x4, braw[nt]);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[j], bq[j], acc[nt], 0, 0, 0);
+                    }
+                }
+            }
+            float* pp = part + ks * 16 * PW;
+#pragma unroll
+            for (int nt = 0; nt < kAllN; ++nt) {
+                if (nt >= NTILE) break;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pp[(4 * kg + i) * PW + nt * 16 + n16] = acc[nt][i];
+            }
+        }
+    } else if constexpr (sizeof(T) == 2) {
         using M = MfmaOp<T>;
         using frag = typename M::frag;
         const int nk = (C + 31) >> 5;
@@ -423,6 +505,7 @@ int go_generic(FusedParams p, size_t lds, hipStream_t stream) {
 
 inline bool aligned16(const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; }
 
+
 // layer: the query prologue runs inside the kernel (LayerArgs in p.lay); returns 1 without launching anything when
 // the vector kernel cannot take the problem (alignment, channel counts, LDS), so the caller can fall back to the
 // standalone prologue followed by the plain kernels.
@@ -492,8 +575,14 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
             const int nk = sizeof(T) == 2 ? (C + 31) / 32 : (C + 15) / 16;
             const int GP = (layer && p.lay.Cq > C ? p.lay.Cq : C) + 4;
             const int PP = ((3 * LP + 15) & ~15) + 4;
+            // Projection jobs. D <= 32: each job takes every N tile of one K slice, so g's chunks are read (and in 16 bits
+            // split into hi + lo) once instead of once per N tile; 16-bit types use 4 K slices, one job per SIMD, float32
+            // one per wavefront. Measured on MI355X against one job per (N tile, K slice) (graph-timed µs): fp16 B1
+            // Q300 8.34 -> 8.03, Q50 5.80 -> 5.62, Q100 6.04 -> 5.83, B2 Q300 11.97 -> 11.15, bf16 B1 Q300 8.52 ->
+            // 8.20; float32 B1 Q300 12.45 -> 12.37 (4 slices: 12.80). Larger D keeps one job per (N tile, K slice).
+            const bool alln = NTILE <= kAllN;
             auto k_slices = [&](int w) {
-                int ks = w / NTILE;
+                int ks = !alln ? w / NTILE : sizeof(T) == 2 ? (w < 4 ? w : 4) : w;
                 return ks < 1 ? 1 : ks > nk ? nk : ks;
             };
             // LDS bytes of a workgroup of q rows, w wavefronts, gathered by corner groups sgx
@@ -551,6 +640,7 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
                 p.QT = qt;
                 p.SG = sg;
                 p.KS = ks;
+                p.alln = alln ? 1 : 0;
                 p.qtiles = (g.Q + qt - 1) / qt;
                 if (slices > 0) {
                     p.slices = static_cast<int>(slices);
