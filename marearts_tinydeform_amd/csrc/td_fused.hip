@@ -477,13 +477,13 @@ int go_vec(FusedParams p, size_t lds, hipStream_t stream, int nb = 8) {
 }
 
 // The generic kernel may take up to the CU's whole LDS (wide float64 rows: C = 8192 needs 68 KB at one row per
-// workgroup); launches above 64 KB need the attribute, set once per instantiation.
+// workgroup); launches above 64 KB need the attribute, set once per instantiation and device.
 template <auto Kernel>
 int allow_lds(size_t lds) {
     if (lds <= 65536) return 0;
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(Kernel),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                       static_cast<int>(kGenericLdsBudget));
+    static std::atomic<uint64_t> done{0};
+    const hipError_t attr =
+        allow_dynamic_lds(reinterpret_cast<const void*>(Kernel), static_cast<int>(kGenericLdsBudget), done);
     return attr == hipSuccess ? 0 : set_error(-3, "fused_generic: LDS size attribute refused: %s", hipGetErrorString(attr));
 }
 

@@ -212,9 +212,9 @@ int go_dma(GemmParams p, hipStream_t stream) {
     constexpr size_t stages = static_cast<size_t>(STAGES) * (256 + BN) * 64;
     constexpr size_t out = static_cast<size_t>(256) * (BN + 8) * sizeof(T);
     constexpr size_t lds = stages > out ? stages : out;
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(gemm_dma_kernel<T, WN, STAGES>), hipFuncAttributeMaxDynamicSharedMemorySize,
-        static_cast<int>(lds));
+    static std::atomic<uint64_t> done{0};
+    const hipError_t attr =
+        allow_dynamic_lds(reinterpret_cast<const void*>(gemm_dma_kernel<T, WN, STAGES>), static_cast<int>(lds), done);
     if (attr != hipSuccess) return set_error(-3, "value_proj: LDS size attribute refused: %s", hipGetErrorString(attr));
     p.mt = (p.M + 255) / 256;
     p.nt = (p.NO + BN - 1) / BN;
@@ -398,9 +398,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void g
 template <typename T, int STAGES>
 int go_dma_persistent(GemmParams p, hipStream_t stream) {
     constexpr size_t lds = static_cast<size_t>(STAGES) * 512 * 64;
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(gemm_dma_persistent_kernel<T, STAGES>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    static std::atomic<uint64_t> done{0};
+    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(gemm_dma_persistent_kernel<T, STAGES>),
+                                              static_cast<int>(lds), done);
     if (attr != hipSuccess) return set_error(-3, "value_proj: LDS size attribute refused: %s", hipGetErrorString(attr));
     p.mt = (p.M + 255) / 256;
     p.nt = (p.NO + 255) / 256;

@@ -212,9 +212,9 @@ int go_stream(GemmParams p, int64_t grid, hipStream_t stream) {
     // two token stages and W: 160 KB at K = 256, 80 KB at K = 128
     constexpr size_t lds = static_cast<size_t>(2) * kStreamStep * KB * 64 + static_cast<size_t>(kStreamNO) * KB * 64;
     if constexpr (lds > 65536) {
-        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_stream_kernel<T, KB>),
-                                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                           static_cast<int>(lds));
+        static std::atomic<uint64_t> done{0};
+        const hipError_t attr =
+            allow_dynamic_lds(reinterpret_cast<const void*>(gemm_stream_kernel<T, KB>), static_cast<int>(lds), done);
         if (attr != hipSuccess)
             return set_error(-3, "value_proj: LDS size attribute refused: %s", hipGetErrorString(attr));
     }

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "td_common.h"
 #include "td_prologue.h"
 
@@ -30,6 +32,19 @@ struct SampleTune {
 
 // Compute units of the current device (256 on MI355X), cached per device.
 int cu_count();
+
+// Lets kernel `fn` launch with up to `bytes` of dynamic LDS (above the default 64 KB; MI355X has 160 KB per CU) on the
+// current device. The attribute is set once per device: `done` (one per kernel) holds a bit per device already set.
+inline hipError_t allow_dynamic_lds(const void* fn, int bytes, std::atomic<uint64_t>& done) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = uint64_t{1} << (dev & 63);
+    if (done.load(std::memory_order_acquire) & bit) return hipSuccess;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess) done.fetch_or(bit, std::memory_order_acq_rel);
+    return e;
+}
 
 // Every launcher returns 0, or a negative TD_E* code after recording a message with set_error.
 int set_error(int code, const char* fmt, ...);
