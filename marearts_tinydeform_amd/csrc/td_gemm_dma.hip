@@ -427,7 +427,206 @@ int launch_dma_t(GemmParams p, hipStream_t stream, int variant) {
     }
 }
 
+// Short, wide projections with float32 output, two weight matrices in one launch (the layer's query prologue: the
+// sampling offsets and the attention logits of B * Q query rows): C_j[M, NO_j] = X . W_j^T (+ X2 . W_j^T) + b_j for
+// j = 0, 1, float32 accumulation, stored unrounded. With few rows (600 at C = 1024) a tile's share of the operands
+// bounds the time, since a CU receives at most about 72 GB/s from L2; so the tiles are small enough for every CU
+// to hold one (64 rows x 128 columns; 4 wavefronts of 32 x 64), and both products share one grid.
+//
+// K streams through a ring of STAGES LDS buffers, STAGES - 1 chunks of 32 ahead, by direct global-to-LDS loads,
+// waited for by meet() and laid out with the slot swizzle of gemm_dma_kernel. The product is formed transposed
+// (W rows as the MFMA's rows, X rows as its columns), so a lane ends with four consecutive columns of one row: one
+// 16-byte store, no LDS pass. The two-operand form adds X2 . W^T by a second MFMA on the same W fragment, so X + X2
+// is never rounded. Tiles are numbered column block after column block, C_0's first: the row blocks of a column
+// block sit on one XCD and share its W rows in L2.
+struct PairParams {
+    const void* x;
+    const void* x2;
+    const void* w[2];
+    const void* bias[2];
+    float* c[2];
+    int M, K, no[2];
+    int mt, nt0, tiles, per_xcd;  // 64-row blocks, 128-column blocks of C_0, tiles of both products
+};
+
+template <typename T, int STAGES, bool DUAL>
+__global__ __launch_bounds__(256) void gemm_pair_kernel(PairParams p) {
+    constexpr int KC = 32, ROW = 64, BM = 64, BN = 128, NA = DUAL ? 2 : 1;
+    constexpr int TW = 4, TX = 2;  // 16-row blocks per wavefront: of W (its 64 columns), of each X (its 32 rows)
+    constexpr int X_BYTES = BM * ROW, STAGE_BYTES = (NA * BM + BN) * ROW;
+    constexpr int LOADS = NA + 2;  // 1 KB wavefront loads per chunk: one 16-row block of each X, two of W
+    static_assert(LOADS * (STAGES - 1) <= 63 && STAGES >= 2, "vmcnt range");
+    extern __shared__ __align__(16) unsigned char lds[];
+
+    const int unit = static_cast<int>(blockIdx.x % kXcds) * p.per_xcd + static_cast<int>(blockIdx.x / kXcds);
+    if (unit >= p.tiles) return;
+    const int cb = unit / p.mt, mb = unit - cb * p.mt;
+    const int j = cb < p.nt0 ? 0 : 1;
+    const int n0 = (j == 0 ? cb : cb - p.nt0) * BN, m0 = mb * BM;
+    const int M = p.M, K = p.K, NO = p.no[j];
+    const T* __restrict__ X = static_cast<const T*>(p.x);
+    const T* __restrict__ X2 = static_cast<const T*>(p.x2);
+    const T* __restrict__ W = static_cast<const T*>(p.w[j]);
+    const T* __restrict__ bias = static_cast<const T*>(p.bias[j]);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, kg = lane >> 4;
+    const int wm = wave & 1, wn = wave >> 1;  // the wavefront's rows 32 wm .. + 32 and columns 64 wn .. + 64
+
+    // the bias of the lane's columns, requested first and kept raw until the end (NO % 4 == 0 and an 8-byte
+    // aligned bias: four columns are one 8-byte load, and a column block passes NO only by whole quads)
+    uint2 braw[TW];
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+        const int n = n0 + wn * 64 + t * 16 + 4 * kg;
+        braw[t] = uint2{0u, 0u};
+        if (bias != nullptr && n < NO) braw[t] = *reinterpret_cast<const uint2*>(bias + n);
+    }
+
+    // load sources: wavefront w fills row block w of each X operand and row blocks 2w, 2w + 1 of W; lane =
+    // 4 * (row % 16) + slot, the slot holding piece slot ^ g(row). Rows past M or NO load the last valid row.
+    const int piece = ((lane & 3) ^ swz(lane >> 2)) * 8;
+    int xm = m0 + wave * 16 + (lane >> 2);
+    xm = xm < M ? xm : M - 1;
+    const T* xs = X + static_cast<size_t>(xm) * K + piece;
+    const T* xs2 = DUAL ? X2 + static_cast<size_t>(xm) * K + piece : xs;
+    const T* ws[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        int n = n0 + (2 * wave + i) * 16 + (lane >> 2);
+        n = n < NO ? n : NO - 1;
+        ws[i] = W + static_cast<size_t>(n) * K + piece;
+    }
+    const int nc = K / KC;
+    // one group of loads per step, always: past the last chunk the group re-loads it into a stage that is not
+    // read for the product again, so every wait is the same constant
+    auto issue = [&](int c) {
+        unsigned char* st = lds + (c % STAGES) * STAGE_BYTES;
+        const int k = (c < nc ? c : nc - 1) * KC;
+        load_lds16(xs + k, st + wave * 1024);
+        if constexpr (DUAL) load_lds16(xs2 + k, st + X_BYTES + wave * 1024);
+        load_lds16(ws[0] + k, st + NA * X_BYTES + 2 * wave * 1024);
+        load_lds16(ws[1] + k, st + NA * X_BYTES + (2 * wave + 1) * 1024);
+    };
+
+    f32x4 acc[TW][TX];
+#pragma unroll
+    for (int t = 0; t < TW; ++t)
+#pragma unroll
+        for (int i = 0; i < TX; ++i) acc[t][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int frag = r16 * ROW + ((kg ^ swz(r16)) << 4);
+    const int w_off = NA * X_BYTES + wn * 64 * ROW + frag, x_off = wm * 32 * ROW + frag;
+    auto read_frags = [&](int c, u32x4 (&fw)[TW], u32x4 (&fx)[NA][TX]) {
+        const unsigned char* st = lds + (c % STAGES) * STAGE_BYTES;
+#pragma unroll
+        for (int t = 0; t < TW; ++t) fw[t] = *reinterpret_cast<const u32x4*>(st + w_off + t * 16 * ROW);
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+            for (int i = 0; i < TX; ++i)
+                fx[a][i] = *reinterpret_cast<const u32x4*>(st + x_off + a * X_BYTES + i * 16 * ROW);
+    };
+    // step c: wait for chunk c + 1 and meet (nobody reads chunk c's stage any more), refill that stage with chunk
+    // c + STAGES, read chunk c + 1's fragments, run chunk c's MFMAs on the fragments read one step earlier
+    auto step = [&](int c, const u32x4 (&fw)[TW], const u32x4 (&fx)[NA][TX], u32x4 (&gw)[TW], u32x4 (&gx)[NA][TX]) {
+        meet<LOADS * (STAGES - 2)>();
+        issue(c + STAGES);
+        read_frags(c + 1, gw, gx);
+#pragma unroll
+        for (int t = 0; t < TW; ++t)
+#pragma unroll
+            for (int i = 0; i < TX; ++i) {
+                acc[t][i] = KBlock<T>::mma(fw[t], fx[0][i], acc[t][i]);
+                if constexpr (DUAL) acc[t][i] = KBlock<T>::mma(fw[t], fx[1][i], acc[t][i]);
+            }
+        if constexpr (DUAL) {  // spread the next chunk's reads and loads over the 16 MFMAs
+#pragma unroll
+            for (int r = 0; r < TW + NA * TX; ++r) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            }
+#pragma unroll
+            for (int r = 0; r < LOADS; ++r) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // vector memory read (the LDS load)
+            }
+        }
+        sched_fence();
+    };
+#pragma unroll
+    for (int c = 0; c < STAGES; ++c) issue(c);
+    meet<LOADS * (STAGES - 1)>();
+    u32x4 fw0[TW], fx0[NA][TX], fw1[TW], fx1[NA][TX];
+    read_frags(0, fw0, fx0);
+    for (int c = 0; c < nc; c += 2) {  // nc is even
+        step(c, fw0, fx0, fw1, fx1);
+        step(c + 1, fw1, fx1, fw0, fx0);
+    }
+    meet<0>();  // the tail's re-loads have landed before the workgroup ends
+
+    float* __restrict__ C = p.c[j];
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+        const int n = n0 + wn * 64 + t * 16 + 4 * kg;
+        if (n >= NO) continue;
+        const T* bt = reinterpret_cast<const T*>(&braw[t]);
+        const f32x4 bv = {cvt<float>(bt[0]), cvt<float>(bt[1]), cvt<float>(bt[2]), cvt<float>(bt[3])};
+#pragma unroll
+        for (int i = 0; i < TX; ++i) {
+            const int m = m0 + wm * 32 + i * 16 + r16;
+            if (m < M) *reinterpret_cast<f32x4*>(C + static_cast<size_t>(m) * NO + n) = acc[t][i] + bv;
+        }
+    }
+}
+
+template <typename T, int STAGES, bool DUAL>
+int go_pair(PairParams p, hipStream_t stream) {
+    constexpr size_t lds = static_cast<size_t>(STAGES) * ((DUAL ? 2 : 1) * 64 + 128) * 64;
+    if (lds > 65536) {
+        static std::atomic<uint64_t> done{0};
+        const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(gemm_pair_kernel<T, STAGES, DUAL>),
+                                                  static_cast<int>(lds), done);
+        if (attr != hipSuccess)
+            return set_error(-3, "layer prologue: LDS size attribute refused: %s", hipGetErrorString(attr));
+    }
+    p.per_xcd = (p.tiles + kXcds - 1) / kXcds;
+    hipLaunchKernelGGL((gemm_pair_kernel<T, STAGES, DUAL>), dim3(static_cast<unsigned>(p.per_xcd * kXcds)),
+                       dim3(256), lds, stream, p);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : set_error(-3, "layer prologue launch failed: %s", hipGetErrorString(e));
+}
+
+// 4 stages (64 KB with two operands): C = 1024, 600 rows, 3072 columns in 240 tiles: 20.0 µs for the prologue with
+// its finalize, against 21.3 with 8 stages and 45.9 for two launches of 64 x 64 register-operand tiles (graph-timed).
+template <typename T>
+int launch_pair_t(PairParams p, hipStream_t stream) {
+    return p.x2 != nullptr ? go_pair<T, 4, true>(p, stream) : go_pair<T, 4, false>(p, stream);
+}
+
 }  // namespace
+
+int launch_proj_f32_pair(int dtype, const void* x, const void* x2, const void* w0, const void* b0, float* c0,
+                         int64_t no0, const void* w1, const void* b1, float* c1, int64_t no1, int64_t M, int64_t K,
+                         hipStream_t stream) {
+    const uintptr_t a16 = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(x2) |
+                          reinterpret_cast<uintptr_t>(w0) | reinterpret_cast<uintptr_t>(w1) |
+                          reinterpret_cast<uintptr_t>(c0) | reinterpret_cast<uintptr_t>(c1);
+    const uintptr_t a8 = reinterpret_cast<uintptr_t>(b0) | reinterpret_cast<uintptr_t>(b1);
+    const int64_t lim = int64_t{1} << 31;
+    if ((dtype != kF16 && dtype != kBF16) || a16 % 16 != 0 || a8 % 8 != 0 || K <= 0 || K % 64 != 0 || M <= 0 ||
+        no0 <= 0 || no1 <= 0 || no0 % 4 != 0 || no1 % 4 != 0 || M * K >= lim || no0 * K >= lim || no1 * K >= lim ||
+        M * no0 >= lim || M * no1 >= lim)
+        return 1;
+    PairParams p{x, x2, {w0, w1}, {b0, b1}, {c0, c1}, static_cast<int>(M), static_cast<int>(K),
+                 {static_cast<int>(no0), static_cast<int>(no1)}, 0, 0, 0, 0};
+    p.mt = static_cast<int>((M + 63) / 64);
+    p.nt0 = static_cast<int>((no0 + 127) / 128);
+    const int64_t tiles = static_cast<int64_t>(p.mt) * (p.nt0 + (no1 + 127) / 128);
+    if (tiles >= lim / kXcds) return 1;
+    p.tiles = static_cast<int>(tiles);
+    return dtype == kF16 ? launch_pair_t<f16>(p, stream) : launch_pair_t<bf16>(p, stream);
+}
 
 bool gemm_persistent_fits(int dtype, const GemmParams& p) {
     const uintptr_t al = reinterpret_cast<uintptr_t>(p.a) | reinterpret_cast<uintptr_t>(p.w) |

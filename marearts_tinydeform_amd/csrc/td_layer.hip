@@ -86,6 +86,19 @@ __global__ __launch_bounds__(256) void layer_finalize_kernel(LayerArgs a, Geom g
     off[2 * j + 1] = ly;
 }
 
+// The in-place finalize of the GEMM route's raw offsets and logits (layer_finalize_kernel).
+template <typename T>
+int finalize_prologue(const LayerArgs& la, const Geom& g, hipStream_t stream) {
+    int seg_log2 = 0;
+    while ((1 << seg_log2) < g.LP) ++seg_log2;
+    const int64_t rows = static_cast<int64_t>(g.B) * g.Q * g.H, per_wave = kWave >> seg_log2,
+                  waves = (rows + per_wave - 1) / per_wave;
+    hipLaunchKernelGGL(layer_finalize_kernel<T>, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, stream,
+                       la, g, seg_log2);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : set_error(-3, "layer prologue launch failed: %s", hipGetErrorString(e));
+}
+
 // The prologue as two projections on the GEMM (x . W^T computed as hidden . W^T + pos . W^T, float32 out, straight
 // into loc_out and attn_out) and the in-place finalize. A workgroup of the single-kernel prologue owns 16 queries of
 // one head and streams that head's weights once per 16 queries, so for large problems the weights are read
@@ -99,20 +112,18 @@ int launch_prologue_gemm(const LayerArgs& la, const Geom& g, hipStream_t stream)
                          reinterpret_cast<uintptr_t>(la.loc_out) | reinterpret_cast<uintptr_t>(la.attn_out);
     if (la.Cq <= 0 || la.Cq % V != 0 || al % 16 != 0 || g.P <= 0) return 1;
     const int64_t M = static_cast<int64_t>(g.B) * g.Q, NO = static_cast<int64_t>(g.H) * g.LP;
-    int rc = launch_proj_f32(std::is_same<T, float>::value ? kF32 : std::is_same<T, f16>::value ? kF16 : kBF16,
-                             la.query, la.pos, la.off_w, la.off_b, static_cast<float*>(la.loc_out), M, la.Cq, 2 * NO,
-                             stream);
+    const int dt = std::is_same<T, float>::value ? kF32 : std::is_same<T, f16>::value ? kF16 : kBF16;
+    int rc = launch_proj_f32_pair(dt, la.query, la.pos, la.off_w, la.off_b, static_cast<float*>(la.loc_out), 2 * NO,
+                                  la.aw_w, la.aw_b, static_cast<float*>(la.attn_out), NO, M, la.Cq, stream);
+    if (rc < 0) return rc;
+    if (rc == 0) return finalize_prologue<T>(la, g, stream);
+    rc = launch_proj_f32(dt, la.query, la.pos, la.off_w, la.off_b, static_cast<float*>(la.loc_out), M, la.Cq, 2 * NO,
+                         stream);
     if (rc != 0) return rc;
-    rc = launch_proj_f32(std::is_same<T, float>::value ? kF32 : std::is_same<T, f16>::value ? kF16 : kBF16, la.query,
-                         la.pos, la.aw_w, la.aw_b, static_cast<float*>(la.attn_out), M, la.Cq, NO, stream);
+    rc = launch_proj_f32(dt, la.query, la.pos, la.aw_w, la.aw_b, static_cast<float*>(la.attn_out), M, la.Cq, NO,
+                         stream);
     if (rc != 0) return rc;
-    int seg_log2 = 0;
-    while ((1 << seg_log2) < g.LP) ++seg_log2;
-    const int64_t rows = M * g.H, per_wave = kWave >> seg_log2, waves = (rows + per_wave - 1) / per_wave;
-    hipLaunchKernelGGL(layer_finalize_kernel<T>, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, stream,
-                       la, g, seg_log2);
-    const hipError_t e = hipGetLastError();
-    return e == hipSuccess ? 0 : set_error(-3, "layer prologue launch failed: %s", hipGetErrorString(e));
+    return finalize_prologue<T>(la, g, stream);
 }
 
 constexpr size_t kLdsBudget = 65536;

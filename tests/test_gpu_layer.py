@@ -88,11 +88,15 @@ def test_locations_in_float32(dtype):
 def test_large_prologue_takes_the_gemm_route(dtype):
     # >= 8e8 multiply-adds in the query projections: project mode runs them on the GEMM (hidden . W^T + pos . W^T in
     # float32) and finalizes softmax and locations in place; boxes with 64 samples per head (one row per wavefront)
-    # and points per level with 12 (four rows per wavefront), with and without bias
-    for name, (B, Q, H, D, C, levels, P, rd, rl, bias) in {
-            'boxes': (2, 300, 16, 32, 512, [(40, 40), (20, 20), (10, 10), (5, 5)], 16, 4, '1', True),
-            'points per level': (2, 900, 16, 32, 1024, [(48, 40), (24, 20), (12, 10)], 4, 2, 'L', False)}.items():
-        a = make_layer(B, Q, H, D, C, levels, P, rd, rl, dtype=dtype, bias=bias)
+    # and points per level with 12 (four rows per wavefront), with and without bias. In 16 bits both projections
+    # share one launch of 64 x 128 tiles: 600 and 1800 rows end in a partial row block, 2 * 192 and 192 columns in
+    # a partial column block, and without position embeddings the tiles take one operand.
+    for name, (B, Q, H, D, C, levels, P, rd, rl, bias, pos) in {
+            'boxes': (2, 300, 16, 32, 512, [(40, 40), (20, 20), (10, 10), (5, 5)], 16, 4, '1', True, True),
+            'points per level': (2, 900, 16, 32, 1024, [(48, 40), (24, 20), (12, 10)], 4, 2, 'L', False, True),
+            'no position': (1, 700, 16, 32, 1024, [(40, 40), (20, 20), (10, 10), (5, 5)], 8, 4, '1', True,
+                            False)}.items():
+        a = make_layer(B, Q, H, D, C, levels, P, rd, rl, dtype=dtype, bias=bias, pos=pos)
         ref, ref_attn = olayer.layer(*a[:15], position_embeddings=a[15])
         ref_loc, _ = olayer.locations(a[0], a[2], a[3], a[5], a[6], a[7], a[8], H, P, position_embeddings=a[15])
         dev = to(a[:13], 'cuda') + a[13:15] + to(a[15:], 'cuda')
@@ -113,7 +117,7 @@ def test_large_prologue_takes_the_gemm_route(dtype):
         hidden, memory, rp, shapes, starts, ow, ob, aw, ab, vw, vb = dev[:11]
         N, Cq = memory.shape[1], hidden.shape[2]
         out = torch.empty(B, Q, H * D, dtype=dtype, device='cuda')
-        args = [_native.DTYPE_CODES[dtype], hidden.data_ptr(), dev[15].data_ptr(), rp.data_ptr(), rp.shape[2],
+        args = [_native.DTYPE_CODES[dtype], hidden.data_ptr(), _native._ptr(dev[15]), rp.data_ptr(), rp.shape[2],
                 rp.shape[3], ow.data_ptr(), _native._ptr(ob), aw.data_ptr(), _native._ptr(ab), memory.data_ptr(),
                 vw.data_ptr(), _native._ptr(vb), shapes.data_ptr(), starts.data_ptr(), None, out.data_ptr()]
         sizes = [B, Q, N, Cq, C, H, D, len(levels), P, None]
