@@ -447,9 +447,16 @@ struct PairParams {
     float* c[2];
     int M, K, no[2];
     int mt, nt0, tiles, per_xcd;  // 64-row blocks, 128-column blocks of C_0, tiles of both products
+    LayerArgs la;                 // FIN: the layer (reference points) and its geometry
+    Geom g;
 };
 
-template <typename T, int STAGES, bool DUAL>
+// FIN (the layer prologue, L * P a power of two from 4 to 64): the epilogue also does what layer_finalize_kernel
+// would do afterwards. C_0's columns 2s, 2s + 1 are sample s's offsets, turned into its location; C_1's are the
+// logits, turned into softmax weights over each head's L * P columns, all of which a tile holds: a wavefront's 64
+// columns of a row sit in the four lanes that share the row (lane groups kg = 0..3, 16 each), so a head's maximum
+// and sum take in-lane steps and at most two cross-lane ones.
+template <typename T, int STAGES, bool DUAL, bool FIN>
 __global__ __launch_bounds__(256) void gemm_pair_kernel(PairParams p) {
     constexpr int KC = 32, ROW = 64, BM = 64, BN = 128, NA = DUAL ? 2 : 1;
     constexpr int TW = 4, TX = 2;  // 16-row blocks per wavefront: of W (its 64 columns), of each X (its 32 rows)
@@ -534,12 +541,11 @@ __global__ __launch_bounds__(256) void gemm_pair_kernel(PairParams p) {
         issue(c + STAGES);
         read_frags(c + 1, gw, gx);
 #pragma unroll
-        for (int t = 0; t < TW; ++t)
+        for (int a = 0; a < NA; ++a)  // operand outermost: consecutive MFMAs write different accumulators
 #pragma unroll
-            for (int i = 0; i < TX; ++i) {
-                acc[t][i] = KBlock<T>::mma(fw[t], fx[0][i], acc[t][i]);
-                if constexpr (DUAL) acc[t][i] = KBlock<T>::mma(fw[t], fx[1][i], acc[t][i]);
-            }
+            for (int t = 0; t < TW; ++t)
+#pragma unroll
+                for (int i = 0; i < TX; ++i) acc[t][i] = KBlock<T>::mma(fw[t], fx[a][i], acc[t][i]);
         if constexpr (DUAL) {  // spread the next chunk's reads and loads over the 16 MFMAs
 #pragma unroll
             for (int r = 0; r < TW + NA * TX; ++r) {
@@ -568,47 +574,113 @@ __global__ __launch_bounds__(256) void gemm_pair_kernel(PairParams p) {
     float* __restrict__ C = p.c[j];
 #pragma unroll
     for (int t = 0; t < TW; ++t) {
-        const int n = n0 + wn * 64 + t * 16 + 4 * kg;
-        if (n >= NO) continue;
         const T* bt = reinterpret_cast<const T*>(&braw[t]);
         const f32x4 bv = {cvt<float>(bt[0]), cvt<float>(bt[1]), cvt<float>(bt[2]), cvt<float>(bt[3])};
 #pragma unroll
+        for (int i = 0; i < TX; ++i) acc[t][i] += bv;
+    }
+    if constexpr (FIN) {
+        const Geom& g = p.g;
+        const int LP = g.LP;
+        if (j == 0) {
+#pragma unroll
+            for (int t = 0; t < TW; ++t) {
+                const int n = n0 + wn * 64 + t * 16 + 4 * kg;
+                if (n >= NO) continue;
+                // samples s0 and s0 + 1 of a head (n is a multiple of 4, so both are the same head's)
+                const int s0 = (n >> 1) & (LP - 1), l0 = s0 / g.P, l1 = (s0 + 1) / g.P;
+#pragma unroll
+                for (int i = 0; i < TX; ++i) {
+                    const int m = m0 + wm * 32 + i * 16 + r16;
+                    if (m >= M) continue;
+                    const int b = m / g.Q, q = m - b * g.Q;
+                    const f32x4 v = acc[t][i];
+                    float x0, y0, x1, y1;
+                    layer_location<T, float>(p.la, g, b, q, l0, v[0], v[1], x0, y0);
+                    layer_location<T, float>(p.la, g, b, q, l1, v[2], v[3], x1, y1);
+                    *reinterpret_cast<f32x4*>(C + static_cast<size_t>(m) * NO + n) = f32x4{x0, y0, x1, y1};
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < TX; ++i) {
+                // the lane's columns are t * 16 + 4 kg + e of its wavefront's 64; a head's LP columns share
+                // t >> log2(LP / 16) and kg >> log2(LP / 4). Every lane takes part in the cross-lane steps, valid
+                // or not (columns past NO form whole heads of their own).
+                float mx[TW], sm[TW];
+#pragma unroll
+                for (int t = 0; t < TW; ++t) {
+                    const f32x4 v = acc[t][i];
+                    mx[t] = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+                    if (LP >= 8) mx[t] = fmaxf(mx[t], xor_lane(mx[t], 16));
+                    if (LP >= 16) mx[t] = fmaxf(mx[t], xor_lane(mx[t], 32));
+                }
+                if (LP >= 32) {
+                    mx[0] = mx[1] = fmaxf(mx[0], mx[1]);
+                    mx[2] = mx[3] = fmaxf(mx[2], mx[3]);
+                }
+                if (LP >= 64) mx[0] = mx[1] = mx[2] = mx[3] = fmaxf(mx[0], mx[2]);
+#pragma unroll
+                for (int t = 0; t < TW; ++t) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[t][i][e] = exp_acc(acc[t][i][e] - mx[t]);
+                    const f32x4 v = acc[t][i];
+                    sm[t] = (v[0] + v[1]) + (v[2] + v[3]);
+                    if (LP >= 8) sm[t] += xor_lane(sm[t], 16);
+                    if (LP >= 16) sm[t] += xor_lane(sm[t], 32);
+                }
+                if (LP >= 32) {
+                    sm[0] = sm[1] = sm[0] + sm[1];
+                    sm[2] = sm[3] = sm[2] + sm[3];
+                }
+                if (LP >= 64) sm[0] = sm[1] = sm[2] = sm[3] = sm[0] + sm[2];
+                const int m = m0 + wm * 32 + i * 16 + r16;
+#pragma unroll
+                for (int t = 0; t < TW; ++t) {
+                    const int n = n0 + wn * 64 + t * 16 + 4 * kg;
+                    if (m < M && n < NO)
+                        *reinterpret_cast<f32x4*>(C + static_cast<size_t>(m) * NO + n) = acc[t][i] * (1.f / sm[t]);
+                }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+        const int n = n0 + wn * 64 + t * 16 + 4 * kg;
+        if (n >= NO) continue;
+#pragma unroll
         for (int i = 0; i < TX; ++i) {
             const int m = m0 + wm * 32 + i * 16 + r16;
-            if (m < M) *reinterpret_cast<f32x4*>(C + static_cast<size_t>(m) * NO + n) = acc[t][i] + bv;
+            if (m < M) *reinterpret_cast<f32x4*>(C + static_cast<size_t>(m) * NO + n) = acc[t][i];
         }
     }
 }
 
-template <typename T, int STAGES, bool DUAL>
+template <typename T, int STAGES, bool DUAL, bool FIN>
 int go_pair(PairParams p, hipStream_t stream) {
     constexpr size_t lds = static_cast<size_t>(STAGES) * ((DUAL ? 2 : 1) * 64 + 128) * 64;
-    if (lds > 65536) {
-        static std::atomic<uint64_t> done{0};
-        const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(gemm_pair_kernel<T, STAGES, DUAL>),
-                                                  static_cast<int>(lds), done);
-        if (attr != hipSuccess)
-            return set_error(-3, "layer prologue: LDS size attribute refused: %s", hipGetErrorString(attr));
-    }
+    static_assert(lds <= 65536, "within the default dynamic LDS limit");
     p.per_xcd = (p.tiles + kXcds - 1) / kXcds;
-    hipLaunchKernelGGL((gemm_pair_kernel<T, STAGES, DUAL>), dim3(static_cast<unsigned>(p.per_xcd * kXcds)),
+    hipLaunchKernelGGL((gemm_pair_kernel<T, STAGES, DUAL, FIN>), dim3(static_cast<unsigned>(p.per_xcd * kXcds)),
                        dim3(256), lds, stream, p);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : set_error(-3, "layer prologue launch failed: %s", hipGetErrorString(e));
 }
 
 // 4 stages (64 KB with two operands): C = 1024, 600 rows, 3072 columns in 240 tiles: 20.0 µs for the prologue with
-// its finalize, against 21.3 with 8 stages and 45.9 for two launches of 64 x 64 register-operand tiles (graph-timed).
-template <typename T>
-int launch_pair_t(PairParams p, hipStream_t stream) {
-    return p.x2 != nullptr ? go_pair<T, 4, true>(p, stream) : go_pair<T, 4, false>(p, stream);
+// a separate finalize, against 21.3 with 8 stages and 45.9 for two launches of 64 x 64 register-operand tiles
+// (graph-timed).
+template <typename T, bool FIN>
+int launch_pair_t(const PairParams& p, hipStream_t stream) {
+    return p.x2 != nullptr ? go_pair<T, 4, true, FIN>(p, stream) : go_pair<T, 4, false, FIN>(p, stream);
 }
 
 }  // namespace
 
 int launch_proj_f32_pair(int dtype, const void* x, const void* x2, const void* w0, const void* b0, float* c0,
                          int64_t no0, const void* w1, const void* b1, float* c1, int64_t no1, int64_t M, int64_t K,
-                         hipStream_t stream) {
+                         hipStream_t stream, const LayerArgs* fin, const Geom* g) {
     const uintptr_t a16 = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(x2) |
                           reinterpret_cast<uintptr_t>(w0) | reinterpret_cast<uintptr_t>(w1) |
                           reinterpret_cast<uintptr_t>(c0) | reinterpret_cast<uintptr_t>(c1);
@@ -619,13 +691,21 @@ int launch_proj_f32_pair(int dtype, const void* x, const void* x2, const void* w
         M * no0 >= lim || M * no1 >= lim)
         return 1;
     PairParams p{x, x2, {w0, w1}, {b0, b1}, {c0, c1}, static_cast<int>(M), static_cast<int>(K),
-                 {static_cast<int>(no0), static_cast<int>(no1)}, 0, 0, 0, 0};
+                 {static_cast<int>(no0), static_cast<int>(no1)}, 0, 0, 0, 0, LayerArgs{}, Geom{}};
     p.mt = static_cast<int>((M + 63) / 64);
     p.nt0 = static_cast<int>((no0 + 127) / 128);
     const int64_t tiles = static_cast<int64_t>(p.mt) * (p.nt0 + (no1 + 127) / 128);
     if (tiles >= lim / kXcds) return 1;
     p.tiles = static_cast<int>(tiles);
-    return dtype == kF16 ? launch_pair_t<f16>(p, stream) : launch_pair_t<bf16>(p, stream);
+    const int LP = g != nullptr ? g->LP : 0;
+    if (fin != nullptr && g != nullptr && g->P > 0 && LP >= 4 && LP <= 64 && (LP & (LP - 1)) == 0 &&
+        no1 == static_cast<int64_t>(g->H) * LP && no0 == 2 * no1 && M == static_cast<int64_t>(g->B) * g->Q) {
+        p.la = *fin;
+        p.g = *g;
+        const int rc = dtype == kF16 ? launch_pair_t<f16, true>(p, stream) : launch_pair_t<bf16, true>(p, stream);
+        return rc == 0 ? 2 : rc;
+    }
+    return dtype == kF16 ? launch_pair_t<f16, false>(p, stream) : launch_pair_t<bf16, false>(p, stream);
 }
 
 bool gemm_persistent_fits(int dtype, const GemmParams& p) {

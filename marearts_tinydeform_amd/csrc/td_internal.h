@@ -85,10 +85,13 @@ int launch_proj_f32(int dtype, const void* a, const void* a2, const void* w, con
                     int64_t K, int64_t NO, hipStream_t stream);
 // Two such projections of the same rows in one launch (td_gemm_dma.hip): c_j[M, no_j] = x . w_j^T (+ x2 . w_j^T)
 // + b_j, j = 0, 1; x2, b0 and b1 may be null. 16-bit operands, K % 64 == 0, no_j % 4 == 0, 16-byte aligned x, x2,
-// w_j and c_j, 8-byte aligned biases. Returns 1, launching nothing, when the operands do not qualify.
+// w_j and c_j, 8-byte aligned biases. With fin and g (the layer prologue: c_0 = raw offsets, c_1 = raw logits) and
+// L * P a power of two from 4 to 64, the kernel also finalizes them into locations and softmax weights, as
+// layer_finalize_kernel does, and returns 2. Returns 0 when it launched the raw projections, and 1, launching
+// nothing, when the operands do not qualify.
 int launch_proj_f32_pair(int dtype, const void* x, const void* x2, const void* w0, const void* b0, float* c0,
                          int64_t no0, const void* w1, const void* b1, float* c1, int64_t no1, int64_t M, int64_t K,
-                         hipStream_t stream);
+                         hipStream_t stream, const LayerArgs* fin = nullptr, const Geom* g = nullptr);
 
 int launch_zero(void* out, int64_t bytes, hipStream_t stream);
 

@@ -114,8 +114,9 @@ int launch_prologue_gemm(const LayerArgs& la, const Geom& g, hipStream_t stream)
     const int64_t M = static_cast<int64_t>(g.B) * g.Q, NO = static_cast<int64_t>(g.H) * g.LP;
     const int dt = std::is_same<T, float>::value ? kF32 : std::is_same<T, f16>::value ? kF16 : kBF16;
     int rc = launch_proj_f32_pair(dt, la.query, la.pos, la.off_w, la.off_b, static_cast<float*>(la.loc_out), 2 * NO,
-                                  la.aw_w, la.aw_b, static_cast<float*>(la.attn_out), NO, M, la.Cq, stream);
+                                  la.aw_w, la.aw_b, static_cast<float*>(la.attn_out), NO, M, la.Cq, stream, &la, &g);
     if (rc < 0) return rc;
+    if (rc == 2) return 0;  // finalized in the projections' epilogue
     if (rc == 0) return finalize_prologue<T>(la, g, stream);
     rc = launch_proj_f32(dt, la.query, la.pos, la.off_w, la.off_b, static_cast<float*>(la.loc_out), M, la.Cq, 2 * NO,
                          stream);
