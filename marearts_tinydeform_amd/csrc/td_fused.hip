@@ -151,6 +151,38 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     }
     __syncthreads();
 
+    // One workgroup per CU (12 wavefronts, 6 loads in flight: the balanced-slice shapes of 16-bit problems) has
+    // registers to spare, so each projection job's first two W_h chunks and the epilogue's bias value are requested
+    // here, ahead of the gather's loads: they land while the gather runs instead of after it. (Requested at kernel
+    // start instead, with the location loads, every CU asks for its W_h at once and the locations queue behind:
+    // slower.) The phase-3 loop and the epilogue of these kernels are written apart from the others' (kPre below),
+    // so that the other instantiations compile exactly as before.
+    constexpr bool kPre = WAVES == 12 && NB == 6 && !LAYER;
+    constexpr int KCH = sizeof(T) == 2 ? 32 : 16;  // K per MFMA chunk of a job
+    u32x4 wpre[2][kAllN];
+    T bpre = static_cast<T>(0.f);
+    if constexpr (kPre) {
+        const int pw = tid / kWave, pn16 = tid & 15, pkg = (tid & (kWave - 1)) >> 4;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int nt = 0; nt < kAllN; ++nt) wpre[c][nt] = u32x4{0u, 0u, 0u, 0u};
+        if (p.alln && pw < p.KS) {  // job pw's chunks kb and kb + 1, as phase 3 reads them
+            const int nk = (C + KCH - 1) / KCH;
+            const int kb = pw * nk / p.KS, ke = (pw + 1) * nk / p.KS;
+            const T* wr0 = w + (static_cast<size_t>(h) * D + pn16) * C;
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const int k = (kb + c) * KCH + pkg * (KCH / 4);
+#pragma unroll
+                for (int nt = 0; nt < kAllN; ++nt)
+                    if (kb + c < ke && k < C && nt < NTILE && nt * 16 + pn16 < D)
+                        wpre[c][nt] = *reinterpret_cast<const u32x4*>(wr0 + static_cast<size_t>(nt) * 16 * C + k);
+            }
+        }
+        if (bias != nullptr && tid < QT * D) bpre = bias[static_cast<size_t>(h) * D + tid % D];
+    }
+
     // phase 2: gather C-wide rows, float32 accumulation
     const int GS = CV * SG;
     for (int it = tid; it < QT * GS; it += NTH) {
@@ -202,10 +234,95 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
             inv_sc = ldexpf(1.f, e - 14);
         }
     }
-    if (p.alln) {
+    if (kPre && p.alln) {
+        // as the p.alln block below, with the job's first two W_h chunks taken from wpre
+        const int nk = (C + KCH - 1) / KCH;
+        for (int ks = wave; ks < p.KS; ks += WAVES) {
+            const int kb = ks * nk / p.KS, ke = (ks + 1) * nk / p.KS;
+            f32x4 acc[kAllN];
+            bool dv[kAllN];
+#pragma unroll
+            for (int nt = 0; nt < kAllN; ++nt) {
+                acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                dv[nt] = nt < NTILE && nt * 16 + n16 < D;
+            }
+            const T* wr0 = w + (static_cast<size_t>(h) * D + n16) * C;
+            auto chunk = [&](int kk, const u32x4(&braw)[kAllN]) {
+                const int k = kk * KCH + kg * (KCH / 4);
+                const bool kv = k < C;
+                if constexpr (sizeof(T) == 2) {
+                    using M = MfmaOp<T>;
+                    using frag = typename M::frag;
+                    f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
+                    if (av && kv) {
+                        a0 = *reinterpret_cast<const f32x4*>(ga + k);
+                        a1 = *reinterpret_cast<const f32x4*>(ga + k + 4);
+                        if (two) {
+                            a0 += *reinterpret_cast<const f32x4*>(ga + QT * GP + k);
+                            a1 += *reinterpret_cast<const f32x4*>(ga + QT * GP + k + 4);
+                        }
+                        a0 *= sc;
+                        a1 *= sc;
+                    }
+                    frag hi, lo;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const T x0 = static_cast<T>(a0[i]), x1 = static_cast<T>(a1[i]);
+                        hi[i] = x0;
+                        hi[4 + i] = x1;
+                        lo[i] = static_cast<T>(a0[i] - static_cast<float>(x0));
+                        lo[4 + i] = static_cast<T>(a1[i] - static_cast<float>(x1));
+                    }
+#pragma unroll
+                    for (int nt = 0; nt < kAllN; ++nt) {
+                        if (nt >= NTILE) break;
+                        const frag bf = __builtin_bit_cast(frag, braw[nt]);
+                        acc[nt] = M::mma(hi, bf, acc[nt]);
+                        acc[nt] = M::mma(lo, bf, acc[nt]);
+                    }
+                } else {
+                    f32x4 aq = {0.f, 0.f, 0.f, 0.f};
+                    if (av && kv) {
+                        aq = *reinterpret_cast<const f32x4*>(ga + k);
+                        if (two) aq += *reinterpret_cast<const f32x4*>(ga + QT * GP + k);
+                    }
+#pragma unroll
+                    for (int nt = 0; nt < kAllN; ++nt) {
+                        if (nt >= NTILE) break;
+                        const f32x4 bq = __builtin_bit_cast(f32x4, braw[nt]);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[j], bq[j], acc[nt], 0, 0, 0);
+                    }
+                }
+            };
+            int kk = kb;
+            if (ks == wave) {  // the chunks requested before the gather
+                if (kk < ke) chunk(kk++, wpre[0]);
+                if (kk < ke) chunk(kk++, wpre[1]);
+            }
+            for (; kk < ke; ++kk) {
+                const int k = kk * KCH + kg * (KCH / 4);
+                u32x4 braw[kAllN];
+#pragma unroll
+                for (int nt = 0; nt < kAllN; ++nt) {
+                    braw[nt] = u32x4{0u, 0u, 0u, 0u};
+                    if (dv[nt] && k < C)
+                        braw[nt] = *reinterpret_cast<const u32x4*>(wr0 + static_cast<size_t>(nt) * 16 * C + k);
+                }
+                chunk(kk, braw);
+            }
+            float* pp = part + ks * 16 * PW;
+#pragma unroll
+            for (int nt = 0; nt < kAllN; ++nt) {
+                if (nt >= NTILE) break;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pp[(4 * kg + i) * PW + nt * 16 + n16] = acc[nt][i];
+            }
+        }
+    } else if (p.alln) {
         // every N tile in each job (D <= 16 kAllN): job = K slice, and g's chunk is read (and, in 16 bits, split into
         // hi + lo) once for all N tiles
-        constexpr int KCH = sizeof(T) == 2 ? 32 : 16;  // K per MFMA chunk
         const int nk = (C + KCH - 1) / KCH;
         for (int ks = wave; ks < p.KS; ks += WAVES) {
             const int kb = ks * nk / p.KS, ke = (ks + 1) * nk / p.KS;
@@ -356,6 +473,21 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     __syncthreads();
 
     // epilogue: sum the K slices, add bias * sum of in-map weights, round once
+    if constexpr (kPre) {
+        auto emit = [&](int o, T bv) {
+            const int r = o / D, d = o - r * D;
+            if (r >= nrows) return;
+            float v = part[r * PW + d];
+            for (int ks = 1; ks < p.KS; ++ks) v += part[(ks * 16 + r) * PW + d];
+            v *= inv_sc;
+            if (bias != nullptr) v = fmaf(cvt<float>(bv), two ? wsum[r] + wsum[16 + r] : wsum[r], v);
+            out[(static_cast<size_t>(rbase + r) * g.H + h) * D + d] = static_cast<T>(v);
+        };
+        if (tid < QT * D) emit(tid, bpre);  // the bias value requested before the gather
+        for (int o = tid + NTH; o < QT * D; o += NTH)
+            emit(o, bias != nullptr ? bias[static_cast<size_t>(h) * D + o % D] : static_cast<T>(0.f));
+        return;
+    }
     for (int o = tid; o < QT * D; o += NTH) {
         const int r = o / D, d = o - r * D;
         if (r >= nrows) continue;
