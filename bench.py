@@ -7,8 +7,8 @@ in HBM. Like the reference's bench (bench/bench.py:40-61) the calls are captured
 overhead is excluded: W warm-up steps (one graph replay), then a graph of EXACTLY K steps replayed 7 times, each
 replay bracketed by torch.cuda.synchronize() and timed with events on the replay stream; the best replay gives
 the µs per call, as the reference takes the best of 7 replays of its 100-call graph. A replay's fixed cost (about
-10 µs: the graph launch and the timing events) is inside the timed region, so a short graph reads higher per call
-than a long one (0.5 µs per call at 20 calls).
+10-17 µs: the graph launch and the timing events) is inside the timed region, so a short graph reads higher per call
+than a long one (about 0.85 µs per call at 20 calls).
 
 Prints diagnostics on stderr and ONE JSON line on stdout: value = µs per layer call (auto mode), with per-mode
 times, the roofline of the dominant kernel (algorithmic bytes per launch / its average launch duration, measured
@@ -67,9 +67,10 @@ def log(*a):
 def graph_time_us(fn, steps, warmup, replays=7):
     """µs per call: W warm-up calls (eager on a side stream, then one replay of a W-call graph), then the best of
     `replays` timed replays of a graph of exactly `steps` calls, events recorded on the replay stream (the
-    reference's method, bench/bench.py:40-61). Each timed replay carries a fixed cost of about 10 µs on MI355X
-    (two timing events with nothing between them read 4.2 µs; a one-call graph 18.9 µs against 8.6 µs per further
-    call at the headline), which a short graph spreads over few calls: 0.5 µs per call at 20 calls, 0.1 at 100."""
+    reference's method, bench/bench.py:40-61). Each timed replay carries a fixed cost of 10-17 µs on MI355X
+    (two timing events with nothing between them read 4.2 µs; a one-call graph 26.9 µs against 8.0 µs per further
+    call at the headline), which a short graph spreads over few calls: about 0.85 µs per call at 20 calls, 0.2 at
+    100."""
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
@@ -601,8 +602,8 @@ def main():
         'config': {'workload': args.workload, 'B': B, 'Q': Q, 'N': N, 'C': C, 'H': H, 'D': D, 'L': L, 'P': P,
                    'mode': 'auto'},
         'modes_us': {k: round(v, 2) for k, v in times.items()},
-        'timing': f'best of 7 replays of a {args.steps}-call graph; each replay also carries about 10 µs of fixed '
-                  f'cost (graph launch and the two timing events), {10.0 / args.steps:.2f} µs per call here',
+        'timing': f'best of 7 replays of a {args.steps}-call graph; each replay also carries 10-17 µs of fixed '
+                  f'cost (graph launch and the two timing events), up to {17.0 / args.steps:.2f} µs per call here',
         'auto_pick': pick,
         'kernels_us': {k: round(v, 2) for k, v in kern.items()},
         'queries_per_s': round(B * Q / (times['auto'] * 1e-6)),
