@@ -20,6 +20,25 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+// n / d for 0 <= n < 2^31 and 1 <= d < 2^31 by a multiply-high, an add and a shift (Granlund and Montgomery,
+// "Division by invariant integers using multiplication", PLDI 1994, the round-up form): with l = ceil(log2 d) and
+// mul = floor(2^32 (2^l - d) / d) + 1, n / d = (mulhi(n, mul) + n) >> l; mul < 2^32, and the sum stays below 2^32
+// because mulhi(n, mul) < n < 2^31.
+struct FastDiv {
+    uint32_t mul = 1, shift = 0;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t l = 0;
+    while ((uint64_t{1} << l) < d) ++l;
+    FastDiv f;
+    f.mul = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1);
+    f.shift = l;
+    return f;
+}
+__device__ __forceinline__ uint32_t fast_div(const FastDiv& f, uint32_t n) {
+    return (__umulhi(n, f.mul) + n) >> f.shift;
+}
+
 // Accumulation type: float for float/half/bfloat16, double for double.
 template <typename T>
 struct AccOf {
@@ -164,8 +183,7 @@ __device__ __forceinline__ void corners_at(A lx, A ly, A w, int l, const Geom& g
 // accumulation type A when g.loc_acc is set).
 template <typename T, typename A, bool GENERAL>
 __device__ __forceinline__ void corner4(const T* __restrict__ loc, const T* __restrict__ attn, const Geom& g,
-                                        int64_t row, int j, Corner<A>* out) {
-    const int l = GENERAL ? level_of(g, j) : j / g.P;
+                                        int64_t row, int j, int l, Corner<A>* out) {
     const int64_t idx = row * g.LP + j;
     A lx, ly, w;
     if (GENERAL && g.loc_acc) {
@@ -179,6 +197,11 @@ __device__ __forceinline__ void corner4(const T* __restrict__ loc, const T* __re
         w = cvt<A>(attn[idx]);
     }
     corners_at<A, GENERAL>(lx, ly, w, l, g, row, out);
+}
+template <typename T, typename A, bool GENERAL>
+__device__ __forceinline__ void corner4(const T* __restrict__ loc, const T* __restrict__ attn, const Geom& g,
+                                        int64_t row, int j, Corner<A>* out) {
+    corner4<T, A, GENERAL>(loc, attn, g, row, j, GENERAL ? level_of(g, j) : j / g.P, out);
 }
 
 // ---- vector loads: Bytes-wide raw loads unpacked to float ------------------------------------------------

@@ -6,25 +6,6 @@
 
 namespace td {
 
-// n / d for 0 <= n < 2^31 and 1 <= d < 2^31 by a multiply-high, an add and a shift (Granlund and Montgomery,
-// "Division by invariant integers using multiplication", PLDI 1994, the round-up form): with l = ceil(log2 d) and
-// mul = floor(2^32 (2^l - d) / d) + 1, n / d = (mulhi(n, mul) + n) >> l; mul < 2^32, and the sum stays below 2^32
-// because mulhi(n, mul) < n < 2^31.
-struct FastDiv {
-    uint32_t mul = 1, shift = 0;
-};
-inline FastDiv make_fastdiv(uint32_t d) {
-    uint32_t l = 0;
-    while ((uint64_t{1} << l) < d) ++l;
-    FastDiv f;
-    f.mul = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1);
-    f.shift = l;
-    return f;
-}
-__device__ __forceinline__ uint32_t fast_div(const FastDiv& f, uint32_t n) {
-    return (__umulhi(n, f.mul) + n) >> f.shift;
-}
-
 struct GemmParams {
     const void* a;
     const void* w;
