@@ -42,6 +42,8 @@ struct FusedParams {
     // balanced slices (slices > 0): B * Q = slices * slice_rows + slice_extra rows per head
     int slices = 0, slice_rows = 0, slice_extra = 0;
     int alln = 0;  // projection jobs take every N tile (D <= 64), one K slice each
+    // divisions by L * P, P, the lanes of a row (CV * SG), CV, Q and D by multiply-high (exact below 2^31)
+    FastDiv d_lp, d_p, d_gs, d_cv, d_q, d_d;
 };
 
 // Workgroup index -> work unit (b, query tile, h) with heads fastest. Workgroups are dealt to the 8 XCDs
@@ -133,16 +135,18 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     // phase 1: corner table
     if (tid == 0) *gmax = 0u;
     for (int i = tid; i < QT * LP; i += NTH) {
-        const int r = i / LP, j = i - r * LP;
+        const int r = static_cast<int>(fast_div(p.d_lp, static_cast<uint32_t>(i))), j = i - r * LP;
         Corner<float>* c4 = cw + r * S + 4 * j;
         if (r < nrows) {
             const int64_t row = static_cast<int64_t>(rbase + r) * g.H + h;
             if constexpr (LAYER) {
                 float lx, ly, a;
                 prologue_sample<T, float>(p.lay, g, bimg, q0 + r, h, r, j, pro, PP, rstat, lx, ly, a);
-                corners_at<float, GENERAL>(lx, ly, a, j / g.P, g, row, c4);
+                corners_at<float, GENERAL>(lx, ly, a, static_cast<int>(fast_div(p.d_p, j)), g, row, c4);
+            } else if constexpr (GENERAL) {
+                corner4<T, float, true>(loc, attn, g, row, j, c4);
             } else {
-                corner4<T, float, GENERAL>(loc, attn, g, row, j, c4);
+                corner4<T, float, false>(loc, attn, g, row, j, static_cast<int>(fast_div(p.d_p, j)), c4);
             }
         } else {
 #pragma unroll
@@ -180,14 +184,17 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
                         wpre[c][nt] = *reinterpret_cast<const u32x4*>(wr0 + static_cast<size_t>(nt) * 16 * C + k);
             }
         }
-        if (bias != nullptr && tid < QT * D) bpre = bias[static_cast<size_t>(h) * D + tid % D];
+        if (bias != nullptr && tid < QT * D)
+            bpre = bias[static_cast<size_t>(h) * D + tid - static_cast<int>(fast_div(p.d_d, tid)) * D];
     }
 
     // phase 2: gather C-wide rows, float32 accumulation
     const int GS = CV * SG;
     for (int it = tid; it < QT * GS; it += NTH) {
-        const int r = it / GS, rem = it - r * GS, sg = rem / CV, ch = rem - sg * CV;
-        const T* mb = mem + static_cast<size_t>(r < nrows ? (rbase + r) / g.Q : 0) * g.N * C;
+        const int r = static_cast<int>(fast_div(p.d_gs, static_cast<uint32_t>(it))), rem = it - r * GS;
+        const int sg = static_cast<int>(fast_div(p.d_cv, static_cast<uint32_t>(rem))), ch = rem - sg * CV;
+        const T* mb =
+            mem + static_cast<size_t>(r < nrows ? fast_div(p.d_q, static_cast<uint32_t>(rbase + r)) : 0) * g.N * C;
         float acc[V];
 #pragma unroll
         for (int i = 0; i < V; ++i) acc[i] = 0.f;
@@ -475,7 +482,7 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     // epilogue: sum the K slices, add bias * sum of in-map weights, round once
     if constexpr (kPre) {
         auto emit = [&](int o, T bv) {
-            const int r = o / D, d = o - r * D;
+            const int r = static_cast<int>(fast_div(p.d_d, static_cast<uint32_t>(o))), d = o - r * D;
             if (r >= nrows) return;
             float v = part[r * PW + d];
             for (int ks = 1; ks < p.KS; ++ks) v += part[(ks * 16 + r) * PW + d];
@@ -485,11 +492,13 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
         };
         if (tid < QT * D) emit(tid, bpre);  // the bias value requested before the gather
         for (int o = tid + NTH; o < QT * D; o += NTH)
-            emit(o, bias != nullptr ? bias[static_cast<size_t>(h) * D + o % D] : static_cast<T>(0.f));
+            emit(o, bias != nullptr
+                        ? bias[static_cast<size_t>(h) * D + o - static_cast<int>(fast_div(p.d_d, o)) * D]
+                        : static_cast<T>(0.f));
         return;
     }
     for (int o = tid; o < QT * D; o += NTH) {
-        const int r = o / D, d = o - r * D;
+        const int r = static_cast<int>(fast_div(p.d_d, static_cast<uint32_t>(o))), d = o - r * D;
         if (r >= nrows) continue;
         float v = part[r * PW + d];
         for (int ks = 1; ks < p.KS; ++ks) v += part[(ks * 16 + r) * PW + d];
@@ -772,6 +781,12 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
                 p.QT = qt;
                 p.SG = sg;
                 p.KS = ks;
+                if (LP > 0) p.d_lp = make_fastdiv(static_cast<uint32_t>(LP));
+                if (g.P > 0) p.d_p = make_fastdiv(static_cast<uint32_t>(g.P));
+                p.d_gs = make_fastdiv(static_cast<uint32_t>(CV * sg));
+                p.d_cv = make_fastdiv(static_cast<uint32_t>(CV));
+                if (g.Q > 0) p.d_q = make_fastdiv(static_cast<uint32_t>(g.Q));
+                if (D > 0) p.d_d = make_fastdiv(static_cast<uint32_t>(D));
                 p.alln = alln ? 1 : 0;
                 p.qtiles = (g.Q + qt - 1) / qt;
                 if (slices > 0) {
