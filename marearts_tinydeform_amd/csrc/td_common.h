@@ -277,22 +277,29 @@ struct VecIO<bf16, V> {
 // Weighted sum of gathered rows: acc[0..V) += w_s * row(tok_s)[0..V) for corners s = first, first + step, ...
 // below S, where row(t) = col + t * stride; ws += w_s. Loads are issued NB at a time before any of them is
 // consumed, so NB row reads per lane are in flight together. Corners outside the map (tok < 0) and the padding
-// slots of the last batch read row 0 (always valid) and contribute exactly 0.
-template <typename T, int V, int NB>
+// slots of a last, partial batch read row 0 (always valid) and contribute exactly 0; full batches skip the slot
+// check. OFF32 (callers that know N * stride < 2^32 and N, stride < 2^24): the row offset is one 24-bit multiply
+// instead of a 64-bit one (the gather loops are issue-bound, and the 64-bit product takes three quarter-rate
+// multiplies).
+template <typename T, int V, int NB, bool OFF32 = false>
 __device__ __forceinline__ void gather_sum(const Corner<float>* __restrict__ cr, int S, int first, int step,
                                            const T* __restrict__ col, size_t stride, float* acc, float& ws) {
     using IO = VecIO<T, V>;
-    for (int s0 = first; s0 < S; s0 += step * NB) {
+    auto batch = [&](int s0, bool check) {
         typename IO::raw_t raw[NB];
         float w[NB];
         bool in[NB];
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
             const int s = s0 + u * step;
-            const Corner<float> c = s < S ? cr[s] : Corner<float>{-1, 0.f};
+            const Corner<float> c = !check || s < S ? cr[s] : Corner<float>{-1, 0.f};
             w[u] = c.w;
             in[u] = c.tok >= 0;
-            raw[u] = IO::load(col + static_cast<size_t>(in[u] ? c.tok : 0) * stride);
+            const int t = in[u] ? c.tok : 0;
+            if constexpr (OFF32)
+                raw[u] = IO::load(col + __umul24(static_cast<unsigned>(t), static_cast<unsigned>(stride)));
+            else
+                raw[u] = IO::load(col + static_cast<size_t>(t) * stride);
         }
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
@@ -303,7 +310,10 @@ __device__ __forceinline__ void gather_sum(const Corner<float>* __restrict__ cr,
 #pragma unroll
             for (int i = 0; i < V; ++i) acc[i] = fmaf(w[u], v[i], acc[i]);
         }
-    }
+    };
+    int s0 = first;
+    for (; s0 + step * (NB - 1) < S; s0 += step * NB) batch(s0, false);
+    if (s0 < S) batch(s0, true);
 }
 
 // ---- cross-lane ----------------------------------------------------------------------------------------

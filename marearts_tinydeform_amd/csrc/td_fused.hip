@@ -44,6 +44,7 @@ struct FusedParams {
     int alln = 0;  // projection jobs take every N tile (D <= 64), one K slice each
     // divisions by L * P, P, the lanes of a row (CV * SG), CV, Q and D by multiply-high (exact below 2^31)
     FastDiv d_lp, d_p, d_gs, d_cv, d_q, d_d;
+    int off32 = 0;  // N * C < 2^32, both below 2^24: 32-bit row offsets (gather_sum)
 };
 
 // Workgroup index -> work unit (b, query tile, h) with heads fastest. Workgroups are dealt to the 8 XCDs
@@ -199,7 +200,10 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
 #pragma unroll
         for (int i = 0; i < V; ++i) acc[i] = 0.f;
         float ws = 0.f;
-        gather_sum<T, V, NB>(cw + r * S, S, sg, SG, mb + ch * V, static_cast<size_t>(C), acc, ws);
+        if (p.off32)
+            gather_sum<T, V, NB, true>(cw + r * S, S, sg, SG, mb + ch * V, static_cast<size_t>(C), acc, ws);
+        else
+            gather_sum<T, V, NB, false>(cw + r * S, S, sg, SG, mb + ch * V, static_cast<size_t>(C), acc, ws);
         for (int m = CV; m < GS && m < kWave; m <<= 1) {
 #pragma unroll
             for (int i = 0; i < V; ++i) acc[i] += xor_lane(acc[i], m);
@@ -787,6 +791,8 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
                 p.d_cv = make_fastdiv(static_cast<uint32_t>(CV));
                 if (g.Q > 0) p.d_q = make_fastdiv(static_cast<uint32_t>(g.Q));
                 if (D > 0) p.d_d = make_fastdiv(static_cast<uint32_t>(D));
+                p.off32 = g.N < (1 << 24) && C < (1 << 24) &&
+                                  static_cast<int64_t>(g.N) * C < (int64_t{1} << 32) ? 1 : 0;
                 p.alln = alln ? 1 : 0;
                 p.qtiles = (g.Q + qt - 1) / qt;
                 if (slices > 0) {

@@ -25,6 +25,7 @@ struct SampleParams {
     // (B * Q * H < 2^31) by H, Q and Q * H, instead of the 64-bit division routine (the kernel is issue-bound)
     FastDiv d_lp, d_p, d_gs, d_dv, d_h, d_q, d_qh;
     int fast = 0;
+    int off32 = 0;  // N * (token stride) < 2^32, both below 2^24: 32-bit row offsets (gather_sum)
 };
 
 // Row (b, q, h) of the i-th row in the order the workgroups take them: the output's own order, or with hq (b, h, q),
@@ -103,7 +104,10 @@ __global__ __launch_bounds__(WAVES* kWave) void sample_kernel(SampleParams p) {
 #pragma unroll
         for (int i = 0; i < V; ++i) acc[i] = 0.f;
         float ws = 0.f;
-        gather_sum<T, V, NB>(cw + r * S, S, sg, SG, base, stride, acc, ws);
+        if (p.off32)
+            gather_sum<T, V, NB, true>(cw + r * S, S, sg, SG, base, stride, acc, ws);
+        else
+            gather_sum<T, V, NB, false>(cw + r * S, S, sg, SG, base, stride, acc, ws);
         for (int m = DV; m < GS; m <<= 1) {
 #pragma unroll
             for (int i = 0; i < V; ++i) acc[i] += xor_lane(acc[i], m);
@@ -242,6 +246,8 @@ int launch_sample_t(SampleParams p, hipStream_t stream, const SampleTune& tune) 
     p.d_gs = make_fastdiv(static_cast<uint32_t>(GS));
     p.d_dv = make_fastdiv(static_cast<uint32_t>(DV));
     p.fast = p.rows < (int64_t{1} << 31) && g.H > 0 && g.Q > 0 ? 1 : 0;
+    const int64_t tstride = g.value_hm ? D : static_cast<int64_t>(g.H) * D;
+    p.off32 = g.N < (1 << 24) && tstride < (1 << 24) && static_cast<int64_t>(g.N) * tstride < (int64_t{1} << 32) ? 1 : 0;
     if (p.fast) {
         p.d_h = make_fastdiv(static_cast<uint32_t>(g.H));
         p.d_q = make_fastdiv(static_cast<uint32_t>(g.Q));
