@@ -123,6 +123,14 @@ struct Corner {
 // GENERAL = false compiles the reference's case only (P points on every level, bilinear, no mask); kernels are
 // instantiated both ways and the launchers pick GENERAL = true only when a mask, per-level point counts, the
 // discrete method or accumulation-type locations are in use, so the common path carries none of their cost.
+// What a corner-table entry holds for token t: the token (sb = 0; -1 when outside), or its row's byte offset
+// t * sb, for the buffer-load gathers (gather_sum_buf), with kOutside, past any buffer of under 2 GB, when outside.
+constexpr int kOutside = static_cast<int>(0x80000000u);
+__device__ __forceinline__ int corner_ref(bool in, int64_t t, int sb) {
+    if (sb == 0) return in ? static_cast<int>(t) : -1;
+    return in ? static_cast<int>(t) * sb : kOutside;
+}
+
 struct LevelGeom {
     int hl, wl;   // height, width
     int64_t st;   // first token
@@ -135,7 +143,7 @@ __device__ __forceinline__ LevelGeom level_geom(const Geom& g, int l) {
 // load it once).
 template <typename A, bool GENERAL>
 __device__ __forceinline__ void corners_lv(A lx, A ly, A w, const LevelGeom& lg, const Geom& g, int64_t row,
-                                           Corner<A>* out) {
+                                           Corner<A>* out, int sb = 0) {
     const int hl = lg.hl, wl = lg.wl;
     const int64_t st = lg.st;
     if (GENERAL && g.discrete) {
@@ -147,10 +155,10 @@ __device__ __forceinline__ void corners_lv(A lx, A ly, A w, const LevelGeom& lg,
         const int64_t t = st + static_cast<int64_t>(yi) * wl + xi;
         bool in = wl > 0 && hl > 0 && t >= 0 && t < g.N;
         if (in && g.mask != nullptr) in = g.mask[(row / (static_cast<int64_t>(g.Q) * g.H)) * g.N + t] == 0;
-        out[0].tok = in ? static_cast<int>(t) : -1;
+        out[0].tok = corner_ref(in, t, sb);
         out[0].w = in ? w : static_cast<A>(0);
 #pragma unroll
-        for (int k = 1; k < 4; ++k) out[k] = Corner<A>{-1, static_cast<A>(0)};
+        for (int k = 1; k < 4; ++k) out[k] = Corner<A>{corner_ref(false, 0, sb), static_cast<A>(0)};
         return;
     }
     A x = lx * static_cast<A>(wl) - static_cast<A>(0.5);
@@ -167,15 +175,16 @@ __device__ __forceinline__ void corners_lv(A lx, A ly, A w, const LevelGeom& lg,
         const int64_t t = st + static_cast<int64_t>(yi) * wl + xi;
         bool in = xi >= 0 && xi < wl && yi >= 0 && yi < hl && t >= 0 && t < g.N;
         if (GENERAL && in && g.mask != nullptr) in = g.mask[(row / (static_cast<int64_t>(g.Q) * g.H)) * g.N + t] == 0;
-        out[k].tok = in ? static_cast<int>(t) : -1;
+        out[k].tok = corner_ref(in, t, sb);
         out[k].w = in ? w * (dx ? fx : static_cast<A>(1) - fx) * (dy ? fy : static_cast<A>(1) - fy)
                       : static_cast<A>(0);
     }
 }
 
 template <typename A, bool GENERAL>
-__device__ __forceinline__ void corners_at(A lx, A ly, A w, int l, const Geom& g, int64_t row, Corner<A>* out) {
-    corners_lv<A, GENERAL>(lx, ly, w, level_geom(g, l), g, row, out);
+__device__ __forceinline__ void corners_at(A lx, A ly, A w, int l, const Geom& g, int64_t row, Corner<A>* out,
+                                           int sb = 0) {
+    corners_lv<A, GENERAL>(lx, ly, w, level_geom(g, l), g, row, out, sb);
 }
 
 // The corners of sample j (j = l * P + p, or the running index over per-level point counts) of row `row`, with the
@@ -183,7 +192,7 @@ __device__ __forceinline__ void corners_at(A lx, A ly, A w, int l, const Geom& g
 // accumulation type A when g.loc_acc is set).
 template <typename T, typename A, bool GENERAL>
 __device__ __forceinline__ void corner4(const T* __restrict__ loc, const T* __restrict__ attn, const Geom& g,
-                                        int64_t row, int j, int l, Corner<A>* out) {
+                                        int64_t row, int j, int l, Corner<A>* out, int sb = 0) {
     const int64_t idx = row * g.LP + j;
     A lx, ly, w;
     if (GENERAL && g.loc_acc) {
@@ -196,12 +205,12 @@ __device__ __forceinline__ void corner4(const T* __restrict__ loc, const T* __re
         ly = cvt<A>(loc[2 * idx + 1]);
         w = cvt<A>(attn[idx]);
     }
-    corners_at<A, GENERAL>(lx, ly, w, l, g, row, out);
+    corners_at<A, GENERAL>(lx, ly, w, l, g, row, out, sb);
 }
 template <typename T, typename A, bool GENERAL>
 __device__ __forceinline__ void corner4(const T* __restrict__ loc, const T* __restrict__ attn, const Geom& g,
-                                        int64_t row, int j, Corner<A>* out) {
-    corner4<T, A, GENERAL>(loc, attn, g, row, j, GENERAL ? level_of(g, j) : j / g.P, out);
+                                        int64_t row, int j, Corner<A>* out, int sb = 0) {
+    corner4<T, A, GENERAL>(loc, attn, g, row, j, GENERAL ? level_of(g, j) : j / g.P, out, sb);
 }
 
 // ---- vector loads: Bytes-wide raw loads unpacked to float ------------------------------------------------
@@ -278,10 +287,8 @@ struct VecIO<bf16, V> {
 // below S, where row(t) = col + t * stride; ws += w_s. Loads are issued NB at a time before any of them is
 // consumed, so NB row reads per lane are in flight together. Corners outside the map (tok < 0) and the padding
 // slots of a last, partial batch read row 0 (always valid) and contribute exactly 0; full batches skip the slot
-// check. OFF32 (callers that know N * stride < 2^32 and N, stride < 2^24): the row offset is one 24-bit multiply
-// instead of a 64-bit one (the gather loops are issue-bound, and the 64-bit product takes three quarter-rate
-// multiplies).
-template <typename T, int V, int NB, bool OFF32 = false>
+// check (the gather loops are bound by the instructions they issue).
+template <typename T, int V, int NB>
 __device__ __forceinline__ void gather_sum(const Corner<float>* __restrict__ cr, int S, int first, int step,
                                            const T* __restrict__ col, size_t stride, float* acc, float& ws) {
     using IO = VecIO<T, V>;
@@ -295,17 +302,61 @@ __device__ __forceinline__ void gather_sum(const Corner<float>* __restrict__ cr,
             const Corner<float> c = !check || s < S ? cr[s] : Corner<float>{-1, 0.f};
             w[u] = c.w;
             in[u] = c.tok >= 0;
-            const int t = in[u] ? c.tok : 0;
-            if constexpr (OFF32)
-                raw[u] = IO::load(col + __umul24(static_cast<unsigned>(t), static_cast<unsigned>(stride)));
-            else
-                raw[u] = IO::load(col + static_cast<size_t>(t) * stride);
+            raw[u] = IO::load(col + static_cast<size_t>(in[u] ? c.tok : 0) * stride);
         }
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
             const typename IO::raw_t r = in[u] ? raw[u] : IO::zero();
             float v[V];
             IO::unpack(r, v);
+            ws += w[u];
+#pragma unroll
+            for (int i = 0; i < V; ++i) acc[i] = fmaf(w[u], v[i], acc[i]);
+        }
+    };
+    int s0 = first;
+    for (; s0 + step * (NB - 1) < S; s0 += step * NB) batch(s0, false);
+    if (s0 < S) batch(s0, true);
+}
+
+// A raw buffer over [base, base + bytes), bytes < 2^31: loads past the end return zeros (gfx9 range checking).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+template <typename R>
+__device__ __forceinline__ R buffer_load(__amdgpu_buffer_rsrc_t rsrc, unsigned off) {
+    if constexpr (sizeof(R) == 16)
+        return __builtin_bit_cast(R, __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(off), 0, 0));
+    else if constexpr (sizeof(R) == 8)
+        return __builtin_bit_cast(R, __builtin_amdgcn_raw_buffer_load_b64(rsrc, static_cast<int>(off), 0, 0));
+    else
+        return __builtin_bit_cast(R, __builtin_amdgcn_raw_buffer_load_b32(rsrc, static_cast<int>(off), 0, 0));
+}
+
+// gather_sum over a corner table of byte offsets (corner_ref with sb = the row stride in bytes): row s is at
+// byte lane_off + off_s of the buffer, and an outside corner's offset (kOutside + lane_off) lies past its end, so
+// the load itself returns zeros: per corner one add instead of a multiply, a 64-bit address and a select of the
+// loaded data. V * sizeof(T) must be 4, 8 or 16 bytes.
+template <typename T, int V, int NB>
+__device__ __forceinline__ void gather_sum_buf(const Corner<float>* __restrict__ cr, int S, int first, int step,
+                                               __amdgpu_buffer_rsrc_t rsrc, unsigned lane_off, float* acc, float& ws) {
+    using IO = VecIO<T, V>;
+    using R = typename IO::raw_t;
+    static_assert(sizeof(R) == 4 || sizeof(R) == 8 || sizeof(R) == 16, "buffer load width");
+    auto batch = [&](int s0, bool check) {
+        R raw[NB];
+        float w[NB];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int s = s0 + u * step;
+            const Corner<float> c = !check || s < S ? cr[s] : Corner<float>{kOutside, 0.f};
+            w[u] = c.w;
+            raw[u] = buffer_load<R>(rsrc, static_cast<unsigned>(c.tok) + lane_off);
+        }
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            float v[V];
+            IO::unpack(raw[u], v);
             ws += w[u];
 #pragma unroll
             for (int i = 0; i < V; ++i) acc[i] = fmaf(w[u], v[i], acc[i]);

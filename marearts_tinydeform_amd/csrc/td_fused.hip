@@ -44,7 +44,8 @@ struct FusedParams {
     int alln = 0;  // projection jobs take every N tile (D <= 64), one K slice each
     // divisions by L * P, P, the lanes of a row (CV * SG), CV, Q and D by multiply-high (exact below 2^31)
     FastDiv d_lp, d_p, d_gs, d_cv, d_q, d_d;
-    int off32 = 0;  // N * C < 2^32, both below 2^24: 32-bit row offsets (gather_sum)
+    int buf = 0;    // memory under 2 GB (mem_bytes): corner table of byte offsets, buffer-load gather (gather_sum_buf)
+    int mem_bytes = 0;
 };
 
 // Workgroup index -> work unit (b, query tile, h) with heads fastest. Workgroups are dealt to the 8 XCDs
@@ -133,7 +134,8 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
         __syncthreads();
     }
 
-    // phase 1: corner table
+    // phase 1: corner table (tokens, or with p.buf the rows' byte offsets)
+    const int sb = p.buf ? C * static_cast<int>(sizeof(T)) : 0;
     if (tid == 0) *gmax = 0u;
     for (int i = tid; i < QT * LP; i += NTH) {
         const int r = static_cast<int>(fast_div(p.d_lp, static_cast<uint32_t>(i))), j = i - r * LP;
@@ -143,15 +145,15 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
             if constexpr (LAYER) {
                 float lx, ly, a;
                 prologue_sample<T, float>(p.lay, g, bimg, q0 + r, h, r, j, pro, PP, rstat, lx, ly, a);
-                corners_at<float, GENERAL>(lx, ly, a, static_cast<int>(fast_div(p.d_p, j)), g, row, c4);
+                corners_at<float, GENERAL>(lx, ly, a, static_cast<int>(fast_div(p.d_p, j)), g, row, c4, sb);
             } else if constexpr (GENERAL) {
-                corner4<T, float, true>(loc, attn, g, row, j, c4);
+                corner4<T, float, true>(loc, attn, g, row, j, c4, sb);
             } else {
-                corner4<T, float, false>(loc, attn, g, row, j, static_cast<int>(fast_div(p.d_p, j)), c4);
+                corner4<T, float, false>(loc, attn, g, row, j, static_cast<int>(fast_div(p.d_p, j)), c4, sb);
             }
         } else {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) c4[k] = Corner<float>{-1, 0.f};
+            for (int k = 0; k < 4; ++k) c4[k] = Corner<float>{p.buf ? kOutside : -1, 0.f};
         }
     }
     __syncthreads();
@@ -194,16 +196,18 @@ __global__ __launch_bounds__(WAVES* kWave) void fused_vec_kernel(FusedParams p) 
     for (int it = tid; it < QT * GS; it += NTH) {
         const int r = static_cast<int>(fast_div(p.d_gs, static_cast<uint32_t>(it))), rem = it - r * GS;
         const int sg = static_cast<int>(fast_div(p.d_cv, static_cast<uint32_t>(rem))), ch = rem - sg * CV;
-        const T* mb =
-            mem + static_cast<size_t>(r < nrows ? fast_div(p.d_q, static_cast<uint32_t>(rbase + r)) : 0) * g.N * C;
+        const uint32_t bimg_r = r < nrows ? fast_div(p.d_q, static_cast<uint32_t>(rbase + r)) : 0;
+        const T* mb = mem + static_cast<size_t>(bimg_r) * g.N * C;
         float acc[V];
 #pragma unroll
         for (int i = 0; i < V; ++i) acc[i] = 0.f;
         float ws = 0.f;
-        if (p.off32)
-            gather_sum<T, V, NB, true>(cw + r * S, S, sg, SG, mb + ch * V, static_cast<size_t>(C), acc, ws);
+        if (p.buf)
+            gather_sum_buf<T, V, NB>(cw + r * S, S, sg, SG, buffer_of(mem, p.mem_bytes),
+                                     (bimg_r * static_cast<uint32_t>(g.N) * C + ch * V) * static_cast<uint32_t>(sizeof(T)),
+                                     acc, ws);
         else
-            gather_sum<T, V, NB, false>(cw + r * S, S, sg, SG, mb + ch * V, static_cast<size_t>(C), acc, ws);
+            gather_sum<T, V, NB>(cw + r * S, S, sg, SG, mb + ch * V, static_cast<size_t>(C), acc, ws);
         for (int m = CV; m < GS && m < kWave; m <<= 1) {
 #pragma unroll
             for (int i = 0; i < V; ++i) acc[i] += xor_lane(acc[i], m);
@@ -791,8 +795,9 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
                 p.d_cv = make_fastdiv(static_cast<uint32_t>(CV));
                 if (g.Q > 0) p.d_q = make_fastdiv(static_cast<uint32_t>(g.Q));
                 if (D > 0) p.d_d = make_fastdiv(static_cast<uint32_t>(D));
-                p.off32 = g.N < (1 << 24) && C < (1 << 24) &&
-                                  static_cast<int64_t>(g.N) * C < (int64_t{1} << 32) ? 1 : 0;
+                const int64_t mem_bytes = static_cast<int64_t>(g.B) * g.N * C * static_cast<int64_t>(sizeof(T));
+                p.buf = mem_bytes > 0 && mem_bytes < (int64_t{1} << 31) ? 1 : 0;
+                p.mem_bytes = p.buf ? static_cast<int>(mem_bytes) : 0;
                 p.alln = alln ? 1 : 0;
                 p.qtiles = (g.Q + qt - 1) / qt;
                 if (slices > 0) {

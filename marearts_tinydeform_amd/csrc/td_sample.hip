@@ -25,7 +25,8 @@ struct SampleParams {
     // (B * Q * H < 2^31) by H, Q and Q * H, instead of the 64-bit division routine (the kernel is issue-bound)
     FastDiv d_lp, d_p, d_gs, d_dv, d_h, d_q, d_qh;
     int fast = 0;
-    int off32 = 0;  // N * (token stride) < 2^32, both below 2^24: 32-bit row offsets (gather_sum)
+    int buf = 0;    // value under 2 GB (val_bytes): corner table of byte offsets, buffer-load gather (gather_sum_buf)
+    int val_bytes = 0;
 };
 
 // Row (b, q, h) of the i-th row in the order the workgroups take them: the output's own order, or with hq (b, h, q),
@@ -63,18 +64,20 @@ __global__ __launch_bounds__(WAVES* kWave) void sample_kernel(SampleParams p) {
     if (rblock >= p.blocks) return;
     const int64_t row0 = static_cast<int64_t>(rblock) * RB;
 
+    // corner table: tokens, or with p.buf the rows' byte offsets
+    const int sb = p.buf ? (g.value_hm ? D : HD) * static_cast<int>(sizeof(T)) : 0;
     for (int i = tid; i < RB * LP; i += NTH) {
         const int r = static_cast<int>(fast_div(p.d_lp, static_cast<uint32_t>(i))), j = i - r * LP;
         Corner<float>* c4 = cw + r * S + 4 * j;
         if (row0 + r < p.rows) {
             const int64_t row = sample_row(p, row0 + r);
             if constexpr (GENERAL)
-                corner4<T, float, true>(loc, attn, g, row, j, c4);
+                corner4<T, float, true>(loc, attn, g, row, j, c4, sb);
             else
-                corner4<T, float, false>(loc, attn, g, row, j, static_cast<int>(fast_div(p.d_p, j)), c4);
+                corner4<T, float, false>(loc, attn, g, row, j, static_cast<int>(fast_div(p.d_p, j)), c4, sb);
         } else {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) c4[k] = Corner<float>{-1, 0.f};
+            for (int k = 0; k < 4; ++k) c4[k] = Corner<float>{p.buf ? kOutside : -1, 0.f};
         }
     }
     __syncthreads();
@@ -104,10 +107,16 @@ __global__ __launch_bounds__(WAVES* kWave) void sample_kernel(SampleParams p) {
 #pragma unroll
         for (int i = 0; i < V; ++i) acc[i] = 0.f;
         float ws = 0.f;
-        if (p.off32)
-            gather_sum<T, V, NB, true>(cw + r * S, S, sg, SG, base, stride, acc, ws);
-        else
-            gather_sum<T, V, NB, false>(cw + r * S, S, sg, SG, base, stride, acc, ws);
+        bool done = false;
+        if constexpr (V * sizeof(T) >= 4) {
+            if (p.buf) {
+                const uint32_t lane_off =
+                    static_cast<uint32_t>(base - value) * static_cast<uint32_t>(sizeof(T));  // < val_bytes < 2^31
+                gather_sum_buf<T, V, NB>(cw + r * S, S, sg, SG, buffer_of(value, p.val_bytes), lane_off, acc, ws);
+                done = true;
+            }
+        }
+        if (!done) gather_sum<T, V, NB>(cw + r * S, S, sg, SG, base, stride, acc, ws);
         for (int m = DV; m < GS; m <<= 1) {
 #pragma unroll
             for (int i = 0; i < V; ++i) acc[i] += xor_lane(acc[i], m);
@@ -246,8 +255,9 @@ int launch_sample_t(SampleParams p, hipStream_t stream, const SampleTune& tune) 
     p.d_gs = make_fastdiv(static_cast<uint32_t>(GS));
     p.d_dv = make_fastdiv(static_cast<uint32_t>(DV));
     p.fast = p.rows < (int64_t{1} << 31) && g.H > 0 && g.Q > 0 ? 1 : 0;
-    const int64_t tstride = g.value_hm ? D : static_cast<int64_t>(g.H) * D;
-    p.off32 = g.N < (1 << 24) && tstride < (1 << 24) && static_cast<int64_t>(g.N) * tstride < (int64_t{1} << 32) ? 1 : 0;
+    const int64_t val_bytes = static_cast<int64_t>(g.B) * g.N * g.H * D * static_cast<int64_t>(sizeof(T));
+    p.buf = V * static_cast<int>(sizeof(T)) >= 4 && val_bytes > 0 && val_bytes < (int64_t{1} << 31) ? 1 : 0;
+    p.val_bytes = p.buf ? static_cast<int>(val_bytes) : 0;
     if (p.fast) {
         p.d_h = make_fastdiv(static_cast<uint32_t>(g.H));
         p.d_q = make_fastdiv(static_cast<uint32_t>(g.Q));
