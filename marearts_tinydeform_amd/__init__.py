@@ -30,8 +30,8 @@ MODES = ('auto', 'fused', 'project')
 # held-out grid (1.36 against 1.07). When the fused kernel's projection took every N tile per job (3-4% faster at
 # small problems), the 16-bit fused line was scaled by 0.96, and when both gathers moved to buffer loads with
 # multiply-high index arithmetic (fused 10-17% faster, the sampler 15-30%) by 0.90 more: every case of the fit grid
-# within 10% again (worst 1.095; unscaled 1.123) and 102 of the 108 held-out cases (unscaled 101; a least-squares
-# refit 99).
+# within 10% again (worst 1.094; unscaled 1.123) and 101 to 103 of the 108 held-out cases over two runs (unscaled
+# 101; a least-squares refit 99).
 #   fused   = f0 + f1 * gathered_mb
 #   project = p0 + p1 * gemm_mb + p2 * gemm_gflop + p3 * gemm_rounds_k + p4 * sample_mb
 FUSED_LIMIT = {
