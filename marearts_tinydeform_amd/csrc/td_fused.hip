@@ -9,7 +9,8 @@
 // fused_vec_kernel (float / half / bfloat16, C a multiple of 16 bytes, 16-byte aligned memory and weight):
 //   workgroup = (b, tile of QT queries, h), or for small problems (h, balanced slice of the B * Q rows of head h:
 //            every CU then holds the same number of rows to within one); heads vary fastest across workgroups.
-//   phase 1  corner table of the QT rows into LDS.
+//   phase 1  corner table of the QT rows into LDS (with memory under 2 GB, each corner row's byte offset, so that
+//            phase 2 gathers by raw buffer loads and an outside corner's load returns zeros).
 //   phase 2  gather: CV*SG lanes per row, lane = (corner group sg, 16-byte channel chunk ch); each lane sums
 //            every SG-th corner of its row with float32 FMAs, the SG partial sums meet by cross-lane adds,
 //            and g lands in LDS as float32.

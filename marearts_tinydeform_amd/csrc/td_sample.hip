@@ -6,6 +6,8 @@
 // Each row is served by DV*SG lanes: lane = (corner group sg, chunk ch of V elements), so one load
 // instruction of a wavefront fetches 64 / (DV*SG) * SG rows' D-wide corner rows at once; the SG partial sums
 // of a row meet by cross-lane adds (lanes DV, 2*DV, ... apart) and the row is stored with V-element stores.
+// With a value tensor under 2 GB the corner table holds byte offsets and the rows come by raw buffer loads
+// (gather_sum_buf), an outside corner's load returning zeros.
 #include "td_internal.h"
 
 namespace td {
