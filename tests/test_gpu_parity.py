@@ -364,6 +364,35 @@ def test_sample_head_order_on_large_values(dtype):
     assert_close(f'sample_heads (b, h, q) order {dtype}', got_h, ref, atol, rtol)
 
 
+def test_tensors_of_2gb_take_the_64bit_gather():
+    # Memory and value tensors of 2 GB or more are gathered with 64-bit addresses instead of 32-bit buffer offsets.
+    # Level 0 is a 2048 x 2048 map of zero rows whose samples carry weight 0, so the result is that of level 1 alone
+    # (a 32 x 32 map at the tensor's end, past 2^31 bytes), which the oracle computes on the small problem.
+    B, Q, H, D, C, P, dtype = 1, 16, 8, 32, 256, 4, torch.float16
+    big, small = (2048, 2048), (32, 32)
+    N0, N1 = big[0] * big[1], small[0] * small[1]
+    assert (N0 + N1) * C * 2 >= 2 ** 31
+    args = make(B, Q, H, D, C, [small], P, dtype=dtype)
+    mem1, w, b, _, _, loc1, attn1 = args
+    g = torch.Generator().manual_seed(17)
+    loc0 = torch.rand(B, Q, H, 1, P, 2, generator=g).to(dtype)
+    loc = torch.cat([loc0, loc1], dim=3)
+    attn = torch.cat([torch.zeros(B, Q, H, 1, P, dtype=dtype), attn1], dim=3)
+    ref = bruteforce.deform_attn(*args)
+    memory = torch.zeros(B, N0 + N1, C, dtype=dtype, device='cuda')
+    memory[:, N0:] = mem1.cuda()
+    shapes = torch.tensor([big, small], dtype=torch.int64, device='cuda')
+    starts = torch.tensor([0, N0], dtype=torch.int64, device='cuda')
+    dev = [memory, w.cuda(), b.cuda(), shapes, starts, loc.cuda(), attn.cuda()]
+    atol, rtol = TOL[dtype]
+    for mode in ('fused', 'project'):
+        say(f'  2 GB memory [{mode}]')
+        out = run(dev, mode)
+        assert_close(f'2 GB memory [{mode}]', out.double().cpu().numpy(), ref, atol, rtol)
+    del memory, dev
+    torch.cuda.empty_cache()
+
+
 def test_graph_capture_replays_match_eager():
     args = to(workload(1, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.float16), 'cuda')
     for mode in MODES:
