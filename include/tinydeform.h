@@ -134,7 +134,7 @@ int td_project_forward(int dtype, const void* memory, const void* value_weight, 
  * serving loops, harnesses that forbid hipMalloc. A problem whose projected values (B*N*H*D elements of dtype) exceed
  * the array is refused with TD_E_ARG (td_project_forward with a workspace takes it). Every call on one GPU shares
  * that GPU's array, so calls that overlap on one GPU (other streams, other host threads) race; the stream's device
- * must be the current device. Same results as td_project_forward, bit for bit.
+ * must be the current device (else TD_E_ARG). Same results as td_project_forward, bit for bit.
  */
 #define TD_NOALLOC_SCRATCH_BYTES 67108864 /* 64 MiB per GPU */
 int td_project_forward_noalloc(int dtype, const void* memory, const void* value_weight, const void* value_bias,

@@ -384,10 +384,11 @@ def project_forward_noalloc(memory, weight, bias, spatial_shapes, level_start_in
         raise RuntimeError('out must be a contiguous [B, Q, H*D] tensor of the memory dtype on its device')
     if out.numel() == 0:
         return out
-    _check(lib_.td_project_forward_noalloc(DTYPE_CODES[memory.dtype], mem.data_ptr(), w.data_ptr(), _ptr(b),
-                                           sh.data_ptr(), st.data_ptr(), lc.data_ptr(), aw.data_ptr(), _ptr(mask),
-                                           1 if loc_acc else 0, out.data_ptr(), B, Q, N, C, H, HD // H, L, P,
-                                           _stream(dev)))
+    with torch.cuda.device(dev):  # the library resolves its scratch array on the current device
+        _check(lib_.td_project_forward_noalloc(DTYPE_CODES[memory.dtype], mem.data_ptr(), w.data_ptr(), _ptr(b),
+                                               sh.data_ptr(), st.data_ptr(), lc.data_ptr(), aw.data_ptr(), _ptr(mask),
+                                               1 if loc_acc else 0, out.data_ptr(), B, Q, N, C, H, HD // H, L, P,
+                                               _stream(dev)))
     return out
 
 

@@ -23,30 +23,33 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-// Device address of `scratch` on the current device (resolved once per device); nullptr after recording an error.
-void* device_scratch() {
-    int dev = -1;
+// Device address of `scratch` on the stream's device, resolved once per device with that device current. The
+// stream's device must be the current one: hipGetSymbolAddress answers for the current device, and the kernels run
+// on the stream's, so a mismatch would hand one GPU's address to another's kernels. Returns 0 with *out set, or the
+// error code it recorded.
+int device_scratch(hipStream_t stream, void** out) {
+    int dev = -1, sdev = -1;
     hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) {
-        set_error(TD_E_LAUNCH, "noalloc: no current HIP device: %s", hipGetErrorString(e));
-        return nullptr;
-    }
-    if (dev < 0 || dev >= kMaxDevices) {
-        set_error(TD_E_ARG, "noalloc: device %d is beyond the %d this library serves", dev, kMaxDevices);
-        return nullptr;
-    }
+    if (e != hipSuccess) return set_error(TD_E_LAUNCH, "noalloc: no current HIP device: %s", hipGetErrorString(e));
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess)
+        return set_error(TD_E_ARG, "noalloc: cannot tell the stream's device: %s", hipGetErrorString(e));
+    if (sdev != dev)
+        return set_error(TD_E_ARG, "noalloc: the stream belongs to device %d but device %d is current (make the "
+                         "stream's device current)", sdev, dev);
+    if (dev < 0 || dev >= kMaxDevices)
+        return set_error(TD_E_ARG, "noalloc: device %d is beyond the %d this library serves", dev, kMaxDevices);
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
     if (g_scratch_ptr[dev] == nullptr) {
         void* ptr = nullptr;
         e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || ptr == nullptr) {
-            set_error(TD_E_LAUNCH, "noalloc: hipGetSymbolAddress of the scratch array failed on device %d: %s", dev,
-                      hipGetErrorString(e));
-            return nullptr;
-        }
+        if (e != hipSuccess || ptr == nullptr)
+            return set_error(TD_E_LAUNCH, "noalloc: hipGetSymbolAddress of the scratch array failed on device %d: %s",
+                             dev, hipGetErrorString(e));
         g_scratch_ptr[dev] = ptr;
     }
-    return g_scratch_ptr[dev];
+    *out = g_scratch_ptr[dev];
+    return 0;
 }
 
 }  // namespace
@@ -68,8 +71,9 @@ extern "C" int td_project_forward_noalloc(int dtype, const void* memory, const v
                          "scratch array (use td_project_forward with a workspace)",
                          static_cast<long long>(B * N * H * D * elem_size(dtype)),
                          static_cast<long long>(TD_NOALLOC_SCRATCH_BYTES));
-    void* ws = device_scratch();
-    if (ws == nullptr) return TD_E_LAUNCH;
+    void* ws = nullptr;
+    const int rc = device_scratch(static_cast<hipStream_t>(stream), &ws);
+    if (rc != 0) return rc;
     return project_forward(dtype, memory, value_weight, value_bias, spatial_shapes, level_start_index,
                            sampling_locations, attention_weights, padding_mask, loc_acc, ws, TD_NOALLOC_SCRATCH_BYTES,
                            out, B, Q, N, C, H, D, L, P, stream);

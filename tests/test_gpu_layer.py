@@ -153,9 +153,13 @@ def test_wide_projection_weights(Q, in_kernel):
         assert rc == _native.TD_E_WORKSPACE
 
 
-@pytest.mark.parametrize('L,P,dtype', [(1, 4, torch.bfloat16), (2, 4, torch.float16), (4, 4, torch.bfloat16),
-                                       (4, 8, torch.float16)])
-def test_gemm_route_finalizes_in_its_epilogue(L, P, dtype):
+@pytest.mark.parametrize('L,P,dtype,ref_dim,ref_levels', [
+    (1, 4, torch.bfloat16, 4, '1'), (2, 4, torch.float16, 4, '1'), (4, 4, torch.bfloat16, 4, '1'),
+    (4, 8, torch.float16, 4, '1'),
+    # point references (divided by each level's width and height), one per level, and boxes per level
+    (4, 4, torch.bfloat16, 2, 'L'), (2, 8, torch.float16, 2, 'L'), (2, 2, torch.float16, 2, '1'),
+    (4, 2, torch.bfloat16, 4, 'L')])
+def test_gemm_route_finalizes_in_its_epilogue(L, P, dtype, ref_dim, ref_levels):
     # In 16 bits with L * P a power of two from 4 to 64 the projections' epilogue turns offsets into locations and
     # logits into softmax weights (a head's L * P logits of a row sit in one to four lanes of one or two 16-column
     # blocks); the other cases of the GEMM route (64 samples, 12 samples) are in test_large_prologue_takes_the_gemm_route.
@@ -164,10 +168,10 @@ def test_gemm_route_finalizes_in_its_epilogue(L, P, dtype):
     rows = -(-int(8e8) // (H * 3 * LP * Cq))
     B, Q = 2, rows // 2 + 7
     levels = [(8, 10), (4, 5), (2, 3), (1, 2)][:L]
-    a = make_layer(B, Q, H, 32, Cq, levels, P, 4, '1', dtype=dtype)
+    a = make_layer(B, Q, H, 32, Cq, levels, P, ref_dim, ref_levels, dtype=dtype)
     ref_loc, ref_attn = olayer.locations(a[0], a[2], a[3], a[5], a[6], a[7], a[8], H, P, position_embeddings=a[15])
     dev = to(a[:13], 'cuda') + a[13:15] + to(a[15:], 'cuda')
-    say(f'  epilogue finalize L{L} P{P} {dtype} B{B} Q{Q}')
+    say(f'  epilogue finalize L{L} P{P} {dtype} ref {ref_dim}/{ref_levels} B{B} Q{Q}')
     loc, attn = _native.layer_prologue(dev[0], dev[15], dev[2], dev[5], dev[6], dev[7], dev[8], dev[3], H, P)
     torch.cuda.synchronize()
     lt = LOC_TOL[dtype]

@@ -364,33 +364,75 @@ def test_sample_head_order_on_large_values(dtype):
     assert_close(f'sample_heads (b, h, q) order {dtype}', got_h, ref, atol, rtol)
 
 
-def test_tensors_of_2gb_take_the_64bit_gather():
-    # Memory and value tensors of 2 GB or more are gathered with 64-bit addresses instead of 32-bit buffer offsets.
-    # Level 0 is a 2048 x 2048 map of zero rows whose samples carry weight 0, so the result is that of level 1 alone
-    # (a 32 x 32 map at the tensor's end, past 2^31 bytes), which the oracle computes on the small problem.
-    B, Q, H, D, C, P, dtype = 1, 16, 8, 32, 256, 4, torch.float16
-    big, small = (2048, 2048), (32, 32)
-    N0, N1 = big[0] * big[1], small[0] * small[1]
-    assert (N0 + N1) * C * 2 >= 2 ** 31
+def big_memory_case(name, dtype, Q, tokens, masked):
+    """One image whose memory has `tokens` C-wide rows: filler levels of zero rows (a 2048-wide map, then a one-row
+    map for the remainder) whose samples carry weight 0, and a 32 x 32 level of random rows at the tensor's end. The
+    result is that of the last level alone, which the oracle computes on the small problem. Query 0 samples the
+    last token of the tensor in every head (bilinear x0 = y0 = 31), so the last rows are read whichever way the
+    kernels address them. With `masked`, a padding mask over a fifth of the small level's tokens (and none of the
+    filler) makes the kernels take their general corner rule."""
+    B, H, D, C, P, small = 1, 8, 32, 256, 4, (32, 32)
+    N1 = small[0] * small[1]
+    fill = tokens - N1
+    h0 = fill // 2048
+    levels = [(h0, 2048)] + ([(1, fill - h0 * 2048)] if fill > h0 * 2048 else [])
+    LF = len(levels)
     args = make(B, Q, H, D, C, [small], P, dtype=dtype)
     mem1, w, b, _, _, loc1, attn1 = args
+    loc1[0, 0, :, 0, 0] = 1 - 0.25 / 32   # x = y = 31.25: corner (31, 31) is the last token
+    loc1[0, 0, :, 0, 1] = 1.0             # x = y = 31.5
+    args[5] = loc1
     g = torch.Generator().manual_seed(17)
-    loc0 = torch.rand(B, Q, H, 1, P, 2, generator=g).to(dtype)
+    mask1 = torch.rand(B, N1, generator=g) < 0.2 if masked else None
+    loc0 = torch.rand(B, Q, H, LF, P, 2, generator=g).to(dtype)
     loc = torch.cat([loc0, loc1], dim=3)
-    attn = torch.cat([torch.zeros(B, Q, H, 1, P, dtype=dtype), attn1], dim=3)
-    ref = bruteforce.deform_attn(*args)
-    memory = torch.zeros(B, N0 + N1, C, dtype=dtype, device='cuda')
-    memory[:, N0:] = mem1.cuda()
-    shapes = torch.tensor([big, small], dtype=torch.int64, device='cuda')
-    starts = torch.tensor([0, N0], dtype=torch.int64, device='cuda')
+    attn = torch.cat([torch.zeros(B, Q, H, LF, P, dtype=dtype), attn1], dim=3)
+    ref = bruteforce.deform_attn(*args, padding_mask=mask1)
+    memory = torch.zeros(B, tokens, C, dtype=dtype, device='cuda')
+    memory[:, fill:] = mem1.cuda()
+    shapes = torch.tensor(levels + [small], dtype=torch.int64, device='cuda')
+    starts = torch.tensor([0, h0 * 2048, fill][:LF + 1], dtype=torch.int64, device='cuda')
+    mask = None
+    if masked:
+        mask = torch.zeros(B, tokens, dtype=torch.bool, device='cuda')
+        mask[:, fill:] = mask1.cuda()
     dev = [memory, w.cuda(), b.cuda(), shapes, starts, loc.cuda(), attn.cuda()]
     atol, rtol = TOL[dtype]
     for mode in ('fused', 'project'):
-        say(f'  2 GB memory [{mode}]')
-        out = run(dev, mode)
-        assert_close(f'2 GB memory [{mode}]', out.double().cpu().numpy(), ref, atol, rtol)
-    del memory, dev
+        say(f'  {name} {dtype} Q{Q} tokens {tokens} ({tokens * C * memory.element_size()} bytes)'
+            f'{" masked" if masked else ""} [{mode}]')
+        with torch.inference_mode():
+            out = td.ma_deform_attn(*dev, mode=mode, padding_mask=mask)
+        torch.cuda.synchronize()
+        assert_close(f'{name} {dtype} Q{Q} [{mode}]', out.double().cpu().numpy(), ref, atol, rtol)
+    del memory, dev, mask
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize('dtype,Q,masked', [
+    (torch.float16, 16, False),    # 128 rows: two-wavefront balanced slices; head-major sampler
+    (torch.bfloat16, 16, False),
+    (torch.float32, 16, False),    # token-major sampler (float32 head rows of 128 bytes)
+    (torch.float16, 1024, False),  # 8192 rows: 8-wavefront query tiles
+    (torch.bfloat16, 16, True),    # padding mask: the general corner rule's kernels
+])
+def test_tensors_of_2gb_take_the_64bit_gather(dtype, Q, masked):
+    # Memory and value tensors of 2 GB or more are gathered with 64-bit addresses instead of 32-bit buffer offsets
+    # (memory and value have the same bytes here: H * D = C).
+    row = 256 * torch.empty(0, dtype=dtype).element_size()
+    tokens = 2 ** 31 // row + 1024
+    assert tokens * row >= 2 ** 31
+    big_memory_case('2 GB memory', dtype, Q, tokens, masked)
+
+
+@pytest.mark.parametrize('dtype', [torch.float16, torch.float32])
+def test_tensors_just_under_2gb_keep_the_buffer_gather(dtype):
+    # 4 KB short of 2^31 bytes: the buffer-load gathers at the top of their range, where the last rows' offsets
+    # t * row + lane offset come closest to the outside corners' 2^31.
+    row = 256 * torch.empty(0, dtype=dtype).element_size()
+    tokens = (2 ** 31 - 4096) // row
+    assert (tokens + 1) * row > 2 ** 31 - 4096 and tokens * row < 2 ** 31
+    big_memory_case('memory under 2 GB', dtype, 16, tokens, False)
 
 
 def test_graph_capture_replays_match_eager():
