@@ -11,12 +11,17 @@ the µs per call, as the reference takes the best of 7 replays of its 100-call g
 than a long one (about 0.85 µs per call at 20 calls).
 
 Prints diagnostics on stderr and ONE JSON line on stdout: value = µs per layer call (auto mode), with per-mode
-times, the roofline of the dominant kernel (algorithmic bytes per launch / its average launch duration, measured
-the same way on its own stream), the effective byte rate of the path (algorithmic bytes / time: gathered rows
-count every time they are read, L2 hits included) next to the HBM rate the counters measured (bytes that reached
+times, the roofline of the dominant kernel (algorithmic bytes or flops per launch / its average launch duration,
+measured the same way on its own stream), the effective byte rate of the path (algorithmic bytes / time: gathered
+rows count every time they are read, L2 hits included) next to the HBM rate the counters measured (bytes that reached
 the memory fabric per launch, from the committed rocprofv3 --pmc summary, / the same time), and the CPU baseline
 (the oracle's torch restatement of the reference's PyTorch path, float32, on this host's cores, timed on a
-bounded sample).
+bounded sample). For the gather kernels (fused mode, the sampler) the roofline's bound is "l2-gather": the rate at
+which all CUs receive randomly chosen rows of the kernel's width from a buffer of the gathered tensor's size,
+measured in the same run by td_probe_gather, with the HBM figures beside it.
+
+Other modes: --table (the reference's sweep), --fit-auto / --holdout (the auto selector), --ceiling (the gather
+ceiling over row widths and buffer sizes), --trace-run and --pmc-run (short runs for rocprofv3).
 """
 
 import argparse
@@ -38,7 +43,6 @@ from inputs import DINO_LEVELS, LIMIT_LEVELS, RTDETR_LEVELS, workload  # noqa: E
 
 HBM_PEAK = 8.0e12        # bytes/s, MI355X HBM3E
 MFMA_PEAK_16 = 2.5e15    # flop/s, dense fp16/bf16
-L2_GATHER_GBPS = 21000.0  # GB/s, all CUs reading random 512-byte rows from L2 (probe measurement on MI355X)
 FUSED_KERNELS = ('fused_vec_kernel',)
 
 WORKLOADS = {
@@ -274,6 +278,67 @@ def project_halves(dev, H, D, dtype):
             lambda v: _native.sample_forward(v, H, *dev[3:]))
 
 
+def gather_ceiling(row_bytes, buf_bytes, target_bytes=1 << 30):
+    """GB/s at which all CUs together receive randomly chosen rows of `row_bytes` from a buffer of `buf_bytes`:
+    td_probe_gather (the gather kernels' 16-byte buffer loads, 8 in flight per lane, row_bytes / 16 lanes per row)
+    reading about `target_bytes` per launch, graph-timed like the operator; the best of four occupancies. With the
+    memory tensor's size this is the ceiling of the fused kernel's gather phase, whose rows mostly sit in L2 (what
+    L2 misses comes from the MALL or HBM, as in the kernel)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    buf = torch.zeros(max(buf_bytes // 16, row_bytes // 16), 4, dtype=torch.int32, device='cuda')
+    best = None
+    for waves, per_cu in ((4, 2), (8, 1), (8, 2), (4, 4)):
+        wg = cus * per_cu
+        sink = torch.zeros(wg, dtype=torch.int32, device='cuda')
+        loads = max(8, target_bytes // (wg * waves * 64 * 16) // 8 * 8)
+        nbytes = wg * waves * 64 * loads * 16
+        t = graph_time_us(lambda: _native.probe_gather(buf, row_bytes, loads, wg, waves, sink), 10, 2)
+        rate = nbytes / (t * 1e-6) / 1e9
+        if best is None or rate > best['gbps']:
+            best = {'gbps': round(rate, 1), 'row_bytes': row_bytes, 'buffer_bytes': buf.numel() * 4,
+                    'workgroups': wg, 'waves': waves, 'loads_per_lane': loads, 'us': round(t, 2)}
+    del buf
+    return best
+
+
+CEILING_ROWS = (64, 128, 256, 512, 1024)
+CEILING_BUFFERS = (('2 MB', 2 << 20), ('RT-DETR 640 memory, fp16 B1 (4.3 MB)', 8400 * 256 * 2),
+                   ('RT-DETR 640 memory, bf16 B8 (34.4 MB)', 8 * 8400 * 256 * 2),
+                   ('DINO 4-level value, fp16 B4 (45.5 MB)', 4 * 22223 * 256 * 2), ('512 MB', 512 << 20))
+
+
+def ceiling_table():
+    """--ceiling: the gather ceiling for every row width and buffer size of CEILING_ROWS x CEILING_BUFFERS, as a
+    markdown table on stdout and one JSON line."""
+    rows = []
+    log(f'{torch.cuda.get_device_name()} ({torch.cuda.get_device_properties(0).gcnArchName}), '
+        f'{torch.cuda.get_device_properties(0).multi_processor_count} CUs')
+    for name, nbytes in CEILING_BUFFERS:
+        for rb in CEILING_ROWS:
+            c = gather_ceiling(rb, nbytes)
+            c['buffer'] = name
+            rows.append(c)
+            log(f'  {name:40s} rows of {rb:5d} B: {c["gbps"]:9.1f} GB/s ({c["workgroups"]} x {c["waves"]} waves)')
+    print('| buffer | ' + ' | '.join(f'{r} B rows' for r in CEILING_ROWS) + ' |')
+    print('|---|' + '---:|' * len(CEILING_ROWS))
+    for name, _ in CEILING_BUFFERS:
+        print(f'| {name} | ' + ' | '.join(f'{c["gbps"]:.0f}' for c in rows if c['buffer'] == name) + ' |')
+    print(json.dumps({'gather_ceiling_gbps': rows}), flush=True)
+
+
+def trace_run(dev, steps, warmup):
+    """--trace-run, for rocprofv3 --kernel-trace: a graph of `steps` operator calls (mode auto) and a graph of
+    `steps` launches of an empty kernel, each timed as the headline is (best of 7 replays). The empty kernel's
+    traced duration is what the tracer reports for a dispatch with no work; the operator's traced duration less
+    that is comparable with its graph-timed µs per call, which this run prints."""
+    with torch.inference_mode():
+        op = graph_time_us(lambda: td.ma_deform_attn(*dev), steps, warmup)
+        empty = graph_time_us(lambda: _native.probe_empty(1), steps, warmup)
+    log(f'trace run: operator {op:.2f} µs per call, empty kernel {empty:.2f} µs per launch ({steps}-call graphs)')
+    print(json.dumps({'trace_run': {'steps': steps, 'operator_us_per_call': round(op, 3),
+                                    'empty_us_per_launch': round(empty, 3)}}), flush=True)
+
+
 def pmc_run(dev, H, steps):
     src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device='cuda')
     dst = torch.empty_like(src)
@@ -477,6 +542,12 @@ def main():
     ap.add_argument('--channels', type=int, default=256, help='--table: C')
     ap.add_argument('--heads', type=int, default=8, help='--table: H')
     ap.add_argument('--points', type=int, default=4, help='--table: P')
+    ap.add_argument('--ceiling', action='store_true',
+                    help='the gather ceiling (td_probe_gather) for row widths 64..1024 bytes and buffers from 2 MB '
+                         'to 512 MB, as a markdown table')
+    ap.add_argument('--trace-run', action='store_true',
+                    help='for rocprofv3 --kernel-trace: --steps operator calls and --steps empty kernels, each in '
+                         'a graph timed like the headline')
     ap.add_argument('--pmc-run', action='store_true',
                     help='for rocprofv3 --pmc: one plain copy of COPY_BYTES (the counter calibration), then '
                          '--steps eager calls of the fused kernel, the value projection and the sampling kernel')
@@ -498,6 +569,9 @@ def main():
     if args.table:
         table(args)
         return
+    if args.ceiling:
+        ceiling_table()
+        return
 
     spec = WORKLOADS[args.workload]
     B, Q, H, D, C, levels, P, dtype, bias, loc_dist = spec
@@ -512,6 +586,9 @@ def main():
 
     if args.pmc_run:
         pmc_run(dev, H, args.steps)
+        return
+    if args.trace_run:
+        trace_run(dev, args.steps, args.warmup)
         return
 
     pick = td.choose_mode(dev[0], dev[1], dev[5])
@@ -547,14 +624,21 @@ def main():
                 f'{tr["pytorch_train_step"]:.2f} µs')
             kern.update(tr)
 
+    # Roofline of the dominant kernel. The gather kernels read rows that mostly sit in L2, so their bound is the rate
+    # at which the CUs receive such rows ("l2-gather"), measured here, on this device, by td_probe_gather with the
+    # kernel's row width over a buffer of the gathered tensor's size; the HBM figures (counter-measured bytes over the
+    # same time, and the algorithmic bytes against 8 TB/s) stand beside it.
+    ceiling = None
     if pick == 'fused':
-        dom, bytes_, t = 'fused', alg['fused_bytes'], times['fused']
-        roof = {'kernel': 'fused_vec_kernel', 'bound': 'hbm', 'achieved': bytes_ / (t * 1e-6) / 1e9, 'peak': 8000.0,
-                'unit': 'GB/s'}
+        t = times['fused']
+        ceiling = gather_ceiling(C * s, B * N * C * s)
+        roof = {'kernel': 'fused_vec_kernel', 'bound': 'l2-gather', 'achieved': alg['fused_bytes'] / (t * 1e-6) / 1e9,
+                'peak': ceiling['gbps'], 'unit': 'GB/s'}
     else:
         t_gemm, t_smp = kern.get('value_proj', times['project']), kern.get('sample', 0.0)
         gk = gemm_kernel(B * N, C, H * D, s)
         if t_gemm >= t_smp:
+            t = t_gemm
             flops = alg['gemm_flops']
             if dtype in (torch.float16, torch.bfloat16) and flops / alg['gemm_bytes'] > MFMA_PEAK_16 / HBM_PEAK:
                 roof = {'kernel': gk, 'bound': 'mfma', 'achieved': flops / (t_gemm * 1e-6) / 1e12,
@@ -563,11 +647,20 @@ def main():
                 roof = {'kernel': gk, 'bound': 'hbm',
                         'achieved': alg['gemm_bytes'] / (t_gemm * 1e-6) / 1e9, 'peak': 8000.0, 'unit': 'GB/s'}
         else:
-            roof = {'kernel': 'sample_kernel', 'bound': 'hbm', 'achieved': alg['sample_bytes'] / (t_smp * 1e-6) / 1e9,
-                    'peak': 8000.0, 'unit': 'GB/s'}
+            t = t_smp
+            ceiling = gather_ceiling(D * s, B * N * H * D * s)
+            roof = {'kernel': 'sample_kernel', 'bound': 'l2-gather',
+                    'achieved': alg['sample_bytes'] / (t_smp * 1e-6) / 1e9, 'peak': ceiling['gbps'], 'unit': 'GB/s'}
     roof['achieved'] = round(roof['achieved'], 1)
     roof['frac'] = round(roof['achieved'] / roof['peak'], 4)
     roof['traffic'] = measured_traffic(args.workload, roof['kernel'])
+    if ceiling is not None:
+        roof['ceiling_probe'] = ceiling
+        roof['hbm'] = {'achieved': None if roof['traffic'] is None else round(roof['traffic'] / (t * 1e-6) / 1e9, 1),
+                       'peak': 8000.0, 'unit': 'GB/s', 'what': 'counter-measured HBM bytes per launch / time'}
+        if roof['hbm']['achieved'] is not None:
+            roof['hbm']['frac'] = round(roof['hbm']['achieved'] / 8000.0, 4)
+        roof['algorithmic_vs_hbm_peak'] = round(roof['achieved'] / 8000.0, 4)
 
     path_bytes = alg['fused_bytes'] if pick == 'fused' else alg['gemm_bytes'] + alg['sample_bytes']
     # HBM rate from the counters: the bytes the path's kernels moved to and from the memory fabric per launch
@@ -577,13 +670,6 @@ def main():
     else:
         parts = [measured_traffic(args.workload, k) for k in (gemm_kernel(B * N, C, H * D, s), 'sample_kernel')]
         traffic = None if None in parts else sum(parts)
-    gather = None
-    if roof['kernel'] in FUSED_KERNELS or roof['kernel'] == 'sample_kernel':
-        # the gather kernels read rows that mostly sit in L2: the other ceiling is the rate at which the CUs
-        # receive randomly addressed rows from L2, measured by a probe at 21 TB/s for 512-byte (and 128-byte) rows
-        gather = {'achieved': roof['achieved'], 'ceiling': L2_GATHER_GBPS, 'unit': 'GB/s',
-                  'frac': round(roof['achieved'] / L2_GATHER_GBPS, 4),
-                  'what': 'effective gather rate against the L2 ceiling for random 512-byte rows'}
     result = {
         'metric': ('µs per layer call (value_proj+MSDeformAttn) RT-DETR-640 fp16 B=1 Q=300; HBM GB/s'
                    if args.workload == 'rtdetr640-fp16-b1-q300'
@@ -610,7 +696,6 @@ def main():
         'effective_gbps': round(path_bytes / (times['auto'] * 1e-6) / 1e9, 1),
         'hbm_gbps': None if traffic is None else round(traffic / (times['auto'] * 1e-6) / 1e9, 1),
         'roofline': roof,
-        'gather_ceiling': gather,
     }
     if not args.no_cpu:
         log('CPU baseline ...')

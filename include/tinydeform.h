@@ -266,6 +266,23 @@ int64_t td_weight_grad_workspace(int dtype, int64_t M, int64_t HD, int64_t C);
 int td_weight_grad(int dtype, const void* grad_value, const void* memory, void* grad_weight, void* grad_bias,
                    int64_t M, int64_t HD, int64_t C, void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * Measurement kernels. No counterpart in the reference and no part of the operator: the benchmark uses them to
+ * calibrate what it reports.
+ *
+ * td_probe_empty: `launches` launches of a kernel that does nothing (one wavefront). Traced, it gives the duration
+ * a kernel tracer reports for a dispatch with no work.
+ *
+ * td_probe_gather: one launch of `workgroups` workgroups of `waves` wavefronts that read randomly chosen rows of
+ * buf [bytes] (below 2 GB), row_bytes / 16 lanes per row by 16-byte buffer loads, 8 loads in flight per lane,
+ * loads_per_lane (a multiple of 8) per lane in all: the gather kernels' access pattern, at the rate the CUs can
+ * receive such rows. sink: `workgroups` 32-bit words, written only when the loaded data xor to 0x5a5a5a5a (never
+ * for a zero buffer).
+ */
+int td_probe_empty(int64_t launches, void* stream);
+int td_probe_gather(const void* buf, int64_t bytes, int64_t row_bytes, int64_t loads_per_lane, int64_t workgroups,
+                    int64_t waves, void* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,7 +21,7 @@ LIB = os.path.join(HERE, 'libtinydeform.so')
 ARCH = 'gfx950'
 
 SOURCES = ['td_abi.hip', 'td_fused.hip', 'td_sample.hip', 'td_gemm.hip', 'td_gemm_dma.hip', 'td_gemm_stream.hip',
-           'td_layer.hip', 'td_backward.hip', 'td_noalloc.hip']
+           'td_layer.hip', 'td_backward.hip', 'td_noalloc.hip', 'td_probe.hip']
 
 # per-source additions: the direct-to-LDS GEMM keeps its MFMA accumulators in architectural VGPRs (in the
 # accumulator-register form the compiler copies every accumulator through a temporary in the inner loop)

@@ -43,6 +43,8 @@ SIGNATURES = {
     'td_weight_grad': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     'td_value_proj_plan': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64]),
     'td_project_forward_noalloc': (_int, [_int] + [_vp] * 8 + [_int, _vp] + [_i64] * 8 + [_vp]),
+    'td_probe_empty': (_int, [_i64, _vp]),
+    'td_probe_gather': (_int, [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
 }
 
 TD_E_WORKSPACE = -4  # td_layer_fused_forward: the problem needs loc_out / attn_out
@@ -677,3 +679,25 @@ def layer_sample_forward(value, heads, spatial_shapes, level_start_index, loc, a
                                         lc.data_ptr(), aw.data_ptr(), _ptr(mask), out.data_ptr(), B, Q, N, H, HD // H,
                                         L, P, _stream(dev)))
     return out
+
+
+# ---- measurement kernels (not part of the operator; the benchmark's calibration) ----------------------------------
+
+def probe_empty(launches, device=None):
+    """`launches` launches of an empty kernel on the current stream of `device` (td_probe_empty)."""
+    lib_ = _require()
+    dev = torch.device('cuda', torch.cuda.current_device()) if device is None else torch.device(device)
+    _check(lib_.td_probe_empty(launches, _stream(dev)))
+
+
+def probe_gather(buf, row_bytes, loads_per_lane, workgroups, waves, sink):
+    """One launch of the random-row gather probe over the bytes of `buf` (td_probe_gather); returns the bytes it
+    reads. sink: an int32 tensor of at least `workgroups` elements on the same device."""
+    lib_ = _require()
+    if not buf.is_cuda or not buf.is_contiguous() or sink.device != buf.device or sink.numel() < workgroups or \
+            sink.element_size() != 4:
+        raise RuntimeError('probe_gather: contiguous device buffer and a 32-bit sink of one word per workgroup')
+    nbytes = buf.numel() * buf.element_size()
+    _check(lib_.td_probe_gather(buf.data_ptr(), nbytes, row_bytes, loads_per_lane, workgroups, waves,
+                                sink.data_ptr(), _stream(buf.device)))
+    return workgroups * waves * 64 * loads_per_lane * 16
