@@ -361,25 +361,58 @@ def pmc_run(dev, H, steps):
 
 
 def auto_grid():
-    """The shapes the auto selector is fitted on: RT-DETR 640 (the reference's bench grid: 3 dtypes x batch 1/4/8
-    x 50..900 queries, and batch 2 in 16 bits), a C=512 model (batch 1/2/4), DINO 4-level and the C=1024 / 64-sample
-    limit shape."""
+    """The shapes the auto selector is fitted on:
+      * RT-DETR 640 (the reference's bench grid: 3 dtypes x batch 1/4/8 x 50..900 queries; batch 2 in 16 bits), a
+        C = 512 model (batch 1/2/4), DINO 4-level and the C = 1024 / 64-sample limit shape;
+      * RT-DETR 640 at 150/450/750 queries and batch 2/3/6 in all three dtypes, uniform and clustered locations;
+        C = 512 at those query counts; a five-level map; C = 768 (12 heads of 64);
+      * other widths and level layouts: C = 128 (4 heads of 32), C = 320 (10 heads of 32: rows under a wavefront),
+        C = 896 (14 heads of 64), one and two levels with 8 and 16 points, in 16 bits and float32; C = 448, 576 and
+        704 on DINO 4-level and five-level maps in 16 bits."""
+    five = [(100, 100), (50, 50), (25, 25), (13, 13), (7, 7)]
     cases = []
     for dt in (torch.float32, torch.float16, torch.bfloat16):
         for B in (1, 4, 8):
             for Q in (50, 100, 200, 300, 600, 900):
                 cases.append(('rtdetr640', B, Q, 8, 32, 256, RTDETR_LEVELS, 4, dt, True, 'uniform'))
+        for B in (2, 3, 6):
+            for Q in (150, 450, 750):
+                for ld in ('uniform', 'clustered'):
+                    cases.append(('rtdetr640', B, Q, 8, 32, 256, RTDETR_LEVELS, 4, dt, True, ld))
     for dt in (torch.float16, torch.bfloat16):
         for Q in (100, 300, 600, 900):
             cases.append(('rtdetr640', 2, Q, 8, 32, 256, RTDETR_LEVELS, 4, dt, True, 'uniform'))
         for B in (1, 2, 4):
             for Q in (100, 300, 600, 900):
                 cases.append(('c512', B, Q, 8, 64, 512, RTDETR_LEVELS, 4, dt, True, 'uniform'))
+        for B in (1, 2, 3, 6):
+            for Q in (150, 450, 750):
+                cases.append(('c512', B, Q, 8, 64, 512, RTDETR_LEVELS, 4, dt, True, 'uniform'))
         for B, Q in ((1, 300), (4, 300), (4, 900), (8, 900)):
             cases.append(('dino4l', B, Q, 8, 32, 256, DINO_LEVELS, 4, dt, True, 'outside10'))
+        for B in (1, 2, 5):
+            for Q in (150, 450, 750):
+                cases.append(('c768', B, Q, 12, 64, 768, RTDETR_LEVELS, 4, dt, True, 'uniform'))
+    for dt in (torch.float32, torch.float16):
+        for B in (1, 3):
+            for Q in (150, 450, 750):
+                cases.append(('five-level', B, Q, 8, 32, 256, five, 4, dt, True, 'uniform'))
     for Q in (50, 300, 900):
         for B in (1, 2):
             cases.append(('limit', B, Q, 16, 64, 1024, LIMIT_LEVELS, 16, torch.bfloat16, False, 'uniform'))
+    for dt in (torch.float32, torch.float16, torch.bfloat16):
+        for B, Q in ((1, 100), (1, 600), (2, 300), (4, 300), (8, 600)):
+            cases.append(('c128', B, Q, 4, 32, 128, RTDETR_LEVELS, 4, dt, True, 'uniform'))
+            cases.append(('c320', B, Q, 10, 32, 320, RTDETR_LEVELS, 4, dt, True, 'uniform'))
+            cases.append(('one-level-p16', B, Q, 8, 32, 256, [(60, 80)], 16, dt, True, 'uniform'))
+            cases.append(('two-level-p8', B, Q, 8, 32, 256, [(64, 64), (32, 32)], 8, dt, True, 'uniform'))
+        for B, Q in ((1, 300), (2, 300), (3, 600)):
+            cases.append(('c896', B, Q, 14, 64, 896, RTDETR_LEVELS, 4, dt, True, 'uniform'))
+    for dt in (torch.float16, torch.bfloat16):
+        for C, H, D in ((448, 14, 32), (576, 9, 64), (704, 11, 64)):
+            for levels, lname in ((DINO_LEVELS, 'dino4l'), (five, 'five-level')):
+                for B, Q in ((1, 200), (2, 400), (4, 800), (6, 200)):
+                    cases.append((f'{lname} c{C}', B, Q, H, D, C, levels, 4, dt, True, 'uniform'))
     return cases
 
 
@@ -396,41 +429,38 @@ def measure_grid(cases):
             N, L = dev[0].shape[1], len(levels)
             steps = 100 if B * Q * C < 2_000_000 else 20
             t = {m: graph_time_us(lambda m=m: td.ma_deform_attn(*dev, mode=m), steps, 5) for m in ('fused', 'project')}
+            # the project path's halves on their own (the kernels td_project_forward runs)
+            proj, smp = project_halves(dev, H, D, dt)
+            value = proj()
+            t['gemm'] = graph_time_us(proj, steps, 5)
+            t['sample'] = graph_time_us(lambda: smp(value), steps, 5)
+            del value
             cur = td.choose_mode(dev[0], dev[1], dev[5])
-            best = min(t.values())
+            best = min(t['fused'], t['project'])
             rows.append(dict(case=name, dtype=DTYPE_NAMES[dt], B=B, Q=Q, H=H, D=D, C=C, N=N, L=L, P=P, loc=ld,
-                             s=dev[0].element_size(), fused=t['fused'], project=t['project'], current_pick=cur,
-                             current_loss=round(t[cur] / best, 3)))
+                             s=dev[0].element_size(), fused=t['fused'], project=t['project'], gemm=t['gemm'],
+                             sample=t['sample'], current_pick=cur, current_loss=round(t[cur] / best, 3)))
             log(f'{name:9s} {DTYPE_NAMES[dt]:4s} B={B} Q={Q:3d} {ld:9s} fused {t["fused"]:8.2f} project '
-                f'{t["project"]:8.2f} auto picks {cur} ({t[cur] / best:.3f} of the faster)')
+                f'{t["project"]:8.2f} (gemm {t["gemm"]:7.2f}, sample {t["sample"]:7.2f}) auto picks {cur} '
+                f'({t[cur] / best:.3f} of the faster)')
             del dev
             torch.cuda.empty_cache()
     return rows
 
 
 def holdout_grid():
-    """Shapes the auto selector was not fitted on: query counts (150/450/750), batch sizes (2/3/6 for RT-DETR), a
-    channel width never fitted (C=768, 12 heads), a level count (5) and a location distribution (clustered) outside
-    auto_grid()."""
+    """Shapes the auto selector is not fitted on: 250/500/1000 queries, batch 5 and 7, widths 384 (12 heads of 32)
+    and 640 (10 heads of 64), four- and five-level maps, uniform and clustered locations, in float16 and bfloat16."""
+    four = [(100, 167), (50, 84), (25, 42), (13, 21)]
     five = [(100, 100), (50, 50), (25, 25), (13, 13), (7, 7)]
     cases = []
-    for dt in (torch.float32, torch.float16, torch.bfloat16):
-        for B in (2, 3, 6):
-            for Q in (150, 450, 750):
-                for ld in ('uniform', 'clustered'):
-                    cases.append(('rtdetr640', B, Q, 8, 32, 256, RTDETR_LEVELS, 4, dt, True, ld))
     for dt in (torch.float16, torch.bfloat16):
-        for B in (1, 2, 3, 6):
-            for Q in (150, 450, 750):
-                cases.append(('c512', B, Q, 8, 64, 512, RTDETR_LEVELS, 4, dt, True, 'uniform'))
-    for dt in (torch.float32, torch.float16):
-        for B in (1, 3):
-            for Q in (150, 450, 750):
-                cases.append(('five-level', B, Q, 8, 32, 256, five, 4, dt, True, 'uniform'))
-    for dt in (torch.float16, torch.bfloat16):
-        for B in (1, 2, 5):
-            for Q in (150, 450, 750):
-                cases.append(('c768', B, Q, 12, 64, 768, RTDETR_LEVELS, 4, dt, True, 'uniform'))
+        for C, H, D in ((384, 12, 32), (640, 10, 64)):
+            for levels, lname in ((four, 'four-level'), (five, 'five-level')):
+                for B in (5, 7):
+                    for Q in (250, 500, 1000):
+                        for ld in ('uniform', 'clustered'):
+                            cases.append((f'{lname} c{C}', B, Q, H, D, C, levels, 4, dt, True, ld))
     return cases
 
 
@@ -448,38 +478,67 @@ def holdout(out_path):
                    'cases': len(rows)}, f, indent=1)
 
 
-def fit_auto(out_path):
-    """Measure both modes over auto_grid(), fit FUSED_LIMIT's linear cost model per dtype family by non-negative
-    least squares on relative error, and report every case's loss of the fitted and the current selector."""
+def fit_table(rows):
+    """FUSED_LIMIT's per-dtype cost lines from measured rows: the fused, GEMM and sampler terms of cost_features each
+    fitted to their kernel's time by non-negative least squares on relative error, then project mode's gap (what the
+    pair costs beyond its two kernels timed apart: the hand-over, and the sampler reading values the GEMM has just
+    written rather than a warm copy) over gap_features, by the same method against the measured project time. One
+    table for float32, one shared by float16 and bfloat16."""
     import numpy as np
     from scipy.optimize import nnls
-    rows = measure_grid(auto_grid())
     table = {}
     for fam in (('f32',), ('f16', 'bf16')):
         xs = [r for r in rows if r['dtype'] in fam]
+        if not xs:
+            continue
         feats = [cost_features(r['B'], r['Q'], r['H'], r['D'], r['C'], r['N'], r['L'], r['P'], r['s']) for r in xs]
-        Ff = np.array([f[0] for f in feats])
-        Fp = np.array([f[1] for f in feats])
-        tf = np.array([r['fused'] for r in xs])
+        coef = {}
+        for i, key in enumerate(('fused', 'gemm', 'sample')):
+            F = np.array([f[i] for f in feats])
+            t = np.array([r[key] for r in xs])
+            coef[key], _ = nnls(F / t[:, None], np.ones(len(xs)))
+        pred = np.array([np.dot(coef['gemm'], f[1]) + np.dot(coef['sample'], f[2]) for f in feats])
         tp = np.array([r['project'] for r in xs])
-        cf, _ = nnls(Ff / tf[:, None], np.ones(len(xs)))
-        cp, _ = nnls(Fp / tp[:, None], np.ones(len(xs)))
+        G = np.array([td.gap_features(r['B'], r['Q'], r['N'], r['H'], r['D'], r['L'], r['P'], r['s']) for r in xs])
+        gap, _ = nnls(G / tp[:, None], 1.0 - pred / tp)
+        entry = {k: [round(float(c), 4) for c in v] for k, v in coef.items()}
+        entry['gap'] = [round(float(c), 4) for c in gap]
         for fd in fam:
-            table[fd] = {'fused': [round(float(c), 4) for c in cf], 'project': [round(float(c), 4) for c in cp]}
-        for r, a, b in zip(xs, Ff @ cf, Fp @ cp):
-            r['fitted_pick'] = 'fused' if a <= b else 'project'
+            table[fd] = entry
+    return table
+
+
+def score(rows, table):
+    """Each row's pick under `table` and its loss (time of the pick / time of the faster mode)."""
+    def dot(c, x):
+        return sum(a * b for a, b in zip(c, x))
     for r in rows:
-        best = min(r['fused'], r['project'])
-        r['fitted_loss'] = round(r[r['fitted_pick']] / best, 3)
+        coef = table[r['dtype']]
+        ff, fg, fs = cost_features(r['B'], r['Q'], r['H'], r['D'], r['C'], r['N'], r['L'], r['P'], r['s'])
+        pf = dot(coef['fused'], ff)
+        pp = dot(coef['gemm'], fg) + dot(coef['sample'], fs) + dot(
+            coef['gap'], td.gap_features(r['B'], r['Q'], r['N'], r['H'], r['D'], r['L'], r['P'], r['s']))
+        r['fitted_pick'] = 'fused' if pf <= pp else 'project'
+        r['fitted_loss'] = round(r[r['fitted_pick']] / min(r['fused'], r['project']), 3)
+        r['predicted'] = {'fused': round(pf, 2), 'project': round(pp, 2)}
+    return rows
+
+
+def fit_auto(out_path):
+    """Measure both modes and the project path's two kernels over auto_grid(), fit the cost lines (fit_table), and
+    report every case's loss under the fitted and the current selector."""
+    rows = measure_grid(auto_grid())
+    table = fit_table(rows)
+    score(rows, table)
     worst_fit = max(r['fitted_loss'] for r in rows)
     worst_cur = max(r['current_loss'] for r in rows)
-    within = sum(r['current_loss'] <= 1.10 for r in rows)
+    within = sum(r['fitted_loss'] <= 1.10 for r in rows)
     log(f'fitted table: {json.dumps(table)}')
-    log(f'worst auto/best ratio: fitted {worst_fit:.3f}, current table {worst_cur:.3f}; '
-        f'current within 10%: {within}/{len(rows)}')
+    log(f'worst auto/best ratio: fitted {worst_fit:.3f} ({within}/{len(rows)} within 10%), current table '
+        f'{worst_cur:.3f}')
     with open(out_path, 'w') as f:
         json.dump({'table': table, 'rows': rows, 'worst_fitted': worst_fit, 'worst_current': worst_cur,
-                   'current_within_10pct': within, 'cases': len(rows)}, f, indent=1)
+                   'fitted_within_10pct': within, 'cases': len(rows)}, f, indent=1)
 
 
 def table(args):

@@ -229,6 +229,23 @@ int td_value_proj_plan(int dtype, const void* memory, const void* weight, const 
                        int64_t M, int64_t K, int64_t NO, int64_t head_major_N, int64_t H);
 
 /*
+ * Launch shapes the size rules of td_fused_forward and td_sample_forward pick for these sizes, written to plan[8]
+ * without launching anything or reading memory (aligned = 1: operands on 16-byte boundaries, the usual case). No
+ * counterpart in the reference; the auto selector's cost model (choose_mode) is built on them, as the kernels' time
+ * follows the rows their busiest CUs hold.
+ *   td_fused_plan:  plan = {kernel (0 vector, 1 generic, -1 none), workgroups, wavefronts per workgroup, rows per
+ *                   workgroup, balanced slices per head (0: query tiles), rows of the largest workgroup, corner
+ *                   groups per row, corner loads in flight per lane}
+ *   td_sample_plan: plan = {workgroups (-1 in plan[0]: none), wavefronts per workgroup, rows per workgroup, corner
+ *                   groups per row, elements per load, 1 when rows go in (b, h, q) order, corner loads in flight per
+ *                   lane, 0}; head_major = 1 for the [B, H, N, D] value layout of td_sample_forward_heads.
+ */
+int td_fused_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t C, int64_t H, int64_t D, int64_t L, int64_t P,
+                  int aligned, int64_t* plan);
+int td_sample_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D, int64_t L, int64_t P,
+                   int head_major, int aligned, int64_t* plan);
+
+/*
  * Backward (training). No counterpart in the reference, whose operator is inference only (README.md:61); these are
  * the gradients of its reference computation (reference.py:13-40: value = memory . W^T + b, then bilinear
  * grid_sample with zero padding, align_corners=False, weighted by the attention), for callers that train through

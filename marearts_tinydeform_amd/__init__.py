@@ -6,6 +6,7 @@ libtinydeform.so; CPU tensors run the PyTorch reference path. Inference only.
 """
 
 import functools
+import math
 
 import torch
 
@@ -13,51 +14,134 @@ from . import _native
 from .reference import layer_locations_reference, ma_deform_attn_layer_reference, ma_deform_attn_reference
 
 __all__ = ['ma_deform_attn', 'ma_deform_attn_reference', 'choose_mode', 'ma_deform_sample', 'ma_deform_sample_v2',
-           'predict_us', 'cost_features', 'ma_deform_attn_layer', 'ma_deform_attn_layer_reference', 'layer_locations_reference',
+           'predict_us', 'cost_features', 'gap_features', 'ma_deform_attn_layer', 'ma_deform_attn_layer_reference', 'layer_locations_reference',
            'MSDeformAttnLayer', 'ma_deform_attn_train', 'ma_deform_sample_train']
-__version__ = '0.1.0'
+__version__ = '0.1.1'  # the version of the reference API this package implements (marearts_tinydeform 0.1.1)
 
 MODES = ('auto', 'fused', 'project')
 
 # 'auto' compares predicted times of the two orders (reference marearts_tinydeform/__init__.py:21-46 uses one
 # threshold on queries * levels * points * 4 / (tokens * head_dim); on MI355X the value GEMM is cheap next to
-# gathering C-wide rows, so the crossover also moves with C and one threshold cannot place it). Per dtype, each
-# mode's time in µs is a linear function of the work it does (cost_features), fitted to MI355X (gfx950)
-# measurements of both modes (bench.py --fit-auto: RT-DETR 640 shapes at batch 1/2/4/8 and 50..900 queries, C = 512
-# at batch 1/2/4, DINO 4-level and C = 1024 shapes; checked on shapes outside that grid with bench.py --holdout).
-# The coefficients were kept when the deep-K GEMM became persistent 256 x 256 tiles (and gemm_rounds_k began counting
-# them): a refit on the new measurements matched them on the fit grid (worst auto/best 1.044) and did worse on the
-# held-out grid (1.36 against 1.07). When the fused kernel's projection took every N tile per job (3-4% faster at
-# small problems), the 16-bit fused line was scaled by 0.96, and when both gathers moved to buffer loads with
-# multiply-high index arithmetic (fused 10-17% faster, the sampler 15-30%) by 0.90 more: every case of the fit grid
-# within 10% again (worst 1.094; unscaled 1.123) and 101 to 103 of the 108 held-out cases over two runs (unscaled
-# 101; a least-squares refit 99).
-#   fused   = f0 + f1 * gathered_mb
-#   project = p0 + p1 * gemm_mb + p2 * gemm_gflop + p3 * gemm_rounds_k + p4 * sample_mb
+# gathering C-wide rows, so the crossover also moves with C and one threshold cannot place it). Per dtype, the fused
+# kernel's time, the value GEMM's and the sampler's are each a linear function of terms that follow the kernels' own
+# launch shapes (cost_features: the library's size rules, td_fused_plan / td_sample_plan / td_value_proj_plan, give
+# the rows and tiles the busiest CU holds), and project mode is the GEMM plus the sampler plus a fitted gap. The
+# coefficients are fitted by bench.py --fit-auto to MI355X (gfx950) measurements of the three kernels and both modes
+# and checked on a grid of shapes the fit never saw (bench.py --holdout).
 FUSED_LIMIT = {
-    torch.float32: {'fused': (7.4791, 0.0478), 'project': (13.9906, 0.6181, 0.0000, 0.0000, 0.0877)},
-    torch.float16: {'fused': (4.9276, 0.0503), 'project': (11.5020, 0.1554, 0.0000, 10.1974, 0.0925)},
-    torch.bfloat16: {'fused': (4.9276, 0.0503), 'project': (11.5020, 0.1554, 0.0000, 10.1974, 0.0925)},
+    torch.float32: {'fused': (3.7445, 7.6027, 0.0, 7.5341, 8.5712, 0.0, 0.4613, 0.0809, 3.7466),
+                    'gemm': (3.358, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 9.0783, 0.0612, 0.6669, 8.083),
+                    'sample': (2.6256, 0.0528, 0.0, 0.0134, 0.1157),
+                    'gap': (0.408, 0.0131, 0.1278, 0.0015)},
+    torch.float16: {'fused': (3.5241, 8.2634, 0.0, 7.7144, 8.1228, 0.0, 0.4747, 0.1105, 1.7771),
+                    'gemm': (4.2365, 0.1527, 1.1673, 0.1162, 0.0, 16.3373, 0.1835, 0.0, 0.0, 0.0, 0.0),
+                    'sample': (2.8545, 0.056, 0.0, 0.0424, 0.0063),
+                    'gap': (0.7467, 0.0183, 0.0619, 0.0436)},
 }
+FUSED_LIMIT[torch.bfloat16] = FUSED_LIMIT[torch.float16]
+# The reference's table for GPUs of compute capability below 8 (marearts_tinydeform/__init__.py:30), kept so that code
+# written against that module finds it. An (a, b) entry is the reference's rule: 'fused' while
+# Q * L * P * 4 / (N * D) < a + b / B. No AMD GPU reports such a capability, so _limits never returns it here; a caller
+# may also put (a, b) entries into FUSED_LIMIT to get the reference's rule back.
+FUSED_LIMIT_SM75 = {torch.float32: (0.068, 0.0), torch.float16: (0.020, 0.0), torch.bfloat16: (0.132, 0.0)}
+
+CUS, XCDS, L2_BYTES = 256, 8, 4 << 20  # MI355X: compute units, XCDs (each with its own L2), L2 bytes per XCD
+_PLAN_DTYPE = {2: torch.float16, 4: torch.float32, 8: torch.float64}  # the size rules depend on the element size
+# output tile (rows x columns) of each register- and LDS-tiled value-GEMM variant (td_gemm.hip pick_variant)
+_GEMM_TILES = {2: (64, 128), 5: (64, 64), 9: (128, 128), 13: (128, 128), 23: (64, 32), 24: (32, 32), 25: (64, 64)}
 
 
-def cost_features(B, Q, H, D, C, N, L, P, s):
-    """The work each mode does, the terms of its cost line: ([1, gathered_mb], [1, gemm_mb, gemm_gflop,
-    gemm_rounds_k, sample_mb]) with s the element size in bytes:
-      gathered_mb    B*Q*H*L*P*4*C*s / 1e6   C-wide corner rows read by 'fused'
-      gemm_mb        B*N*(C + H*D)*s / 1e6   value GEMM traffic of 'project'
-      gemm_gflop     2*B*N*C*H*D / 1e9       value GEMM work of 'project' for C < 512 (the bandwidth-bound kernels)
-      gemm_rounds_k  rounds of 256 x 256 output tiles over MI355X's 256 CUs, times C / 1e3, for C >= 512 (the
-                     direct-to-LDS kernels, whose time goes by the busiest CU's count of tiles, each as long as K)
-      sample_mb      B*Q*H*L*P*4*D*s / 1e6   D-wide corner rows read by 'project'"""
-    samples = B * Q * H * L * P * 4
-    HD, M = H * D, B * N
-    if C >= 512:
-        tiles = -(-M // 256) * -(-HD // 256)
-        narrow, deep = 0.0, -(-tiles // 256) * C / 1e3
-    else:
-        narrow, deep = 2 * M * C * HD / 1e9, 0.0
-    return ([1.0, samples * C * s / 1e6], [1.0, M * (C + HD) * s / 1e6, narrow, deep, samples * D * s / 1e6])
+def _rows_touched(N, L, B, Q, H, P):
+    """Expected memory rows one XCD reads in one launch for uniformly spread locations: the kernels deal (image,
+    query) rows to the XCDs in contiguous ranges, so an XCD samples ceil(B / 8) images, each level l (sizes taken to
+    shrink 4x per level, as in FPN-style maps) receiving that XCD's share of the rows' 4 P corner reads."""
+    if N <= 0 or L <= 0:
+        return 0.0
+    w = [4.0 ** -l for l in range(L)]
+    imgs = max(1, -(-B // XCDS))
+    reads = B * Q * H * P * 4 / XCDS / imgs
+    return imgs * sum(n * -math.expm1(-reads / n) for n in (N * x / sum(w) for x in w))
+
+
+def _beyond_l2(per_xcd_mb, fill_mb):
+    """The share of an XCD's gathered bytes whose rows do not fit its L2."""
+    return per_xcd_mb * max(0.0, 1.0 - L2_BYTES / 1e6 / fill_mb) if fill_mb > 0 else 0.0
+
+
+def gap_features(B, Q, N, H, D, L, P, s):
+    """Terms of what project mode costs beyond its GEMM and sampler timed apart: [1, value_mb, warm_sample_mb,
+    warm_rows_mb]. value_mb: the projected values the GEMM writes and the sampler then reads. Timed alone, the sampler
+    finds values that fit the XCDs' L2s (8 x 4 MB) still cached from its previous launch; after the GEMM it reads them
+    from further out: warm_sample_mb, its corner reads, and warm_rows_mb, the value rows its XCDs touch, each times
+    the share of the values those L2s could hold."""
+    value = B * N * H * D * s
+    warm = max(0.0, 1.0 - value / (XCDS * L2_BYTES))
+    return [1.0, value / 1e6, B * Q * H * L * P * 4 * D * s / 1e6 * warm,
+            XCDS * _rows_touched(N, L, B, Q, H, P) * H * D * s / 1e6 * warm]
+
+
+def cost_features(B, Q, H, D, C, N, L, P, s, aligned=True):
+    """The terms of each kernel's cost line, from the kernels' launch shapes (s: the element size in bytes):
+      fused  [1, slices_mb, two_mb, tiles_mb, wide_mb, generic_mb, fill_mb, spill_mb, proj_mflop]
+        *_mb      the C-wide corner rows the busiest CU gathers (its workgroups times the rows of the largest), in the
+                  slot of the launch shape the fused size rule picks: balanced slices of one wavefront per row, rows
+                  of two wavefronts, query tiles, rows wider than a wavefront, the generic kernel
+        fill_mb   memory rows each XCD's L2 pulls in per launch (_rows_touched)
+        spill_mb  gathered bytes per XCD whose rows do not fit its L2
+        proj_mflop the busiest CU's projection work, its workgroups' rows (at least one 16-row MFMA tile each) x C x D
+      gemm   [1, stream_mb, tiled_busy_gflop, tiled_mb, deep_rounds, deep_rounds_k, deep_mb, f32_busy_gflop, f32_mb,
+              other_gflop, f32_direct_busy_gflop]
+        terms of the kernel the value-projection size rule picks: the streaming kernel's bytes in whole 32-token steps
+        per CU; the tiled 16-bit kernels' flops in the busiest CU's tile count (times the CU count) and their bytes;
+        the deep-K direct-to-LDS kernels' tile rounds on the busiest CU, those times K / 1e3, and their bytes;
+        float32 tiles (busiest CU and bytes, as for 16 bits; the 64 x 128 tiles that read A straight from memory in a
+        slot of their own); the flops of the float32 and generic kernels
+      sample [1, sample_mb, busy_mb, fill_mb, spill_mb]
+        the D-wide corner rows the sampler reads, those of its busiest CU, value rows each XCD's L2 pulls in, and the
+        gathered bytes per XCD beyond its L2"""
+    S = 4 * L * P
+    pdt = _PLAN_DTYPE.get(s, torch.float32)
+    touched = _rows_touched(N, L, B, Q, H, P)
+    per_xcd = B * Q * H * S / XCDS
+    fp = _native.fused_plan(pdt, B, Q, N, C, H, D, L, P, aligned)
+    fused = [1.0] + [0.0] * 8
+    if fp[0] >= 0:
+        lanes = fp[6] * (C * s // 16)
+        cls = 4 if fp[0] == 1 else 3 if lanes > 64 else 2 if fp[4] == 0 else 1 if lanes == 128 else 0
+        fused[1 + cls] = -(-fp[1] // CUS) * fp[5] * S * C * s / 1e6
+        fused[6] = touched * C * s / 1e6
+        fused[7] = _beyond_l2(per_xcd * C * s / 1e6, fused[6])
+        fused[8] = -(-fp[1] // CUS) * max(fp[5], 16) * C * D * 2 / 1e6
+    M, K, NO = B * N, C, H * D
+    hm = s in (2, 4) and D * s <= 64 and D * s % 16 == 0  # td_project_forward's head-major value
+    v = _native.value_proj_plan(pdt, M, K, NO, heads=H if hm else None, N=N if hm else None) if M * NO > 0 else -1
+    mb, gf = M * (K + NO) * s / 1e6, 2.0 * M * K * NO / 1e9
+    gemm = [1.0] + [0.0] * 10
+    if v == 22:
+        gemm[1] = -(-(-(-M // CUS)) // 32) * 32 * (K + NO) * s * CUS / 1e6
+    elif v in (14, 18):
+        mt, nt = -(-M // 256), -(-NO // 256)
+        per = -(-(mt * nt) // XCDS)
+        G = min((CUS // XCDS) // nt * nt, -(-per // nt) * nt)
+        rounds = -(-per // G) if v == 18 and G > 0 else -(-(mt * -(-NO // 128)) // (2 * CUS))
+        gemm[4], gemm[5], gemm[6] = rounds, rounds * K / 1e3, mb
+    elif v in _GEMM_TILES:
+        tm, tn = _GEMM_TILES[v]
+        busy = -(-(-(-M // tm) * -(-NO // tn)) // CUS) * tm * tn * K * 2.0 * CUS / 1e9
+        if s == 2:
+            gemm[2], gemm[3] = busy, mb
+        else:
+            gemm[7 if v != 2 else 10], gemm[8], gemm[9] = busy, mb, gf
+    elif v >= 0:
+        gemm[9] = gf
+    sample = [1.0, 0.0, 0.0, 0.0, 0.0]
+    sp = _native.sample_plan(pdt, B, Q, N, H, D, L, P, hm) if M * NO > 0 else [-1] * 8
+    if sp[0] >= 0:
+        sample[1] = B * Q * H * S * D * s / 1e6
+        sample[2] = -(-sp[0] // CUS) * sp[2] * S * D * s / 1e6
+        sample[3] = touched * H * D * s / 1e6
+        sample[4] = _beyond_l2(per_xcd * D * s / 1e6, sample[3])
+    return fused, gemm, sample
 
 
 # cost tables by GPU architecture (gcnArchName without feature suffixes)
@@ -70,7 +154,16 @@ def _arch(device_index):
 
 @functools.lru_cache(maxsize=None)
 def _limits(device_index):
-    return ARCH_LIMITS.get(_arch(device_index), FUSED_LIMIT)
+    """The cost table of a device: FUSED_LIMIT_SM75 below compute capability 8, as the reference chooses
+    (marearts_tinydeform/__init__.py:33-36), otherwise the table of its architecture (gcnArchName), else
+    FUSED_LIMIT."""
+    major, _ = torch.cuda.get_device_capability(device_index)
+    if major < 8:
+        return FUSED_LIMIT_SM75
+    try:
+        return ARCH_LIMITS.get(_arch(device_index), FUSED_LIMIT)
+    except (RuntimeError, AssertionError, AttributeError):  # no device properties (a CPU-only process)
+        return FUSED_LIMIT
 
 
 def predict_us(memory, value_weight, sampling_locations, table=None):
@@ -79,22 +172,43 @@ def predict_us(memory, value_weight, sampling_locations, table=None):
     return _predict(memory, value_weight, Q, H, L, P, table)
 
 
+def _coef(memory, table=None):
+    if table is None:
+        table = _limits(memory.get_device()) if memory.is_cuda else FUSED_LIMIT
+    return table.get(memory.dtype, table[torch.float16])
+
+
 def _predict(memory, value_weight, Q, H, L, P, table=None):
     B, N, C = memory.shape
     HD = value_weight.shape[0]
     D = HD // max(H, 1)
     s = memory.element_size()
-    if table is None:
-        table = _limits(memory.get_device()) if memory.is_cuda else FUSED_LIMIT
-    coef = table.get(memory.dtype, table[torch.float16])
-    ff, fp = cost_features(B, Q, H, D, C, N, L, P, s)
-    return {'fused': sum(c * x for c, x in zip(coef['fused'], ff)),
-            'project': sum(c * x for c, x in zip(coef['project'], fp))}
+    coef = _coef(memory, table)
+    if isinstance(coef, tuple):
+        raise ValueError('a threshold table (a, b) gives a mode, not times: use choose_mode')
+    aligned = (memory.data_ptr() | value_weight.data_ptr()) % 16 == 0
+    ff, fg, fs = cost_features(B, Q, H, D, C, N, L, P, s, aligned)
+    def dot(c, x):
+        return sum(a * b for a, b in zip(c, x))
+    return {'fused': dot(coef['fused'], ff),
+            'project': dot(coef['gemm'], fg) + dot(coef['sample'], fs) +
+                       dot(coef['gap'], gap_features(B, Q, N, H, D, L, P, s))}
 
 
 def choose_mode(memory, value_weight, sampling_locations):
     """The mode 'auto' runs: 'fused' for few queries per image, 'project' (project every token first) for many."""
-    t = predict_us(memory, value_weight, sampling_locations)
+    _, Q, H, L, P, _ = sampling_locations.shape
+    return _pick(memory, value_weight, Q, H, L, P)
+
+
+def _pick(memory, value_weight, Q, H, L, P):
+    coef = _coef(memory)
+    if isinstance(coef, tuple):  # a reference-style threshold (a, b)
+        B, N, _ = memory.shape
+        D = value_weight.shape[0] // max(H, 1)
+        a, b = coef
+        return 'fused' if Q * L * P * 4 / max(N * D, 1) < a + b / max(B, 1) else 'project'
+    t = _predict(memory, value_weight, Q, H, L, P)
     return 'fused' if t['fused'] <= t['project'] else 'project'
 
 
@@ -225,8 +339,7 @@ def _layer(hidden_states, memory, reference_points, spatial_shapes, level_start_
     B, Q, Cq, H, L, P = _native.check_layer(memory, hidden_states, reference_points, ow, ob, aw, ab, position,
                                             spatial_shapes, num_heads, num_points)
     if mode == 'auto':
-        t = _predict(memory, value_weight, Q, H, L, P)
-        mode = 'fused' if t['fused'] <= t['project'] else 'project'
+        mode = _pick(memory, value_weight, Q, H, L, P)
     if mode == 'fused':
         core, la = _native.layer_fused_forward(hidden_states, position, reference_points, ow, ob, aw, ab, memory,
                                                value_weight, value_bias, spatial_shapes, level_start_index, H, P,

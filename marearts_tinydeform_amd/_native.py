@@ -43,6 +43,8 @@ SIGNATURES = {
     'td_weight_grad': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     'td_value_proj_plan': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64]),
     'td_project_forward_noalloc': (_int, [_int] + [_vp] * 8 + [_int, _vp] + [_i64] * 8 + [_vp]),
+    'td_fused_plan': (_int, [_int] + [_i64] * 8 + [_int, _vp]),
+    'td_sample_plan': (_int, [_int] + [_i64] * 7 + [_int, _int, _vp]),
     'td_probe_empty': (_int, [_i64, _vp]),
     'td_probe_gather': (_int, [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
 }
@@ -701,3 +703,26 @@ def probe_gather(buf, row_bytes, loads_per_lane, workgroups, waves, sink):
     _check(lib_.td_probe_gather(buf.data_ptr(), nbytes, row_bytes, loads_per_lane, workgroups, waves,
                                 sink.data_ptr(), _stream(buf.device)))
     return workgroups * waves * 64 * loads_per_lane * 16
+
+
+# ---- launch plans (the kernels' size rules, evaluated without launching; no device needed) -----------------------
+
+def fused_plan(dtype, B, Q, N, C, H, D, L, P, aligned=True):
+    """td_fused_plan: [kernel (0 vector, 1 generic, -1 none), workgroups, wavefronts per workgroup, rows per
+    workgroup, balanced slices per head (0: query tiles), rows of the largest workgroup, corner groups per row,
+    corner loads in flight per lane]."""
+    lib_ = _require()
+    out = (ctypes.c_int64 * 8)()
+    _check(lib_.td_fused_plan(DTYPE_CODES[dtype], B, Q, N, C, H, D, L, P, 1 if aligned else 0, out))
+    return list(out)
+
+
+def sample_plan(dtype, B, Q, N, H, D, L, P, head_major=False, aligned=True):
+    """td_sample_plan: [workgroups (-1: none), wavefronts per workgroup, rows per workgroup, corner groups per row,
+    elements per load, 1 for rows in (b, h, q) order, corner loads in flight per lane, 0]."""
+    lib_ = _require()
+    out = (ctypes.c_int64 * 8)()
+    _check(lib_.td_sample_plan(DTYPE_CODES[dtype], B, Q, N, H, D, L, P, 1 if head_major else 0,
+                               1 if aligned else 0, out))
+    return list(out)
+

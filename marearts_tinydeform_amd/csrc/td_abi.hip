@@ -108,6 +108,71 @@ extern "C" int td_version(void) { return 100; }
 
 extern "C" const char* td_last_error(void) { return g_last_error.c_str(); }
 
+namespace {
+
+// Sizes a plan query accepts: those the forward entries accept (check_geometry without the pointers).
+int check_plan_sizes(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D, int64_t L, int64_t P,
+                     int64_t* plan) {
+    g_last_error.clear();
+    if (plan == nullptr) return set_error(TD_E_ARG, "null pointer argument");
+    for (int i = 0; i < 8; ++i) plan[i] = 0;
+    if (!dtype_ok(dtype)) return set_error(TD_E_DTYPE, "unknown dtype code %d", dtype);
+    if (B < 0 || Q < 0 || N < 0 || H <= 0 || D < 0 || L < 0 || P < 0) return set_error(TD_E_ARG, "invalid sizes");
+    if (N > kInt32Max || L * P > kMaxLevelPoints || B * Q * H > kInt32Max || H * D > kInt32Max)
+        return set_error(TD_E_ARG, "sizes beyond the operator's limits");
+    return TD_OK;
+}
+
+// Stand-ins for the buffers of a plan query: never read. `aligned` = 0 gives addresses off 16-byte alignment.
+const void* plan_ptr(int aligned) { return reinterpret_cast<const void*>(aligned ? 0x10000 : 0x10002); }
+
+}  // namespace
+
+extern "C" int td_fused_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t C, int64_t H, int64_t D, int64_t L,
+                             int64_t P, int aligned, int64_t* plan) {
+    int rc = check_plan_sizes(dtype, B, Q, N, H, D, L, P, plan);
+    if (rc != TD_OK) return rc;
+    if (C < 0 || C > kMaxChannels) return set_error(TD_E_ARG, "channels must be <= %d", kMaxChannels);
+    if (B * Q * H * D == 0 || N == 0 || L * P == 0) {
+        plan[0] = -1;  // no kernel: an empty output, or a zero fill
+        return TD_OK;
+    }
+    Geom g{nullptr, nullptr, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N), static_cast<int>(H),
+           static_cast<int>(D), static_cast<int>(L), static_cast<int>(P), nullptr};
+    set_levels(g, nullptr);
+    LaunchPlan lp;
+    FusedTune tune;
+    tune.plan = &lp;
+    const void* ptr = plan_ptr(aligned);
+    rc = launch_fused(dtype, ptr, ptr, nullptr, g, static_cast<int>(C), ptr, ptr, const_cast<void*>(ptr), nullptr,
+                      tune);
+    if (rc != 0) return rc;
+    for (int i = 0; i < 8; ++i) plan[i] = lp.v[i];
+    return TD_OK;
+}
+
+extern "C" int td_sample_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_t D, int64_t L, int64_t P,
+                              int head_major, int aligned, int64_t* plan) {
+    int rc = check_plan_sizes(dtype, B, Q, N, H, D, L, P, plan);
+    if (rc != TD_OK) return rc;
+    if (B * Q * H * D == 0 || N == 0 || L * P == 0) {
+        plan[0] = -1;
+        return TD_OK;
+    }
+    Geom g{nullptr, nullptr, static_cast<int>(B), static_cast<int>(Q), static_cast<int>(N), static_cast<int>(H),
+           static_cast<int>(D), static_cast<int>(L), static_cast<int>(P), nullptr};
+    set_levels(g, nullptr);
+    g.value_hm = head_major ? 1 : 0;
+    LaunchPlan lp;
+    SampleTune tune;
+    tune.plan = &lp;
+    const void* ptr = plan_ptr(aligned);
+    rc = launch_sample(dtype, ptr, g, ptr, ptr, const_cast<void*>(ptr), nullptr, tune);
+    if (rc != 0) return rc;
+    for (int i = 0; i < 8; ++i) plan[i] = lp.v[i];
+    return TD_OK;
+}
+
 extern "C" int td_fused_forward_masked(int dtype, const void* memory, const void* value_weight,
                                        const void* value_bias, const int64_t* spatial_shapes,
                                        const int64_t* level_start_index, const void* sampling_locations,

@@ -811,6 +811,12 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
                     p.slice_rows = static_cast<int>(BQ / slices);
                     p.slice_extra = static_cast<int>(BQ % slices);
                 }
+                if (tune.plan != nullptr) {
+                    const int64_t units = slices > 0 ? slices * g.H : static_cast<int64_t>(g.B) * g.H * p.qtiles;
+                    const int64_t rows_max = slices > 0 ? p.slice_rows + (p.slice_extra > 0 ? 1 : 0) : qt;
+                    *tune.plan = LaunchPlan{{0, units, waves, qt, slices, rows_max, sg, p.g.general() ? 8 : nb}};
+                    return 0;
+                }
                 // corner loads in flight per lane: 8 (6 for the slice shapes above that need it)
                 if (layer) {
                     switch (waves) {
@@ -844,6 +850,10 @@ int launch_fused_t(FusedParams p, hipStream_t stream, const FusedTune& tune, boo
     p.SG = 1;
     p.KS = 1;
     p.qtiles = (g.Q + qt - 1) / qt;
+    if (tune.plan != nullptr) {
+        *tune.plan = LaunchPlan{{1, static_cast<int64_t>(g.B) * g.H * p.qtiles, 4, qt, 0, qt, 1, 1}};
+        return 0;
+    }
     return go_generic<T, 4>(p, lds(qt), stream);
 }
 

@@ -15,12 +15,22 @@ enum Dtype { kF32 = 0, kF16 = 1, kBF16 = 2, kF64 = 3 };
 
 inline int elem_size(int dtype) { return dtype == kF64 ? 8 : dtype == kF32 ? 4 : 2; }
 
+// The launch shape a launcher chose, reported instead of launching when a tune struct's `plan` is set (the size
+// rules of td_fused_plan / td_sample_plan, for the auto selector's cost model). No memory is read.
+struct LaunchPlan {
+    int64_t v[8] = {};
+};
+
 // Launch shape of the fused kernels; zero fields are chosen by the launcher.
 struct FusedTune {
     int qt = 0;     // query rows per workgroup (1..16)
     int sg = 0;     // corner split per row (power of two)
     int waves = 0;  // wavefronts per workgroup (4 or 8)
     int generic = 0;  // 1 forces the generic kernel
+    // set: fill it (kernel: 0 vector, 1 generic; workgroups; wavefronts per workgroup; rows per workgroup; balanced
+    // slices per head, 0 for query tiles; rows of the largest workgroup; corner groups per row; corner loads in
+    // flight per lane) and return 0 without launching
+    LaunchPlan* plan = nullptr;
 };
 
 // Launch shape of the sampling kernel; zero fields are chosen by the launcher.
@@ -28,6 +38,9 @@ struct SampleTune {
     int sg = 0;
     int waves = 0;
     int vec = 0;  // elements per load
+    // set: fill it (workgroups; wavefronts per workgroup; rows per workgroup; corner groups per row; elements per
+    // load; 1 for rows in (b, h, q) order; corner loads in flight per lane) and return 0 without launching
+    LaunchPlan* plan = nullptr;
 };
 
 // Compute units of the current device (256 on MI355X), cached per device.

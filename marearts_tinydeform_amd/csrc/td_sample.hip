@@ -280,6 +280,11 @@ int launch_sample_t(SampleParams p, hipStream_t stream, const SampleTune& tune) 
     //    slower (DINO encoder 85 -> 91).
     const int64_t image_bytes = static_cast<int64_t>(g.N) * g.H * D * static_cast<int64_t>(sizeof(T));
     p.hq = !self_attn && image_bytes >= (int64_t{10} << 20) && 2 * static_cast<int64_t>(g.Q) * LP >= g.N ? 1 : 0;
+    if (tune.plan != nullptr) {
+        const int per = 4 * LP / sg;
+        *tune.plan = LaunchPlan{{(p.rows + rb - 1) / rb, waves, rb, sg, V, p.hq, per % 8 != 0 && per % 6 == 0 ? 6 : 8}};
+        return 0;
+    }
     switch (V) {
         case 1: return go_waves<T, 1>(p, waves, lds(rb), stream);
         case 2: return go_waves<T, 2>(p, waves, lds(rb), stream);
@@ -292,13 +297,17 @@ int launch_sample_t(SampleParams p, hipStream_t stream, const SampleTune& tune) 
     return set_error(-1, "sample: unsupported vector width %d", V);
 }
 
-int launch_sample_f64(SampleParams p, hipStream_t stream) {
+int launch_sample_f64(SampleParams p, hipStream_t stream, LaunchPlan* plan) {
     const int S = 4 * p.g.LP;
     int rb = 4;
     while (rb > 1 && static_cast<size_t>(rb) * S * sizeof(Corner<double>) > kLdsBudget) --rb;
     p.RB = rb;
     p.SG = 1;
     const int64_t blocks = (p.rows + rb - 1) / rb;
+    if (plan != nullptr) {
+        *plan = LaunchPlan{{blocks, 4, rb, 1, 1, 0, 1}};
+        return 0;
+    }
     hipLaunchKernelGGL((sample_f64_kernel<4>), dim3(static_cast<unsigned>(blocks)), dim3(4 * kWave),
                        static_cast<size_t>(rb) * S * sizeof(Corner<double>), stream, p);
     const hipError_t e = hipGetLastError();
@@ -314,7 +323,7 @@ int launch_sample(int dtype, const void* value, const Geom& g, const void* loc, 
         case kF32: return launch_sample_t<float>(p, stream, tune);
         case kF16: return launch_sample_t<f16>(p, stream, tune);
         case kBF16: return launch_sample_t<bf16>(p, stream, tune);
-        case kF64: return launch_sample_f64(p, stream);
+        case kF64: return launch_sample_f64(p, stream, tune.plan);
         default: return set_error(-2, "unknown dtype code %d", dtype);
     }
 }

@@ -32,12 +32,14 @@ def lib():
 
 
 def test_header_declares_the_entry_points():
-    assert header_functions() == ['td_fused_forward', 'td_fused_forward_masked', 'td_input_grad', 'td_last_error',
+    assert header_functions() == ['td_fused_forward', 'td_fused_forward_masked', 'td_fused_plan', 'td_input_grad',
+                                  'td_last_error',
                                   'td_layer_fused_forward', 'td_layer_prologue', 'td_layer_sample_forward',
                                   'td_probe_empty', 'td_probe_gather',
                                   'td_project_forward', 'td_project_forward_noalloc', 'td_sample_backward',
                                   'td_sample_forward',
                                   'td_sample_forward_heads', 'td_sample_forward_masked', 'td_sample_forward_v2',
+                                  'td_sample_plan',
                                   'td_value_proj', 'td_value_proj_heads', 'td_value_proj_plan', 'td_version',
                                   'td_weight_grad',
                                   'td_weight_grad_workspace']

@@ -2,6 +2,8 @@
 141-163) and the host-side validation of csrc/ma_deform_fused.cu:236-266, 298-308, 333, exercised without a GPU."""
 
 import numpy as np
+import math
+
 import pytest
 import torch
 
@@ -54,34 +56,74 @@ def test_auto_picks_fused_for_few_queries():
     assert td.choose_mode(many[0], many[1], many[5]) == 'project'
 
 
+def test_auto_limits_follow_the_gpu_generation(monkeypatch):
+    # reference tests/test_correctness.py:156-163: compute capability 8.x takes FUSED_LIMIT, 7.x FUSED_LIMIT_SM75 (no
+    # device properties here: a CPU-only process falls back to FUSED_LIMIT)
+    def no_props(i):
+        raise RuntimeError('no device')
+    monkeypatch.setattr(torch.cuda, 'get_device_properties', no_props)
+    for cap, table in (((8, 9), td.FUSED_LIMIT), ((7, 5), td.FUSED_LIMIT_SM75)):
+        monkeypatch.setattr(torch.cuda, 'get_device_capability', lambda device=None, cap=cap: cap)
+        assert td._limits.__wrapped__(0) is table
+
+
 def test_auto_limits_follow_the_gpu_architecture(monkeypatch):
-    # the reference keys its table by compute capability (tests/test_correctness.py:156-163); here by gcnArchName
+    # on AMD GPUs (capability 9.x: gfx942, gfx950) the table is chosen by gcnArchName
     class Props:
         def __init__(self, arch):
             self.gcnArchName = arch
 
+    monkeypatch.setattr(torch.cuda, 'get_device_capability', lambda device=None: (9, 5))
     for arch, table in (('gfx950:sramecc+:xnack-', td.FUSED_LIMIT), ('gfx942', td.FUSED_LIMIT)):
         monkeypatch.setattr(torch.cuda, 'get_device_properties', lambda i, arch=arch: Props(arch))
         assert td._limits.__wrapped__(0) is table
     assert td.ARCH_LIMITS['gfx950'] is td.FUSED_LIMIT
 
 
+def test_reference_threshold_tables_keep_the_reference_rule(monkeypatch):
+    # an (a, b) entry is the reference's rule: fused while Q * L * P * 4 / (N * D) < a + b / B
+    # (marearts_tinydeform/__init__.py:39-46); FUSED_LIMIT_SM75 holds the reference's values
+    assert td.FUSED_LIMIT_SM75[torch.float16] == (0.020, 0.0) and td.__version__ == '0.1.1'
+    monkeypatch.setitem(td.FUSED_LIMIT, torch.float32, (0.073, 0.032))
+    few = make(1, 50, 8, 32, 256, RTDETR_LEVELS, 4)    # r = 50 * 12 * 4 / (8400 * 32) = 0.0089 < 0.105
+    many = make(1, 600, 8, 32, 256, RTDETR_LEVELS, 4)  # r = 0.107
+    assert td.choose_mode(few[0], few[1], few[5]) == 'fused'
+    assert td.choose_mode(many[0], many[1], many[5]) == 'project'
+    with pytest.raises(ValueError):
+        td.predict_us(few[0], few[1], few[5])
+
+
 def test_cost_tables_are_sane():
-    ff, fp = td.cost_features(1, 300, 8, 32, 256, 8400, 3, 4, 2)
+    ff, fg, fs = td.cost_features(1, 300, 8, 32, 256, 8400, 3, 4, 2)
+    gf = td.gap_features(1, 300, 8400, 8, 32, 3, 4, 2)
     for dtype in (torch.float32, torch.float16, torch.bfloat16):
         coef = td.FUSED_LIMIT[dtype]
-        assert len(coef['fused']) == len(ff) and len(coef['project']) == len(fp)
-        assert all(c >= 0 for c in coef['fused'] + coef['project'])
+        assert [len(coef[k]) for k in ('fused', 'gemm', 'sample', 'gap')] == [len(ff), len(fg), len(fs), len(gf)]
+        assert all(c >= 0 for k in ('fused', 'gemm', 'sample', 'gap') for c in coef[k])
 
 
-def test_cost_features_split_the_gemm_by_depth():
-    # narrow K: the GEMM's flops; deep K (C >= 512): whole rounds of 256 x 256 tiles over 256 CUs, times K
-    ff, fp = td.cost_features(1, 300, 8, 32, 256, 8400, 3, 4, 2)
-    assert fp[2] == pytest.approx(2 * 8400 * 256 * 256 / 1e9) and fp[3] == 0.0
-    assert ff[1] == pytest.approx(300 * 8 * 12 * 4 * 256 * 2 / 1e6)
-    _, fp = td.cost_features(2, 300, 16, 64, 1024, 21760, 4, 16, 2)
-    tiles = (43520 // 256) * (1024 // 256)  # 170 x 4 = 680 tiles: 3 rounds on 256 CUs
-    assert fp[2] == 0.0 and fp[3] == pytest.approx(-(-tiles // 256) * 1024 / 1e3)
+def test_cost_features_follow_the_launch_plans():
+    # RT-DETR 640 fp16 B1 Q300: one balanced slice of 9-10 rows per CU (12 wavefronts), 256 workgroups; the GEMM takes
+    # 64 x 64 tiles (528 of them: 3 on the busiest CU); the sampler 600 workgroups of 4 rows
+    ff, fg, fs = td.cost_features(1, 300, 8, 32, 256, 8400, 3, 4, 2)
+    assert _native.fused_plan(torch.float16, 1, 300, 8400, 256, 8, 32, 3, 4)[:6] == [0, 256, 12, 10, 32, 10]
+    assert ff[1] == pytest.approx(10 * 48 * 256 * 2 / 1e6) and ff[2:6] == [0.0] * 4
+    assert ff[8] == pytest.approx(16 * 256 * 32 * 2 / 1e6)
+    assert _native.value_proj_plan(torch.float16, 8400, 256, 256, heads=8, N=8400) == 25
+    assert fg[2] == pytest.approx(3 * 64 * 64 * 256 * 2 * 256 / 1e9) and fg[3] == pytest.approx(8400 * 512 * 2 / 1e6)
+    assert _native.sample_plan(torch.float16, 1, 300, 8400, 8, 32, 3, 4, head_major=True)[:3] == [600, 2, 4]
+    assert fs[1] == pytest.approx(300 * 8 * 48 * 32 * 2 / 1e6) and fs[2] == pytest.approx(3 * 4 * 48 * 32 * 2 / 1e6)
+    # each XCD's L2 pulls in the rows its queries touch: 4800 corner reads per level over levels of 6400, 1600 and
+    # 400 tokens (the 4:1 level sizes are exact here)
+    touched = sum(n * (1 - math.exp(-4800 / n)) for n in (6400, 1600, 400))
+    assert ff[6] == pytest.approx(touched * 512 / 1e6)
+    # C = 1024 B2 (43520 x 1024 x 1024): the persistent GEMM's 680 tiles of 256 x 256, 85 per XCD over 32
+    # workgroups: 3 rounds
+    _, fg, _ = td.cost_features(2, 300, 16, 64, 1024, 21760, 4, 16, 2)
+    assert fg[4] == 3 and fg[5] == pytest.approx(3 * 1.024) and fg[1:4] == [0.0] * 3
+    # C = 256 B8 (67200 rows): the streaming GEMM, 263 tokens per CU in 9 steps of 32
+    _, fg, _ = td.cost_features(8, 300, 8, 32, 256, 8400, 3, 4, 2)
+    assert fg[1] == pytest.approx(9 * 32 * 512 * 2 * 256 / 1e6)
 
 
 def test_auto_crossover_moves_with_queries_batch_and_channels():
