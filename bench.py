@@ -21,7 +21,8 @@ which all CUs receive randomly chosen rows of the kernel's width from a buffer o
 measured in the same run by td_probe_gather, with the HBM figures beside it.
 
 Other modes: --table (the reference's sweep), --fit-auto / --holdout (the auto selector), --ceiling (the gather
-ceiling over row widths and buffer sizes), --trace-run and --pmc-run (short runs for rocprofv3).
+ceiling over row widths and buffer sizes), --phases (the fused kernel's phase timeline, from the measurement build
+libtinydeform_phases.so), --trace-run and --pmc-run (short runs for rocprofv3).
 """
 
 import argparse
@@ -339,6 +340,104 @@ def trace_run(dev, steps, warmup):
                                     'empty_us_per_launch': round(empty, 3)}}), flush=True)
 
 
+# what the phase stamps of libtinydeform_phases.so mark (slot: point), in the order a wavefront passes them
+PHASE_POINTS = [(11, 'kernel entry'), (0, 'rows decoded'), (1, 'corner table barrier passed'), (2, 'gather done'),
+                (3, 'gather barrier passed'), (4, 'projection set up'), (5, 'projection job start'),
+                (6, 'first W chunk done'), (7, 'MFMAs done'), (8, 'partial sums stored'),
+                (9, 'projection barrier passed'), (10, 'outputs stored')]
+# per-wavefront phases (from slot, to slot, name, which wavefronts: all / gatherers / jobs)
+PHASE_SPANS = [(11, 0, 'entry to rows decoded (kernel arguments)', 'all'),
+               (0, 1, 'corner table (locations, weights, corners; barrier)', 'all'),
+               (1, 2, 'gather of the wavefront\'s row', 'gatherers'),
+               (2, 3, 'wait at the gather barrier', 'all'),
+               (3, 5, 'projection set-up', 'jobs'),
+               (5, 7, 'projection job (MFMAs)', 'jobs'),
+               (7, 8, 'partial sums to LDS', 'jobs'),
+               (8, 9, 'wait at the projection barrier', 'all'),
+               (9, 10, 'epilogue (K slices summed, bias, stores)', 'all')]
+
+
+def phases_run(dev, steps, warmup):
+    """--phases: the fused kernel's timeline, from libtinydeform_phases.so (td_fused.hip built with
+    TD_PHASE_STAMPS: every wavefront of the one-slice-per-CU kernel reads the GPU's 100 MHz real-time counter at its
+    phase boundaries). The operator is graph-timed like the headline with the plain library and with the
+    instrumented one; the stamps are those of the last call of the last replay, a call that ran back to back with
+    the one before it. Prints a markdown summary and one JSON line."""
+    import ctypes
+    import numpy as np
+    path = os.path.join(os.path.dirname(_native.LIB_PATH), 'libtinydeform_phases.so')
+    lib = _native.load(path)
+    if lib is None:
+        raise SystemExit(f'measurement build missing ({_native.load_error}): python -m marearts_tinydeform_amd._build')
+    lib.td_phase_stamps.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    lib.td_phase_stamps.restype = ctypes.c_int
+    B, Q, H, L, P = dev[5].shape[:5]
+    C, HD = dev[0].shape[2], dev[1].shape[0]
+    plan = _native.fused_plan(dev[0].dtype, B, Q, dev[0].shape[1], C, H, HD // H, L, P)
+    if plan[0] != 0 or plan[2] != 12 or plan[4] == 0:
+        raise SystemExit(f'this workload does not launch the instrumented shape (one 12-wavefront slice per CU): '
+                         f'plan {plan}')
+    plain = _native.lib
+    with torch.inference_mode():
+        t_plain = graph_time_us(lambda: td.ma_deform_attn(*dev, mode='fused'), steps, warmup)
+        _native.lib = lib
+        try:
+            t_inst = graph_time_us(lambda: td.ma_deform_attn(*dev, mode='fused'), steps, warmup)
+            torch.cuda.synchronize()
+            n = 1024 * 12 * 16
+            buf = np.zeros(n, dtype=np.uint64)
+            if lib.td_phase_stamps(buf.ctypes.data, n) != 0:
+                raise SystemExit('td_phase_stamps failed')
+        finally:
+            _native.lib = plain
+    wgs = min(plan[1], 1024)
+    st = buf.reshape(1024, 12, 16)[:wgs].astype(np.int64)
+    seen = st > 0
+    t0 = st[:, :, 11][seen[:, :, 11]].min()
+    rel = np.where(seen, (st - t0) * 10, -1)  # ns from the first wavefront's entry
+    gatherers = (B * Q) // plan[4]  # every slice holds at least this many rows, one per wavefront
+    jobs = np.zeros(12, dtype=bool)
+    jobs[:4] = True  # the K-slice jobs: one per SIMD
+
+    def pct(x):
+        x = np.asarray(x)
+        return {'n': int(x.size), 'p0': float(np.min(x)), 'p50': float(np.median(x)),
+                'p90': float(np.percentile(x, 90)), 'max': float(np.max(x))}
+
+    points = []
+    for slot, name in PHASE_POINTS:
+        v = rel[:, :, slot]
+        points.append((name, pct(v[v >= 0])))
+    spans = []
+    for a, b, name, who in PHASE_SPANS:
+        waves = slice(0, gatherers) if who == 'gatherers' else jobs if who == 'jobs' else slice(None)
+        x, y = rel[:, waves, a], rel[:, waves, b]
+        ok = (x >= 0) & (y >= 0)
+        spans.append((name, who, pct((y - x)[ok])))
+    log(f'phases: {wgs} workgroups x 12 wavefronts; {t_plain:.2f} µs per call plain, {t_inst:.2f} instrumented')
+    print(f'Graph-timed µs per call ({steps}-call graph): {t_plain:.2f} with libtinydeform.so, {t_inst:.2f} with '
+          f'the instrumented build. Launch plan: {plan[1]} workgroups of 12 wavefronts, {plan[4]} slices of '
+          f'{gatherers}-{plan[5]} rows.')
+    print()
+    print('Points, ns after the first wavefront entered the kernel (every wavefront of every workgroup):')
+    print()
+    print('| point | wavefronts | p0 | p50 | p90 | max |')
+    print('|---|---:|---:|---:|---:|---:|')
+    for name, q in points:
+        print(f'| {name} | {q["n"]} | {q["p0"]:.0f} | {q["p50"]:.0f} | {q["p90"]:.0f} | {q["max"]:.0f} |')
+    print()
+    print('Phases, ns per wavefront ("gatherers": the wavefronts that gather a row in every workgroup; "jobs": the '
+          'four projection jobs):')
+    print()
+    print('| phase | wavefronts | n | p0 | p50 | p90 | max |')
+    print('|---|---|---:|---:|---:|---:|---:|')
+    for name, who, q in spans:
+        print(f'| {name} | {who} | {q["n"]} | {q["p0"]:.0f} | {q["p50"]:.0f} | {q["p90"]:.0f} | {q["max"]:.0f} |')
+    print(json.dumps({'phases': {'us_per_call': round(t_plain, 3), 'us_per_call_instrumented': round(t_inst, 3),
+                                 'plan': list(plan), 'points_ns': dict(points),
+                                 'spans_ns': {name: q for name, _, q in spans}}}), flush=True)
+
+
 def pmc_run(dev, H, steps):
     src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device='cuda')
     dst = torch.empty_like(src)
@@ -607,6 +706,8 @@ def main():
     ap.add_argument('--trace-run', action='store_true',
                     help='for rocprofv3 --kernel-trace: --steps operator calls and --steps empty kernels, each in '
                          'a graph timed like the headline')
+    ap.add_argument('--phases', action='store_true',
+                    help='the fused kernel\'s phase timeline from the measurement build libtinydeform_phases.so')
     ap.add_argument('--pmc-run', action='store_true',
                     help='for rocprofv3 --pmc: one plain copy of COPY_BYTES (the counter calibration), then '
                          '--steps eager calls of the fused kernel, the value projection and the sampling kernel')
@@ -648,6 +749,9 @@ def main():
         return
     if args.trace_run:
         trace_run(dev, args.steps, args.warmup)
+        return
+    if args.phases:
+        phases_run(dev, args.steps, args.warmup)
         return
 
     pick = td.choose_mode(dev[0], dev[1], dev[5])

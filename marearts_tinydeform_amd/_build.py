@@ -5,6 +5,10 @@
 Each source is compiled to an object under _build/ (in parallel), then linked into libtinydeform.so next to
 this file, where marearts_tinydeform_amd._native loads it. No torch extension machinery (and so no hipify) is
 involved: the library exports the C ABI of include/tinydeform.h and is loaded with ctypes.
+
+The same run links libtinydeform_phases.so, a measurement build: td_fused.hip compiled with TD_PHASE_STAMPS, so
+that the fused kernel records when its wavefronts pass each phase (bench.py --phases reads them). The package
+never loads it.
 """
 
 import concurrent.futures
@@ -18,6 +22,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, 'csrc')
 BUILD = os.path.join(HERE, '_build')
 LIB = os.path.join(HERE, 'libtinydeform.so')
+PHASES_LIB = os.path.join(HERE, 'libtinydeform_phases.so')
+PHASES_SOURCE = 'td_fused.hip'  # the one source that differs in the measurement build
 ARCH = 'gfx950'
 
 SOURCES = ['td_abi.hip', 'td_fused.hip', 'td_sample.hip', 'td_gemm.hip', 'td_gemm_dma.hip', 'td_gemm_stream.hip',
@@ -43,29 +49,46 @@ def hipcc():
     return path
 
 
-def _compile(src):
-    obj = os.path.join(BUILD, os.path.splitext(src)[0] + '.o')
-    cmd = [hipcc()] + HIPCC_FLAGS + EXTRA_FLAGS.get(src, []) + ['-c', os.path.join(CSRC, src), '-o', obj]
+def _compile(job):
+    src, phases = job
+    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ('_phases' if phases else '') + '.o')
+    defs = ['-DTD_PHASE_STAMPS'] if phases else []
+    cmd = [hipcc()] + HIPCC_FLAGS + EXTRA_FLAGS.get(src, []) + defs + ['-c', os.path.join(CSRC, src), '-o', obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f'hipcc failed on {src}:\n{res.stdout}\n{res.stderr}')
     return obj
 
 
-def build(verbose=False):
-    """Compile every HIP source and link libtinydeform.so; returns the library path."""
-    os.makedirs(BUILD, exist_ok=True)
-    workers = min(len(SOURCES), max(1, (os.cpu_count() or 2) // 2))
-    with concurrent.futures.ThreadPoolExecutor(workers) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB + '.tmp'
+def _link(objs, lib):
+    tmp = lib + '.tmp'
     cmd = [hipcc(), f'--offload-arch={ARCH}', '-shared', '-fPIC', '-o', tmp] + objs
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f'link failed:\n{res.stdout}\n{res.stderr}')
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose=False, phases=True):
+    """Compile every HIP source and link libtinydeform.so (and, with phases, libtinydeform_phases.so); returns the
+    library path."""
+    os.makedirs(BUILD, exist_ok=True)
+    jobs = [(src, False) for src in SOURCES] + ([(PHASES_SOURCE, True)] if phases else [])
+    # the two largest sources first, so that they do not start last
+    jobs.sort(key=lambda j: j[0] != PHASES_SOURCE)
+    workers = min(len(jobs), max(1, (os.cpu_count() or 2) // 2))
+    with concurrent.futures.ThreadPoolExecutor(workers) as ex:
+        objs = list(ex.map(_compile, jobs))
+    plain = [o for o, (_, ph) in zip(objs, jobs) if not ph]
+    _link(plain, LIB)
     if verbose:
         print('built', LIB)
+    if phases:
+        swap = {os.path.join(BUILD, os.path.splitext(PHASES_SOURCE)[0] + '.o'): o
+                for o, (_, ph) in zip(objs, jobs) if ph}
+        _link([swap.get(o, o) for o in plain], PHASES_LIB)
+        if verbose:
+            print('built', PHASES_LIB)
     return LIB
 
 

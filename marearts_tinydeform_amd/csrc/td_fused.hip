@@ -24,6 +24,44 @@
 #include "td_internal.h"
 #include "td_prologue.h"
 
+// Phase stamps (built only with TD_PHASE_STAMPS, as libtinydeform_phases.so; never in libtinydeform.so). The
+// instantiation that one-slice-per-CU launches use (12 wavefronts, 6 loads in flight, 16-bit) reads the 100 MHz
+// real-time counter at its phase boundaries into registers and, at its end, lane 0 of every wavefront of the first
+// kPhaseWgs workgroups stores its 16 stamps to td_phase_stamp_buf[workgroup][wavefront][16], so a launch's
+// timeline costs no memory traffic until the wavefront is done. Slots: 11 kernel entry, 0 rows decoded, 1 corner
+// table barrier passed, 2 gather done, 3 gather barrier passed, 4 projection set up, 5 job start, 6 first chunk done,
+// 7 MFMAs done, 8 partial sums stored, 9 projection barrier passed, 10 outputs stored; 0 where a wavefront passed
+// no such point. td_phase_stamps() copies the buffer to the host.
+#ifdef TD_PHASE_STAMPS
+constexpr int kPhaseWgs = 1024;
+__device__ unsigned long long td_phase_stamp_buf[kPhaseWgs * 12 * 16];
+extern "C" int td_phase_stamps(void* host, int64_t count) {
+    if (host == nullptr || count < 0 || count > int64_t{kPhaseWgs} * 12 * 16) return -1;
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(td_phase_stamp_buf), static_cast<size_t>(count) * 8) == hipSuccess
+               ? 0 : -1;
+}
+#define TD_STAMP(i)                                                                     \
+    do {                                                                                \
+        if constexpr (kStamp) stamps_[i] = __builtin_amdgcn_s_memrealtime();            \
+    } while (0)
+#define TD_STAMP_FLUSH()                                                                \
+    do {                                                                                \
+        if constexpr (kStamp) {                                                         \
+            if ((threadIdx.x & (kWave - 1)) == 0 && blockIdx.x < kPhaseWgs) {           \
+                unsigned long long* d_ = td_phase_stamp_buf + (blockIdx.x * 12 + threadIdx.x / kWave) * 16; \
+                for (int i_ = 0; i_ < 16; ++i_) d_[i_] = stamps_[i_];                   \
+            }                                                                           \
+        }                                                                               \
+    } while (0)
+#else
+#define TD_STAMP(i) \
+    do {            \
+    } while (0)
+#define TD_STAMP_FLUSH() \
+    do {                 \
+    } while (0)
+#endif
+
 namespace td {
 namespace {
 
@@ -76,6 +114,11 @@ __global__ __launch_bounds__(WAVES* kWave)
 __attribute__((amdgpu_waves_per_eu(std::is_same<T, bf16>::value && WAVES == 8 && NB == 8 && !GENERAL && !LAYER ? 8 : 1)))
 void fused_vec_kernel(FusedParams p) {
     constexpr int NTH = WAVES * kWave;
+#ifdef TD_PHASE_STAMPS
+    constexpr bool kStamp = WAVES == 12 && NB == 6 && !LAYER;
+    [[maybe_unused]] unsigned long long stamps_[16] = {};
+#endif
+    TD_STAMP(11);
     constexpr int V = 16 / static_cast<int>(sizeof(T));
     const Geom& g = p.g;
     const int C = p.C, QT = p.QT, SG = p.SG, CV = C / V;
@@ -141,6 +184,7 @@ void fused_vec_kernel(FusedParams p) {
     }
 
     // phase 1: corner table (tokens, or with p.buf the rows' byte offsets)
+    TD_STAMP(0);
     const int sb = p.buf ? C * static_cast<int>(sizeof(T)) : 0;
     if (tid == 0) *gmax = 0u;
     for (int i = tid; i < QT * LP; i += NTH) {
@@ -163,6 +207,7 @@ void fused_vec_kernel(FusedParams p) {
         }
     }
     __syncthreads();
+    TD_STAMP(1);
 
     // One workgroup per CU (12 wavefronts, 6 loads in flight: the balanced-slice shapes of 16-bit problems) has
     // registers to spare, so each projection job's first two W_h chunks and the epilogue's bias value are requested
@@ -235,7 +280,9 @@ void fused_vec_kernel(FusedParams p) {
             }
         }
     }
+    TD_STAMP(2);
     __syncthreads();
+    TD_STAMP(3);
 
     // phase 3: out[16 x D] = g[16 x C] . W_h^T on MFMA; job = K slice with every N tile (p.alln), else (N tile, K slice)
     const int wave = tid / kWave, lane = tid & (kWave - 1);
@@ -255,6 +302,7 @@ void fused_vec_kernel(FusedParams p) {
             inv_sc = ldexpf(1.f, e - 14);
         }
     }
+    TD_STAMP(4);
     if (kPre && p.alln) {
         // as the p.alln block below, with the job's first two W_h chunks taken from wpre
         const int nk = (C + KCH - 1) / KCH;
@@ -318,8 +366,10 @@ void fused_vec_kernel(FusedParams p) {
                 }
             };
             int kk = kb;
+            TD_STAMP(5);
             if (ks == wave) {  // the chunks requested before the gather
                 if (kk < ke) chunk(kk++, wpre[0]);
+                TD_STAMP(6);
                 if (kk < ke) chunk(kk++, wpre[1]);
             }
             for (; kk < ke; ++kk) {
@@ -333,6 +383,7 @@ void fused_vec_kernel(FusedParams p) {
                 }
                 chunk(kk, braw);
             }
+            TD_STAMP(7);
             float* pp = part + ks * 16 * PW;
 #pragma unroll
             for (int nt = 0; nt < kAllN; ++nt) {
@@ -491,7 +542,9 @@ void fused_vec_kernel(FusedParams p) {
             for (int i = 0; i < 4; ++i) pp[(4 * kg + i) * PW + nt * 16 + n16] = acc[i];
         }
     }
+    TD_STAMP(8);
     __syncthreads();
+    TD_STAMP(9);
 
     // epilogue: sum the K slices, add bias * sum of in-map weights, round once
     if constexpr (kPre) {
@@ -509,6 +562,8 @@ void fused_vec_kernel(FusedParams p) {
             emit(o, bias != nullptr
                         ? bias[static_cast<size_t>(h) * D + o - static_cast<int>(fast_div(p.d_d, o)) * D]
                         : static_cast<T>(0.f));
+        TD_STAMP(10);
+        TD_STAMP_FLUSH();
         return;
     }
     for (int o = tid; o < QT * D; o += NTH) {

@@ -46,12 +46,14 @@ DEEP_K = [
 # 16-bit (M, K, bias, kernel) with NO = 256, every row checked: the streaming kernel from 14000 rows at K = 256 and
 # 8000 at K = 128. Each CU takes an equal share of M (shares differ by one row) in steps of 32 tokens, the last one
 # partial: one step per CU (8000, 8100 at K = 128, where fewer than 256 workgroups run), two (16384), shares off the
-# step size (14000, 36001, 44447, 20011, 70003), whole steps (131072 = 256 x 16 x 32), with and without bias.
+# step size (14000, 36001, 44447, 20011, 70003, 76801, 100003), whole steps (131072 = 256 x 16 x 32), with and
+# without bias, up to 22 steps per CU (177784 at K = 128).
 STREAM = [
     (14000, 256, True, 22), (16384, 256, True, 22), (16800, 256, False, 22), (33600, 256, False, 22),
-    (36001, 256, True, 22), (44447, 256, False, 22), (67200, 256, True, 22), (88892, 256, True, 22),
-    (131072, 256, True, 22), (8000, 128, True, 22), (8100, 128, False, 22), (20011, 128, True, 22),
-    (44447, 128, False, 22), (70003, 128, True, 22),
+    (36001, 256, True, 22), (44447, 256, False, 22), (67200, 256, True, 22), (76801, 256, False, 22),
+    (88892, 256, True, 22), (131072, 256, True, 22), (8000, 128, True, 22), (8100, 128, False, 22),
+    (20011, 128, True, 22), (44447, 128, False, 22), (70003, 128, True, 22), (100003, 128, True, 22),
+    (177784, 128, False, 22),
     (13999, 256, True, 25),    # one row short of the streaming kernel's range
     (7999, 128, True, 25),
 ]

@@ -140,6 +140,8 @@ def test_auto_crossover_moves_with_queries_batch_and_channels():
     assert pick(1, 900, 8, 32, 256, RTDETR_LEVELS, 4) == 'fused'
     assert pick(4, 300, 8, 32, 256, RTDETR_LEVELS, 4) == 'fused'
     assert pick(4, 600, 8, 32, 256, RTDETR_LEVELS, 4) == 'project'
+    # batch 8, 300 queries, bfloat16: fused 22.5 against project 24.1 µs (1000-call graphs)
+    assert pick(8, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.bfloat16) == 'fused'
     assert pick(8, 900, 8, 32, 256, RTDETR_LEVELS, 4) == 'project'
     limit = [(128, 128), (64, 64), (32, 32), (16, 16)]
     assert pick(2, 50, 16, 64, 1024, limit, 16, torch.bfloat16) == 'fused'
