@@ -17,8 +17,8 @@ rows count every time they are read, L2 hits included) next to the HBM rate the 
 the memory fabric per launch, from the committed rocprofv3 --pmc summary, / the same time), and the CPU baseline
 (the oracle's torch restatement of the reference's PyTorch path, float32, on this host's cores, timed on a
 bounded sample). For the gather kernels (fused mode, the sampler) the roofline's bound is "l2-gather": the rate at
-which all CUs receive randomly chosen rows of the kernel's width from a buffer of the gathered tensor's size,
-measured in the same run by td_probe_gather, with the HBM figures beside it.
+which all CUs receive randomly chosen rows of the kernel's width from L2 (a buffer of the gathered tensor's size, at
+most one XCD's 4 MB L2), measured in the same run by td_probe_gather, with the HBM figures beside it.
 
 Other modes: --table (the reference's sweep), --fit-auto / --holdout (the auto selector), --ceiling (the gather
 ceiling over row widths and buffer sizes), --phases (the fused kernel's phase timeline, from the measurement build
@@ -284,8 +284,10 @@ def gather_ceiling(row_bytes, buf_bytes, target_bytes=1 << 30):
     td_probe_gather (the gather kernels' 16-byte buffer loads, 8 in flight per lane, row_bytes / 16 lanes per row)
     reading about `target_bytes` per launch, graph-timed like the operator; the best of four occupancies. With the
     memory tensor's size this is the ceiling of the fused kernel's gather phase, whose rows mostly sit in L2 (what
-    L2 misses comes from the MALL or HBM, as in the kernel)."""
+    L2 misses comes from the MALL or HBM, as in the kernel). Rows wider than the probe's widest (1024 bytes, e.g.
+    C = 1024 in 16 bits) are probed as 1024-byte rows: the rate is flat from 256-byte rows up."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
+    row_bytes = min(row_bytes, 1024)
     buf = torch.zeros(max(buf_bytes // 16, row_bytes // 16), 4, dtype=torch.int32, device='cuda')
     best = None
     for waves, per_cu in ((4, 2), (8, 1), (8, 2), (4, 4)):
@@ -788,13 +790,15 @@ def main():
             kern.update(tr)
 
     # Roofline of the dominant kernel. The gather kernels read rows that mostly sit in L2, so their bound is the rate
-    # at which the CUs receive such rows ("l2-gather"), measured here, on this device, by td_probe_gather with the
-    # kernel's row width over a buffer of the gathered tensor's size; the HBM figures (counter-measured bytes over the
-    # same time, and the algorithmic bytes against 8 TB/s) stand beside it.
+    # at which the CUs receive such rows from L2 ("l2-gather"), measured here, on this device, by td_probe_gather with
+    # the kernel's row width over an L2-resident buffer (the gathered tensor, or one XCD's 4 MB of it when larger: the
+    # kernels deal each XCD a contiguous share of the work, whose rows it keeps in its own L2, so the probe's random
+    # rows over a whole large tensor would understate what the kernels reach). The HBM figures (counter-measured bytes
+    # over the same time, and the algorithmic bytes against 8 TB/s) stand beside it.
     ceiling = None
     if pick == 'fused':
         t = times['fused']
-        ceiling = gather_ceiling(C * s, B * N * C * s)
+        ceiling = gather_ceiling(C * s, min(B * N * C * s, td.L2_BYTES))
         roof = {'kernel': 'fused_vec_kernel', 'bound': 'l2-gather', 'achieved': alg['fused_bytes'] / (t * 1e-6) / 1e9,
                 'peak': ceiling['gbps'], 'unit': 'GB/s'}
     else:
@@ -811,7 +815,8 @@ def main():
                         'achieved': alg['gemm_bytes'] / (t_gemm * 1e-6) / 1e9, 'peak': 8000.0, 'unit': 'GB/s'}
         else:
             t = t_smp
-            ceiling = gather_ceiling(D * s, B * N * H * D * s)
+            # with the head-major value the two corners (x0, x0 + 1) of a row are one 2 D-wide run
+            ceiling = gather_ceiling((2 if head_major(dtype, D) else 1) * D * s, min(B * N * H * D * s, td.L2_BYTES))
             roof = {'kernel': 'sample_kernel', 'bound': 'l2-gather',
                     'achieved': alg['sample_bytes'] / (t_smp * 1e-6) / 1e9, 'peak': ceiling['gbps'], 'unit': 'GB/s'}
     roof['achieved'] = round(roof['achieved'], 1)

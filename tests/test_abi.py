@@ -52,6 +52,18 @@ def test_library_exports_every_declared_symbol(lib):
     assert set(header_functions()) == set(_native.SIGNATURES)
 
 
+def test_measurement_build_exports_the_same_abi_and_its_stamps(lib):
+    # libtinydeform_phases.so (bench.py --phases) is the same library with the fused kernel's phase stamps: every
+    # entry point of the header, plus td_phase_stamps, which the product library does not have
+    path = os.path.join(os.path.dirname(_native.LIB_PATH), 'libtinydeform_phases.so')
+    assert os.path.exists(path), 'libtinydeform_phases.so is not built: run __graft_entry__.build()'
+    raw = ctypes.CDLL(path)
+    for name in header_functions():
+        assert hasattr(raw, name), name
+    assert hasattr(raw, 'td_phase_stamps')
+    assert not hasattr(ctypes.CDLL(_native.LIB_PATH), 'td_phase_stamps')
+
+
 def test_header_constants_match_python(lib):
     d = header_defines()
     assert d['TD_MAX_LEVEL_POINTS'] == _native.MAX_LEVEL_POINTS
