@@ -350,7 +350,7 @@ PHASE_POINTS = [(11, 'kernel entry'), (0, 'rows decoded'), (1, 'corner table bar
 # per-wavefront phases (from slot, to slot, name, which wavefronts: all / gatherers / jobs)
 PHASE_SPANS = [(11, 0, 'entry to rows decoded (kernel arguments)', 'all'),
                (0, 1, 'corner table (locations, weights, corners; barrier)', 'all'),
-               (1, 2, 'gather of the wavefront\'s row', 'gatherers'),
+               (1, 2, 'gather of the wavefront\'s rows', 'gatherers'),
                (2, 3, 'wait at the gather barrier', 'all'),
                (3, 5, 'projection set-up', 'jobs'),
                (5, 7, 'projection job (MFMAs)', 'jobs'),
@@ -361,10 +361,10 @@ PHASE_SPANS = [(11, 0, 'entry to rows decoded (kernel arguments)', 'all'),
 
 def phases_run(dev, steps, warmup):
     """--phases: the fused kernel's timeline, from libtinydeform_phases.so (td_fused.hip built with
-    TD_PHASE_STAMPS: every wavefront of the one-slice-per-CU kernel reads the GPU's 100 MHz real-time counter at its
-    phase boundaries). The operator is graph-timed like the headline with the plain library and with the
-    instrumented one; the stamps are those of the last call of the last replay, a call that ran back to back with
-    the one before it. Prints a markdown summary and one JSON line."""
+    TD_PHASE_STAMPS: every wavefront of the vector kernel reads the GPU's 100 MHz real-time counter at its phase
+    boundaries; the first 1024 workgroups keep theirs). The operator is graph-timed like the headline with the plain
+    library and with the instrumented one; the stamps are those of the last call of the last replay, a call that ran
+    back to back with the one before it. Prints a markdown summary and one JSON line."""
     import ctypes
     import numpy as np
     path = os.path.join(os.path.dirname(_native.LIB_PATH), 'libtinydeform_phases.so')
@@ -376,9 +376,8 @@ def phases_run(dev, steps, warmup):
     B, Q, H, L, P = dev[5].shape[:5]
     C, HD = dev[0].shape[2], dev[1].shape[0]
     plan = _native.fused_plan(dev[0].dtype, B, Q, dev[0].shape[1], C, H, HD // H, L, P)
-    if plan[0] != 0 or plan[2] != 12 or plan[4] == 0:
-        raise SystemExit(f'this workload does not launch the instrumented shape (one 12-wavefront slice per CU): '
-                         f'plan {plan}')
+    if plan[0] != 0:
+        raise SystemExit(f'this workload launches the generic fused kernel, which has no stamps: plan {plan}')
     plain = _native.lib
     with torch.inference_mode():
         t_plain = graph_time_us(lambda: td.ma_deform_attn(*dev, mode='fused'), steps, warmup)
@@ -397,9 +396,12 @@ def phases_run(dev, steps, warmup):
     seen = st > 0
     t0 = st[:, :, 11][seen[:, :, 11]].min()
     rel = np.where(seen, (st - t0) * 10, -1)  # ns from the first wavefront's entry
-    gatherers = (B * Q) // plan[4]  # every slice holds at least this many rows, one per wavefront
-    jobs = np.zeros(12, dtype=bool)
-    jobs[:4] = True  # the K-slice jobs: one per SIMD
+    # the wavefronts that gather rows in every workgroup: the fewest rows a workgroup holds (a slice's, or a full
+    # query tile's) times the lanes of a row (16-byte chunks times corner groups), in wavefronts
+    rows_min = (B * Q) // plan[4] if plan[4] > 0 else plan[3]
+    lanes = C * dev[0].element_size() // 16 * plan[6]
+    gatherers = min(plan[2], -(-rows_min * lanes // 64))
+    jobs = (rel[:, :, 5] >= 0).any(axis=0)  # the wavefronts that ran a projection job (those stamped at its start)
 
     def pct(x):
         x = np.asarray(x)
@@ -409,27 +411,32 @@ def phases_run(dev, steps, warmup):
     points = []
     for slot, name in PHASE_POINTS:
         v = rel[:, :, slot]
-        points.append((name, pct(v[v >= 0])))
+        if (v >= 0).any():
+            points.append((name, pct(v[v >= 0])))
     spans = []
     for a, b, name, who in PHASE_SPANS:
         waves = slice(0, gatherers) if who == 'gatherers' else jobs if who == 'jobs' else slice(None)
         x, y = rel[:, waves, a], rel[:, waves, b]
         ok = (x >= 0) & (y >= 0)
-        spans.append((name, who, pct((y - x)[ok])))
-    log(f'phases: {wgs} workgroups x 12 wavefronts; {t_plain:.2f} µs per call plain, {t_inst:.2f} instrumented')
+        if ok.any():
+            spans.append((name, who, pct((y - x)[ok])))
+    log(f'phases: {wgs} workgroups x {plan[2]} wavefronts; {t_plain:.2f} µs per call plain, {t_inst:.2f} '
+        f'instrumented')
+    shape = (f'{plan[4]} slices per head of {rows_min}-{plan[5]} rows' if plan[4] > 0 else
+             f'query tiles of {plan[3]} rows')
     print(f'Graph-timed µs per call ({steps}-call graph): {t_plain:.2f} with libtinydeform.so, {t_inst:.2f} with '
-          f'the instrumented build. Launch plan: {plan[1]} workgroups of 12 wavefronts, {plan[4]} slices of '
-          f'{gatherers}-{plan[5]} rows.')
+          f'the instrumented build. Launch plan: {plan[1]} workgroups of {plan[2]} wavefronts, {shape}, '
+          f'{plan[6]} corner groups per row, {plan[7]} loads in flight per lane.')
     print()
-    print('Points, ns after the first wavefront entered the kernel (every wavefront of every workgroup):')
+    print(f'Points, ns after the first wavefront entered the kernel (every wavefront of the first {wgs} workgroups):')
     print()
     print('| point | wavefronts | p0 | p50 | p90 | max |')
     print('|---|---:|---:|---:|---:|---:|')
     for name, q in points:
         print(f'| {name} | {q["n"]} | {q["p0"]:.0f} | {q["p50"]:.0f} | {q["p90"]:.0f} | {q["max"]:.0f} |')
     print()
-    print('Phases, ns per wavefront ("gatherers": the wavefronts that gather a row in every workgroup; "jobs": the '
-          'four projection jobs):')
+    print(f'Phases, ns per wavefront ("gatherers": the first {gatherers} wavefronts, which gather rows in every '
+          f'workgroup; "jobs": the wavefronts that ran a projection job; stamped in the first {wgs} workgroups):')
     print()
     print('| phase | wavefronts | n | p0 | p50 | p90 | max |')
     print('|---|---|---:|---:|---:|---:|---:|')

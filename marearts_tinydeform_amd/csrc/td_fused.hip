@@ -24,14 +24,15 @@
 #include "td_internal.h"
 #include "td_prologue.h"
 
-// Phase stamps (built only with TD_PHASE_STAMPS, as libtinydeform_phases.so; never in libtinydeform.so). The
-// instantiation that one-slice-per-CU launches use (12 wavefronts, 6 loads in flight, 16-bit) reads the 100 MHz
-// real-time counter at its phase boundaries into registers and, at its end, lane 0 of every wavefront of the first
-// kPhaseWgs workgroups stores its 16 stamps to td_phase_stamp_buf[workgroup][wavefront][16], so a launch's
-// timeline costs no memory traffic until the wavefront is done. Slots: 11 kernel entry, 0 rows decoded, 1 corner
-// table barrier passed, 2 gather done, 3 gather barrier passed, 4 projection set up, 5 job start, 6 first chunk done,
-// 7 MFMAs done, 8 partial sums stored, 9 projection barrier passed, 10 outputs stored; 0 where a wavefront passed
-// no such point. td_phase_stamps() copies the buffer to the host.
+// Phase stamps (built only with TD_PHASE_STAMPS, as libtinydeform_phases.so; never in libtinydeform.so). Every
+// instantiation of the operator's vector kernel reads the 100 MHz real-time counter at its phase boundaries into
+// registers and, at its end, lane 0 of every wavefront of the first kPhaseWgs workgroups stores its 16 stamps to
+// td_phase_stamp_buf[workgroup][wavefront][16] (12 wavefront slots per workgroup), so a launch's timeline costs no
+// memory traffic until the wavefront is done. Slots: 11 kernel entry, 0 rows decoded, 1 corner table barrier
+// passed, 2 gather done, 3 gather barrier passed, 4 projection set up, 5 job start, 6 first chunk done (the
+// one-slice-per-CU 16-bit kernel only), 7 MFMAs done, 8 partial sums stored, 9 projection barrier passed, 10 outputs
+// stored; 0 where a wavefront passed no such point (5 and 7 are not stamped in the jobs of one (N tile, K slice)).
+// td_phase_stamps() copies the buffer to the host.
 #ifdef TD_PHASE_STAMPS
 constexpr int kPhaseWgs = 1024;
 __device__ unsigned long long td_phase_stamp_buf[kPhaseWgs * 12 * 16];
@@ -115,7 +116,7 @@ __attribute__((amdgpu_waves_per_eu(std::is_same<T, bf16>::value && WAVES == 8 &&
 void fused_vec_kernel(FusedParams p) {
     constexpr int NTH = WAVES * kWave;
 #ifdef TD_PHASE_STAMPS
-    constexpr bool kStamp = WAVES == 12 && NB == 6 && !LAYER;
+    constexpr bool kStamp = !LAYER && WAVES <= 12;
     [[maybe_unused]] unsigned long long stamps_[16] = {};
 #endif
     TD_STAMP(11);
@@ -397,6 +398,7 @@ void fused_vec_kernel(FusedParams p) {
         // hi + lo) once for all N tiles
         const int nk = (C + KCH - 1) / KCH;
         for (int ks = wave; ks < p.KS; ks += WAVES) {
+            TD_STAMP(5);
             const int kb = ks * nk / p.KS, ke = (ks + 1) * nk / p.KS;
             f32x4 acc[kAllN];
             bool dv[kAllN];
@@ -462,6 +464,7 @@ void fused_vec_kernel(FusedParams p) {
                     }
                 }
             }
+            TD_STAMP(7);
             float* pp = part + ks * 16 * PW;
 #pragma unroll
             for (int nt = 0; nt < kAllN; ++nt) {
@@ -576,6 +579,8 @@ void fused_vec_kernel(FusedParams p) {
             v = fmaf(cvt<float>(bias[static_cast<size_t>(h) * D + d]), two ? wsum[r] + wsum[16 + r] : wsum[r], v);
         out[(static_cast<size_t>(rbase + r) * g.H + h) * D + d] = static_cast<T>(v);
     }
+    TD_STAMP(10);
+    TD_STAMP_FLUSH();
 }
 
 template <typename T, int WAVES, bool GENERAL>

@@ -665,19 +665,19 @@ def test_dfine_sample_v2(dtype, method):
         td.ma_deform_sample_v2(value.cuda(), shapes.cuda(), starts.cuda(), loc.cuda(), attn.cuda(), points, 'nope')
 
 
-@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
-def test_phase_stamp_build_computes_what_the_library_computes(dtype):
+@pytest.mark.parametrize('dtype,B', [(torch.float16, 1), (torch.bfloat16, 1), (torch.float32, 1), (torch.bfloat16, 8)])
+def test_phase_stamp_build_computes_what_the_library_computes(dtype, B):
     # bench.py --phases times libtinydeform_phases.so: the same fused kernel with stamps. Its outputs must be the
-    # library's bit for bit at the headline shape (RT-DETR 640, B1 Q300: one 12-wavefront slice per CU, the stamped
-    # instantiation), and every wavefront's stamps must follow the kernel's phase order.
+    # library's bit for bit (RT-DETR 640, Q300: one slice per CU at B1, 16-row query tiles at B8), and every
+    # stamped wavefront's stamps must follow the kernel's phase order.
     import ctypes
     path = os.path.join(os.path.dirname(_native.LIB_PATH), 'libtinydeform_phases.so')
     phases = _native.load(path)
     assert phases is not None, _native.load_error
     phases.td_phase_stamps.argtypes = [ctypes.c_void_p, ctypes.c_int64]
     phases.td_phase_stamps.restype = ctypes.c_int
-    say(f'  phase build, {dtype}, B1 Q300')
-    dev = to(workload(1, 300, 8, 32, 256, RTDETR_LEVELS, 4, dtype), 'cuda')
+    say(f'  phase build, {dtype}, B{B} Q300')
+    dev = to(workload(B, 300, 8, 32, 256, RTDETR_LEVELS, 4, dtype), 'cuda')
     want = run(dev, 'fused')
     plain = _native.lib
     try:
@@ -689,8 +689,9 @@ def test_phase_stamp_build_computes_what_the_library_computes(dtype):
     n = 1024 * 12 * 16
     buf = np.zeros(n, dtype=np.uint64)
     assert phases.td_phase_stamps(buf.ctypes.data, n) == 0
-    st = buf.reshape(1024, 12, 16)[:256].astype(np.int64)
-    order = [11, 0, 1, 2, 3, 4, 9, 10]  # entry .. outputs stored, passed by every wavefront of the 256 workgroups
+    plan = _native.fused_plan(dtype, B, 300, 8400, 256, 8, 32, 3, 4)
+    st = buf.reshape(1024, 12, 16)[:min(plan[1], 1024), :plan[2]].astype(np.int64)
+    order = [11, 0, 1, 2, 3, 4, 8, 9, 10]  # entry .. outputs stored: every wavefront of every stamped workgroup
     seq = st[:, :, order]
     assert (seq > 0).all()
     assert (np.diff(seq, axis=-1) >= 0).all()
