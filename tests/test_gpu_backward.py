@@ -44,6 +44,20 @@ def gpu_grads(args, grad_out, dtype, mask=None):
     return {n: None if leaves[p] is None else leaves[p].grad for n, p in zip(NAMES, POS)}, out
 
 
+def boundary_distance(loc, levels):
+    """The smallest distance, in pixels, of a sample's x = loc * W - 0.5 (or y) from an integer that is not 0: where
+    the two coincide exactly the float32 and float64 floors agree."""
+    best = float('inf')
+    for l, (hl, wl) in enumerate(levels):
+        for k, size in ((0, wl), (1, hl)):
+            c = loc[..., l, :, k].double() * size - 0.5
+            dist = (c - c.round()).abs()
+            dist = dist[dist > 0]
+            if dist.numel():
+                best = min(best, float(dist.min()))
+    return best
+
+
 def check(name, got, ref, dtype):
     if ref is None:
         assert got is None, name
@@ -212,3 +226,30 @@ def test_encoder_shape_gradients(dtype, with_mask):
         for n in NAMES:
             check(f'encoder Q={Q} {dtype} d{n}', grads[n], ref[n], dtype)
 
+
+
+@pytest.mark.parametrize('dtype,D', [(torch.float16, 8), (torch.bfloat16, 16), (torch.float16, 64),
+                                     (torch.float32, 4), (torch.float32, 32)])
+@pytest.mark.parametrize('loc_dist', ['encoder', 'uniform'])
+def test_dense_query_gradients(dtype, D, loc_dist):
+    # many queries per token (Q = 2N, 8 samples each: 32 corner hits per token and head on average), with encoder
+    # locations (each query samples around its own token, so neighbouring queries add into the same value-gradient
+    # rows) and uniform ones; head widths 4 to 64 in every 16/32-bit type, Q = 2N and 2N - 2
+    levels = [(24, 32), (12, 16)]
+    N = sum(h * w for h, w in levels)
+    for Q in (2 * N, 2 * N - 2):
+        # the location gradient of bilinear sampling jumps where a sample crosses a pixel boundary; a sample within
+        # float32 rounding of one (x = loc * W - 0.5 carries about 2e-6 pixel of rounding at W = 32) is floored to
+        # one side here and possibly the other in the float64 oracle, so the seed is the first from 7 whose samples
+        # all lie at least 1e-5 pixel from a boundary
+        for seed in range(7, 200):
+            args = workload(1, Q, 4, D, 64, levels, 4, dtype, loc_dist=loc_dist, seed=seed)
+            if boundary_distance(args[5], levels) >= 1e-5:
+                break
+        assert boundary_distance(args[5], levels) >= 1e-5
+        go = grad_out_for(args)
+        say(f'  backward dense queries Q={Q} D={D} {dtype} {loc_dist}')
+        grads, _ = gpu_grads(args, go, dtype)
+        ref = gridsample.deform_attn_grads(*args, go.to(dtype))
+        for n in NAMES:
+            check(f'dense Q={Q} D={D} {dtype} {loc_dist} d{n}', grads[n], ref[n], dtype)
