@@ -28,13 +28,13 @@ struct Taps {
     A fx, fy;
 };
 
+// taps_at_b takes the row's image b (for the padding mask); taps_at derives it from the row index (b, q, h).
 template <typename A>
-__device__ __forceinline__ Taps<A> taps_at(A lx, A ly, int l, const Geom& g, int64_t row) {
+__device__ __forceinline__ Taps<A> taps_at_b(A lx, A ly, int l, const Geom& g, int64_t b) {
     Taps<A> t;
     const int hl = static_cast<int>(g.shapes[2 * l]);
     const int wl = static_cast<int>(g.shapes[2 * l + 1]);
     const int64_t st = g.starts[l];
-    const int64_t b = row / (static_cast<int64_t>(g.Q) * g.H);
     if (g.discrete) {
         const A fx = fmin(fmax(lx * static_cast<A>(wl) + static_cast<A>(0.5), static_cast<A>(-1)), static_cast<A>(wl));
         const A fy = fmin(fmax(ly * static_cast<A>(hl) + static_cast<A>(0.5), static_cast<A>(-1)), static_cast<A>(hl));
@@ -69,6 +69,11 @@ __device__ __forceinline__ Taps<A> taps_at(A lx, A ly, int l, const Geom& g, int
 }
 
 template <typename A>
+__device__ __forceinline__ Taps<A> taps_at(A lx, A ly, int l, const Geom& g, int64_t row) {
+    return taps_at_b<A>(lx, ly, l, g, row / (static_cast<int64_t>(g.Q) * g.H));
+}
+
+template <typename A>
 __device__ __forceinline__ A tap_weight(const Taps<A>& t, int k) {
     return ((k & 1) ? t.fx : static_cast<A>(1) - t.fx) * ((k >> 1) ? t.fy : static_cast<A>(1) - t.fy);
 }
@@ -90,7 +95,8 @@ struct BackParams {
     void* grad_loc;    // [rows, LP, 2] element type (accumulation type with g.loc_acc)
     void* grad_attn;   // [rows, LP]
     Geom g;
-    int LG;  // lanes per sample: a power of two, LG * CE >= D
+    int LG;           // lanes per sample: a power of two, LG * CE >= D
+    int scatter = 1;  // sample_backward_vec_kernel: 0 leaves the value gradient to scatter_bucket_kernel
 };
 
 // One wavefront per row (b, q, h); its LP samples go 64 / LG at a time, LG lanes per sample, lane `sub` of a sample
@@ -481,7 +487,7 @@ __global__ __launch_bounds__(256) void sample_backward_vec_kernel(BackParams p) 
     }
 
     // value-gradient atomics: LG lanes per sample (LG = D rounded up to a power of two), lane sub adds channel sub
-    {
+    if (p.scatter) {
         const int LG = p.LG, per = kWave / LG, slot = lane / LG, sub = lane - slot * LG;
         if (sub >= D) return;
         const A gr = cvt<A>(go[sub]);
@@ -501,6 +507,233 @@ __global__ __launch_bounds__(256) void sample_backward_vec_kernel(BackParams p) 
                 atomic_add(gv + static_cast<int64_t>(tk) * HD, bt.a * w * gr);
             }
         }
+    }
+}
+
+// The value-gradient scatter where many queries sample the same neighbourhood (encoder self-attention: every token
+// a query, sampling a few pixels around itself on every level). The scatter is bound by the float atomics, at a
+// rate per 128-byte line; consecutive queries of one head touch overlapping pixels (16 of them about 2.4 times fewer
+// pixels than corners on DINO-style encoder inputs), so their corners are summed per pixel first and each touched
+// pixel goes out once. Workgroup = (image b, head h, QT consecutive queries), one (row, sample) per thread; per level:
+//   * the bounding box of the level's in-map corners (LDS min / max);
+//   * if it holds at most kBucketPix pixels: a counting sort of the corners by pixel (an integer LDS atomic per corner
+//     gives its rank in the pixel's bucket; a workgroup scan of the counts gives each bucket's start and the list
+//     of touched pixels and their tokens); then D lanes per touched pixel sum its bucket's a * w_c * g_r from LDS,
+//     without atomics, and add the sums to grad_value (one D-wide atomic per channel group);
+//   * otherwise the level's corners are added to grad_value directly, as sample_backward_vec_kernel does.
+// D is a power of two from 4 to 64 (lane = channel tid % D), P > 0. The sums reach grad_value in another order than
+// the direct scatter's, so the two agree to float rounding.
+constexpr int kBucketPix = 1024;  // bounding-box pixels per level at most
+constexpr int kBucketEnt = 1024;  // corner entries per level at most: QT * P * 4 with QT * L * P <= 256
+
+struct BucketParams {
+    const void* loc;
+    const void* attn;
+    const void* grad_out;
+    void* grad_value;  // [B, N, H * D] float, zeroed
+    Geom g;
+    int QT, qtiles, units, per_xcd;
+    FastDiv d_lp, d_p;  // divisions by L * P and P
+};
+
+// minimum and maximum over the 64 lanes of a wavefront (every lane receives them)
+__device__ __forceinline__ int wave_min(int v) {
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) v = min(v, __builtin_amdgcn_ds_bpermute((lane_id() ^ m) << 2, v));
+    return v;
+}
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) v = max(v, __builtin_amdgcn_ds_bpermute((lane_id() ^ m) << 2, v));
+    return v;
+}
+
+// inclusive prefix sum over the 64 lanes of a wavefront
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int t = __builtin_amdgcn_ds_bpermute((lane - off) << 2, v);
+        if (lane >= off) v += t;
+    }
+    return v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void scatter_bucket_kernel(BucketParams bp) {
+    using A = float;
+    constexpr int NTH = 256;
+    const Geom& g = bp.g;
+    const int D = g.D, HD = g.H * g.D, LP = g.LP, P = g.P, QT = bp.QT;
+    const int unit = (blockIdx.x % kXcds) * bp.per_xcd + blockIdx.x / kXcds;
+    if (unit >= bp.units) return;  // the whole workgroup
+    const int qt = unit % bp.qtiles, bh = unit / bp.qtiles;
+    const int h = bh % g.H, b = bh / g.H;
+    const int q0 = qt * QT, nq = g.Q - q0 < QT ? g.Q - q0 : QT;
+    const int tid = threadIdx.x, d = tid & (D - 1), grp = tid / D, ngrp = NTH / D;
+    const int wave = tid >> 6, lane = tid & (kWave - 1);
+
+    __shared__ A gr[256];                  // [QT][D] (QT * D <= 16 * 16 ... 4 * 64)
+    __shared__ int etok[kBucketEnt];       // corner token, -1 outside
+    __shared__ A ecoef[kBucketEnt];        // a * w_c
+    __shared__ int erow[kBucketEnt];       // the corner's row offset in gr (r * D)
+    __shared__ int cnt[kBucketPix];        // corners per window pixel
+    __shared__ int base[kBucketPix];       // start of the pixel's bucket in list
+    __shared__ int tpix[kBucketEnt];       // touched pixels (compacted)
+    __shared__ int ttok[kBucketEnt];       // their tokens
+    __shared__ int list[kBucketEnt];       // entries bucketed by pixel
+    __shared__ int boxw[4][4];  // per wavefront: min x, min y, max x, max y
+    __shared__ int wtot[4];
+
+    const T* __restrict__ go = static_cast<const T*>(bp.grad_out);
+    A* __restrict__ gv = static_cast<A*>(bp.grad_value) + static_cast<int64_t>(b) * g.N * HD + static_cast<int64_t>(h) * D;
+    for (int i = tid; i < nq * D; i += NTH) {
+        const int r = i / D;
+        gr[i] = cvt<A>(go[(static_cast<int64_t>(b) * g.Q + q0 + r) * HD + static_cast<int64_t>(h) * D + (i - r * D)]);
+    }
+
+    // this thread's sample (row r, sample j of level lt): its four corners' tokens, pixels and coefficients
+    int tk[4] = {-1, -1, -1, -1}, cx[4] = {0, 0, 0, 0}, cy[4] = {0, 0, 0, 0};
+    A cf[4] = {0, 0, 0, 0};
+    int lt = -1, r = 0, jp = 0;
+    if (tid < nq * LP) {
+        r = static_cast<int>(fast_div(bp.d_lp, static_cast<uint32_t>(tid)));
+        const int j = tid - r * LP;
+        lt = static_cast<int>(fast_div(bp.d_p, static_cast<uint32_t>(j)));
+        jp = j - lt * P;
+        const int64_t row = (static_cast<int64_t>(b) * g.Q + q0 + r) * g.H + h, idx = row * LP + j;
+        A lx, ly, a;
+        if (g.loc_acc) {
+            lx = static_cast<const A*>(bp.loc)[2 * idx];
+            ly = static_cast<const A*>(bp.loc)[2 * idx + 1];
+            a = static_cast<const A*>(bp.attn)[idx];
+        } else {
+            lx = cvt<A>(static_cast<const T*>(bp.loc)[2 * idx]);
+            ly = cvt<A>(static_cast<const T*>(bp.loc)[2 * idx + 1]);
+            a = cvt<A>(static_cast<const T*>(bp.attn)[idx]);
+        }
+        const Taps<A> t = taps_at_b<A>(lx, ly, lt, g, b);
+        const int wl = static_cast<int>(g.shapes[2 * lt + 1]);
+        const int64_t st = g.starts[lt];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            tk[k] = t.tok[k];
+            cf[k] = g.discrete ? (k == 0 ? a : static_cast<A>(0)) : a * tap_weight(t, k);
+            if (tk[k] >= 0) {
+                const int loc = static_cast<int>(tk[k] - st);
+                cy[k] = loc / wl;
+                cx[k] = loc - cy[k] * wl;
+            }
+        }
+    }
+
+    for (int l = 0; l < g.L; ++l) {
+        const int ne = nq * P * 4;  // the level's corner entries
+        const bool mine = lt == l;
+        int mnx = 0x7fffffff, mny = 0x7fffffff, mxx = -1, mxy = -1;
+        if (mine) {
+            const int e0 = (r * P + jp) * 4;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                etok[e0 + k] = tk[k];
+                ecoef[e0 + k] = cf[k];
+                erow[e0 + k] = r * D;
+                if (tk[k] >= 0) {
+                    mnx = min(mnx, cx[k]);
+                    mny = min(mny, cy[k]);
+                    mxx = max(mxx, cx[k]);
+                    mxy = max(mxy, cy[k]);
+                }
+            }
+        }
+        mnx = wave_min(mnx);
+        mny = wave_min(mny);
+        mxx = wave_max(mxx);
+        mxy = wave_max(mxy);
+        if (lane == 0) {
+            boxw[wave][0] = mnx;
+            boxw[wave][1] = mny;
+            boxw[wave][2] = mxx;
+            boxw[wave][3] = mxy;
+        }
+        __syncthreads();  // the level's entries and the wavefronts' boxes (and, first, the grad_out rows) are in place
+        const int x0 = min(min(boxw[0][0], boxw[1][0]), min(boxw[2][0], boxw[3][0]));
+        const int y0 = min(min(boxw[0][1], boxw[1][1]), min(boxw[2][1], boxw[3][1]));
+        const int x1 = max(max(boxw[0][2], boxw[1][2]), max(boxw[2][2], boxw[3][2]));
+        const int y1 = max(max(boxw[0][3], boxw[1][3]), max(boxw[2][3], boxw[3][3]));
+        if (x1 >= x0) {  // the level has in-map corners (uniform)
+            const int bw = x1 - x0 + 1;
+            const int64_t npix64 = static_cast<int64_t>(bw) * (y1 - y0 + 1);
+            if (npix64 <= kBucketPix) {
+                const int npix = static_cast<int>(npix64);
+                const int wl = static_cast<int>(g.shapes[2 * l + 1]);
+                const int64_t st = g.starts[l];
+                for (int i = tid; i < npix; i += NTH) cnt[i] = 0;
+                __syncthreads();
+                int px[4], rank[4];
+                if (mine) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        px[k] = (cy[k] - y0) * bw + (cx[k] - x0);
+                        rank[k] = tk[k] >= 0 ? atomicAdd(&cnt[px[k]], 1) : 0;
+                    }
+                }
+                __syncthreads();
+                // workgroup scan of the counts: thread t owns pixels [t * k, t * k + k), k = ceil(npix / 256) <= 4;
+                // packed (touched pixels << 16) | corners
+                const int kp = (npix + NTH - 1) / NTH, p0 = tid * kp;
+                int own = 0;
+                for (int i = 0; i < kp; ++i) {
+                    const int pp = p0 + i;
+                    const int c = pp < npix ? cnt[pp] : 0;
+                    own += c + (c > 0 ? (1 << 16) : 0);
+                }
+                const int incl = wave_incl_scan(own);
+                if (lane == kWave - 1) wtot[wave] = incl;
+                __syncthreads();
+                int before = 0;
+                for (int w = 0; w < wave; ++w) before += wtot[w];
+                const int total = wtot[0] + wtot[1] + wtot[2] + wtot[3];
+                int run = before + incl - own;  // exclusive
+                for (int i = 0; i < kp; ++i) {
+                    const int pp = p0 + i;
+                    if (pp >= npix) break;
+                    const int c = cnt[pp];
+                    base[pp] = run & 0xffff;
+                    if (c > 0) {
+                        const int ti = run >> 16;
+                        tpix[ti] = pp;
+                        const int yy = pp / bw;
+                        ttok[ti] = static_cast<int>(st + static_cast<int64_t>(y0 + yy) * wl + (x0 + pp - yy * bw));
+                    }
+                    run += c + (c > 0 ? (1 << 16) : 0);
+                }
+                __syncthreads();
+                if (mine) {
+                    const int e0 = (r * P + jp) * 4;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (tk[k] >= 0) list[base[px[k]] + rank[k]] = e0 + k;
+                }
+                __syncthreads();
+                const int ntouched = total >> 16;
+                for (int ti = grp; ti < ntouched; ti += ngrp) {
+                    const int pp = tpix[ti], s0 = base[pp], n = cnt[pp];
+                    A v = 0;
+                    for (int i = 0; i < n; ++i) {
+                        const int e = list[s0 + i];
+                        v += ecoef[e] * gr[erow[e] + d];
+                    }
+                    atomic_add(gv + static_cast<int64_t>(ttok[ti]) * HD + d, v);
+                }
+            } else {
+                for (int e = grp; e < ne; e += ngrp) {
+                    const int t = etok[e];
+                    if (t >= 0) atomic_add(gv + static_cast<int64_t>(t) * HD + d, ecoef[e] * gr[erow[e] + d]);
+                }
+            }
+        }
+        __syncthreads();  // the buckets, the entries and the boxes are free for the next level
     }
 }
 
@@ -789,14 +1022,45 @@ int sample_backward_vec_go(BackParams p, hipStream_t stream) {
     return launched("sample backward");
 }
 
+// The bucketed scatter pays where the corners of neighbouring queries overlap: at least 16 corner hits per token
+// and head on average (encoder self-attention: 64 at DINO's 4 levels x 4 points; decoders: 2-4).
+inline bool bucket_scatter_pays(const Geom& g) {
+    return is_pow2(g.D) && g.D >= 4 && g.D <= 64 && g.P > 0 && g.N > 0 && g.LP > 0 && g.LP <= 256 &&
+           static_cast<int64_t>(g.Q) * g.LP * 4 >= int64_t{16} * g.N;
+}
+
+template <typename T>
+int scatter_bucket_go(const BackParams& p, hipStream_t stream) {
+    const Geom& g = p.g;
+    BucketParams bp{p.loc, p.attn, p.grad_out, p.grad_value, g, 0, 0, 0, 0, {}, {}};
+    bp.QT = 256 / g.LP > 16 ? 16 : 256 / g.LP;
+    if (bp.QT * g.D > 256) bp.QT = 256 / g.D;  // the grad_out rows' LDS
+    bp.qtiles = (g.Q + bp.QT - 1) / bp.QT;
+    const int64_t units = static_cast<int64_t>(g.B) * g.H * bp.qtiles;
+    if (units == 0) return 0;
+    if (units > (int64_t{1} << 30)) return set_error(-1, "sample backward: too many query tiles");
+    bp.units = static_cast<int>(units);
+    bp.per_xcd = static_cast<int>((units + kXcds - 1) / kXcds);
+    bp.d_lp = make_fastdiv(static_cast<uint32_t>(g.LP));
+    bp.d_p = make_fastdiv(static_cast<uint32_t>(g.P));
+    hipLaunchKernelGGL(scatter_bucket_kernel<T>, dim3(static_cast<unsigned>(bp.per_xcd * kXcds)), dim3(256), 0, stream,
+                       bp);
+    return launched("sample backward scatter");
+}
+
 template <typename T>
 int sample_backward_t(const BackParams& p, hipStream_t stream) {
     constexpr int V = 16 / static_cast<int>(sizeof(T));
     if constexpr (sizeof(T) <= 4) {
         // 16-byte value loads need D a multiple of V and 16-byte aligned value rows
         if (p.g.D <= 64 && p.g.D % V == 0 && is_pow2(p.g.D / V) && reinterpret_cast<uintptr_t>(p.value) % 16 == 0 &&
-            reinterpret_cast<uintptr_t>(p.grad_out) % 16 == 0)
-            return sample_backward_vec_go<T>(p, stream);
+            reinterpret_cast<uintptr_t>(p.grad_out) % 16 == 0) {
+            if (!bucket_scatter_pays(p.g)) return sample_backward_vec_go<T>(p, stream);
+            BackParams q = p;
+            q.scatter = 0;  // the dot products and the location and weight gradients only
+            const int rc = sample_backward_vec_go<T>(q, stream);
+            return rc != 0 ? rc : scatter_bucket_go<T>(p, stream);
+        }
     }
     if (p.g.D <= 64) return sample_backward_batched_go<T>(p, stream);
     if (p.g.D <= 128) return sample_backward_go<T, 2>(p, stream);

@@ -232,9 +232,10 @@ def test_encoder_shape_gradients(dtype, with_mask):
                                      (torch.float32, 4), (torch.float32, 32)])
 @pytest.mark.parametrize('loc_dist', ['encoder', 'uniform'])
 def test_dense_query_gradients(dtype, D, loc_dist):
-    # many queries per token (Q = 2N, 8 samples each: 32 corner hits per token and head on average), with encoder
-    # locations (each query samples around its own token, so neighbouring queries add into the same value-gradient
-    # rows) and uniform ones; head widths 4 to 64 in every 16/32-bit type, Q = 2N and 2N - 2
+    # many queries per token (Q = 2N, 8 samples each: 32 corner hits per token and head on average), so the value
+    # gradient goes through the bucketed scatter (scatter_bucket_kernel): with encoder locations each level's corners
+    # of 16 consecutive queries fit its window and are summed per pixel; with uniform ones they do not and the
+    # kernel adds them directly. Head widths 4 to 64 in every 16/32-bit type, Q = 2N and 2N - 2 (a ragged last tile)
     levels = [(24, 32), (12, 16)]
     N = sum(h * w for h, w in levels)
     for Q in (2 * N, 2 * N - 2):
