@@ -510,6 +510,170 @@ __global__ __launch_bounds__(256) void sample_backward_vec_kernel(BackParams p) 
     }
 }
 
+// Sums of v[0..NB) over the n consecutive lanes of an aligned group (n = 1, 2, 4, 8 or 16; uniform), every lane of
+// the group receiving them, by DPP moves within rows of 16 lanes: quad exchanges (lane ^ 1, lane ^ 2), then the
+// half-row and row mirrors, which pair each lane with one of the other quad or octet, all of whose lanes hold that
+// group's sums.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+template <int NB>
+__device__ __forceinline__ void group_sums(float (&v)[NB], int n) {
+    if (n > 1) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) v[u] += dpp_mov<0xb1>(v[u]);  // quad_perm [1, 0, 3, 2]
+    }
+    if (n > 2) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) v[u] += dpp_mov<0x4e>(v[u]);  // quad_perm [2, 3, 0, 1]
+    }
+    if (n > 4) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) v[u] += dpp_mov<0x141>(v[u]);  // row_half_mirror
+    }
+    if (n > 8) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) v[u] += dpp_mov<0x140>(v[u]);  // row_mirror
+    }
+}
+
+// The location and attention-weight gradients alone, for the value gradient's bucketed scatter
+// (scatter_bucket_kernel), laid out like the forward sampler (td_sample.hip) rather than one row per wavefront.
+// A workgroup takes RB rows, in (b, h, q) order, so that the workgroups of an XCD work through one or two heads of one
+// image:
+//   * taps: thread (row r, sample j) computes the sample's taps, writes its four corners' byte offsets in the value
+//     buffer into LDS (kOutside when outside) and keeps the fractional position and weight in registers;
+//   * dots: lane (r, corner group sg, chunk ch of V channels) loads V channels of corners sg, sg + SG, ... of row r by
+//     raw buffer loads (an outside corner's load returns zeros), NB in flight, dots them with its chunk of grad_out
+//     and sums the DV = D / V chunks of a corner across lanes (group_sums); d_c = value[t_c] . g_r into LDS;
+//   * thread (r, j) turns its four d_c into the gradients, as sample_backward_vec_kernel does.
+// Needs 16- or 32-bit types, D / V a power of two up to 16, value under 2 GB and B * Q * H * L * P below 2^31.
+struct LocAttnParams {
+    BackParams p;
+    int RB, SG, blocks, per_xcd, val_bytes;
+    FastDiv d_lp, d_gs, d_dv, d_q, d_h;  // divisions by L * P, DV * SG, DV, Q and H
+};
+
+template <typename T, int V, int NB>
+__global__ __launch_bounds__(256) void loc_attn_backward_kernel(LocAttnParams lp) {
+    constexpr int NTH = 256;
+    using A = float;
+    using IO = VecIO<T, V>;
+    using R = typename IO::raw_t;
+    const BackParams& p = lp.p;
+    const Geom& g = p.g;
+    const int LP = g.LP, S = 4 * LP, D = g.D, HD = g.H * D, DV = D / V, SG = lp.SG, GS = DV * SG, RB = lp.RB;
+    __shared__ int off[4 * NTH];  // [RB][S] corner byte offsets (RB * LP <= NTH)
+    __shared__ A dots[4 * NTH];   // [RB][S] value row . grad_out row
+    const int tid = threadIdx.x;
+    const int blk = (blockIdx.x % kXcds) * lp.per_xcd + blockIdx.x / kXcds;
+    if (blk >= lp.blocks) return;  // the whole workgroup
+    const int rows = g.B * g.Q * g.H, i0 = blk * RB;
+    // row (b, q, h) of the i-th row in (b, h, q) order
+    const auto row_of = [&](int i, int& b, int& h) {
+        const int bh = static_cast<int>(fast_div(lp.d_q, static_cast<uint32_t>(i))), q = i - bh * g.Q;
+        b = static_cast<int>(fast_div(lp.d_h, static_cast<uint32_t>(bh)));
+        h = bh - b * g.H;
+        return (b * g.Q + q) * g.H + h;
+    };
+
+    const int sb = HD * static_cast<int>(sizeof(T));
+    A fx = 0, fy = 0, a = 0, wl = 0, hl = 0;
+    int64_t idx = -1;  // this thread's sample, -1 for none
+    int rs = 0, js = 0;
+    if (tid < RB * LP) {
+        rs = static_cast<int>(fast_div(lp.d_lp, static_cast<uint32_t>(tid)));
+        js = tid - rs * LP;
+        int* o4 = off + rs * S + 4 * js;
+        if (i0 + rs < rows) {
+            int b, h;
+            const int row = row_of(i0 + rs, b, h);
+            idx = static_cast<int64_t>(row) * LP + js;
+            A lx, ly;
+            sample_input<T, A>(p, idx, lx, ly, a);
+            const int l = level_of(g, js);
+            const Taps<A> t = taps_at_b<A>(lx, ly, l, g, b);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o4[k] = t.tok[k] >= 0 ? t.tok[k] * sb : kOutside;
+            fx = t.fx;
+            fy = t.fy;
+            wl = static_cast<A>(g.shapes[2 * l + 1]);
+            hl = static_cast<A>(g.shapes[2 * l]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o4[k] = kOutside;
+        }
+    }
+    __syncthreads();
+
+    const __amdgpu_buffer_rsrc_t rsrc = buffer_of(p.value, lp.val_bytes);
+    const T* __restrict__ go = static_cast<const T*>(p.grad_out);
+    for (int it = tid; it < RB * GS; it += NTH) {
+        const int r = static_cast<int>(fast_div(lp.d_gs, static_cast<uint32_t>(it))), rem = it - r * GS;
+        const int sg = static_cast<int>(fast_div(lp.d_dv, static_cast<uint32_t>(rem))), ch = rem - sg * DV;
+        int b = 0, h = 0, row = 0;
+        const bool valid = i0 + r < rows;
+        if (valid) row = row_of(i0 + r, b, h);
+        A gc[V];
+        IO::unpack(valid ? IO::load(go + static_cast<int64_t>(row) * D + ch * V) : IO::zero(), gc);
+        const unsigned lane_off =
+            static_cast<unsigned>((static_cast<int64_t>(b) * g.N * HD + h * D + ch * V) * static_cast<int>(sizeof(T)));
+        const int* __restrict__ orow = off + r * S;
+        A* __restrict__ drow = dots + r * S;
+        for (int s0 = sg; s0 < S; s0 += SG * NB) {
+            R raw[NB];
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                const int s = s0 + u * SG;
+                raw[u] = buffer_load<R>(rsrc, static_cast<unsigned>(s < S ? orow[s] : kOutside) + lane_off);
+            }
+            A d[NB];
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                A v[V];
+                IO::unpack(raw[u], v);
+                d[u] = 0;
+#pragma unroll
+                for (int e = 0; e < V; ++e) d[u] = fmaf(v[e], gc[e], d[u]);
+            }
+            group_sums(d, DV);
+            if (ch == 0) {
+#pragma unroll
+                for (int u = 0; u < NB; ++u)
+                    if (s0 + u * SG < S) drow[s0 + u * SG] = d[u];
+            }
+        }
+    }
+    __syncthreads();
+
+    if (idx >= 0) {
+        A d[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) d[k] = dots[rs * S + 4 * js + k];
+        A ga, gx = 0, gy = 0;
+        if (g.discrete) {
+            ga = d[0];
+        } else {
+            const A one = 1;
+            ga = (one - fx) * (one - fy) * d[0] + fx * (one - fy) * d[1] + (one - fx) * fy * d[2] + fx * fy * d[3];
+            const A dvx = (one - fy) * (d[1] - d[0]) + fy * (d[3] - d[2]);
+            const A dvy = (one - fx) * (d[2] - d[0]) + fx * (d[3] - d[1]);
+            gx = a * dvx * wl;
+            gy = a * dvy * hl;
+        }
+        if (g.loc_acc) {
+            static_cast<A*>(p.grad_loc)[2 * idx] = gx;
+            static_cast<A*>(p.grad_loc)[2 * idx + 1] = gy;
+            static_cast<A*>(p.grad_attn)[idx] = ga;
+        } else {
+            static_cast<T*>(p.grad_loc)[2 * idx] = static_cast<T>(gx);
+            static_cast<T*>(p.grad_loc)[2 * idx + 1] = static_cast<T>(gy);
+            static_cast<T*>(p.grad_attn)[idx] = static_cast<T>(ga);
+        }
+    }
+}
+
 // The value-gradient scatter where many queries sample the same neighbourhood (encoder self-attention: every token
 // a query, sampling a few pixels around itself on every level). The scatter is bound by the float atomics, at a
 // rate per 128-byte line; consecutive queries of one head touch overlapping pixels (16 of them about 2.4 times fewer
@@ -559,10 +723,10 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
     return v;
 }
 
-template <typename T>
-__global__ __launch_bounds__(256) void scatter_bucket_kernel(BucketParams bp) {
+template <typename T, int NTH>
+__global__ __launch_bounds__(NTH) void scatter_bucket_kernel(BucketParams bp) {
     using A = float;
-    constexpr int NTH = 256;
+    constexpr int NW = NTH / kWave;
     const Geom& g = bp.g;
     const int D = g.D, HD = g.H * g.D, LP = g.LP, P = g.P, QT = bp.QT;
     const int unit = (blockIdx.x % kXcds) * bp.per_xcd + blockIdx.x / kXcds;
@@ -573,7 +737,7 @@ __global__ __launch_bounds__(256) void scatter_bucket_kernel(BucketParams bp) {
     const int tid = threadIdx.x, d = tid & (D - 1), grp = tid / D, ngrp = NTH / D;
     const int wave = tid >> 6, lane = tid & (kWave - 1);
 
-    __shared__ A gr[256];                  // [QT][D] (QT * D <= 16 * 16 ... 4 * 64)
+    __shared__ A gr[NTH];                  // [QT][D] (QT * D <= NTH)
     __shared__ int etok[kBucketEnt];       // corner token, -1 outside
     __shared__ A ecoef[kBucketEnt];        // a * w_c
     __shared__ int erow[kBucketEnt];       // the corner's row offset in gr (r * D)
@@ -582,8 +746,8 @@ __global__ __launch_bounds__(256) void scatter_bucket_kernel(BucketParams bp) {
     __shared__ int tpix[kBucketEnt];       // touched pixels (compacted)
     __shared__ int ttok[kBucketEnt];       // their tokens
     __shared__ int list[kBucketEnt];       // entries bucketed by pixel
-    __shared__ int boxw[4][4];  // per wavefront: min x, min y, max x, max y
-    __shared__ int wtot[4];
+    __shared__ int boxw[NW][4];  // per wavefront: min x, min y, max x, max y
+    __shared__ int wtot[NW];
 
     const T* __restrict__ go = static_cast<const T*>(bp.grad_out);
     A* __restrict__ gv = static_cast<A*>(bp.grad_value) + static_cast<int64_t>(b) * g.N * HD + static_cast<int64_t>(h) * D;
@@ -657,10 +821,14 @@ __global__ __launch_bounds__(256) void scatter_bucket_kernel(BucketParams bp) {
             boxw[wave][3] = mxy;
         }
         __syncthreads();  // the level's entries and the wavefronts' boxes (and, first, the grad_out rows) are in place
-        const int x0 = min(min(boxw[0][0], boxw[1][0]), min(boxw[2][0], boxw[3][0]));
-        const int y0 = min(min(boxw[0][1], boxw[1][1]), min(boxw[2][1], boxw[3][1]));
-        const int x1 = max(max(boxw[0][2], boxw[1][2]), max(boxw[2][2], boxw[3][2]));
-        const int y1 = max(max(boxw[0][3], boxw[1][3]), max(boxw[2][3], boxw[3][3]));
+        int x0 = boxw[0][0], y0 = boxw[0][1], x1 = boxw[0][2], y1 = boxw[0][3];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            x0 = min(x0, boxw[w][0]);
+            y0 = min(y0, boxw[w][1]);
+            x1 = max(x1, boxw[w][2]);
+            y1 = max(y1, boxw[w][3]);
+        }
         if (x1 >= x0) {  // the level has in-map corners (uniform)
             const int bw = x1 - x0 + 1;
             const int64_t npix64 = static_cast<int64_t>(bw) * (y1 - y0 + 1);
@@ -679,7 +847,7 @@ __global__ __launch_bounds__(256) void scatter_bucket_kernel(BucketParams bp) {
                     }
                 }
                 __syncthreads();
-                // workgroup scan of the counts: thread t owns pixels [t * k, t * k + k), k = ceil(npix / 256) <= 4;
+                // workgroup scan of the counts: thread t owns pixels [t * k, t * k + k), k = ceil(npix / NTH) <= 4;
                 // packed (touched pixels << 16) | corners
                 const int kp = (npix + NTH - 1) / NTH, p0 = tid * kp;
                 int own = 0;
@@ -693,7 +861,9 @@ __global__ __launch_bounds__(256) void scatter_bucket_kernel(BucketParams bp) {
                 __syncthreads();
                 int before = 0;
                 for (int w = 0; w < wave; ++w) before += wtot[w];
-                const int total = wtot[0] + wtot[1] + wtot[2] + wtot[3];
+                int total = 0;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) total += wtot[w];
                 int run = before + incl - own;  // exclusive
                 for (int i = 0; i < kp; ++i) {
                     const int pp = p0 + i;
@@ -1033,8 +1203,13 @@ template <typename T>
 int scatter_bucket_go(const BackParams& p, hipStream_t stream) {
     const Geom& g = p.g;
     BucketParams bp{p.loc, p.attn, p.grad_out, p.grad_value, g, 0, 0, 0, 0, {}, {}};
-    bp.QT = 256 / g.LP > 16 ? 16 : 256 / g.LP;
-    if (bp.QT * g.D > 256) bp.QT = 256 / g.D;  // the grad_out rows' LDS
+    constexpr int NTH = 512;
+    // QT rows of one (row, sample) per thread, QT * P * 4 corner entries per level, QT * D grad_out floats
+    bp.QT = 32;
+    if (bp.QT > NTH / g.LP) bp.QT = NTH / g.LP;
+    if (bp.QT > kBucketEnt / (4 * g.P)) bp.QT = kBucketEnt / (4 * g.P);
+    if (bp.QT * g.D > NTH) bp.QT = NTH / g.D;
+    if (bp.QT < 1) return set_error(-1, "sample backward: no bucket shape for these sizes");
     bp.qtiles = (g.Q + bp.QT - 1) / bp.QT;
     const int64_t units = static_cast<int64_t>(g.B) * g.H * bp.qtiles;
     if (units == 0) return 0;
@@ -1043,9 +1218,38 @@ int scatter_bucket_go(const BackParams& p, hipStream_t stream) {
     bp.per_xcd = static_cast<int>((units + kXcds - 1) / kXcds);
     bp.d_lp = make_fastdiv(static_cast<uint32_t>(g.LP));
     bp.d_p = make_fastdiv(static_cast<uint32_t>(g.P));
-    hipLaunchKernelGGL(scatter_bucket_kernel<T>, dim3(static_cast<unsigned>(bp.per_xcd * kXcds)), dim3(256), 0, stream,
-                       bp);
+    hipLaunchKernelGGL((scatter_bucket_kernel<T, NTH>), dim3(static_cast<unsigned>(bp.per_xcd * kXcds)), dim3(NTH), 0,
+                       stream, bp);
     return launched("sample backward scatter");
+}
+
+// loc_attn_backward_kernel's shape: RB = 256 / LP rows a workgroup, SG corner groups a row (every thread a lane
+// where RB * DV <= 256); 0 when the kernel does not fit (the caller then takes sample_backward_vec_kernel)
+template <typename T>
+int loc_attn_backward_go(const BackParams& p, hipStream_t stream) {
+    constexpr int V = 16 / static_cast<int>(sizeof(T)), NTH = 256;
+    const Geom& g = p.g;
+    const int64_t rows = static_cast<int64_t>(g.B) * g.Q * g.H;
+    const int64_t vbytes = static_cast<int64_t>(g.B) * g.N * g.H * g.D * static_cast<int64_t>(sizeof(T));
+    const int DV = g.D / V;
+    if (g.LP <= 0 || g.LP > NTH || DV > 16 || rows * g.LP >= (int64_t{1} << 31) || vbytes >= (int64_t{1} << 31))
+        return 1;
+    LocAttnParams lp{p, 0, 0, 0, 0, 0, {}, {}, {}, {}, {}};
+    lp.RB = NTH / g.LP;
+    lp.SG = NTH / (lp.RB * DV) > 0 ? NTH / (lp.RB * DV) : 1;
+    const int64_t blocks = (rows + lp.RB - 1) / lp.RB;
+    lp.blocks = static_cast<int>(blocks);
+    lp.per_xcd = static_cast<int>((blocks + kXcds - 1) / kXcds);
+    lp.val_bytes = static_cast<int>(vbytes);
+    lp.d_lp = make_fastdiv(static_cast<uint32_t>(g.LP));
+    lp.d_gs = make_fastdiv(static_cast<uint32_t>(DV * lp.SG));
+    lp.d_dv = make_fastdiv(static_cast<uint32_t>(DV));
+    lp.d_q = make_fastdiv(static_cast<uint32_t>(g.Q));
+    lp.d_h = make_fastdiv(static_cast<uint32_t>(g.H));
+    if (rows == 0) return 0;
+    hipLaunchKernelGGL((loc_attn_backward_kernel<T, V, 8>), dim3(static_cast<unsigned>(lp.per_xcd * kXcds)), dim3(NTH),
+                       0, stream, lp);
+    return launched("sample backward locations");
 }
 
 template <typename T>
@@ -1056,9 +1260,12 @@ int sample_backward_t(const BackParams& p, hipStream_t stream) {
         if (p.g.D <= 64 && p.g.D % V == 0 && is_pow2(p.g.D / V) && reinterpret_cast<uintptr_t>(p.value) % 16 == 0 &&
             reinterpret_cast<uintptr_t>(p.grad_out) % 16 == 0) {
             if (!bucket_scatter_pays(p.g)) return sample_backward_vec_go<T>(p, stream);
-            BackParams q = p;
-            q.scatter = 0;  // the dot products and the location and weight gradients only
-            const int rc = sample_backward_vec_go<T>(q, stream);
+            int rc = loc_attn_backward_go<T>(p, stream);
+            if (rc == 1) {
+                BackParams q = p;
+                q.scatter = 0;  // the dot products and the location and weight gradients only
+                rc = sample_backward_vec_go<T>(q, stream);
+            }
             return rc != 0 ? rc : scatter_bucket_go<T>(p, stream);
         }
     }

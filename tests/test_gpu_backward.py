@@ -228,15 +228,17 @@ def test_encoder_shape_gradients(dtype, with_mask):
 
 
 
-@pytest.mark.parametrize('dtype,D', [(torch.float16, 8), (torch.bfloat16, 16), (torch.float16, 64),
-                                     (torch.float32, 4), (torch.float32, 32)])
+@pytest.mark.parametrize('dtype,D,nlev', [(torch.float16, 8, 2), (torch.bfloat16, 16, 2), (torch.float16, 64, 2),
+                                          (torch.float32, 4, 2), (torch.float32, 32, 2), (torch.float32, 64, 3)])
 @pytest.mark.parametrize('loc_dist', ['encoder', 'uniform'])
-def test_dense_query_gradients(dtype, D, loc_dist):
-    # many queries per token (Q = 2N, 8 samples each: 32 corner hits per token and head on average), so the value
-    # gradient goes through the bucketed scatter (scatter_bucket_kernel): with encoder locations each level's corners
-    # of 16 consecutive queries fit its window and are summed per pixel; with uniform ones they do not and the
-    # kernel adds them directly. Head widths 4 to 64 in every 16/32-bit type, Q = 2N and 2N - 2 (a ragged last tile)
-    levels = [(24, 32), (12, 16)]
+def test_dense_query_gradients(dtype, D, nlev, loc_dist):
+    # many queries per token (Q = 2N, 4 points a level: 16 or more corner hits per token and head on average), so the
+    # value gradient goes through the bucketed scatter (scatter_bucket_kernel) and the location and weight gradients
+    # through loc_attn_backward_kernel: with encoder locations each level's corners of consecutive queries fit its
+    # window and are summed per pixel; with uniform ones they do not and the kernel adds them directly. Head widths 4
+    # to 64 in every 16/32-bit type (1 to 16 lanes a corner row in the dot products), two levels (8 samples a row) or
+    # three (12: 21 rows a workgroup, four threads idle), Q = 2N and 2N - 2 (a ragged last tile)
+    levels = [(24, 32), (12, 16), (6, 8)][:nlev]
     N = sum(h * w for h, w in levels)
     for Q in (2 * N, 2 * N - 2):
         # the location gradient of bilinear sampling jumps where a sample crosses a pixel boundary; a sample within
@@ -249,7 +251,7 @@ def test_dense_query_gradients(dtype, D, loc_dist):
                 break
         assert boundary_distance(args[5], levels) >= 1e-5
         go = grad_out_for(args)
-        say(f'  backward dense queries Q={Q} D={D} {dtype} {loc_dist}')
+        say(f'  backward dense queries Q={Q} D={D} L={nlev} {dtype} {loc_dist}')
         grads, _ = gpu_grads(args, go, dtype)
         ref = gridsample.deform_attn_grads(*args, go.to(dtype))
         for n in NAMES:
