@@ -997,8 +997,10 @@ __global__ __launch_bounds__(256) void wgrad_kernel(WgradParams p) {
     const T* __restrict__ X = static_cast<const T*>(p.X);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r16 = lane & 15, kg = lane >> 4;
     const int wm = wave >> 1, wn = wave & 1;
-    // this thread's pieces: token rows mm[0] = 2 rp and mm[1] = 2 rp + 1, columns cc[u] = cb .. cb + E - 1
-    const int rp = tid / (TL / E), cb = (tid % (TL / E)) * E;
+    // this thread's pieces: token rows mm[0] = 2 rp and mm[1] = 2 rp + 1, columns cc[u] = cb .. cb + E - 1; the KB / 2
+    // token pairs run across consecutive lanes, so that a transposed store instruction (rows cb + e, 2 rp) spreads
+    // over the LDS banks (2-way at most), where 16 column groups of one pair would meet in one or two banks
+    const int rp = tid % (KB / 2), cb = (tid / (KB / 2)) * E;
     const int mm[PIECES] = {2 * rp, 2 * rp + 1};
     const int cc[PIECES] = {cb, cb};
     f32x4 acc[4][4];
