@@ -682,13 +682,21 @@ __global__ __launch_bounds__(256) void loc_attn_backward_kernel(LocAttnParams lp
 //   * the bounding box of the level's in-map corners (LDS min / max);
 //   * if it holds at most kBucketPix pixels: a counting sort of the corners by pixel (an integer LDS atomic per corner
 //     gives its rank in the pixel's bucket; a workgroup scan of the counts gives each bucket's start and the list
-//     of touched pixels and their tokens); then D lanes per touched pixel sum its bucket's a * w_c * g_r from LDS,
-//     without atomics, and add the sums to grad_value (one D-wide atomic per channel group);
+//     of touched pixels with their buckets' start, count and token); then D lanes per touched pixel sum its
+//     bucket's a * w_c * g_r from LDS, without atomics, and add the sums to grad_value (one D-wide atomic per channel
+//     group). A bucket entry holds its coefficient and grad_out row itself, so a sum reads two LDS values per entry,
+//     one after the other (the entry, then the row's channel);
 //   * otherwise the level's corners are added to grad_value directly, as sample_backward_vec_kernel does.
 // D is a power of two from 4 to 64 (lane = channel tid % D), P > 0. The sums reach grad_value in another order than
 // the direct scatter's, so the two agree to float rounding.
 constexpr int kBucketPix = 1024;  // bounding-box pixels per level at most
 constexpr int kBucketEnt = 1024;  // corner entries per level at most: QT * P * 4 with QT * L * P <= 256
+
+// a bucketed corner: its coefficient a * w_c and the offset of its grad_out row in LDS (r * D)
+struct alignas(8) BucketEntry {
+    float coef;
+    int row;
+};
 
 struct BucketParams {
     const void* loc;
@@ -743,9 +751,8 @@ __global__ __launch_bounds__(NTH) void scatter_bucket_kernel(BucketParams bp) {
     __shared__ int erow[kBucketEnt];       // the corner's row offset in gr (r * D)
     __shared__ int cnt[kBucketPix];        // corners per window pixel
     __shared__ int base[kBucketPix];       // start of the pixel's bucket in list
-    __shared__ int tpix[kBucketEnt];       // touched pixels (compacted)
-    __shared__ int ttok[kBucketEnt];       // their tokens
-    __shared__ int list[kBucketEnt];       // entries bucketed by pixel
+    __shared__ int2 tinfo[kBucketEnt];     // touched pixels (compacted): bucket start | count << 16, token
+    __shared__ BucketEntry lent[kBucketEnt];  // entries bucketed by pixel: a * w_c and grad_out row offset
     __shared__ int boxw[NW][4];  // per wavefront: min x, min y, max x, max y
     __shared__ int wtot[NW];
 
@@ -871,30 +878,37 @@ __global__ __launch_bounds__(NTH) void scatter_bucket_kernel(BucketParams bp) {
                     const int c = cnt[pp];
                     base[pp] = run & 0xffff;
                     if (c > 0) {
-                        const int ti = run >> 16;
-                        tpix[ti] = pp;
                         const int yy = pp / bw;
-                        ttok[ti] = static_cast<int>(st + static_cast<int64_t>(y0 + yy) * wl + (x0 + pp - yy * bw));
+                        tinfo[run >> 16] = make_int2((run & 0xffff) | c << 16,
+                                                     static_cast<int>(st + static_cast<int64_t>(y0 + yy) * wl +
+                                                                      (x0 + pp - yy * bw)));
                     }
                     run += c + (c > 0 ? (1 << 16) : 0);
                 }
                 __syncthreads();
                 if (mine) {
-                    const int e0 = (r * P + jp) * 4;
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        if (tk[k] >= 0) list[base[px[k]] + rank[k]] = e0 + k;
+                        if (tk[k] >= 0) lent[base[px[k]] + rank[k]] = BucketEntry{cf[k], r * D};
                 }
                 __syncthreads();
                 const int ntouched = total >> 16;
                 for (int ti = grp; ti < ntouched; ti += ngrp) {
-                    const int pp = tpix[ti], s0 = base[pp], n = cnt[pp];
+                    const int2 info = tinfo[ti];
+                    const int s0 = info.x & 0xffff, n = info.x >> 16;
                     A v = 0;
-                    for (int i = 0; i < n; ++i) {
-                        const int e = list[s0 + i];
-                        v += ecoef[e] * gr[erow[e] + d];
+                    int i = 0;
+                    for (; i + 1 < n; i += 2) {  // two entries' reads in flight
+                        const BucketEntry u = lent[s0 + i], w = lent[s0 + i + 1];
+                        const A gu = gr[u.row + d], gw = gr[w.row + d];
+                        v += u.coef * gu;
+                        v += w.coef * gw;
                     }
-                    atomic_add(gv + static_cast<int64_t>(ttok[ti]) * HD + d, v);
+                    if (i < n) {
+                        const BucketEntry u = lent[s0 + i];
+                        v += u.coef * gr[u.row + d];
+                    }
+                    atomic_add(gv + static_cast<int64_t>(info.y) * HD + d, v);
                 }
             } else {
                 for (int e = grp; e < ne; e += ngrp) {
