@@ -679,7 +679,8 @@ __global__ __launch_bounds__(256) void loc_attn_backward_kernel(LocAttnParams lp
 // rate per 128-byte line; consecutive queries of one head touch overlapping pixels (16 of them about 2.4 times fewer
 // pixels than corners on DINO-style encoder inputs), so their corners are summed per pixel first and each touched
 // pixel goes out once. Workgroup = (image b, head h, QT consecutive queries), one (row, sample) per thread; per level:
-//   * the bounding box of the level's in-map corners (LDS min / max);
+//   * the bounding box of the level's in-map corners (wavefront min / max by DPP, then over the wavefronts in LDS;
+//     the boxes of up to 8 levels are found together, behind one barrier);
 //   * if it holds at most kBucketPix pixels: a counting sort of the corners by pixel (an integer LDS atomic per corner
 //     gives its rank in the pixel's bucket; a workgroup scan of the counts gives each bucket's start and the list
 //     of touched pixels with their buckets' start, count and token); then D lanes per touched pixel sum its
@@ -687,6 +688,8 @@ __global__ __launch_bounds__(256) void loc_attn_backward_kernel(LocAttnParams lp
 //     group). A bucket entry holds its coefficient and grad_out row itself, so a sum reads two LDS values per entry,
 //     one after the other (the entry, then the row's channel);
 //   * otherwise the level's corners are added to grad_value directly, as sample_backward_vec_kernel does.
+// Five barriers per bucketed level: the ranks, the scan's wavefront totals, the bucket starts, the list, the sums
+// (the counts are cleared during the sums for the next level).
 // D is a power of two from 4 to 64 (lane = channel tid % D), P > 0. The sums reach grad_value in another order than
 // the direct scatter's, so the two agree to float rounding.
 constexpr int kBucketPix = 1024;  // bounding-box pixels per level at most
@@ -708,33 +711,47 @@ struct BucketParams {
     FastDiv d_lp, d_p;  // divisions by L * P and P
 };
 
-// minimum and maximum over the 64 lanes of a wavefront (every lane receives them)
+// Reductions over the 64 lanes of a wavefront by DPP moves within rows of 16 lanes (every lane of a row then holds
+// the row's result) and reads of lanes 0, 16, 32 and 48: no LDS round trips. All 64 lanes must be active.
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov_i(int x) {
+    return __builtin_amdgcn_mov_dpp(x, CTRL, 0xf, 0xf, false);
+}
 __device__ __forceinline__ int wave_min(int v) {
-#pragma unroll
-    for (int m = 32; m > 0; m >>= 1) v = min(v, __builtin_amdgcn_ds_bpermute((lane_id() ^ m) << 2, v));
-    return v;
+    v = min(v, dpp_mov_i<0xb1>(v));   // quad_perm [1, 0, 3, 2]
+    v = min(v, dpp_mov_i<0x4e>(v));   // quad_perm [2, 3, 0, 1]
+    v = min(v, dpp_mov_i<0x141>(v));  // row_half_mirror
+    v = min(v, dpp_mov_i<0x140>(v));  // row_mirror
+    return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
 __device__ __forceinline__ int wave_max(int v) {
-#pragma unroll
-    for (int m = 32; m > 0; m >>= 1) v = max(v, __builtin_amdgcn_ds_bpermute((lane_id() ^ m) << 2, v));
-    return v;
+    v = max(v, dpp_mov_i<0xb1>(v));
+    v = max(v, dpp_mov_i<0x4e>(v));
+    v = max(v, dpp_mov_i<0x141>(v));
+    v = max(v, dpp_mov_i<0x140>(v));
+    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
 
-// inclusive prefix sum over the 64 lanes of a wavefront
+// Inclusive prefix sum over the 64 lanes of a wavefront: within each row by adds of the row shifted right by 1, 2, 4
+// and 8 lanes (lanes shifted in from outside the row read 0), then each row plus the totals of the rows before it.
+// All 64 lanes must be active.
 __device__ __forceinline__ int wave_incl_scan(int v) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        const int t = __builtin_amdgcn_ds_bpermute((lane - off) << 2, v);
-        if (lane >= off) v += t;
-    }
-    return v;
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31);
+    const int r2 = __builtin_amdgcn_readlane(v, 47), row = lane_id() >> 4;
+    return v + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
 }
 
 template <typename T, int NTH>
 __global__ __launch_bounds__(NTH) void scatter_bucket_kernel(BucketParams bp) {
     using A = float;
     constexpr int NW = NTH / kWave;
+    constexpr int LB = 8;  // levels whose bounding boxes are found together
     const Geom& g = bp.g;
     const int D = g.D, HD = g.H * g.D, LP = g.LP, P = g.P, QT = bp.QT;
     const int unit = (blockIdx.x % kXcds) * bp.per_xcd + blockIdx.x / kXcds;
@@ -745,15 +762,15 @@ __global__ __launch_bounds__(NTH) void scatter_bucket_kernel(BucketParams bp) {
     const int tid = threadIdx.x, d = tid & (D - 1), grp = tid / D, ngrp = NTH / D;
     const int wave = tid >> 6, lane = tid & (kWave - 1);
 
-    __shared__ A gr[NTH];                  // [QT][D] (QT * D <= NTH)
-    __shared__ int etok[kBucketEnt];       // corner token, -1 outside
-    __shared__ A ecoef[kBucketEnt];        // a * w_c
-    __shared__ int erow[kBucketEnt];       // the corner's row offset in gr (r * D)
-    __shared__ int cnt[kBucketPix];        // corners per window pixel
-    __shared__ int base[kBucketPix];       // start of the pixel's bucket in list
-    __shared__ int2 tinfo[kBucketEnt];     // touched pixels (compacted): bucket start | count << 16, token
+    __shared__ A gr[NTH];                     // [QT][D] (QT * D <= NTH)
+    __shared__ int etok[kBucketEnt];          // direct levels: corner token, -1 outside
+    __shared__ A ecoef[kBucketEnt];           // a * w_c
+    __shared__ int erow[kBucketEnt];          // the corner's row offset in gr (r * D)
+    __shared__ int cnt[kBucketPix];           // corners per window pixel (zero between levels)
+    __shared__ int base[kBucketPix];          // start of the pixel's bucket in lent
+    __shared__ int2 tinfo[kBucketEnt];        // touched pixels (compacted): bucket start | count << 16, token
     __shared__ BucketEntry lent[kBucketEnt];  // entries bucketed by pixel: a * w_c and grad_out row offset
-    __shared__ int boxw[NW][4];  // per wavefront: min x, min y, max x, max y
+    __shared__ int boxw[LB][NW][4];           // per level and wavefront: min x, min y, max x, max y
     __shared__ int wtot[NW];
 
     const T* __restrict__ go = static_cast<const T*>(bp.grad_out);
@@ -762,6 +779,7 @@ __global__ __launch_bounds__(NTH) void scatter_bucket_kernel(BucketParams bp) {
         const int r = i / D;
         gr[i] = cvt<A>(go[(static_cast<int64_t>(b) * g.Q + q0 + r) * HD + static_cast<int64_t>(h) * D + (i - r * D)]);
     }
+    for (int i = tid; i < kBucketPix; i += NTH) cnt[i] = 0;
 
     // this thread's sample (row r, sample j of level lt): its four corners' tokens, pixels and coefficients
     int tk[4] = {-1, -1, -1, -1}, cx[4] = {0, 0, 0, 0}, cy[4] = {0, 0, 0, 0};
@@ -799,125 +817,137 @@ __global__ __launch_bounds__(NTH) void scatter_bucket_kernel(BucketParams bp) {
     }
 
     for (int l = 0; l < g.L; ++l) {
-        const int ne = nq * P * 4;  // the level's corner entries
-        const bool mine = lt == l;
-        int mnx = 0x7fffffff, mny = 0x7fffffff, mxx = -1, mxy = -1;
-        if (mine) {
-            const int e0 = (r * P + jp) * 4;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                etok[e0 + k] = tk[k];
-                ecoef[e0 + k] = cf[k];
-                erow[e0 + k] = r * D;
-                if (tk[k] >= 0) {
-                    mnx = min(mnx, cx[k]);
-                    mny = min(mny, cy[k]);
-                    mxx = max(mxx, cx[k]);
-                    mxy = max(mxy, cy[k]);
-                }
-            }
-        }
-        mnx = wave_min(mnx);
-        mny = wave_min(mny);
-        mxx = wave_max(mxx);
-        mxy = wave_max(mxy);
-        if (lane == 0) {
-            boxw[wave][0] = mnx;
-            boxw[wave][1] = mny;
-            boxw[wave][2] = mxx;
-            boxw[wave][3] = mxy;
-        }
-        __syncthreads();  // the level's entries and the wavefronts' boxes (and, first, the grad_out rows) are in place
-        int x0 = boxw[0][0], y0 = boxw[0][1], x1 = boxw[0][2], y1 = boxw[0][3];
-#pragma unroll
-        for (int w = 1; w < NW; ++w) {
-            x0 = min(x0, boxw[w][0]);
-            y0 = min(y0, boxw[w][1]);
-            x1 = max(x1, boxw[w][2]);
-            y1 = max(y1, boxw[w][3]);
-        }
-        if (x1 >= x0) {  // the level has in-map corners (uniform)
-            const int bw = x1 - x0 + 1;
-            const int64_t npix64 = static_cast<int64_t>(bw) * (y1 - y0 + 1);
-            if (npix64 <= kBucketPix) {
-                const int npix = static_cast<int>(npix64);
-                const int wl = static_cast<int>(g.shapes[2 * l + 1]);
-                const int64_t st = g.starts[l];
-                for (int i = tid; i < npix; i += NTH) cnt[i] = 0;
-                __syncthreads();
-                int px[4], rank[4];
-                if (mine) {
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        px[k] = (cy[k] - y0) * bw + (cx[k] - x0);
-                        rank[k] = tk[k] >= 0 ? atomicAdd(&cnt[px[k]], 1) : 0;
-                    }
-                }
-                __syncthreads();
-                // workgroup scan of the counts: thread t owns pixels [t * k, t * k + k), k = ceil(npix / NTH) <= 4;
-                // packed (touched pixels << 16) | corners
-                const int kp = (npix + NTH - 1) / NTH, p0 = tid * kp;
-                int own = 0;
-                for (int i = 0; i < kp; ++i) {
-                    const int pp = p0 + i;
-                    const int c = pp < npix ? cnt[pp] : 0;
-                    own += c + (c > 0 ? (1 << 16) : 0);
-                }
-                const int incl = wave_incl_scan(own);
-                if (lane == kWave - 1) wtot[wave] = incl;
-                __syncthreads();
-                int before = 0;
-                for (int w = 0; w < wave; ++w) before += wtot[w];
-                int total = 0;
-#pragma unroll
-                for (int w = 0; w < NW; ++w) total += wtot[w];
-                int run = before + incl - own;  // exclusive
-                for (int i = 0; i < kp; ++i) {
-                    const int pp = p0 + i;
-                    if (pp >= npix) break;
-                    const int c = cnt[pp];
-                    base[pp] = run & 0xffff;
-                    if (c > 0) {
-                        const int yy = pp / bw;
-                        tinfo[run >> 16] = make_int2((run & 0xffff) | c << 16,
-                                                     static_cast<int>(st + static_cast<int64_t>(y0 + yy) * wl +
-                                                                      (x0 + pp - yy * bw)));
-                    }
-                    run += c + (c > 0 ? (1 << 16) : 0);
-                }
-                __syncthreads();
-                if (mine) {
+        if (l % LB == 0) {
+            // bounding boxes of the in-map corners of levels l .. l + LB - 1, per wavefront
+            if (l > 0) __syncthreads();  // every wavefront has read the previous group's boxes
+            for (int ll = l; ll < g.L && ll < l + LB; ++ll) {
+                int mnx = 0x7fffffff, mny = 0x7fffffff, mxx = -1, mxy = -1;
+                if (lt == ll) {
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        if (tk[k] >= 0) lent[base[px[k]] + rank[k]] = BucketEntry{cf[k], r * D};
+                        if (tk[k] >= 0) {
+                            mnx = min(mnx, cx[k]);
+                            mny = min(mny, cy[k]);
+                            mxx = max(mxx, cx[k]);
+                            mxy = max(mxy, cy[k]);
+                        }
                 }
-                __syncthreads();
-                const int ntouched = total >> 16;
-                for (int ti = grp; ti < ntouched; ti += ngrp) {
-                    const int2 info = tinfo[ti];
-                    const int s0 = info.x & 0xffff, n = info.x >> 16;
-                    A v = 0;
-                    int i = 0;
-                    for (; i + 1 < n; i += 2) {  // two entries' reads in flight
-                        const BucketEntry u = lent[s0 + i], w = lent[s0 + i + 1];
-                        const A gu = gr[u.row + d], gw = gr[w.row + d];
-                        v += u.coef * gu;
-                        v += w.coef * gw;
-                    }
-                    if (i < n) {
-                        const BucketEntry u = lent[s0 + i];
-                        v += u.coef * gr[u.row + d];
-                    }
-                    atomic_add(gv + static_cast<int64_t>(info.y) * HD + d, v);
-                }
-            } else {
-                for (int e = grp; e < ne; e += ngrp) {
-                    const int t = etok[e];
-                    if (t >= 0) atomic_add(gv + static_cast<int64_t>(t) * HD + d, ecoef[e] * gr[erow[e] + d]);
+                mnx = wave_min(mnx);
+                mny = wave_min(mny);
+                mxx = wave_max(mxx);
+                mxy = wave_max(mxy);
+                if (lane == 0) {
+                    boxw[ll - l][wave][0] = mnx;
+                    boxw[ll - l][wave][1] = mny;
+                    boxw[ll - l][wave][2] = mxx;
+                    boxw[ll - l][wave][3] = mxy;
                 }
             }
+            __syncthreads();  // the boxes (and, first, the grad_out rows and the zeroed counts) are in place
         }
-        __syncthreads();  // the buckets, the entries and the boxes are free for the next level
+        const int lb = l % LB;
+        int x0 = boxw[lb][0][0], y0 = boxw[lb][0][1], x1 = boxw[lb][0][2], y1 = boxw[lb][0][3];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            x0 = min(x0, boxw[lb][w][0]);
+            y0 = min(y0, boxw[lb][w][1]);
+            x1 = max(x1, boxw[lb][w][2]);
+            y1 = max(y1, boxw[lb][w][3]);
+        }
+        if (x1 < x0) continue;  // no in-map corner on this level (uniform)
+        const bool mine = lt == l;
+        const int bw = x1 - x0 + 1;
+        const int64_t npix64 = static_cast<int64_t>(bw) * (y1 - y0 + 1);
+        if (npix64 <= kBucketPix) {
+            const int npix = static_cast<int>(npix64);
+            const int wl = static_cast<int>(g.shapes[2 * l + 1]);
+            const int64_t st = g.starts[l];
+            int px[4], rank[4];
+            if (mine) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    px[k] = (cy[k] - y0) * bw + (cx[k] - x0);
+                    rank[k] = tk[k] >= 0 ? atomicAdd(&cnt[px[k]], 1) : 0;
+                }
+            }
+            __syncthreads();
+            // workgroup scan of the counts: thread t owns pixels [t * k, t * k + k), k = ceil(npix / NTH);
+            // packed (touched pixels << 16) | corners
+            const int kp = (npix + NTH - 1) / NTH, p0 = tid * kp;
+            int own = 0;
+            for (int i = 0; i < kp; ++i) {
+                const int pp = p0 + i;
+                const int c = pp < npix ? cnt[pp] : 0;
+                own += c + (c > 0 ? (1 << 16) : 0);
+            }
+            const int incl = wave_incl_scan(own);
+            if (lane == kWave - 1) wtot[wave] = incl;
+            __syncthreads();
+            int before = 0;
+            for (int w = 0; w < wave; ++w) before += wtot[w];
+            int total = 0;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) total += wtot[w];
+            int run = before + incl - own;  // exclusive
+            for (int i = 0; i < kp; ++i) {
+                const int pp = p0 + i;
+                if (pp >= npix) break;
+                const int c = cnt[pp];
+                base[pp] = run & 0xffff;
+                if (c > 0) {
+                    const int yy = pp / bw;
+                    tinfo[run >> 16] = make_int2((run & 0xffff) | c << 16,
+                                                 static_cast<int>(st + static_cast<int64_t>(y0 + yy) * wl +
+                                                                  (x0 + pp - yy * bw)));
+                }
+                run += c + (c > 0 ? (1 << 16) : 0);
+            }
+            __syncthreads();
+            if (mine) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (tk[k] >= 0) lent[base[px[k]] + rank[k]] = BucketEntry{cf[k], r * D};
+            }
+            __syncthreads();
+            // the counts are no longer read (the touched pixels carry theirs): cleared for the next level
+            for (int i = tid; i < npix; i += NTH) cnt[i] = 0;
+            const int ntouched = total >> 16;
+            for (int ti = grp; ti < ntouched; ti += ngrp) {
+                const int2 info = tinfo[ti];
+                const int s0 = info.x & 0xffff, n = info.x >> 16;
+                A v = 0;
+                int i = 0;
+                for (; i + 1 < n; i += 2) {  // two entries' reads in flight
+                    const BucketEntry u = lent[s0 + i], w = lent[s0 + i + 1];
+                    const A gu = gr[u.row + d], gw = gr[w.row + d];
+                    v += u.coef * gu;
+                    v += w.coef * gw;
+                }
+                if (i < n) {
+                    const BucketEntry u = lent[s0 + i];
+                    v += u.coef * gr[u.row + d];
+                }
+                atomic_add(gv + static_cast<int64_t>(info.y) * HD + d, v);
+            }
+            __syncthreads();  // the counts are zero and the buckets free for the next level
+        } else {
+            if (mine) {
+                const int e0 = (r * P + jp) * 4;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    etok[e0 + k] = tk[k];
+                    ecoef[e0 + k] = cf[k];
+                    erow[e0 + k] = r * D;
+                }
+            }
+            __syncthreads();
+            const int ne = nq * P * 4;  // the level's corner entries
+            for (int e = grp; e < ne; e += ngrp) {
+                const int t = etok[e];
+                if (t >= 0) atomic_add(gv + static_cast<int64_t>(t) * HD + d, ecoef[e] * gr[erow[e] + d]);
+            }
+            __syncthreads();  // the entries are free for the next level
+        }
     }
 }
 
