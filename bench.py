@@ -22,7 +22,7 @@ most one XCD's 4 MB L2), measured in the same run by td_probe_gather, with the H
 
 Other modes: --table (the reference's sweep), --fit-auto / --holdout (the auto selector), --ceiling (the gather
 ceiling over row widths and buffer sizes), --phases (the fused kernel's phase timeline, from the measurement build
-libtinydeform_phases.so), --trace-run and --pmc-run (short runs for rocprofv3).
+libtinydeform_phases.so), --trace-run, --train-run and --pmc-run (short runs for rocprofv3).
 """
 
 import argparse
@@ -150,10 +150,11 @@ def layer_times(B, Q, H, D, C, levels, P, dtype, steps, warmup):
     return out
 
 
-def train_times(cpu_args, steps, warmup):
-    """µs per training step of the operator (forward + backward, gradients for memory, value_weight, value_bias,
-    the locations and the attention weights, for a fixed random grad_out): ma_deform_attn_train on the library's
-    kernels, and the PyTorch reference path (F.linear + grid_sample) under autograd on the same device."""
+def train_steps(cpu_args):
+    """The training step of the operator and of the PyTorch reference path (F.linear + grid_sample under autograd)
+    on the same device, as two callables: the gradients set to None (optimizer.zero_grad's default), the forward, and
+    the backward of a fixed random grad_out, with gradients for memory, value_weight, value_bias, the locations and
+    the attention weights (so no step accumulates into the previous step's gradients)."""
     dev = [None if t is None else t.cuda() for t in cpu_args]
     ref_args = list(dev)
     ref_args[3], ref_args[4] = cpu_args[3], cpu_args[4]  # the reference reads the level shapes on the host
@@ -162,11 +163,26 @@ def train_times(cpu_args, steps, warmup):
     B, Q = dev[5].shape[:2]
     go = torch.randn(B, Q, dev[1].shape[0], generator=torch.Generator().manual_seed(1)).to(dev[0].dtype).cuda()
 
+    def zero_grad():
+        for t in leaves:
+            if t is not None and t.requires_grad:
+                t.grad = None
+
     def ours():
+        zero_grad()
         torch.autograd.backward(td.ma_deform_attn_train(*leaves), go)
 
     def pytorch():
+        zero_grad()
         torch.autograd.backward(td.ma_deform_attn_reference(*ref_leaves), go)
+
+    return ours, pytorch
+
+
+def train_times(cpu_args, steps, warmup):
+    """µs per training step (train_steps) of the operator on the library's kernels (ma_deform_attn_train) and of the
+    PyTorch reference path, graph-timed."""
+    ours, pytorch = train_steps(cpu_args)
 
     out = {}
     for name, fn, n in (('train_step', ours, steps), ('pytorch_train_step', pytorch, min(steps, 100))):
@@ -327,6 +343,26 @@ def ceiling_table():
     for name, _ in CEILING_BUFFERS:
         print(f'| {name} | ' + ' | '.join(f'{c["gbps"]:.0f}' for c in rows if c['buffer'] == name) + ' |')
     print(json.dumps({'gather_ceiling_gbps': rows}), flush=True)
+
+
+def train_run(cpu_args, steps, warmup):
+    """--train-run, for rocprofv3 --kernel-trace: `warmup`, then `steps` eager training steps of the operator
+    (train_steps), then the same step graph-timed and, as in --trace-run, a graph of `steps` empty kernels, whose
+    traced duration is the tracer's cost per dispatch."""
+    ours, _ = train_steps(cpu_args)
+    for _ in range(warmup):
+        ours()
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        ours()
+    torch.cuda.synchronize()
+    t = graph_time_us(ours, steps, min(warmup, 10))
+    with torch.inference_mode():
+        empty = graph_time_us(lambda: _native.probe_empty(1), steps, min(warmup, 10))
+    log(f'train run: {steps} eager steps traced; graph-timed {t:.2f} µs per step, empty kernel {empty:.2f} µs per '
+        f'launch')
+    print(json.dumps({'train_run': {'steps': steps, 'train_step_us': round(t, 3),
+                                    'empty_us_per_launch': round(empty, 3)}}), flush=True)
 
 
 def trace_run(dev, steps, warmup):
@@ -715,6 +751,9 @@ def main():
     ap.add_argument('--trace-run', action='store_true',
                     help='for rocprofv3 --kernel-trace: --steps operator calls and --steps empty kernels, each in '
                          'a graph timed like the headline')
+    ap.add_argument('--train-run', action='store_true',
+                    help='for rocprofv3 --kernel-trace: --steps eager training steps of the operator (forward and '
+                         'backward), then the same step graph-timed')
     ap.add_argument('--phases', action='store_true',
                     help='the fused kernel\'s phase timeline from the measurement build libtinydeform_phases.so')
     ap.add_argument('--pmc-run', action='store_true',
@@ -758,6 +797,9 @@ def main():
         return
     if args.trace_run:
         trace_run(dev, args.steps, args.warmup)
+        return
+    if args.train_run:
+        train_run(cpu_args, args.steps, args.warmup)
         return
     if args.phases:
         phases_run(dev, args.steps, args.warmup)

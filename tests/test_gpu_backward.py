@@ -172,6 +172,47 @@ def test_headline_shape_backward():
     assert torch.equal(out.detach(), fwd)
 
 
+def test_training_step_graph_replays_match_oracle():
+    # the training step (gradients set to None, forward, backward) captured in a graph, as the benchmark times it:
+    # every replay must give all five gradients (the backward's accumulator is cleared by a kernel, not a memset),
+    # each checked against the float64 oracle, with eager work on the device between the replays
+    args = workload(1, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.float16, seed=11)
+    go = grad_out_for(args)
+    ref = gridsample.deform_attn_grads(*args, go.to(torch.float16))
+    dev = [None if t is None else t.cuda() for t in args]
+    leaves = [t.requires_grad_(True) if (i in (0, 1, 2, 5, 6) and t is not None) else t for i, t in enumerate(dev)]
+    g = go.to(torch.float16).cuda()
+
+    def step():
+        for t in leaves:
+            if t is not None and t.requires_grad:
+                t.grad = None
+        torch.autograd.backward(td.ma_deform_attn_train(*leaves), g)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for i in range(4):
+        for t in leaves:
+            if t is not None and t.requires_grad:
+                t.grad.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        say(f'  training step graph replay {i}')
+        grads = {n: None if leaves[j] is None else leaves[j].grad for n, j in zip(NAMES, (0, 1, 2, 5, 6))}
+        for n in NAMES:
+            check(f'replay {i} d{n}', grads[n], ref[n], torch.float16)
+        with torch.no_grad():
+            _ = dev[0].float().sum().item()  # eager work between replays
+
+
 def test_module_training_step_matches_cpu():
     # MSDeformAttnLayer with grad: PyTorch prologue and output_proj, the library's operator; parameter gradients of
     # one step against the same module on the CPU in float64 (the reference path under autograd)
