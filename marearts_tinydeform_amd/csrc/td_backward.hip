@@ -1390,14 +1390,17 @@ int launch_transpose(int dtype, const void* src, void* dst, int64_t R, int64_t C
     return launched("transpose");
 }
 
-// Split count and workspace of the weight gradient: about 512 workgroups, at least 256 tokens per split.
+// Split count and workspace of the weight gradient: about 512 workgroups, at least four token steps per split (64
+// tokens in float32, 128 otherwise). Measured on the training step at 8400 tokens (256 x 256), against 256 tokens
+// per split: float32 117.0 -> 99.0 us with 64-token splits (105.8 with 128), 16-bit 63.3 -> 62.7 with 128 (63.4
+// with 64); problems of 32768 tokens and more already had their 512 workgroups.
 void wgrad_plan(int64_t M, int64_t NO, int64_t K, int dtype, int* splits, int* chunk, int64_t* ws_bytes) {
     const int64_t tiles = ((NO + kWgTile - 1) / kWgTile) * ((K + kWgTile - 1) / kWgTile);
+    const int kb = dtype == kF32 ? 16 : 32;
     int64_t s = (512 + tiles - 1) / tiles;
-    const int64_t max_s = (M + 255) / 256;
+    const int64_t max_s = (M + 4 * kb - 1) / (4 * kb);
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;
-    const int kb = dtype == kF32 ? 16 : 32;
     int64_t c = (M + s - 1) / s;
     c = (c + kb - 1) / kb * kb;
     s = c > 0 ? (M + c - 1) / c : 1;
