@@ -172,6 +172,24 @@ def test_headline_shape_backward():
     assert torch.equal(out.detach(), fwd)
 
 
+@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize('loc_dist', ['encoder', 'uniform'])
+def test_dense_query_gradients_nine_levels(dtype, loc_dist):
+    # the bucketed scatter finds the bounding boxes of 8 levels at a time: nine levels cross that boundary (a second
+    # group of boxes, behind a barrier that waits for every wavefront to have read the first group's), with 2
+    # points a level (18 samples a row, 28 rows a workgroup)
+    levels = [(16, 16), (12, 12), (10, 10), (8, 8), (6, 6), (5, 5), (4, 4), (3, 3), (2, 2)]
+    N = sum(h * w for h, w in levels)
+    for Q in (2 * N, 2 * N - 3):
+        args = workload(1, Q, 4, 16, 64, levels, 2, dtype, loc_dist=loc_dist, seed=21)
+        go = grad_out_for(args)
+        say(f'  backward dense queries, nine levels, Q={Q} {dtype} {loc_dist}')
+        grads, _ = gpu_grads(args, go, dtype)
+        ref = gridsample.deform_attn_grads(*args, go.to(dtype))
+        for n in NAMES:
+            check(f'nine levels Q={Q} {dtype} {loc_dist} d{n}', grads[n], ref[n], dtype)
+
+
 def test_training_step_graph_replays_match_oracle():
     # the training step (gradients set to None, forward, backward) captured in a graph, as the benchmark times it:
     # every replay must give all five gradients (the backward's accumulator is cleared by a kernel, not a memset),
