@@ -284,6 +284,16 @@ int td_weight_grad(int dtype, const void* grad_value, const void* memory, void* 
                    int64_t M, int64_t HD, int64_t C, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * td_input_grad and td_weight_grad of the same grad_value in one call, with the same arguments, results and
+ * workspace (td_weight_grad_workspace; TD_E_WORKSPACE before anything is launched when it is smaller). Where the
+ * input gradient's GEMM takes the small-grid tiles (below about 14000 tokens of 256 channels in 16 bits) its tiles
+ * and the weight gradient's share one launch; no counterpart in the reference, whose operator is inference only.
+ */
+int td_input_weight_grad(int dtype, const void* grad_value, const void* value_weight, void* weight_t,
+                         const void* memory, void* grad_memory, void* grad_weight, void* grad_bias, int64_t M,
+                         int64_t HD, int64_t C, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Measurement kernels. No counterpart in the reference and no part of the operator: the benchmark uses them to
  * calibrate what it reports.
  *

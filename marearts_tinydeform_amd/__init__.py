@@ -381,9 +381,13 @@ class _DeformAttnFunction(torch.autograd.Function):
         memory, weight, value, shapes, starts, loc, attn, mask = ctx.saved_tensors
         need = ctx.needs_input_grad
         gv, gl, ga = _native.sample_backward(value, loc.shape[2], shapes, starts, loc, attn, grad_out, mask)
-        gm = _native.input_grad(gv, weight) if need[0] else None
-        gw = gb = None
-        if need[1] or (need[2] and ctx.has_bias):
+        need_w = need[1] or (need[2] and ctx.has_bias)
+        gm = gw = gb = None
+        if need[0] and need_w:  # one call: at small sizes the two share a launch
+            gm, gw, gb = _native.input_weight_grad(gv, weight, memory, with_bias=ctx.has_bias and need[2])
+        elif need[0]:
+            gm = _native.input_grad(gv, weight)
+        elif need_w:
             gw, gb = _native.weight_grad(gv, memory, with_bias=ctx.has_bias and need[2])
         return (gm, gw if need[1] else None, gb, None, None, gl if need[5] else None, ga if need[6] else None, None)
 

@@ -40,6 +40,7 @@ SIGNATURES = {
     'td_sample_backward': (_int, [_int] + [_vp] * 11 + [_i64] * 7 + [_vp]),
     'td_input_grad': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     'td_weight_grad_workspace': (_i64, [_int, _i64, _i64, _i64]),
+    'td_input_weight_grad': (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     'td_weight_grad': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     'td_value_proj_plan': (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64]),
     'td_project_forward_noalloc': (_int, [_int] + [_vp] * 8 + [_int, _vp] + [_i64] * 8 + [_vp]),
@@ -508,6 +509,30 @@ def weight_grad(grad_value, memory, with_bias=True):
     _check(lib_.td_weight_grad(code, g.data_ptr(), mem.data_ptr(), gw.data_ptr(), _ptr(gb), B * N, HD, C,
                                ws.data_ptr(), ws_bytes, _stream(dev)))
     return gw, gb
+
+
+def input_weight_grad(grad_value, weight, memory, with_bias=True):
+    """input_grad and weight_grad of the same grad_value in one call (td_input_weight_grad): (grad_memory [B, N, C],
+    grad_weight [H * D, C], grad_bias [H * D] or None)."""
+    lib_ = _require()
+    B, N, HD = grad_value.shape
+    C = memory.size(2)
+    if weight.shape != (HD, C) or weight.dtype != grad_value.dtype or weight.device != grad_value.device:
+        raise RuntimeError('weight must be [H * D, C] like value_weight')
+    if memory.shape[:2] != (B, N) or memory.dtype != grad_value.dtype or memory.device != grad_value.device:
+        raise RuntimeError('memory must be [B, N, C] with the tokens of grad_value')
+    dev, dt = grad_value.device, grad_value.dtype
+    g, w, mem = grad_value.contiguous(), weight.contiguous(), memory.contiguous()
+    wt = torch.empty((C, HD), dtype=dt, device=dev)
+    gm = torch.empty((B, N, C), dtype=dt, device=dev)
+    gw = torch.empty((HD, C), dtype=dt, device=dev)
+    gb = torch.empty((HD,), dtype=dt, device=dev) if with_bias else None
+    code = DTYPE_CODES[dt]
+    ws_bytes = int(lib_.td_weight_grad_workspace(code, B * N, HD, C))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    _check(lib_.td_input_weight_grad(code, g.data_ptr(), w.data_ptr(), wt.data_ptr(), mem.data_ptr(), gm.data_ptr(),
+                                     gw.data_ptr(), _ptr(gb), B * N, HD, C, ws.data_ptr(), ws_bytes, _stream(dev)))
+    return gm, gw, gb
 
 
 def acc_dtype(dtype):

@@ -581,6 +581,31 @@ extern "C" int64_t td_weight_grad_workspace(int dtype, int64_t M, int64_t HD, in
     return bytes;
 }
 
+extern "C" int td_input_weight_grad(int dtype, const void* grad_value, const void* value_weight, void* weight_t,
+                                    const void* memory, void* grad_memory, void* grad_weight, void* grad_bias,
+                                    int64_t M, int64_t HD, int64_t C, void* workspace, int64_t workspace_bytes,
+                                    void* stream) {
+    g_last_error.clear();
+    if (!dtype_ok(dtype)) return set_error(TD_E_DTYPE, "unknown dtype code %d", dtype);
+    if (M < 0 || HD < 0 || C < 0) return set_error(TD_E_ARG, "sizes must be non-negative");
+    if (M > kInt32Max || HD > kInt32Max || C > kInt32Max) return set_error(TD_E_ARG, "GEMM size exceeds int32");
+    if (M == 0 || HD == 0 || C == 0) {  // the two entries' own handling of empty sizes
+        int rc = td_input_grad(dtype, grad_value, value_weight, weight_t, grad_memory, M, HD, C, stream);
+        if (rc != TD_OK) return rc;
+        return td_weight_grad(dtype, grad_value, memory, grad_weight, grad_bias, M, HD, C, workspace, workspace_bytes,
+                              stream);
+    }
+    if (grad_value == nullptr || value_weight == nullptr || weight_t == nullptr || memory == nullptr ||
+        grad_memory == nullptr || grad_weight == nullptr)
+        return set_error(TD_E_ARG, "null pointer argument");
+    const int64_t need = td_weight_grad_workspace(dtype, M, HD, C);
+    if (workspace == nullptr || workspace_bytes < need)
+        return set_error(TD_E_WORKSPACE, "weight gradient: workspace of %lld bytes needed, %lld given",
+                         static_cast<long long>(need), static_cast<long long>(workspace_bytes));
+    return launch_input_weight_grad(dtype, grad_value, value_weight, weight_t, memory, grad_memory, grad_weight,
+                                    grad_bias, M, HD, C, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
 extern "C" int td_weight_grad(int dtype, const void* grad_value, const void* memory, void* grad_weight,
                               void* grad_bias, int64_t M, int64_t HD, int64_t C, void* workspace,
                               int64_t workspace_bytes, void* stream) {

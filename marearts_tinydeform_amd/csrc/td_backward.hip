@@ -15,7 +15,7 @@
 // (x = loc_x W_l - 0.5, so dx/dloc_x = W_l; corner k has dx = k & 1, dy = k >> 1.) A location clamped to the map's
 // guard band has all four corners outside, so its gradient is 0, as for grid_sample's zero padding. Discrete
 // sampling (D-FINE) is piecewise constant in the location: its location gradient is 0.
-#include "td_gemm.h"
+#include "td_gemm_mfma.h"
 
 namespace td {
 namespace {
@@ -1024,17 +1024,22 @@ struct alignas(2 * sizeof(T)) Pair {
     T v[2];
 };
 
+// LDS of one wgrad tile: the staged G and X slices, kWgTile rows of KBlock<T>::kK + 16 / sizeof(T) elements each
+template <typename T>
+constexpr size_t wgrad_slice_bytes() {
+    return sizeof(T) * kWgTile * (KBlock<T>::kK + 16 / sizeof(T));
+}
+
+// Workgroup `bid` of the weight gradient's grid (tile and split), with gs and xs its two LDS slices.
 template <typename T, bool VEC>
-__global__ __launch_bounds__(256) void wgrad_kernel(WgradParams p) {
+__device__ __forceinline__ void wgrad_tile(const WgradParams& p, int bid, T* __restrict__ gs, T* __restrict__ xs) {
     constexpr int E = 16 / static_cast<int>(sizeof(T));  // elements per 16 bytes
     constexpr int KB = KBlock<T>::kK;                     // tokens per MFMA step
     constexpr int LD = KB + E;                            // LDS pitch (elements) of a staged transposed row
     constexpr int TL = kWgTile, PIECES = KB * (TL / E) / 256;
     static_assert(PIECES == 2, "two pieces per thread");
-    __shared__ __align__(16) T gs[TL * LD];
-    __shared__ __align__(16) T xs[TL * LD];
     const int tiles = p.nt * p.ct;
-    const int s = blockIdx.x / tiles, tile = blockIdx.x - s * tiles;
+    const int s = bid / tiles, tile = bid - s * tiles;
     const int n0 = (tile / p.ct) * TL, c0 = (tile % p.ct) * TL;
     const int m_begin = s * p.chunk, m_end = min(p.M, m_begin + p.chunk);
     const T* __restrict__ G = static_cast<const T*>(p.G);
@@ -1129,6 +1134,35 @@ __global__ __launch_bounds__(256) void wgrad_kernel(WgradParams p) {
             }
         }
     if (do_b && tid < TL && n0 + tid < p.NO) p.bpart[static_cast<int64_t>(s) * p.NO + n0 + tid] = bsum;
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void wgrad_kernel(WgradParams p) {
+    __shared__ __align__(16) unsigned char lds[2 * wgrad_slice_bytes<T>()];
+    wgrad_tile<T, VEC>(p, blockIdx.x, reinterpret_cast<T*>(lds), reinterpret_cast<T*>(lds + wgrad_slice_bytes<T>()));
+}
+
+// The input gradient's GEMM (grad_memory = G . W, on the 64 x 64 two-stage tiles the value projection's size rule
+// picks below about 14000 tokens of 256 channels) and the weight gradient in one launch: they read the same G and
+// nothing of each other, and each alone leaves most of the GPU idle at those sizes (about 500 and 260 workgroups of
+// a few rounds of loads each). Workgroups [0, gemm_blocks) take GEMM tiles (numbered as the GEMM's own launch numbers
+// them), the rest the weight gradient's tiles and splits; both run in the same 256 threads on one LDS buffer.
+template <typename T>
+using InGradGemm = GemmMfmaTile<T, 4, 1, 1, 4, 4, 2>;
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void input_weight_grad_kernel(GemmParams gp, WgradParams wp, int gemm_blocks) {
+    using G = InGradGemm<T>;
+    constexpr size_t kW = wgrad_slice_bytes<T>();
+    constexpr size_t kL = G::kLds > 2 * kW ? G::kLds : 2 * kW;
+    static_assert(G::NTH == 256, "the GEMM tile runs in the weight gradient's 256 threads");
+    __shared__ __align__(16) unsigned char lds[kL];
+    const int b = blockIdx.x;
+    if (b < gemm_blocks) {
+        const int tile = tile_of(gp, b);
+        if (tile >= 0) G::run(gp, tile, lds);
+    } else {
+        wgrad_tile<T, VEC>(wp, b - gemm_blocks, reinterpret_cast<T*>(lds), reinterpret_cast<T*>(lds + kW));
+    }
 }
 
 // float64: the same sums on the vector ALUs, one thread per output of the tile
@@ -1390,6 +1424,25 @@ int launch_transpose(int dtype, const void* src, void* dst, int64_t R, int64_t C
     return launched("transpose");
 }
 
+// grad_memory = G . W (through W^T, as td_input_grad computes it) and the weight gradient of the same G: where the
+// value projection's size rule picks the 64 x 64 two-stage tiles for the input gradient, its tiles and the weight
+// gradient's run in one launch (input_weight_grad_kernel); otherwise the two run one after the other. The workspace
+// is the weight gradient's (td_weight_grad_workspace). M, HD and C are positive.
+int launch_input_weight_grad(int dtype, const void* G, const void* W, void* Wt, const void* X, void* gm, void* gw,
+                             void* gb, int64_t M, int64_t HD, int64_t C, void* workspace, int64_t ws_bytes,
+                             hipStream_t stream) {
+    int rc = launch_transpose(dtype, W, Wt, HD, C, stream);
+    if (rc != 0) return rc;
+    if (value_proj_plan(dtype, G, Wt, nullptr, gm, M, HD, C, 0, 0) == 25) {
+        const GemmParams gp{G, Wt, nullptr, gm, static_cast<int>(M), static_cast<int>(HD), static_cast<int>(C),
+                            0, 0, 0};
+        return launch_wgrad(dtype, G, X, gw, gb, M, HD, C, workspace, ws_bytes, stream, &gp);
+    }
+    rc = launch_value_proj(dtype, G, Wt, nullptr, gm, M, HD, C, stream);
+    if (rc != 0) return rc;
+    return launch_wgrad(dtype, G, X, gw, gb, M, HD, C, workspace, ws_bytes, stream);
+}
+
 // Split count and workspace of the weight gradient: about 512 workgroups, at least four token steps per split (64
 // tokens in float32, 128 otherwise). Measured on the training step at 8400 tokens (256 x 256), against 256 tokens
 // per split: float32 117.0 -> 99.0 us with 64-token splits (105.8 with 128), 16-bit 63.3 -> 62.7 with 128 (63.4
@@ -1412,7 +1465,7 @@ void wgrad_plan(int64_t M, int64_t NO, int64_t K, int dtype, int* splits, int* c
 }
 
 int launch_wgrad(int dtype, const void* G, const void* X, void* gw, void* gb, int64_t M, int64_t NO, int64_t K,
-                 void* workspace, int64_t ws_bytes, hipStream_t stream) {
+                 void* workspace, int64_t ws_bytes, hipStream_t stream, const GemmParams* with_gemm) {
     int splits = 1, chunk = 32;
     int64_t need = 0;
     wgrad_plan(M, NO, K, dtype, &splits, &chunk, &need);
@@ -1450,16 +1503,53 @@ int launch_wgrad(int dtype, const void* G, const void* X, void* gw, void* gb, in
     const int E = dtype == kF32 ? 4 : 8;
     const bool vec = NO % E == 0 && K % E == 0 &&
                      ((reinterpret_cast<uintptr_t>(G) | reinterpret_cast<uintptr_t>(X)) % 16) == 0;
-    switch (dtype * 2 + (vec ? 1 : 0)) {
-        case kF32 * 2: hipLaunchKernelGGL((wgrad_kernel<float, false>), grid, dim3(256), 0, stream, p); break;
-        case kF32 * 2 + 1: hipLaunchKernelGGL((wgrad_kernel<float, true>), grid, dim3(256), 0, stream, p); break;
-        case kF16 * 2: hipLaunchKernelGGL((wgrad_kernel<f16, false>), grid, dim3(256), 0, stream, p); break;
-        case kF16 * 2 + 1: hipLaunchKernelGGL((wgrad_kernel<f16, true>), grid, dim3(256), 0, stream, p); break;
-        case kBF16 * 2: hipLaunchKernelGGL((wgrad_kernel<bf16, false>), grid, dim3(256), 0, stream, p); break;
-        case kBF16 * 2 + 1: hipLaunchKernelGGL((wgrad_kernel<bf16, true>), grid, dim3(256), 0, stream, p); break;
-        default: return set_error(-2, "unknown dtype code %d", dtype);
+    if (with_gemm != nullptr) {
+        // the input gradient's GEMM tiles first, numbered as its own launch numbers them, then the weight gradient's
+        GemmParams gp = *with_gemm;
+        gp.mt = (gp.M + 63) / 64;
+        gp.nt = (gp.NO + 63) / 64;
+        gp.per_xcd = static_cast<int>((static_cast<int64_t>(gp.mt) * gp.nt + kXcds - 1) / kXcds);
+        const int gemm_blocks = gp.per_xcd * kXcds;
+        const dim3 cgrid(static_cast<unsigned>(gemm_blocks + static_cast<int64_t>(grid.x)));
+        switch (dtype * 2 + (vec ? 1 : 0)) {
+            case kF32 * 2:
+                hipLaunchKernelGGL((input_weight_grad_kernel<float, false>), cgrid, dim3(256), 0, stream, gp, p,
+                                   gemm_blocks);
+                break;
+            case kF32 * 2 + 1:
+                hipLaunchKernelGGL((input_weight_grad_kernel<float, true>), cgrid, dim3(256), 0, stream, gp, p,
+                                   gemm_blocks);
+                break;
+            case kF16 * 2:
+                hipLaunchKernelGGL((input_weight_grad_kernel<f16, false>), cgrid, dim3(256), 0, stream, gp, p,
+                                   gemm_blocks);
+                break;
+            case kF16 * 2 + 1:
+                hipLaunchKernelGGL((input_weight_grad_kernel<f16, true>), cgrid, dim3(256), 0, stream, gp, p,
+                                   gemm_blocks);
+                break;
+            case kBF16 * 2:
+                hipLaunchKernelGGL((input_weight_grad_kernel<bf16, false>), cgrid, dim3(256), 0, stream, gp, p,
+                                   gemm_blocks);
+                break;
+            case kBF16 * 2 + 1:
+                hipLaunchKernelGGL((input_weight_grad_kernel<bf16, true>), cgrid, dim3(256), 0, stream, gp, p,
+                                   gemm_blocks);
+                break;
+            default: return set_error(-2, "unknown dtype code %d", dtype);
+        }
+    } else {
+        switch (dtype * 2 + (vec ? 1 : 0)) {
+            case kF32 * 2: hipLaunchKernelGGL((wgrad_kernel<float, false>), grid, dim3(256), 0, stream, p); break;
+            case kF32 * 2 + 1: hipLaunchKernelGGL((wgrad_kernel<float, true>), grid, dim3(256), 0, stream, p); break;
+            case kF16 * 2: hipLaunchKernelGGL((wgrad_kernel<f16, false>), grid, dim3(256), 0, stream, p); break;
+            case kF16 * 2 + 1: hipLaunchKernelGGL((wgrad_kernel<f16, true>), grid, dim3(256), 0, stream, p); break;
+            case kBF16 * 2: hipLaunchKernelGGL((wgrad_kernel<bf16, false>), grid, dim3(256), 0, stream, p); break;
+            case kBF16 * 2 + 1: hipLaunchKernelGGL((wgrad_kernel<bf16, true>), grid, dim3(256), 0, stream, p); break;
+            default: return set_error(-2, "unknown dtype code %d", dtype);
+        }
     }
-    int rc = launched("weight gradient");
+    int rc = launched(with_gemm != nullptr ? "input and weight gradients" : "weight gradient");
     if (rc != 0) return rc;
     switch (dtype) {
         case kF32: hipLaunchKernelGGL((wgrad_reduce_kernel<float, float>), rgrid, dim3(256), 0, stream, p.part,

@@ -37,11 +37,11 @@ __device__ __forceinline__ size_t out_index(const GemmParams& p, int m, int n) {
 
 // Linear tile index for this workgroup; -1 when the workgroup has no tile. Workgroups are dealt to the 8 XCDs
 // round-robin, so consecutive tiles (the N tiles of one M tile) land on one XCD and share its L2.
-__device__ __forceinline__ int tile_of(const GemmParams& p) {
-    const int id = blockIdx.x;
+__device__ __forceinline__ int tile_of(const GemmParams& p, int id) {
     const int tile = (id % kXcds) * p.per_xcd + id / kXcds;
     return tile < p.mt * p.nt ? tile : -1;
 }
+__device__ __forceinline__ int tile_of(const GemmParams& p) { return tile_of(p, static_cast<int>(blockIdx.x)); }
 
 // One 16-byte K block of an MFMA: 16-bit types take one v_mfma_f32_16x16x32 (K = 32 = 4 lane groups x 8),
 // float32 takes four v_mfma_f32_16x16x4_f32 on the components of a float4 (K = 16 = 4 lane groups x 4, lane group

@@ -33,7 +33,7 @@ def lib():
 
 def test_header_declares_the_entry_points():
     assert header_functions() == ['td_fused_forward', 'td_fused_forward_masked', 'td_fused_plan', 'td_input_grad',
-                                  'td_last_error',
+                                  'td_input_weight_grad', 'td_last_error',
                                   'td_layer_fused_forward', 'td_layer_prologue', 'td_layer_sample_forward',
                                   'td_probe_empty', 'td_probe_gather',
                                   'td_project_forward', 'td_project_forward_noalloc', 'td_sample_backward',
@@ -209,6 +209,14 @@ def test_backward_entries_reject_on_host(lib):
     assert 'workspace' in lib.td_last_error().decode()
     assert lib.td_weight_grad(1, None, None, None, None, 8400, 256, 256, 16, need, None) == E['TD_E_ARG']
     assert lib.td_weight_grad(1, 16, 16, 16, None, 8400, 0, 256, 16, need, None) == 0  # nothing to compute
+    # both projection gradients in one call: the same checks, the workspace before anything is launched
+    iwg = lib.td_input_weight_grad
+    assert iwg(9, 16, 16, 16, 16, 16, 16, 16, 8400, 256, 256, 16, need, None) == E['TD_E_DTYPE']
+    assert iwg(1, 16, 16, 16, 16, 16, 16, 16, -1, 256, 256, 16, need, None) == E['TD_E_ARG']
+    assert iwg(1, 16, 16, 16, 16, 16, 16, 16, 8400, 256, 256, 16, need - 1, None) == E['TD_E_WORKSPACE']
+    assert 'workspace' in lib.td_last_error().decode()
+    assert iwg(1, 16, 16, 16, 16, None, 16, 16, 8400, 256, 256, 16, need, None) == E['TD_E_ARG']
+    assert iwg(1, 16, 16, None, 16, 16, 16, 16, 8400, 256, 256, 16, need, None) == E['TD_E_ARG']
 
 
 @pytest.mark.parametrize('dtype,M,NO,K', [(1, 8400, 256, 256), (2, 43520, 1024, 1024), (0, 100, 48, 40),

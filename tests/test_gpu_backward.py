@@ -148,6 +148,28 @@ def test_projection_gradients_alone(dtype):
         check('grad_bias', gb, G.sum(0).numpy(), dtype)
 
 
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16, torch.bfloat16, torch.float64])
+def test_input_and_weight_gradients_in_one_call(dtype):
+    # td_input_weight_grad against td_input_grad and td_weight_grad, bit for bit: (1, 8400, 256, 256) and the two
+    # ragged shapes (M, N and K off the tiles; C a multiple of 8 or not, so the weight gradient stages 16-byte pieces
+    # or scalars) share one launch in 16/32 bits; the others take the two kernels one after the other
+    g = torch.Generator().manual_seed(12)
+    for (B, N, C, HD) in ((1, 8400, 256, 256), (1, 5000, 264, 136), (1, 5000, 260, 136), (2, 77, 40, 48),
+                          (1, 1000, 1024, 96)):
+        gv = torch.randn(B, N, HD, generator=g).to(dtype).cuda()
+        mem = torch.randn(B, N, C, generator=g).to(dtype).cuda()
+        w = (torch.randn(HD, C, generator=g) / C ** 0.5).to(dtype).cuda()
+        say(f'  input and weight gradients {dtype} {(B, N, C, HD)}')
+        gm, gw, gb = _native.input_weight_grad(gv, w, mem)
+        gm1 = _native.input_grad(gv, w)
+        gw1, gb1 = _native.weight_grad(gv, mem)
+        torch.cuda.synchronize()
+        assert torch.equal(gm, gm1) and torch.equal(gw, gw1) and torch.equal(gb, gb1)
+        G, X = gv.double().cpu().reshape(-1, HD), mem.double().cpu().reshape(-1, C)
+        check('grad_memory', gm, (G @ w.double().cpu()).reshape(B, N, C).numpy(), dtype)
+        check('grad_weight', gw, (G.T @ X).numpy(), dtype)
+
+
 def test_weight_gradient_is_deterministic():
     g = torch.Generator().manual_seed(1)
     gv = torch.randn(1, 8400, 256, generator=g).half().cuda()
