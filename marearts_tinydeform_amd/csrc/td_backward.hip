@@ -693,6 +693,7 @@ __global__ __launch_bounds__(256) void loc_attn_backward_kernel(LocAttnParams lp
 // D is a power of two from 4 to 64 (lane = channel tid % D), P > 0. The sums reach grad_value in another order than
 // the direct scatter's, so the two agree to float rounding.
 constexpr int kBucketPix = 1024;  // bounding-box pixels per level at most
+constexpr int kTileW = 8, kTileH = 4;  // self-attention tiles: 8 x 4 pixels of a level's map (QT = 32 queries)
 constexpr int kBucketEnt = 1024;  // corner entries per level at most: QT * P * 4 with QT * L * P <= 256
 
 // a bucketed corner: its coefficient a * w_c and the offset of its grad_out row in LDS (r * D)
@@ -747,22 +748,17 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
     return v + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
 }
 
-template <typename T, int NTH>
-__global__ __launch_bounds__(NTH) void scatter_bucket_kernel(BucketParams bp) {
+template <typename T, int NTH, bool TILE2D>
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(6))) void scatter_bucket_kernel(BucketParams bp) {
     using A = float;
     constexpr int NW = NTH / kWave;
     constexpr int LB = 8;  // levels whose bounding boxes are found together
     const Geom& g = bp.g;
     const int D = g.D, HD = g.H * g.D, LP = g.LP, P = g.P, QT = bp.QT;
-    const int unit = (blockIdx.x % kXcds) * bp.per_xcd + blockIdx.x / kXcds;
-    if (unit >= bp.units) return;  // the whole workgroup
-    const int qt = unit % bp.qtiles, bh = unit / bp.qtiles;
-    const int h = bh % g.H, b = bh / g.H;
-    const int q0 = qt * QT, nq = g.Q - q0 < QT ? g.Q - q0 : QT;
     const int tid = threadIdx.x, d = tid & (D - 1), grp = tid / D, ngrp = NTH / D;
     const int wave = tid >> 6, lane = tid & (kWave - 1);
 
-    __shared__ A gr[NTH];                     // [QT][D] (QT * D <= NTH)
+    __shared__ A gr[2 * NTH];                 // [QT][D] (QT * D <= 2 * NTH)
     __shared__ int etok[kBucketEnt];          // direct levels: corner token, -1 outside
     __shared__ A ecoef[kBucketEnt];           // a * w_c
     __shared__ int erow[kBucketEnt];          // the corner's row offset in gr (r * D)
@@ -774,179 +770,231 @@ __global__ __launch_bounds__(NTH) void scatter_bucket_kernel(BucketParams bp) {
     __shared__ int wtot[NW];
 
     const T* __restrict__ go = static_cast<const T*>(bp.grad_out);
-    A* __restrict__ gv = static_cast<A*>(bp.grad_value) + static_cast<int64_t>(b) * g.N * HD + static_cast<int64_t>(h) * D;
-    for (int i = tid; i < nq * D; i += NTH) {
-        const int r = i / D;
-        gr[i] = cvt<A>(go[(static_cast<int64_t>(b) * g.Q + q0 + r) * HD + static_cast<int64_t>(h) * D + (i - r * D)]);
-    }
     for (int i = tid; i < kBucketPix; i += NTH) cnt[i] = 0;
 
-    // this thread's sample (row r, sample j of level lt): its four corners' tokens, pixels and coefficients
-    int tk[4] = {-1, -1, -1, -1}, cx[4] = {0, 0, 0, 0}, cy[4] = {0, 0, 0, 0};
-    A cf[4] = {0, 0, 0, 0};
-    int lt = -1, r = 0, jp = 0;
-    if (tid < nq * LP) {
-        r = static_cast<int>(fast_div(bp.d_lp, static_cast<uint32_t>(tid)));
-        const int j = tid - r * LP;
-        lt = static_cast<int>(fast_div(bp.d_p, static_cast<uint32_t>(j)));
-        jp = j - lt * P;
-        const int64_t row = (static_cast<int64_t>(b) * g.Q + q0 + r) * g.H + h, idx = row * LP + j;
-        A lx, ly, a;
-        if (g.loc_acc) {
-            lx = static_cast<const A*>(bp.loc)[2 * idx];
-            ly = static_cast<const A*>(bp.loc)[2 * idx + 1];
-            a = static_cast<const A*>(bp.attn)[idx];
-        } else {
-            lx = cvt<A>(static_cast<const T*>(bp.loc)[2 * idx]);
-            ly = cvt<A>(static_cast<const T*>(bp.loc)[2 * idx + 1]);
-            a = cvt<A>(static_cast<const T*>(bp.attn)[idx]);
+    // One tile: rows r < QT of image b and head h, row r being query query_of(r) (-1: no query; its samples have
+    // no corner in the map)
+    auto tile = [&](int b, int h, auto query_of) {
+        A* __restrict__ gv =
+            static_cast<A*>(bp.grad_value) + static_cast<int64_t>(b) * g.N * HD + static_cast<int64_t>(h) * D;
+        for (int i = tid; i < QT * D; i += NTH) {
+            const int r = i / D, q = query_of(r);
+            gr[i] = q >= 0 ? cvt<A>(go[(static_cast<int64_t>(b) * g.Q + q) * HD + static_cast<int64_t>(h) * D +
+                                       (i - r * D)])
+                           : static_cast<A>(0);
         }
-        const Taps<A> t = taps_at_b<A>(lx, ly, lt, g, b);
-        const int wl = static_cast<int>(g.shapes[2 * lt + 1]);
-        const int64_t st = g.starts[lt];
+
+        // this thread's sample (row r, sample j of level lt): its four corners' tokens, pixels and coefficients
+        int tk[4] = {-1, -1, -1, -1}, cx[4] = {0, 0, 0, 0}, cy[4] = {0, 0, 0, 0};
+        A cf[4] = {0, 0, 0, 0};
+        int lt = -1, r = 0, jp = 0;
+        if (tid < QT * LP) {
+            r = static_cast<int>(fast_div(bp.d_lp, static_cast<uint32_t>(tid)));
+            const int j = tid - r * LP;
+            lt = static_cast<int>(fast_div(bp.d_p, static_cast<uint32_t>(j)));
+            jp = j - lt * P;
+            const int q = query_of(r);
+            if (q >= 0) {
+                const int64_t row = (static_cast<int64_t>(b) * g.Q + q) * g.H + h, idx = row * LP + j;
+                A lx, ly, a;
+                if (g.loc_acc) {
+                    lx = static_cast<const A*>(bp.loc)[2 * idx];
+                    ly = static_cast<const A*>(bp.loc)[2 * idx + 1];
+                    a = static_cast<const A*>(bp.attn)[idx];
+                } else {
+                    lx = cvt<A>(static_cast<const T*>(bp.loc)[2 * idx]);
+                    ly = cvt<A>(static_cast<const T*>(bp.loc)[2 * idx + 1]);
+                    a = cvt<A>(static_cast<const T*>(bp.attn)[idx]);
+                }
+                const Taps<A> t = taps_at_b<A>(lx, ly, lt, g, b);
+                const int wl = static_cast<int>(g.shapes[2 * lt + 1]);
+                const int64_t st = g.starts[lt];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            tk[k] = t.tok[k];
-            cf[k] = g.discrete ? (k == 0 ? a : static_cast<A>(0)) : a * tap_weight(t, k);
-            if (tk[k] >= 0) {
-                const int loc = static_cast<int>(tk[k] - st);
-                cy[k] = loc / wl;
-                cx[k] = loc - cy[k] * wl;
+                for (int k = 0; k < 4; ++k) {
+                    tk[k] = t.tok[k];
+                    cf[k] = g.discrete ? (k == 0 ? a : static_cast<A>(0)) : a * tap_weight(t, k);
+                    if (tk[k] >= 0) {
+                        const int loc = static_cast<int>(tk[k] - st);
+                        cy[k] = loc / wl;
+                        cx[k] = loc - cy[k] * wl;
+                    }
+                }
             }
         }
-    }
 
-    for (int l = 0; l < g.L; ++l) {
-        if (l % LB == 0) {
-            // bounding boxes of the in-map corners of levels l .. l + LB - 1, per wavefront
-            if (l > 0) __syncthreads();  // every wavefront has read the previous group's boxes
-            for (int ll = l; ll < g.L && ll < l + LB; ++ll) {
-                int mnx = 0x7fffffff, mny = 0x7fffffff, mxx = -1, mxy = -1;
-                if (lt == ll) {
+        for (int l = 0; l < g.L; ++l) {
+            if (l % LB == 0) {
+                // bounding boxes of the in-map corners of levels l .. l + LB - 1, per wavefront
+                if (l > 0) __syncthreads();  // every wavefront has read the previous group's boxes
+                for (int ll = l; ll < g.L && ll < l + LB; ++ll) {
+                    int mnx = 0x7fffffff, mny = 0x7fffffff, mxx = -1, mxy = -1;
+                    if (lt == ll) {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (tk[k] >= 0) {
+                                mnx = min(mnx, cx[k]);
+                                mny = min(mny, cy[k]);
+                                mxx = max(mxx, cx[k]);
+                                mxy = max(mxy, cy[k]);
+                            }
+                    }
+                    mnx = wave_min(mnx);
+                    mny = wave_min(mny);
+                    mxx = wave_max(mxx);
+                    mxy = wave_max(mxy);
+                    if (lane == 0) {
+                        boxw[ll - l][wave][0] = mnx;
+                        boxw[ll - l][wave][1] = mny;
+                        boxw[ll - l][wave][2] = mxx;
+                        boxw[ll - l][wave][3] = mxy;
+                    }
+                }
+                __syncthreads();  // the boxes (and, first, the grad_out rows and the zeroed counts) are in place
+            }
+            const int lb = l % LB;
+            int x0 = boxw[lb][0][0], y0 = boxw[lb][0][1], x1 = boxw[lb][0][2], y1 = boxw[lb][0][3];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) {
+                x0 = min(x0, boxw[lb][w][0]);
+                y0 = min(y0, boxw[lb][w][1]);
+                x1 = max(x1, boxw[lb][w][2]);
+                y1 = max(y1, boxw[lb][w][3]);
+            }
+            if (x1 < x0) continue;  // no in-map corner on this level (uniform)
+            const bool mine = lt == l;
+            const int bw = x1 - x0 + 1;
+            const int64_t npix64 = static_cast<int64_t>(bw) * (y1 - y0 + 1);
+            if (npix64 <= kBucketPix) {
+                const int npix = static_cast<int>(npix64);
+                const int wl = static_cast<int>(g.shapes[2 * l + 1]);
+                const int64_t st = g.starts[l];
+                int px[4], rank[4];
+                if (mine) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        px[k] = (cy[k] - y0) * bw + (cx[k] - x0);
+                        rank[k] = tk[k] >= 0 ? atomicAdd(&cnt[px[k]], 1) : 0;
+                    }
+                }
+                __syncthreads();
+                // workgroup scan of the counts: thread t owns pixels [t * k, t * k + k), k = ceil(npix / NTH);
+                // packed (touched pixels << 16) | corners
+                const int kp = (npix + NTH - 1) / NTH, p0 = tid * kp;
+                int own = 0;
+                for (int i = 0; i < kp; ++i) {
+                    const int pp = p0 + i;
+                    const int c = pp < npix ? cnt[pp] : 0;
+                    own += c + (c > 0 ? (1 << 16) : 0);
+                }
+                const int incl = wave_incl_scan(own);
+                if (lane == kWave - 1) wtot[wave] = incl;
+                __syncthreads();
+                int before = 0;
+                for (int w = 0; w < wave; ++w) before += wtot[w];
+                int total = 0;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) total += wtot[w];
+                int run = before + incl - own;  // exclusive
+                for (int i = 0; i < kp; ++i) {
+                    const int pp = p0 + i;
+                    if (pp >= npix) break;
+                    const int c = cnt[pp];
+                    base[pp] = run & 0xffff;
+                    if (c > 0) {
+                        const int yy = pp / bw;
+                        tinfo[run >> 16] = make_int2((run & 0xffff) | c << 16,
+                                                     static_cast<int>(st + static_cast<int64_t>(y0 + yy) * wl +
+                                                                      (x0 + pp - yy * bw)));
+                    }
+                    run += c + (c > 0 ? (1 << 16) : 0);
+                }
+                __syncthreads();
+                if (mine) {
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        if (tk[k] >= 0) {
-                            mnx = min(mnx, cx[k]);
-                            mny = min(mny, cy[k]);
-                            mxx = max(mxx, cx[k]);
-                            mxy = max(mxy, cy[k]);
-                        }
+                        if (tk[k] >= 0) lent[base[px[k]] + rank[k]] = BucketEntry{cf[k], r * D};
                 }
-                mnx = wave_min(mnx);
-                mny = wave_min(mny);
-                mxx = wave_max(mxx);
-                mxy = wave_max(mxy);
-                if (lane == 0) {
-                    boxw[ll - l][wave][0] = mnx;
-                    boxw[ll - l][wave][1] = mny;
-                    boxw[ll - l][wave][2] = mxx;
-                    boxw[ll - l][wave][3] = mxy;
+                __syncthreads();
+                // the counts are no longer read (the touched pixels carry theirs): cleared for the next level
+                for (int i = tid; i < npix; i += NTH) cnt[i] = 0;
+                const int ntouched = total >> 16;
+                for (int ti = grp; ti < ntouched; ti += ngrp) {
+                    const int2 info = tinfo[ti];
+                    const int s0 = info.x & 0xffff, n = info.x >> 16;
+                    A v = 0;
+                    int i = 0;
+                    for (; i + 1 < n; i += 2) {  // two entries' reads in flight
+                        const BucketEntry u = lent[s0 + i], w = lent[s0 + i + 1];
+                        const A gu = gr[u.row + d], gw = gr[w.row + d];
+                        v += u.coef * gu;
+                        v += w.coef * gw;
+                    }
+                    if (i < n) {
+                        const BucketEntry u = lent[s0 + i];
+                        v += u.coef * gr[u.row + d];
+                    }
+                    atomic_add(gv + static_cast<int64_t>(info.y) * HD + d, v);
                 }
+                __syncthreads();  // the counts are zero and the buckets free for the next level
+            } else {
+                if (mine) {
+                    const int e0 = (r * P + jp) * 4;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        etok[e0 + k] = tk[k];
+                        ecoef[e0 + k] = cf[k];
+                        erow[e0 + k] = r * D;
+                    }
+                }
+                __syncthreads();
+                const int ne = QT * P * 4;  // the level's corner entries (rows without a query: none in the map)
+                for (int e = grp; e < ne; e += ngrp) {
+                    const int t = etok[e];
+                    if (t >= 0) atomic_add(gv + static_cast<int64_t>(t) * HD + d, ecoef[e] * gr[erow[e] + d]);
+                }
+                __syncthreads();  // the entries are free for the next level
             }
-            __syncthreads();  // the boxes (and, first, the grad_out rows and the zeroed counts) are in place
         }
-        const int lb = l % LB;
-        int x0 = boxw[lb][0][0], y0 = boxw[lb][0][1], x1 = boxw[lb][0][2], y1 = boxw[lb][0][3];
-#pragma unroll
-        for (int w = 1; w < NW; ++w) {
-            x0 = min(x0, boxw[lb][w][0]);
-            y0 = min(y0, boxw[lb][w][1]);
-            x1 = max(x1, boxw[lb][w][2]);
-            y1 = max(y1, boxw[lb][w][3]);
+    };
+
+    if constexpr (!TILE2D) {
+        // QT consecutive queries
+        const int unit = (blockIdx.x % kXcds) * bp.per_xcd + blockIdx.x / kXcds;
+        if (unit >= bp.units) return;  // the whole workgroup
+        const int qt = unit % bp.qtiles, bh = unit / bp.qtiles;
+        const int q0 = qt * QT, nq = g.Q - q0 < QT ? g.Q - q0 : QT;
+        tile(bh / g.H, bh % g.H, [&](int r) { return r < nq ? q0 + r : -1; });
+    } else {
+        // self-attention (Q = N, query q at token q's pixel): tiles of kTileW x kTileH pixels of each level's map, in
+        // level order; the level sizes are on the device, so every workgroup counts the tiles and takes every
+        // gridDim.x-th
+        auto level_tiles = [&](int l, int& nbx) {
+            const int wl = static_cast<int>(g.shapes[2 * l + 1]), hl = static_cast<int>(g.shapes[2 * l]);
+            nbx = (wl + kTileW - 1) / kTileW;
+            return nbx * ((hl + kTileH - 1) / kTileH);
+        };
+        int per_bh = 0;
+        for (int l = 0; l < g.L; ++l) {
+            int nbx;
+            per_bh += level_tiles(l, nbx);
         }
-        if (x1 < x0) continue;  // no in-map corner on this level (uniform)
-        const bool mine = lt == l;
-        const int bw = x1 - x0 + 1;
-        const int64_t npix64 = static_cast<int64_t>(bw) * (y1 - y0 + 1);
-        if (npix64 <= kBucketPix) {
-            const int npix = static_cast<int>(npix64);
-            const int wl = static_cast<int>(g.shapes[2 * l + 1]);
-            const int64_t st = g.starts[l];
-            int px[4], rank[4];
-            if (mine) {
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    px[k] = (cy[k] - y0) * bw + (cx[k] - x0);
-                    rank[k] = tk[k] >= 0 ? atomicAdd(&cnt[px[k]], 1) : 0;
-                }
+        const int tiles = g.B * g.H * per_bh;
+        for (int t = blockIdx.x; t < tiles; t += gridDim.x) {
+            __syncthreads();  // every wavefront is done with the previous tile's LDS
+            const int bh = t / per_bh;
+            int rest = t - bh * per_bh, lq = 0, nbx = 1;
+            for (; lq < g.L; ++lq) {
+                const int n = level_tiles(lq, nbx);
+                if (rest < n) break;
+                rest -= n;
             }
-            __syncthreads();
-            // workgroup scan of the counts: thread t owns pixels [t * k, t * k + k), k = ceil(npix / NTH);
-            // packed (touched pixels << 16) | corners
-            const int kp = (npix + NTH - 1) / NTH, p0 = tid * kp;
-            int own = 0;
-            for (int i = 0; i < kp; ++i) {
-                const int pp = p0 + i;
-                const int c = pp < npix ? cnt[pp] : 0;
-                own += c + (c > 0 ? (1 << 16) : 0);
-            }
-            const int incl = wave_incl_scan(own);
-            if (lane == kWave - 1) wtot[wave] = incl;
-            __syncthreads();
-            int before = 0;
-            for (int w = 0; w < wave; ++w) before += wtot[w];
-            int total = 0;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) total += wtot[w];
-            int run = before + incl - own;  // exclusive
-            for (int i = 0; i < kp; ++i) {
-                const int pp = p0 + i;
-                if (pp >= npix) break;
-                const int c = cnt[pp];
-                base[pp] = run & 0xffff;
-                if (c > 0) {
-                    const int yy = pp / bw;
-                    tinfo[run >> 16] = make_int2((run & 0xffff) | c << 16,
-                                                 static_cast<int>(st + static_cast<int64_t>(y0 + yy) * wl +
-                                                                  (x0 + pp - yy * bw)));
-                }
-                run += c + (c > 0 ? (1 << 16) : 0);
-            }
-            __syncthreads();
-            if (mine) {
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    if (tk[k] >= 0) lent[base[px[k]] + rank[k]] = BucketEntry{cf[k], r * D};
-            }
-            __syncthreads();
-            // the counts are no longer read (the touched pixels carry theirs): cleared for the next level
-            for (int i = tid; i < npix; i += NTH) cnt[i] = 0;
-            const int ntouched = total >> 16;
-            for (int ti = grp; ti < ntouched; ti += ngrp) {
-                const int2 info = tinfo[ti];
-                const int s0 = info.x & 0xffff, n = info.x >> 16;
-                A v = 0;
-                int i = 0;
-                for (; i + 1 < n; i += 2) {  // two entries' reads in flight
-                    const BucketEntry u = lent[s0 + i], w = lent[s0 + i + 1];
-                    const A gu = gr[u.row + d], gw = gr[w.row + d];
-                    v += u.coef * gu;
-                    v += w.coef * gw;
-                }
-                if (i < n) {
-                    const BucketEntry u = lent[s0 + i];
-                    v += u.coef * gr[u.row + d];
-                }
-                atomic_add(gv + static_cast<int64_t>(info.y) * HD + d, v);
-            }
-            __syncthreads();  // the counts are zero and the buckets free for the next level
-        } else {
-            if (mine) {
-                const int e0 = (r * P + jp) * 4;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    etok[e0 + k] = tk[k];
-                    ecoef[e0 + k] = cf[k];
-                    erow[e0 + k] = r * D;
-                }
-            }
-            __syncthreads();
-            const int ne = nq * P * 4;  // the level's corner entries
-            for (int e = grp; e < ne; e += ngrp) {
-                const int t = etok[e];
-                if (t >= 0) atomic_add(gv + static_cast<int64_t>(t) * HD + d, ecoef[e] * gr[erow[e] + d]);
-            }
-            __syncthreads();  // the entries are free for the next level
+            const int wl = static_cast<int>(g.shapes[2 * lq + 1]), hl = static_cast<int>(g.shapes[2 * lq]);
+            const int x0 = (rest % nbx) * kTileW, y0 = (rest / nbx) * kTileH;
+            const int st = static_cast<int>(g.starts[lq]);
+            tile(bh / g.H, bh % g.H, [&](int r) {
+                const int x = x0 + r % kTileW, y = y0 + r / kTileW;
+                return x < wl && y < hl ? st + y * wl + x : -1;
+            });
         }
     }
 }
@@ -1288,7 +1336,7 @@ int scatter_bucket_go(const BackParams& p, hipStream_t stream) {
     bp.QT = 32;
     if (bp.QT > NTH / g.LP) bp.QT = NTH / g.LP;
     if (bp.QT > kBucketEnt / (4 * g.P)) bp.QT = kBucketEnt / (4 * g.P);
-    if (bp.QT * g.D > NTH) bp.QT = NTH / g.D;
+    if (bp.QT * g.D > 2 * NTH) bp.QT = 2 * NTH / g.D;
     if (bp.QT < 1) return set_error(-1, "sample backward: no bucket shape for these sizes");
     bp.qtiles = (g.Q + bp.QT - 1) / bp.QT;
     const int64_t units = static_cast<int64_t>(g.B) * g.H * bp.qtiles;
@@ -1298,8 +1346,20 @@ int scatter_bucket_go(const BackParams& p, hipStream_t stream) {
     bp.per_xcd = static_cast<int>((units + kXcds - 1) / kXcds);
     bp.d_lp = make_fastdiv(static_cast<uint32_t>(g.LP));
     bp.d_p = make_fastdiv(static_cast<uint32_t>(g.P));
-    hipLaunchKernelGGL((scatter_bucket_kernel<T, NTH>), dim3(static_cast<unsigned>(bp.per_xcd * kXcds)), dim3(NTH), 0,
-                       stream, bp);
+    // Self-attention (as many queries as tokens, 32-query tiles): 8 x 4-pixel tiles of each level's map, which touch
+    // fewer pixels than 32 queries along one map row and never wrap a row; the tile count depends on the level sizes,
+    // which stay on the device, so a grid of three workgroups per CU (what the kernel's registers allow) strides
+    // over them
+    if (g.Q == g.N && bp.QT == kTileW * kTileH && static_cast<int64_t>(g.B) * g.H * g.N <= (int64_t{1} << 30)) {
+        int64_t grid = static_cast<int64_t>(g.B) * g.H * ((g.N + bp.QT - 1) / bp.QT + 2 * g.L);
+        const int64_t resident = 3 * static_cast<int64_t>(cu_count());
+        if (grid > resident) grid = resident;
+        hipLaunchKernelGGL((scatter_bucket_kernel<T, NTH, true>), dim3(static_cast<unsigned>(grid)), dim3(NTH), 0,
+                           stream, bp);
+        return launched("sample backward scatter");
+    }
+    hipLaunchKernelGGL((scatter_bucket_kernel<T, NTH, false>), dim3(static_cast<unsigned>(bp.per_xcd * kXcds)),
+                       dim3(NTH), 0, stream, bp);
     return launched("sample backward scatter");
 }
 

@@ -194,6 +194,28 @@ def test_headline_shape_backward():
     assert torch.equal(out.detach(), fwd)
 
 
+@pytest.mark.parametrize('dtype,D', [(torch.float16, 32), (torch.bfloat16, 16), (torch.float32, 8)])
+@pytest.mark.parametrize('with_mask', [False, True])
+def test_self_attention_tile_gradients(dtype, D, with_mask):
+    # as many queries as tokens: the bucketed scatter takes 8 x 4-pixel tiles of each level's map (query q at token
+    # q), here on maps whose sides are not multiples of 8 or 4 (tiles cut at the right and bottom edges) and a map
+    # narrower than a tile; encoder locations and uniform ones (every window then too large: the direct path)
+    levels = [(25, 37), (13, 19), (7, 10), (3, 5)]
+    N = sum(h * w for h, w in levels)
+    mask = (torch.rand(1, N, generator=torch.Generator().manual_seed(4)) < 0.2) if with_mask else None
+    for loc_dist in ('encoder', 'uniform'):
+        for seed in range(31, 300):
+            args = workload(1, N, 4, D, 64, levels, 4, dtype, loc_dist=loc_dist, seed=seed)
+            if dtype != torch.float32 or boundary_distance(args[5], levels) >= 1e-5:
+                break
+        go = grad_out_for(args)
+        say(f'  backward self-attention tiles N={N} D={D} {dtype} {loc_dist} mask={with_mask}')
+        grads, _ = gpu_grads(args, go, dtype, mask=mask)
+        ref = gridsample.deform_attn_grads(*args, go.to(dtype), padding_mask=mask)
+        for n in NAMES:
+            check(f'tiles D={D} {dtype} {loc_dist} d{n}', grads[n], ref[n], dtype)
+
+
 @pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize('loc_dist', ['encoder', 'uniform'])
 def test_dense_query_gradients_nine_levels(dtype, loc_dist):
