@@ -1503,14 +1503,17 @@ int launch_input_weight_grad(int dtype, const void* G, const void* W, void* Wt, 
     return launch_wgrad(dtype, G, X, gw, gb, M, HD, C, workspace, ws_bytes, stream);
 }
 
-// Split count and workspace of the weight gradient: about 512 workgroups, at least four token steps per split (64
-// tokens in float32, 128 otherwise). Measured on the training step at 8400 tokens (256 x 256), against 256 tokens
-// per split: float32 117.0 -> 99.0 us with 64-token splits (105.8 with 128), 16-bit 63.3 -> 62.7 with 128 (63.4
-// with 64); problems of 32768 tokens and more already had their 512 workgroups.
+// Split count and workspace of the weight gradient: about 512 workgroups (1024 for large outputs), at least four
+// token steps per split (64 tokens in float32, 128 otherwise). Measured on the training step at 8400 tokens
+// (256 x 256), against 256 tokens per split: float32 117.0 -> 99.0 us with 64-token splits (105.8 with 128), 16-bit
+// 63.3 -> 62.7 with 128 (63.4 with 64); problems of 32768 tokens and more already had their 512 workgroups.
 void wgrad_plan(int64_t M, int64_t NO, int64_t K, int dtype, int* splits, int* chunk, int64_t* ws_bytes) {
     const int64_t tiles = ((NO + kWgTile - 1) / kWgTile) * ((K + kWgTile - 1) / kWgTile);
     const int kb = dtype == kF32 ? 16 : 32;
-    int64_t s = (512 + tiles - 1) / tiles;
+    // 1024 workgroups from 64 output tiles (C = 1024): training step at C = 1024 bf16 B2 Q300 913.0 -> 895.2 us; at
+    // 4 tiles (C = 256) 1024 lost 1.5-5% (DINO B4 Q900, bf16 B8 Q300, the DINO encoder: more partials to reduce)
+    const int64_t target = tiles >= 64 ? 1024 : 512;
+    int64_t s = (target + tiles - 1) / tiles;
     const int64_t max_s = (M + 4 * kb - 1) / (4 * kb);
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;

@@ -222,12 +222,13 @@ def test_backward_entries_reject_on_host(lib):
 @pytest.mark.parametrize('dtype,M,NO,K', [(1, 8400, 256, 256), (2, 43520, 1024, 1024), (0, 100, 48, 40),
                                           (3, 5, 16, 8), (1, 0, 64, 64)])
 def test_weight_grad_workspace_plan(lib, dtype, M, NO, K):
-    # split-K plan: about 512 workgroups of 128 x 128 outputs, splits of at least four MFMA K steps (64 tokens for
-    # float32, 128 otherwise) rounded up to the MFMA K (16 tokens for float32, 32 otherwise), float32 partials
-    # (float64 for float64) plus bias partials
+    # split-K plan: about 512 workgroups of 128 x 128 outputs (1024 from 64 tiles), splits of at least four MFMA K
+    # steps (64 tokens for float32, 128 otherwise) rounded up to the MFMA K (16 tokens for float32, 32 otherwise),
+    # float32 partials (float64 for float64) plus bias partials
     tiles = -(-NO // 128) * -(-K // 128)
     kb = 16 if dtype == 0 else 32
-    s = max(1, min(-(-512 // tiles), -(-M // (4 * kb))))
+    target = 1024 if tiles >= 64 else 512  # 1024 workgroups for 64 output tiles and more
+    s = max(1, min(-(-target // tiles), -(-M // (4 * kb))))
     chunk = -(-M // s) if M else 0
     chunk = -(-chunk // kb) * kb
     s = -(-M // chunk) if chunk else 1
