@@ -345,6 +345,40 @@ def ceiling_table():
     print(json.dumps({'gather_ceiling_gbps': rows}), flush=True)
 
 
+ATOMIC_BUFFERS = (('RT-DETR 640 value gradient, B1 (8.6 MB)', 8400 * 256 * 4),
+                  ('DINO 4-level value gradient, B4 (91 MB)', 4 * 22223 * 256 * 4))
+
+
+def atomic_table():
+    """--atomic-ceiling: the float-atomic probe (td_probe_atomic) with groups of 16, 32 and 64 lanes (chunks of 64,
+    128 and 256 bytes), the chunks chosen at random or in sequence, over buffers the size of the value-gradient
+    accumulators, graph-timed (best of 7 replays of 10 launches): lane-group adds and 128-byte lines per second, as a
+    markdown table on stdout and one JSON line."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    log(f'{torch.cuda.get_device_name()} ({torch.cuda.get_device_properties(0).gcnArchName}), {cus} CUs')
+    rows = []
+    for name, nbytes in ATOMIC_BUFFERS:
+        buf = torch.zeros(nbytes // 4, dtype=torch.float32, device='cuda')
+        for lanes in (16, 32, 64):
+            for random in (True, False):
+                wg, per = cus * 8, 64
+                adds = wg * (256 // lanes) * per
+                t = graph_time_us(lambda: _native.probe_atomic(buf, lanes, per, wg, random), 10, 2)
+                r = {'buffer': name, 'lanes': lanes, 'bytes': 4 * lanes, 'order': 'random' if random else 'sequential',
+                     'g_adds_per_s': round(adds / t / 1e3, 2),
+                     'g_lines_per_s': round(adds * lanes * 4 / 128 / t / 1e3, 2), 'us': round(t, 1)}
+                rows.append(r)
+                log(f'  {name:40s} {lanes:2d} lanes ({4 * lanes:3d} B) {r["order"]:10s}: {r["g_adds_per_s"]:6.2f} G '
+                    f'adds/s, {r["g_lines_per_s"]:6.2f} G lines/s')
+        del buf
+    print('| buffer | lanes per add (bytes) | order | G adds/s | G 128-byte lines/s |')
+    print('|---|---:|---|---:|---:|')
+    for r in rows:
+        print(f'| {r["buffer"]} | {r["lanes"]} ({r["bytes"]}) | {r["order"]} | {r["g_adds_per_s"]:.2f} | '
+              f'{r["g_lines_per_s"]:.2f} |')
+    print(json.dumps({'atomic_ceiling': rows}), flush=True)
+
+
 def train_run(cpu_args, steps, warmup):
     """--train-run, for rocprofv3 --kernel-trace: `warmup`, then `steps` eager training steps of the operator
     (train_steps), then the same step graph-timed and, as in --trace-run, a graph of `steps` empty kernels, whose
@@ -748,6 +782,9 @@ def main():
     ap.add_argument('--ceiling', action='store_true',
                     help='the gather ceiling (td_probe_gather) for row widths 64..1024 bytes and buffers from 2 MB '
                          'to 512 MB, as a markdown table')
+    ap.add_argument('--atomic-ceiling', action='store_true',
+                    help='the float-atomic probe (td_probe_atomic): adds of 64-, 128- and 256-byte chunks, random or '
+                         'in sequence, over value-gradient-sized buffers, as a markdown table')
     ap.add_argument('--trace-run', action='store_true',
                     help='for rocprofv3 --kernel-trace: --steps operator calls and --steps empty kernels, each in '
                          'a graph timed like the headline')
@@ -779,6 +816,9 @@ def main():
         return
     if args.ceiling:
         ceiling_table()
+        return
+    if args.atomic_ceiling:
+        atomic_table()
         return
 
     spec = WORKLOADS[args.workload]

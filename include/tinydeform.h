@@ -307,6 +307,14 @@ int td_input_weight_grad(int dtype, const void* grad_value, const void* value_we
  * for a zero buffer).
  */
 int td_probe_empty(int64_t launches, void* stream);
+/*
+ * td_probe_atomic: one launch of `workgroups` workgroups of 256 threads in groups of `lanes` lanes (16, 32 or 64);
+ * each group adds 1.0f, lane by lane, to `adds_per_group` chunks of lanes * 4 bytes of buf [bytes] (float), chosen by
+ * a hash of the step (random != 0) or in sequence: the float atomics of the value-gradient scatter, at the rate the
+ * GPU applies them.
+ */
+int td_probe_atomic(void* buf, int64_t bytes, int64_t lanes, int64_t adds_per_group, int64_t workgroups, int random,
+                    void* stream);
 int td_probe_gather(const void* buf, int64_t bytes, int64_t row_bytes, int64_t loads_per_lane, int64_t workgroups,
                     int64_t waves, void* sink, void* stream);
 

@@ -48,6 +48,7 @@ SIGNATURES = {
     'td_sample_plan': (_int, [_int] + [_i64] * 7 + [_int, _int, _vp]),
     'td_probe_empty': (_int, [_i64, _vp]),
     'td_probe_gather': (_int, [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
+    'td_probe_atomic': (_int, [_vp, _i64, _i64, _i64, _i64, _int, _vp]),
 }
 
 TD_E_WORKSPACE = -4  # td_layer_fused_forward: the problem needs loc_out / attn_out
@@ -728,6 +729,17 @@ def probe_gather(buf, row_bytes, loads_per_lane, workgroups, waves, sink):
     _check(lib_.td_probe_gather(buf.data_ptr(), nbytes, row_bytes, loads_per_lane, workgroups, waves,
                                 sink.data_ptr(), _stream(buf.device)))
     return workgroups * waves * 64 * loads_per_lane * 16
+
+
+def probe_atomic(buf, lanes, adds_per_group, workgroups, random=True):
+    """One launch of the float-atomic probe over the float32 tensor `buf` (td_probe_atomic); returns the number of
+    lane-group adds (each to one chunk of lanes * 4 bytes)."""
+    lib_ = _require()
+    if not buf.is_cuda or not buf.is_contiguous() or buf.dtype != torch.float32:
+        raise RuntimeError('probe_atomic: a contiguous float32 device buffer')
+    _check(lib_.td_probe_atomic(buf.data_ptr(), buf.numel() * 4, lanes, adds_per_group, workgroups, 1 if random else 0,
+                                _stream(buf.device)))
+    return workgroups * (256 // lanes) * adds_per_group
 
 
 # ---- launch plans (the kernels' size rules, evaluated without launching; no device needed) -----------------------

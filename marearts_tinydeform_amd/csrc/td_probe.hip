@@ -8,6 +8,10 @@
 //                      CU at once. With a buffer of the memory tensor's size it measures how fast the CUs receive
 //                      such rows from L2 (and from HBM for what L2 misses): the ceiling of the fused kernel's gather
 //                      phase, which moves mostly L2-resident rows.
+// probe_atomic_kernel  float atomic adds the way the value-gradient scatter issues them: groups of 16, 32 or 64 lanes,
+//                      each group adding to one chunk of 64, 128 or 256 bytes, the chunks chosen by a hash of the
+//                      group's step (as the corners of unrelated queries) or in sequence: the rate the L2s apply
+//                      such atomics at, the ceiling of the backward's scatter.
 #include "../../include/tinydeform.h"
 #include "td_internal.h"
 
@@ -51,6 +55,26 @@ __global__ __launch_bounds__(512) void probe_gather_kernel(ProbeParams p) {
     if (r == 0x5a5a5a5au) p.sink[blockIdx.x] = r;  // keeps the loads; a zero buffer never takes it
 }
 
+__global__ __launch_bounds__(256) void probe_atomic_kernel(float* __restrict__ buf, unsigned chunks, int lanes_log2,
+                                                           unsigned per_group, int random) {
+    const unsigned tid = blockIdx.x * blockDim.x + threadIdx.x;
+    const unsigned lane = tid & ((1u << lanes_log2) - 1u), group = tid >> lanes_log2;
+    for (unsigned i = 0; i < per_group; ++i) {
+        const unsigned k = group * per_group + i;
+        unsigned c;
+        if (random) {
+            unsigned x = k * 2654435761u;
+            x ^= x >> 15;
+            x *= 2246822519u;
+            x ^= x >> 13;
+            c = __umulhi(x, chunks);
+        } else {
+            c = k % chunks;
+        }
+        atomicAdd(buf + (static_cast<size_t>(c) << lanes_log2) + lane, 1.0f);
+    }
+}
+
 }  // namespace
 }  // namespace td
 
@@ -63,6 +87,26 @@ extern "C" int td_probe_empty(int64_t launches, void* stream) {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return set_error(TD_E_LAUNCH, "probe_empty: %s", hipGetErrorString(e));
     }
+    return 0;
+}
+
+extern "C" int td_probe_atomic(void* buf, int64_t bytes, int64_t lanes, int64_t adds_per_group, int64_t workgroups,
+                               int random, void* stream) {
+    if (buf == nullptr) return set_error(TD_E_ARG, "probe_atomic: null buffer");
+    if (lanes != 16 && lanes != 32 && lanes != 64) return set_error(TD_E_ARG, "probe_atomic: lanes must be 16, 32 or 64");
+    const int64_t chunks = bytes / (4 * lanes);
+    if (chunks < 1 || chunks >= (int64_t{1} << 31))
+        return set_error(TD_E_ARG, "probe_atomic: the buffer must hold 1 .. 2^31 - 1 chunks of %lld bytes",
+                         static_cast<long long>(4 * lanes));
+    if (workgroups < 1 || workgroups > (int64_t{1} << 20) || adds_per_group < 1 || adds_per_group > (int64_t{1} << 16))
+        return set_error(TD_E_ARG, "probe_atomic: 1 .. 2^20 workgroups, 1 .. 2^16 adds per lane group");
+    int lanes_log2 = 0;
+    while ((int64_t{1} << lanes_log2) < lanes) ++lanes_log2;
+    hipLaunchKernelGGL(probe_atomic_kernel, dim3(static_cast<unsigned>(workgroups)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<float*>(buf), static_cast<unsigned>(chunks),
+                       lanes_log2, static_cast<unsigned>(adds_per_group), random ? 1 : 0);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(TD_E_LAUNCH, "probe_atomic: %s", hipGetErrorString(e));
     return 0;
 }
 

@@ -35,7 +35,7 @@ def test_header_declares_the_entry_points():
     assert header_functions() == ['td_fused_forward', 'td_fused_forward_masked', 'td_fused_plan', 'td_input_grad',
                                   'td_input_weight_grad', 'td_last_error',
                                   'td_layer_fused_forward', 'td_layer_prologue', 'td_layer_sample_forward',
-                                  'td_probe_empty', 'td_probe_gather',
+                                  'td_probe_atomic', 'td_probe_empty', 'td_probe_gather',
                                   'td_project_forward', 'td_project_forward_noalloc', 'td_sample_backward',
                                   'td_sample_forward',
                                   'td_sample_forward_heads', 'td_sample_forward_masked', 'td_sample_forward_v2',
@@ -217,6 +217,20 @@ def test_backward_entries_reject_on_host(lib):
     assert 'workspace' in lib.td_last_error().decode()
     assert iwg(1, 16, 16, 16, 16, None, 16, 16, 8400, 256, 256, 16, need, None) == E['TD_E_ARG']
     assert iwg(1, 16, 16, None, 16, 16, 16, 16, 8400, 256, 256, 16, need, None) == E['TD_E_ARG']
+
+
+def test_probe_argument_errors(lib):
+    # the measurement kernels refuse bad arguments before launching anything
+    E = header_defines()
+    assert lib.td_probe_empty(-1, None) == E['TD_E_ARG']
+    assert lib.td_probe_gather(None, 1 << 20, 64, 8, 1, 1, 16, None) == E['TD_E_ARG']
+    assert lib.td_probe_gather(16, 1 << 20, 48, 8, 1, 1, 16, None) == E['TD_E_ARG']  # not a power of two
+    assert lib.td_probe_atomic(None, 1 << 20, 32, 1, 1, 1, None) == E['TD_E_ARG']
+    assert lib.td_probe_atomic(16, 1 << 20, 24, 1, 1, 1, None) == E['TD_E_ARG']      # lanes
+    assert lib.td_probe_atomic(16, 64, 32, 1, 1, 1, None) == E['TD_E_ARG']           # less than one chunk
+    assert lib.td_probe_atomic(16, 1 << 20, 32, 0, 1, 1, None) == E['TD_E_ARG']
+    assert lib.td_probe_atomic(16, 1 << 20, 32, 1, 0, 1, None) == E['TD_E_ARG']
+    assert 'probe_atomic' in lib.td_last_error().decode()
 
 
 @pytest.mark.parametrize('dtype,M,NO,K', [(1, 8400, 256, 256), (2, 43520, 1024, 1024), (0, 100, 48, 40),
