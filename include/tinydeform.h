@@ -256,7 +256,10 @@ int td_sample_plan(int dtype, int64_t B, int64_t Q, int64_t N, int64_t H, int64_
  * Sampling half: given grad_out [B, Q, H*D] and the forward's value, locations and weights,
  *   grad_value_acc [B, N, H*D]  float32 (float64 for TD_F64): zeroed, then accumulated (the gradient of value);
  *   grad_value     [B, N, H*D]  dtype, or NULL: grad_value_acc rounded to dtype (may be grad_value_acc itself for
- *                               TD_F32 / TD_F64);
+ *                               TD_F32 / TD_F64). For TD_F16 / TD_BF16 with grad_value given, decoder shapes with
+ *                               many corners (2^18 or more) may have grad_value written directly, by binning the
+ *                               corners by token, with grad_value_acc used as scratch only: its contents are then
+ *                               unspecified, so read the value gradient from grad_value;
  *   grad_loc [B, Q, H, L, P, 2], grad_attn [B, Q, H, L, P]: dtype.
  * padding_mask as in td_sample_forward_masked. Limits as td_sample_forward, and D <= 256.
  */

@@ -552,9 +552,10 @@ extern "C" int td_sample_backward(int dtype, const void* value, const int64_t* s
     g.mask = padding_mask;
     set_levels(g, nullptr);
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    bool direct = false;
     rc = launch_sample_backward(dtype, value, g, sampling_locations, attention_weights, grad_out, grad_value_acc,
-                                grad_loc, grad_attn, s);
-    if (rc != TD_OK || grad_value == nullptr || grad_value == grad_value_acc) return rc;
+                                grad_value == grad_value_acc ? nullptr : grad_value, grad_loc, grad_attn, s, &direct);
+    if (rc != TD_OK || direct || grad_value == nullptr || grad_value == grad_value_acc) return rc;
     return launch_convert(dtype, grad_value_acc, grad_value, B * N * H * D, s);
 }
 

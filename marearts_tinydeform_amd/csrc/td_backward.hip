@@ -372,6 +372,7 @@ __global__ __launch_bounds__(256) void sample_backward_batched_kernel(BackParams
 }
 
 inline bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+inline int ilog2(int x) { return 31 - __builtin_clz(static_cast<unsigned>(x)); }
 
 // The batched form with 16-byte value loads (16/32-bit types, D * element size a multiple of 16, D <= 64). The
 // corner dot products d_c = value[t_c] . g_r need the value rows; the value-gradient atomics need only g_r and the
@@ -999,6 +1000,308 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(6))) void s
     }
 }
 
+// The value gradient by binning the corners by token (decoder shapes, 16-bit types). With few corner hits per token
+// (decoders: 2-4 per token and head) the atomic scatter runs at the GPU's float-atomic rate (about 320 G lane-adds/s,
+// one 128-byte line per corner at D = 32) and needs a zeroed float32 accumulator and a rounding pass. LDS float
+// atomics are no way out: ds_add_f32 runs at about 0.33 lanes per clock per CU (about 200 G lane-adds/s over the GPU,
+// whatever the bank pattern), against about 13 for integer LDS atomics. Instead, per (image b, head h), with bins of
+// TB consecutive tokens (TB = 128, 64 at D = 64):
+//   * sort_count_kernel: each query tile counts its corners into the bins (LDS counters);
+//   * sort_scan_kernel: one workgroup per (b, h) scans the counts, bin-major, into each tile's start within each bin
+//     and each bin's start; then it gives every bin j = 1, 2, 4 ... workgroups, enough that each of the bin's j token
+//     ranges (TB / j tokens) averages at most kSortChunk entries, and lists them;
+//   * sort_fill_kernel: each tile writes its corners as entries {a * w_c, row << 7 | token % TB} into their bins
+//     (ranks within the tile from LDS atomics);
+//   * sort_reduce_kernel: one workgroup per (bin, token range) reads the bin's entries kSortChunk at a time, sorts
+//     those of its range by token in LDS (a counting sort: integer LDS atomics for the ranks), then, kSortProd / D
+//     entries at a time, lane groups compute the products a * w_c * g_row (16 grad_out rows in flight per lane) into
+//     LDS and each token's owner lanes add up its run of products in registers; finally it writes its tokens' rows,
+//     in the element type. The small levels' bins (many corners on few tokens) are so split over several
+//     workgroups, each reading the whole bin's entries (8 bytes each) but loading only its own grad_out rows.
+// No float atomics, no zero fill, no rounding pass. Within a token the products are added in the order the LDS ranks
+// give, so the result agrees with the atomic scatter's to float rounding. The scratch (entries, counts, starts,
+// workgroup list) lives in the caller's float32 accumulator buffer. grad_loc and grad_attn come from
+// loc_attn_backward_kernel.
+constexpr int kSortMaxBins = 8192;  // bins per (b, h) at most (the tiles' LDS counters; 13 bits of a chunk code)
+constexpr int kSortChunk = 1024;    // entries per token range on average at most; entries read per round
+constexpr int kSortProd = 4096;     // product floats in LDS per step of the reduce
+
+// tokens per bin at head width D: TB x D floats = 16 KB (128 at most: the entry keeps token % TB in 7 bits)
+__host__ __device__ constexpr int sort_bin_tokens(int D) { return D >= 64 ? 4096 / D : 128; }
+
+struct SortParams {
+    const void* loc;
+    const void* attn;
+    const void* grad_out;
+    void* grad_value;  // [B, N, H * D] element type
+    Geom g;
+    int QT, qtiles, nb;   // queries per tile (256 / (L * P)), tiles per (b, h), bins per (b, h)
+    int tb_shift;         // log2 of the tokens per bin
+    int maxch;            // reduce workgroups per (b, h) at most
+    int64_t cap;          // entries per (b, h) at most: Q * L * P * 4
+    int* hist;            // [B * H][nb][qtiles]: counts, then each tile's start within its bin
+    int* bin_start;       // [B * H][nb + 1]: start of each bin within the (b, h) region of entries
+    unsigned* chunk_bin;  // [B * H][maxch]: bin | range << 13 | log2(ranges) << 20 of each reduce workgroup
+    int* nch;             // [B * H]: reduce workgroups of the (b, h)
+    uint2* entries;       // [B * H][cap]
+    FastDiv d_lp;
+};
+
+// Thread tid of tile (bh, qt): its sample's four corners (tokens, -1 outside) and coefficients, and its row.
+template <typename T>
+__device__ __forceinline__ bool sort_sample(const SortParams& sp, int bh, int qt, int tid, int (&tk)[4],
+                                            float (&cf)[4], int& row) {
+    const Geom& g = sp.g;
+    if (tid >= sp.QT * g.LP) return false;
+    const int r = static_cast<int>(fast_div(sp.d_lp, static_cast<uint32_t>(tid))), j = tid - r * g.LP;
+    const int q = qt * sp.QT + r;
+    if (q >= g.Q) return false;
+    const int b = bh / g.H, h = bh - b * g.H;
+    row = (b * g.Q + q) * g.H + h;
+    const int64_t idx = static_cast<int64_t>(row) * g.LP + j;
+    float lx, ly, a;
+    if (g.loc_acc) {
+        lx = static_cast<const float*>(sp.loc)[2 * idx];
+        ly = static_cast<const float*>(sp.loc)[2 * idx + 1];
+        a = static_cast<const float*>(sp.attn)[idx];
+    } else {
+        lx = cvt<float>(static_cast<const T*>(sp.loc)[2 * idx]);
+        ly = cvt<float>(static_cast<const T*>(sp.loc)[2 * idx + 1]);
+        a = cvt<float>(static_cast<const T*>(sp.attn)[idx]);
+    }
+    const Taps<float> t = taps_at_b<float>(lx, ly, level_of(g, j), g, b);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        tk[k] = t.tok[k];
+        cf[k] = g.discrete ? (k == 0 ? a : 0.f) : a * tap_weight(t, k);
+    }
+    return true;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void sort_count_kernel(SortParams sp) {
+    extern __shared__ int lc[];  // [nb]
+    const int bh = blockIdx.x / sp.qtiles, qt = blockIdx.x - bh * sp.qtiles;
+    for (int i = threadIdx.x; i < sp.nb; i += 256) lc[i] = 0;
+    __syncthreads();
+    int tk[4], row;
+    float cf[4];
+    if (sort_sample<T>(sp, bh, qt, threadIdx.x, tk, cf, row)) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (tk[k] >= 0) atomicAdd(&lc[tk[k] >> sp.tb_shift], 1);
+    }
+    __syncthreads();
+    int* hist = sp.hist + static_cast<int64_t>(bh) * sp.nb * sp.qtiles;
+    for (int i = threadIdx.x; i < sp.nb; i += 256) hist[static_cast<int64_t>(i) * sp.qtiles + qt] = lc[i];
+}
+
+// One workgroup per (b, h). First the exclusive scan of the nb * qtiles counts (bin-major) in chunks of 4096, each
+// loaded into LDS with coalesced reads, thread t owning 8 consecutive counts (LDS pitch 9 words: the owners' reads
+// spread over the banks), a wavefront scan of the owners' totals, and coalesced writes back; the bins' starts are the
+// scanned values at the bins' first counts (kept in LDS too, bst). Then, 512 bins at a time, each bin's number of
+// token ranges (a block scan gives their places in the list) and the list of reduce workgroups.
+constexpr int kScanTh = 512, kScanK = 8, kScanChunk = kScanTh * kScanK;
+
+__device__ __forceinline__ int block_excl_scan(int x, int* wt, int wave, int lane, int& total) {
+    constexpr int NW = kScanTh / kWave;
+    const int incl = wave_incl_scan(x);  // every lane active
+    if (lane == kWave - 1) wt[wave] = incl;
+    __syncthreads();
+    int run = incl - x, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        run += w < wave ? wt[w] : 0;
+        tot += wt[w];
+    }
+    total = tot;
+    return run;
+}
+
+__global__ __launch_bounds__(kScanTh) void sort_scan_kernel(SortParams sp) {
+    __shared__ int v[kScanTh * (kScanK + 1)];
+    __shared__ int wtot[kScanTh / kWave];
+    extern __shared__ int bst[];  // [nb + 1]: the bins' starts
+    const int bh = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
+    int* hist = sp.hist + static_cast<int64_t>(bh) * sp.nb * sp.qtiles;
+    int* bs = sp.bin_start + static_cast<int64_t>(bh) * (sp.nb + 1);
+    const int n = sp.nb * sp.qtiles;  // < 2^30 (checked on the host)
+    int* mine = v + tid * (kScanK + 1);
+    int carry = 0;
+    for (int c0 = 0; c0 < n; c0 += kScanChunk) {  // uniform: every barrier is reached by the whole workgroup
+        const int len = n - c0 < kScanChunk ? n - c0 : kScanChunk;
+        int hv[kScanK];  // loads at clamped indexes, all in flight together
+#pragma unroll
+        for (int u = 0; u < kScanK; ++u) hv[u] = hist[c0 + min(tid + u * kScanTh, len - 1)];
+#pragma unroll
+        for (int u = 0; u < kScanK; ++u) {
+            const int j = tid + u * kScanTh;
+            v[(j / kScanK) * (kScanK + 1) + j % kScanK] = j < len ? hv[u] : 0;
+        }
+        __syncthreads();  // the chunk is in LDS
+        int own = 0;
+#pragma unroll
+        for (int k = 0; k < kScanK; ++k) own += mine[k];
+        int tot;
+        int run = carry + block_excl_scan(own, wtot, wave, lane, tot);
+#pragma unroll
+        for (int k = 0; k < kScanK; ++k) {
+            const int c = mine[k];
+            mine[k] = run;
+            run += c;
+        }
+        __syncthreads();  // the chunk is scanned
+        for (int j = tid; j < len; j += kScanTh) hist[c0 + j] = v[(j / kScanK) * (kScanK + 1) + j % kScanK];
+        // bins whose first count lies in this chunk
+        for (int bb = (c0 + sp.qtiles - 1) / sp.qtiles + tid; static_cast<int64_t>(bb) * sp.qtiles < c0 + len;
+             bb += kScanTh) {
+            const int j = bb * sp.qtiles - c0;
+            const int st = v[(j / kScanK) * (kScanK + 1) + j % kScanK];
+            bs[bb] = st;
+            bst[bb] = st;
+        }
+        carry += tot;
+        __syncthreads();  // v and wtot are free for the next chunk
+    }
+    if (tid == 0) {
+        bs[sp.nb] = carry;
+        bst[sp.nb] = carry;
+    }
+    __syncthreads();  // every bin's start is in bst
+    unsigned* list = sp.chunk_bin + static_cast<int64_t>(bh) * sp.maxch;
+    int ch_carry = 0;
+    for (int b0 = 0; b0 < sp.nb; b0 += kScanTh) {  // uniform
+        const int bin = b0 + tid;
+        const int cnt = bin < sp.nb ? bst[bin + 1] - bst[bin] : 0;
+        int lj = 0;  // 2^lj token ranges: the fewest with at most kSortChunk entries each on average, TB at most
+        while (lj < sp.tb_shift && (cnt >> lj) > kSortChunk) ++lj;
+        const int nk = bin < sp.nb ? 1 << lj : 0;
+        int tn;
+        const int fn = ch_carry + block_excl_scan(nk, wtot, wave, lane, tn);
+        for (int k = 0; k < nk; ++k)
+            list[fn + k] = static_cast<unsigned>(bin) | static_cast<unsigned>(k) << 13 | static_cast<unsigned>(lj) << 20;
+        ch_carry += tn;
+        __syncthreads();  // wtot is free for the next bins
+    }
+    if (tid == 0) sp.nch[bh] = ch_carry;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void sort_fill_kernel(SortParams sp) {
+    extern __shared__ int lc[];  // [nb]: this tile's running rank per bin
+    const int bh = blockIdx.x / sp.qtiles, qt = blockIdx.x - bh * sp.qtiles;
+    for (int i = threadIdx.x; i < sp.nb; i += 256) lc[i] = 0;
+    __syncthreads();
+    int tk[4], row;
+    float cf[4];
+    if (sort_sample<T>(sp, bh, qt, threadIdx.x, tk, cf, row)) {
+        const int* off = sp.hist + static_cast<int64_t>(bh) * sp.nb * sp.qtiles + qt;
+        uint2* ent = sp.entries + static_cast<int64_t>(bh) * sp.cap;
+        const int tmask = (1 << sp.tb_shift) - 1;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (tk[k] < 0) continue;
+            const int bin = tk[k] >> sp.tb_shift;
+            const int rank = atomicAdd(&lc[bin], 1);
+            ent[off[static_cast<int64_t>(bin) * sp.qtiles] + rank] =
+                make_uint2(__float_as_uint(cf[k]), static_cast<unsigned>(row) << 7 | static_cast<unsigned>(tk[k] & tmask));
+        }
+    }
+}
+
+// One workgroup of 256 threads per (bin, token range) (grid: B * H x maxch; those past the (b, h)'s count return at
+// once). NG = 256 / D lane groups, lane d of a group owning column d; group grp owns the range's tokens grp,
+// grp + NG, ... (TPG = TB / NG of them at most, summed in registers). Rounds of kSortChunk of the bin's entries: loaded
+// 4 a thread (all in flight), those in the range ranked by token (integer LDS atomics) and written to LDS in token
+// order; then steps of CH = kSortProd / D sorted entries: group grp computes the products of entries grp * 16 .. + 15
+// of the step into LDS, and each owner adds up the part of its tokens' runs that lies in the step.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void sort_reduce_kernel(SortParams sp) {
+    constexpr int NTH = 256, NG = NTH / D, TB = sort_bin_tokens(D), TPG = TB / NG, CH = kSortProd / D, EPG = CH / NG;
+    constexpr int PER = kSortChunk / NTH;
+    static_assert(EPG == 16 && TPG >= 1 && TB <= 128 && D >= 8, "reduce shape");
+    const int bh = blockIdx.x / sp.maxch, c = blockIdx.x - bh * sp.maxch;
+    if (c >= sp.nch[bh]) return;  // uniform: before any barrier
+    const Geom& g = sp.g;
+    const int HD = g.H * D;
+    const int b = bh / g.H, h = bh - b * g.H;
+    const int tid = threadIdx.x, d = tid & (D - 1), grp = tid / D, wave = tid >> 6, lane = tid & (kWave - 1);
+    __shared__ float prod[kSortProd];
+    __shared__ uint2 sorted[kSortChunk];
+    __shared__ int cnt[TB], base[TB], wtot[2];
+    const unsigned code = sp.chunk_bin[static_cast<int64_t>(bh) * sp.maxch + c];
+    const int bin = static_cast<int>(code & 0x1fffu), width = TB >> (code >> 20), lo = static_cast<int>((code >> 13) & 0x7fu) * width;
+    const int* bs = sp.bin_start + static_cast<int64_t>(bh) * (sp.nb + 1);
+    const int eb0 = bs[bin], eb1 = bs[bin + 1];
+    const uint2* __restrict__ src = sp.entries + static_cast<int64_t>(bh) * sp.cap;
+    const T* __restrict__ go = static_cast<const T*>(sp.grad_out);
+    float acc[TPG];
+#pragma unroll
+    for (int s = 0; s < TPG; ++s) acc[s] = 0.f;
+    for (int r0 = eb0; r0 < eb1; r0 += kSortChunk) {  // uniform: every barrier is reached by the whole workgroup
+        const int n = min(eb1 - r0, kSortChunk);
+        uint2 ex[PER];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) ex[u] = src[r0 + min(tid + u * NTH, n - 1)];  // clamped: all in flight
+        if (tid < TB) cnt[tid] = 0;
+        __syncthreads();  // the counts are clear
+        int rk[PER];
+        bool in[PER];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int tk = static_cast<int>(ex[u].y & (TB - 1));
+            in[u] = tid + u * NTH < n && static_cast<unsigned>(tk - lo) < static_cast<unsigned>(width);
+            rk[u] = atomicAdd(&cnt[tk], in[u] ? 1 : 0);  // no branch: the four atomics in flight together
+        }
+        __syncthreads();  // the counts are final
+        if (tid < 128) {  // the first two wavefronts, every lane active: scan of the TB counts
+            const int cv = tid < TB ? cnt[tid] : 0;
+            const int incl = wave_incl_scan(cv);
+            if (lane == kWave - 1) wtot[wave] = incl;
+            if (tid < TB) base[tid] = incl - cv;
+        }
+        __syncthreads();
+        if (tid >= kWave && tid < TB) base[tid] += wtot[0];
+        const int mt = wtot[0] + wtot[1];  // entries of the range in this round
+        __syncthreads();  // every token's start is known
+#pragma unroll
+        for (int u = 0; u < PER; ++u)
+            if (in[u]) sorted[base[ex[u].y & (TB - 1)] + rk[u]] = ex[u];
+        __syncthreads();  // the range's entries are in token order
+        for (int s0 = 0; s0 < mt; s0 += CH) {  // uniform
+            const int m = min(CH, mt - s0);
+            {
+                float gv[EPG], cf[EPG];
+#pragma unroll
+                for (int u = 0; u < EPG; ++u) {  // clamped: no branch around the loads
+                    const uint2 x = sorted[s0 + min(grp * EPG + u, m - 1)];
+                    cf[u] = __uint_as_float(x.x);
+                    gv[u] = cvt<float>(go[static_cast<int64_t>(x.y >> 7) * D + d]);
+                }
+#pragma unroll
+                for (int u = 0; u < EPG; ++u)
+                    if (grp * EPG + u < m) prod[(grp * EPG + u) * D + d] = cf[u] * gv[u];
+            }
+            __syncthreads();  // the step's products are in place
+#pragma unroll
+            for (int s = 0; s < TPG; ++s) {
+                const int tl = lo + grp + s * NG;
+                if (grp + s * NG >= width) break;
+                const int i0 = max(base[tl], s0), i1 = min(base[tl] + cnt[tl], s0 + m);
+#pragma unroll 4
+                for (int i = i0; i < i1; ++i) acc[s] += prod[(i - s0) * D + d];
+            }
+            __syncthreads();  // the products are free for the next step
+        }
+    }
+    T* __restrict__ out = static_cast<T*>(sp.grad_value) + static_cast<int64_t>(b) * g.N * HD + h * D + d;
+#pragma unroll
+    for (int s = 0; s < TPG; ++s) {
+        const int t = bin * TB + lo + grp + s * NG;
+        if (grp + s * NG < width && t < g.N) out[static_cast<int64_t>(t) * HD] = static_cast<T>(acc[s]);
+    }
+}
+
 template <typename T, typename A>
 __global__ __launch_bounds__(256) void convert_kernel(const A* __restrict__ src, T* __restrict__ dst, int64_t n) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -1364,7 +1667,8 @@ int scatter_bucket_go(const BackParams& p, hipStream_t stream) {
 }
 
 // loc_attn_backward_kernel's shape: RB = 256 / LP rows a workgroup, SG corner groups a row (every thread a lane
-// where RB * DV <= 256); 0 when the kernel does not fit (the caller then takes sample_backward_vec_kernel)
+// where RB * DV <= 256); 1 without launching when the kernel does not fit (the caller then takes
+// sample_backward_vec_kernel or the atomic scatter)
 template <typename T>
 int loc_attn_backward_go(const BackParams& p, hipStream_t stream) {
     constexpr int V = 16 / static_cast<int>(sizeof(T)), NTH = 256;
@@ -1372,7 +1676,10 @@ int loc_attn_backward_go(const BackParams& p, hipStream_t stream) {
     const int64_t rows = static_cast<int64_t>(g.B) * g.Q * g.H;
     const int64_t vbytes = static_cast<int64_t>(g.B) * g.N * g.H * g.D * static_cast<int64_t>(sizeof(T));
     const int DV = g.D / V;
-    if (g.LP <= 0 || g.LP > NTH || DV > 16 || rows * g.LP >= (int64_t{1} << 31) || vbytes >= (int64_t{1} << 31))
+    // 16-byte value and grad_out loads: D a multiple of V (DV a power of two), 16-byte aligned rows
+    if (g.D % V != 0 || !is_pow2(DV) || DV > 16 || reinterpret_cast<uintptr_t>(p.value) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(p.grad_out) % 16 != 0 || g.LP <= 0 || g.LP > NTH ||
+        rows * g.LP >= (int64_t{1} << 31) || vbytes >= (int64_t{1} << 31))
         return 1;
     LocAttnParams lp{p, 0, 0, 0, 0, 0, {}, {}, {}, {}, {}};
     lp.RB = NTH / g.LP;
@@ -1390,6 +1697,74 @@ int loc_attn_backward_go(const BackParams& p, hipStream_t stream) {
     hipLaunchKernelGGL((loc_attn_backward_kernel<T, V, 8>), dim3(static_cast<unsigned>(lp.per_xcd * kXcds)), dim3(NTH),
                        0, stream, lp);
     return launched("sample backward locations");
+}
+
+// The binned path (sort_count_kernel ... sort_reduce_kernel) for 16-bit types at decoder densities, with the location
+// and weight gradients from loc_attn_backward_kernel; grad_value (the element type) is written
+// directly. Returns 1 without launching when it does not apply: too few corners to pay for its five launches, a dense
+// problem (the bucketed scatter's), a head width other than 8..64 (a power of two), more than kSortMaxBins bins or
+// 2^25 rows, scratch that does not fit in the accumulator buffer (acc_bytes), or shapes loc_attn_backward_kernel
+// does not take (value or grad_out rows not 16-byte aligned).
+constexpr int64_t kSortMinCorners = int64_t{1} << 18;
+
+template <typename T>
+int sample_backward_sorted(const BackParams& p, void* grad_value_t, int64_t acc_bytes, hipStream_t stream) {
+    const Geom& g = p.g;
+    if (grad_value_t == nullptr || grad_value_t == p.grad_value || !is_pow2(g.D) || g.D < 8 || g.D > 64 ||
+        g.LP <= 0 || g.LP > 256 || bucket_scatter_pays(g))
+        return 1;
+    const int64_t rows = static_cast<int64_t>(g.B) * g.Q * g.H;
+    if (rows * g.LP * 4 < kSortMinCorners || rows >= (int64_t{1} << 25)) return 1;
+    SortParams sp{};
+    sp.loc = p.loc;
+    sp.attn = p.attn;
+    sp.grad_out = p.grad_out;
+    sp.grad_value = grad_value_t;
+    sp.g = g;
+    sp.QT = 256 / g.LP;
+    sp.qtiles = (g.Q + sp.QT - 1) / sp.QT;
+    const int tb = sort_bin_tokens(g.D);
+    sp.tb_shift = ilog2(tb);
+    const int64_t nb = (static_cast<int64_t>(g.N) + tb - 1) / tb, BH = static_cast<int64_t>(g.B) * g.H;
+    sp.cap = static_cast<int64_t>(g.Q) * g.LP * 4;
+    // reduce workgroups: a bin of count entries takes j = 1 or the least power of two with count / j <= kSortChunk
+    // (so j < 2 count / kSortChunk), hence at most nb + 2 cap / kSortChunk of them per (b, h)
+    const int64_t maxch = nb + 2 * sp.cap / kSortChunk + 1;
+    if (nb > kSortMaxBins || nb * sp.qtiles >= (int64_t{1} << 30) || BH * maxch >= (int64_t{1} << 31)) return 1;
+    sp.nb = static_cast<int>(nb);
+    sp.maxch = static_cast<int>(maxch);
+    const int64_t ent_bytes = BH * sp.cap * 8;
+    const int64_t ints = BH * nb * sp.qtiles + BH * (nb + 1) + BH * maxch + BH;
+    if (ent_bytes + 4 * ints > acc_bytes) return 1;
+    // the location and weight gradients first (1: its 16-byte loads do not fit these sizes)
+    const int rc = loc_attn_backward_go<T>(p, stream);
+    if (rc != 0) return rc;
+    unsigned char* scratch = static_cast<unsigned char*>(p.grad_value);
+    sp.entries = reinterpret_cast<uint2*>(scratch);
+    sp.hist = reinterpret_cast<int*>(scratch + ent_bytes);
+    sp.bin_start = sp.hist + BH * nb * sp.qtiles;
+    sp.chunk_bin = reinterpret_cast<unsigned*>(sp.bin_start + BH * (nb + 1));
+    sp.nch = reinterpret_cast<int*>(sp.chunk_bin + BH * maxch);
+    sp.d_lp = make_fastdiv(static_cast<uint32_t>(g.LP));
+    const unsigned tiles = static_cast<unsigned>(BH * sp.qtiles);
+    const size_t lds = static_cast<size_t>(nb) * sizeof(int);
+    hipLaunchKernelGGL(sort_count_kernel<T>, dim3(tiles), dim3(256), lds, stream, sp);
+    int r2 = launched("sample backward count");
+    if (r2 != 0) return r2;
+    hipLaunchKernelGGL(sort_scan_kernel, dim3(static_cast<unsigned>(BH)), dim3(kScanTh), lds + sizeof(int), stream, sp);
+    r2 = launched("sample backward scan");
+    if (r2 != 0) return r2;
+    hipLaunchKernelGGL(sort_fill_kernel<T>, dim3(tiles), dim3(256), lds, stream, sp);
+    r2 = launched("sample backward fill");
+    if (r2 != 0) return r2;
+    const dim3 rgrid(static_cast<unsigned>(BH * maxch));
+    switch (g.D) {
+        case 8: hipLaunchKernelGGL((sort_reduce_kernel<T, 8>), rgrid, dim3(256), 0, stream, sp); break;
+        case 16: hipLaunchKernelGGL((sort_reduce_kernel<T, 16>), rgrid, dim3(256), 0, stream, sp); break;
+        case 32: hipLaunchKernelGGL((sort_reduce_kernel<T, 32>), rgrid, dim3(256), 0, stream, sp); break;
+        default: hipLaunchKernelGGL((sort_reduce_kernel<T, 64>), rgrid, dim3(256), 0, stream, sp); break;
+    }
+    return launched("sample backward reduce");
 }
 
 template <typename T>
@@ -1417,13 +1792,23 @@ int sample_backward_t(const BackParams& p, hipStream_t stream) {
 }  // namespace
 
 int launch_sample_backward(int dtype, const void* value, const Geom& g, const void* loc, const void* attn,
-                           const void* grad_out, void* grad_value, void* grad_loc, void* grad_attn,
-                           hipStream_t stream) {
+                           const void* grad_out, void* grad_value, void* grad_value_t, void* grad_loc, void* grad_attn,
+                           hipStream_t stream, bool* direct) {
     if (g.D > kWave * 4) return set_error(-1, "sample backward: head dim %d > %d", g.D, kWave * 4);
     const int acc = dtype == kF64 ? 8 : 4;
-    const int rc = launch_zero(grad_value, static_cast<int64_t>(g.B) * g.N * g.H * g.D * acc, stream);
-    if (rc != 0) return rc;
+    const int64_t acc_bytes = static_cast<int64_t>(g.B) * g.N * g.H * g.D * acc;
     BackParams p{value, loc, attn, grad_out, grad_value, grad_loc, grad_attn, g, 1};
+    *direct = false;
+    if ((dtype == kF16 || dtype == kBF16) && (reinterpret_cast<uintptr_t>(grad_value) % 8) == 0) {
+        const int rs = dtype == kF16 ? sample_backward_sorted<f16>(p, grad_value_t, acc_bytes, stream)
+                                     : sample_backward_sorted<bf16>(p, grad_value_t, acc_bytes, stream);
+        if (rs != 1) {
+            *direct = rs == 0;
+            return rs;
+        }
+    }
+    const int rc = launch_zero(grad_value, acc_bytes, stream);
+    if (rc != 0) return rc;
     switch (dtype) {
         case kF32: return sample_backward_t<float>(p, stream);
         case kF16: return sample_backward_t<f16>(p, stream);

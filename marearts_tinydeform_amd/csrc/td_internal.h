@@ -118,9 +118,11 @@ int project_forward(int dtype, const void* memory, const void* value_weight, con
 
 // Backward (td_backward.hip). grad_value: [B, N, H*D] in the accumulation type, zeroed and accumulated here;
 // grad_loc / grad_attn in the element type (the accumulation type with g.loc_acc).
+// grad_value: the float32 (float64) accumulator; grad_value_t: the element-type gradient or NULL. *direct is set
+// when grad_value_t was written directly (the accumulator then held scratch), else the caller rounds the accumulator.
 int launch_sample_backward(int dtype, const void* value, const Geom& g, const void* loc, const void* attn,
-                           const void* grad_out, void* grad_value, void* grad_loc, void* grad_attn,
-                           hipStream_t stream);
+                           const void* grad_out, void* grad_value, void* grad_value_t, void* grad_loc, void* grad_attn,
+                           hipStream_t stream, bool* direct);
 // dst[i] = src[i] rounded from the accumulation type to dtype
 int launch_convert(int dtype, const void* src_acc, void* dst, int64_t n, hipStream_t stream);
 // dst [Cc, R] = src [R, Cc]^T

@@ -196,6 +196,36 @@ def test_headline_shape_backward():
     assert torch.equal(out.detach(), fwd)
 
 
+SORT_LEVELS = {'four': [(48, 64), (24, 32), (12, 16), (6, 8)], 'wide': [(64, 80), (32, 40), (16, 20)],
+               'big': [(96, 128), (48, 64)]}
+
+
+@pytest.mark.parametrize('dtype,D,shape,Q', [(torch.float16, 32, 'four', 901), (torch.bfloat16, 32, 'four', 901),
+                                             (torch.float16, 64, 'four', 901), (torch.bfloat16, 16, 'wide', 901),
+                                             (torch.float16, 8, 'big', 600), (torch.bfloat16, 8, 'big', 700),
+                                             (torch.bfloat16, 4, 'big', 600)])
+@pytest.mark.parametrize('with_mask', [False, True])
+def test_decoder_sorted_value_gradients(dtype, D, shape, Q, with_mask):
+    # decoder density with many corners (2^18 and more, 16-bit): the value gradient by binning the corners by token
+    # (sort_count_kernel .. sort_reduce_kernel, written once in the element type) and the location and weight
+    # gradients by loc_attn_backward_kernel; Q ragged against the query tiles, clustered and uniform locations.
+    # D = 4 (16-bit): narrower than loc_attn_backward_kernel's 16-byte loads, so the atomic scatter instead
+    levels = SORT_LEVELS[shape]
+    L, P = len(levels), 4
+    N = sum(h * w for h, w in levels)
+    mask = (torch.rand(2, N, generator=torch.Generator().manual_seed(5)) < 0.2) if with_mask else None
+    for loc_dist in ('clustered', 'uniform'):
+        args = workload(2, Q, 8, D, 64, levels, P, dtype, loc_dist=loc_dist, seed=17)
+        # many corners, not dense, the bins' entries within the float32 accumulator
+        assert 2 * Q * 8 * L * P * 4 >= 1 << 18 and Q * L * P * 4 < 16 * N and Q * L * P * 8 <= N * D
+        go = grad_out_for(args)
+        say(f'  backward binned value gradient D={D} L={L} Q={Q} {dtype} {loc_dist} mask={with_mask}')
+        grads, _ = gpu_grads(args, go, dtype, mask=mask)
+        ref = gridsample.deform_attn_grads(*args, go.to(dtype), padding_mask=mask)
+        for n in NAMES:
+            check(f'binned D={D} {dtype} {loc_dist} d{n}', grads[n], ref[n], dtype)
+
+
 @pytest.mark.parametrize('dtype,D', [(torch.float16, 32), (torch.bfloat16, 16), (torch.float32, 8)])
 @pytest.mark.parametrize('with_mask', [False, True])
 def test_self_attention_tile_gradients(dtype, D, with_mask):
