@@ -1012,19 +1012,18 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(6))) void s
 //     ranges (TB / j tokens) averages at most kSortChunk entries, and lists them;
 //   * sort_fill_kernel: each tile writes its corners as entries {a * w_c, row << 7 | token % TB} into their bins
 //     (ranks within the tile from LDS atomics);
-//   * sort_reduce_kernel: one workgroup per (bin, token range) reads the bin's entries kSortChunk at a time, sorts
-//     those of its range by token in LDS (a counting sort: integer LDS atomics for the ranks), then, kSortProd / D
-//     entries at a time, lane groups compute the products a * w_c * g_row (16 grad_out rows in flight per lane) into
-//     LDS and each token's owner lanes add up its run of products in registers; finally it writes its tokens' rows,
-//     in the element type. The small levels' bins (many corners on few tokens) are so split over several
-//     workgroups, each reading the whole bin's entries (8 bytes each) but loading only its own grad_out rows.
+//   * sort_reduce_kernel: one workgroup per (bin, token range) reads the bin's entries kSortChunk at a time and sorts
+//     those of its range in LDS (a counting sort: integer LDS atomics for the ranks) so that each lane group's
+//     tokens' entries lie together; each group then streams through its entries, 16 grad_out rows in flight per
+//     lane, adding the products a * w_c * g_row into its own tokens' float sums in LDS; finally the workgroup writes
+//     its tokens' rows, in the element type. The small levels' bins (many corners on few tokens) are so split over
+//     several workgroups, each reading the whole bin's entries (8 bytes each) but loading only its own grad_out rows.
 // No float atomics, no zero fill, no rounding pass. Within a token the products are added in the order the LDS ranks
 // give, so the result agrees with the atomic scatter's to float rounding. The scratch (entries, counts, starts,
 // workgroup list) lives in the caller's float32 accumulator buffer. grad_loc and grad_attn come from
 // loc_attn_backward_kernel.
 constexpr int kSortMaxBins = 8192;  // bins per (b, h) at most (the tiles' LDS counters; 13 bits of a chunk code)
 constexpr int kSortChunk = 1024;    // entries per token range on average at most; entries read per round
-constexpr int kSortProd = 4096;     // product floats in LDS per step of the reduce
 
 // tokens per bin at head width D: TB x D floats = 16 KB (128 at most: the entry keeps token % TB in 7 bits)
 __host__ __device__ constexpr int sort_bin_tokens(int D) { return D >= 64 ? 4096 / D : 128; }
@@ -1210,48 +1209,52 @@ __global__ __launch_bounds__(256) void sort_fill_kernel(SortParams sp) {
 }
 
 // One workgroup of 256 threads per (bin, token range) (grid: B * H x maxch; those past the (b, h)'s count return at
-// once). NG = 256 / D lane groups, lane d of a group owning column d; group grp owns the range's tokens grp,
-// grp + NG, ... (TPG = TB / NG of them at most, summed in registers). Rounds of kSortChunk of the bin's entries: loaded
-// 4 a thread (all in flight), those in the range ranked by token (integer LDS atomics) and written to LDS in token
-// order; then steps of CH = kSortProd / D sorted entries: group grp computes the products of entries grp * 16 .. + 15
-// of the step into LDS, and each owner adds up the part of its tokens' runs that lies in the step.
+// once); the range's width x D float sums in LDS. A grad_out row is loaded by LPR = D / 4 lanes, 4 elements (8 bytes)
+// each; the NG = 256 / LPR lane groups each own the range's tokens r with r % NG == grp (tokens of a neighbourhood go
+// to different groups). Rounds of kSortChunk of the bin's entries: loaded 4 a thread (all in flight), those in the
+// range ranked (integer LDS atomics) by the key (r % NG) * tpg + r / NG and written to LDS in key order, so that each
+// group's entries lie together, token by token; then each group streams through its own entries, 16 grad_out rows in
+// flight per lane, adding each product into its tokens' LDS sums (no other group writes them, so plain LDS
+// read-modify-writes). The sums are written once, in the element type.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void sort_reduce_kernel(SortParams sp) {
-    constexpr int NTH = 256, NG = NTH / D, TB = sort_bin_tokens(D), TPG = TB / NG, CH = kSortProd / D, EPG = CH / NG;
+    constexpr int NTH = 256, VL = 4, LPR = D / VL, NG = NTH / LPR, TB = sort_bin_tokens(D), U = 16;
     constexpr int PER = kSortChunk / NTH;
-    static_assert(EPG == 16 && TPG >= 1 && TB <= 128 && D >= 8, "reduce shape");
+    using IO = VecIO<T, VL>;
+    static_assert(D >= 8 && TB <= 128 && NG <= TB, "reduce shape");
     const int bh = blockIdx.x / sp.maxch, c = blockIdx.x - bh * sp.maxch;
     if (c >= sp.nch[bh]) return;  // uniform: before any barrier
     const Geom& g = sp.g;
     const int HD = g.H * D;
     const int b = bh / g.H, h = bh - b * g.H;
-    const int tid = threadIdx.x, d = tid & (D - 1), grp = tid / D, wave = tid >> 6, lane = tid & (kWave - 1);
-    __shared__ float prod[kSortProd];
+    const int tid = threadIdx.x, q = tid & (LPR - 1), grp = tid / LPR, wave = tid >> 6, lane = tid & (kWave - 1);
+    __shared__ __attribute__((aligned(16))) float accl[TB * D];
     __shared__ uint2 sorted[kSortChunk];
     __shared__ int cnt[TB], base[TB], wtot[2];
     const unsigned code = sp.chunk_bin[static_cast<int64_t>(bh) * sp.maxch + c];
-    const int bin = static_cast<int>(code & 0x1fffu), width = TB >> (code >> 20), lo = static_cast<int>((code >> 13) & 0x7fu) * width;
+    const int bin = static_cast<int>(code & 0x1fffu), width = TB >> (code >> 20);
+    const int lo = static_cast<int>((code >> 13) & 0x7fu) * width;
+    const int tpg = width >= NG ? width / NG : 1;  // keys per group (width and NG are powers of two)
     const int* bs = sp.bin_start + static_cast<int64_t>(bh) * (sp.nb + 1);
     const int eb0 = bs[bin], eb1 = bs[bin + 1];
     const uint2* __restrict__ src = sp.entries + static_cast<int64_t>(bh) * sp.cap;
-    const T* __restrict__ go = static_cast<const T*>(sp.grad_out);
-    float acc[TPG];
-#pragma unroll
-    for (int s = 0; s < TPG; ++s) acc[s] = 0.f;
+    const T* __restrict__ go = static_cast<const T*>(sp.grad_out) + q * VL;
+    for (int i = tid; i < TB * D / 4; i += NTH) reinterpret_cast<f32x4*>(accl)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int r0 = eb0; r0 < eb1; r0 += kSortChunk) {  // uniform: every barrier is reached by the whole workgroup
         const int n = min(eb1 - r0, kSortChunk);
         uint2 ex[PER];
 #pragma unroll
         for (int u = 0; u < PER; ++u) ex[u] = src[r0 + min(tid + u * NTH, n - 1)];  // clamped: all in flight
         if (tid < TB) cnt[tid] = 0;
-        __syncthreads();  // the counts are clear
-        int rk[PER];
+        __syncthreads();  // the counts are clear (and, the first time, the sums)
+        int rk[PER], key[PER];
         bool in[PER];
 #pragma unroll
         for (int u = 0; u < PER; ++u) {
-            const int tk = static_cast<int>(ex[u].y & (TB - 1));
-            in[u] = tid + u * NTH < n && static_cast<unsigned>(tk - lo) < static_cast<unsigned>(width);
-            rk[u] = atomicAdd(&cnt[tk], in[u] ? 1 : 0);  // no branch: the four atomics in flight together
+            const int r = static_cast<int>(ex[u].y & (TB - 1)) - lo;
+            in[u] = tid + u * NTH < n && static_cast<unsigned>(r) < static_cast<unsigned>(width);
+            key[u] = in[u] ? (r & (NG - 1)) * tpg + r / NG : 0;
+            rk[u] = atomicAdd(&cnt[key[u]], in[u] ? 1 : 0);  // no branch: the four atomics in flight together
         }
         __syncthreads();  // the counts are final
         if (tid < 128) {  // the first two wavefronts, every lane active: scan of the TB counts
@@ -1262,43 +1265,45 @@ __global__ __launch_bounds__(256) void sort_reduce_kernel(SortParams sp) {
         }
         __syncthreads();
         if (tid >= kWave && tid < TB) base[tid] += wtot[0];
-        const int mt = wtot[0] + wtot[1];  // entries of the range in this round
-        __syncthreads();  // every token's start is known
+        __syncthreads();  // every key's start is known
 #pragma unroll
         for (int u = 0; u < PER; ++u)
-            if (in[u]) sorted[base[ex[u].y & (TB - 1)] + rk[u]] = ex[u];
-        __syncthreads();  // the range's entries are in token order
-        for (int s0 = 0; s0 < mt; s0 += CH) {  // uniform
-            const int m = min(CH, mt - s0);
-            {
-                float gv[EPG], cf[EPG];
+            if (in[u]) sorted[base[key[u]] + rk[u]] = ex[u];
+        __syncthreads();  // the range's entries are in key order
+        const int k0 = grp * tpg, sb = base[k0], se = base[k0 + tpg - 1] + cnt[k0 + tpg - 1];
+        for (int i0 = sb; i0 < se; i0 += U) {  // this group's entries, U at a time
+            typename IO::raw_t raw[U];
+            float cf[U];
+            int tl[U];
 #pragma unroll
-                for (int u = 0; u < EPG; ++u) {  // clamped: no branch around the loads
-                    const uint2 x = sorted[s0 + min(grp * EPG + u, m - 1)];
-                    cf[u] = __uint_as_float(x.x);
-                    gv[u] = cvt<float>(go[static_cast<int64_t>(x.y >> 7) * D + d]);
-                }
-#pragma unroll
-                for (int u = 0; u < EPG; ++u)
-                    if (grp * EPG + u < m) prod[(grp * EPG + u) * D + d] = cf[u] * gv[u];
+            for (int u = 0; u < U; ++u) {  // clamped: no branch around the loads
+                const uint2 x = sorted[min(i0 + u, se - 1)];
+                cf[u] = __uint_as_float(x.x);
+                tl[u] = static_cast<int>(x.y & (TB - 1)) - lo;
+                raw[u] = IO::load(go + static_cast<int64_t>(x.y >> 7) * D);
             }
-            __syncthreads();  // the step's products are in place
 #pragma unroll
-            for (int s = 0; s < TPG; ++s) {
-                const int tl = lo + grp + s * NG;
-                if (grp + s * NG >= width) break;
-                const int i0 = max(base[tl], s0), i1 = min(base[tl] + cnt[tl], s0 + m);
-#pragma unroll 4
-                for (int i = i0; i < i1; ++i) acc[s] += prod[(i - s0) * D + d];
+            for (int u = 0; u < U; ++u) {
+                if (i0 + u >= se) continue;  // (no break: the loop stays unrolled, its arrays in registers)
+                float v[VL];
+                IO::unpack(raw[u], v);
+                f32x4* a = reinterpret_cast<f32x4*>(accl + tl[u] * D + q * VL);
+                f32x4 s4 = *a;
+#pragma unroll
+                for (int e = 0; e < VL; ++e) s4[e] += cf[u] * v[e];
+                *a = s4;
             }
-            __syncthreads();  // the products are free for the next step
         }
+        __syncthreads();  // the entries, counts and starts are free for the next round
     }
-    T* __restrict__ out = static_cast<T*>(sp.grad_value) + static_cast<int64_t>(b) * g.N * HD + h * D + d;
-#pragma unroll
-    for (int s = 0; s < TPG; ++s) {
-        const int t = bin * TB + lo + grp + s * NG;
-        if (grp + s * NG < width && t < g.N) out[static_cast<int64_t>(t) * HD] = static_cast<T>(acc[s]);
+    __syncthreads();  // the sums are final (also where the bin has no entries)
+    T* __restrict__ out = static_cast<T*>(sp.grad_value) + static_cast<int64_t>(b) * g.N * HD + h * D;
+    for (int i = tid; i < width * LPR; i += NTH) {
+        const int tl = i / LPR, qq = i & (LPR - 1), t = bin * TB + lo + tl;
+        if (t >= g.N) continue;
+        const f32x4 s4 = reinterpret_cast<const f32x4*>(accl + tl * D)[qq];
+        const float v[VL] = {s4[0], s4[1], s4[2], s4[3]};
+        IO::store(out + static_cast<int64_t>(t) * HD + qq * VL, v);
     }
 }
 
@@ -1700,7 +1705,7 @@ int loc_attn_backward_go(const BackParams& p, hipStream_t stream) {
 }
 
 // The binned path (sort_count_kernel ... sort_reduce_kernel) for 16-bit types at decoder densities, with the location
-// and weight gradients from loc_attn_backward_kernel; grad_value (the element type) is written
+// and weight gradients from loc_attn_backward_kernel; grad_value (the element type, 8-byte aligned) is written
 // directly. Returns 1 without launching when it does not apply: too few corners to pay for its five launches, a dense
 // problem (the bucketed scatter's), a head width other than 8..64 (a power of two), more than kSortMaxBins bins or
 // 2^25 rows, scratch that does not fit in the accumulator buffer (acc_bytes), or shapes loc_attn_backward_kernel
@@ -1710,7 +1715,8 @@ constexpr int64_t kSortMinCorners = int64_t{1} << 18;
 template <typename T>
 int sample_backward_sorted(const BackParams& p, void* grad_value_t, int64_t acc_bytes, hipStream_t stream) {
     const Geom& g = p.g;
-    if (grad_value_t == nullptr || grad_value_t == p.grad_value || !is_pow2(g.D) || g.D < 8 || g.D > 64 ||
+    if (grad_value_t == nullptr || grad_value_t == p.grad_value || reinterpret_cast<uintptr_t>(grad_value_t) % 8 != 0 ||
+        !is_pow2(g.D) || g.D < 8 || g.D > 64 ||
         g.LP <= 0 || g.LP > 256 || bucket_scatter_pays(g))
         return 1;
     const int64_t rows = static_cast<int64_t>(g.B) * g.Q * g.H;
