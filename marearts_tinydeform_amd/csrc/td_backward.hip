@@ -1167,20 +1167,33 @@ __global__ __launch_bounds__(kScanTh) void sort_scan_kernel(SortParams sp) {
         bst[sp.nb] = carry;
     }
     __syncthreads();  // every bin's start is in bst
+    // the list: first the split bins' workgroups (those read several rounds of entries: the longest), then one per
+    // other bin, so that the long ones start first
     unsigned* list = sp.chunk_bin + static_cast<int64_t>(bh) * sp.maxch;
-    int ch_carry = 0;
-    for (int b0 = 0; b0 < sp.nb; b0 += kScanTh) {  // uniform
+    int nsplit = 0;
+    for (int b0 = 0; b0 < sp.nb; b0 += kScanTh) {  // uniform: the split bins' workgroups
         const int bin = b0 + tid;
         const int cnt = bin < sp.nb ? bst[bin + 1] - bst[bin] : 0;
         int lj = 0;  // 2^lj token ranges: the fewest with at most kSortChunk entries each on average, TB at most
         while (lj < sp.tb_shift && (cnt >> lj) > kSortChunk) ++lj;
-        const int nk = bin < sp.nb ? 1 << lj : 0;
+        const int nk = lj > 0 ? 1 << lj : 0;
         int tn;
-        const int fn = ch_carry + block_excl_scan(nk, wtot, wave, lane, tn);
+        const int fn = nsplit + block_excl_scan(nk, wtot, wave, lane, tn);
         for (int k = 0; k < nk; ++k)
             list[fn + k] = static_cast<unsigned>(bin) | static_cast<unsigned>(k) << 13 | static_cast<unsigned>(lj) << 20;
-        ch_carry += tn;
+        nsplit += tn;
         __syncthreads();  // wtot is free for the next bins
+    }
+    int ch_carry = nsplit;
+    for (int b0 = 0; b0 < sp.nb; b0 += kScanTh) {  // uniform: one workgroup per other bin
+        const int bin = b0 + tid;
+        const int cnt = bin < sp.nb ? bst[bin + 1] - bst[bin] : 0;
+        const int one = bin < sp.nb && cnt <= kSortChunk ? 1 : 0;
+        int tn;
+        const int fn = ch_carry + block_excl_scan(one, wtot, wave, lane, tn);
+        if (one) list[fn] = static_cast<unsigned>(bin);
+        ch_carry += tn;
+        __syncthreads();
     }
     if (tid == 0) sp.nch[bh] = ch_carry;
 }
@@ -1208,27 +1221,30 @@ __global__ __launch_bounds__(256) void sort_fill_kernel(SortParams sp) {
     }
 }
 
-// One workgroup of 256 threads per (bin, token range) (grid: B * H x maxch; those past the (b, h)'s count return at
-// once); the range's width x D float sums in LDS. A grad_out row is loaded by LPR = D / 4 lanes, 4 elements (8 bytes)
-// each; the NG = 256 / LPR lane groups each own the range's tokens r with r % NG == grp (tokens of a neighbourhood go
-// to different groups). Rounds of kSortChunk of the bin's entries: loaded 4 a thread (all in flight), those in the
-// range ranked (integer LDS atomics) by the key (r % NG) * tpg + r / NG and written to LDS in key order, so that each
-// group's entries lie together, token by token; then each group streams through its own entries, 16 grad_out rows in
-// flight per lane, adding each product into its tokens' LDS sums (no other group writes them, so plain LDS
-// read-modify-writes). The sums are written once, in the element type.
+// One workgroup of 256 threads per (bin, token range) (grid: maxch x B * H, chunk-major; those past the (b, h)'s
+// count return at once); the range's width x D float sums in LDS. A grad_out row is loaded by LPR = D / 4 lanes,
+// 4 elements (8 bytes) each; the NG = 256 / LPR lane groups each own the range's tokens r with r % NG == grp (tokens
+// of a neighbourhood go to different groups). Rounds of kSortChunk of the bin's entries: loaded 4 a thread (all in
+// flight; the next round's during this one), those in the range ranked (integer LDS atomics) by the key
+// (r % NG) * tpg + r / NG and written to LDS in key order, so that each group's entries lie together, token by
+// token; then each group streams through its own entries, 16 grad_out rows in flight per lane, adding each product
+// into its tokens' LDS sums (no other group writes them, so plain LDS read-modify-writes). The sums are written
+// once, in the element type.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void sort_reduce_kernel(SortParams sp) {
     constexpr int NTH = 256, VL = 4, LPR = D / VL, NG = NTH / LPR, TB = sort_bin_tokens(D), U = 16;
     constexpr int PER = kSortChunk / NTH;
     using IO = VecIO<T, VL>;
     static_assert(D >= 8 && TB <= 128 && NG <= TB, "reduce shape");
-    const int bh = blockIdx.x / sp.maxch, c = blockIdx.x - bh * sp.maxch;
+    constexpr int PITCH = D + 4;  // LDS floats per token's sums: the groups' rows start in different banks
+    const int BH = sp.g.B * sp.g.H;
+    const int c = blockIdx.x / BH, bh = blockIdx.x - c * BH;  // chunk-major: every (b, h)'s first (longest) ones first
     if (c >= sp.nch[bh]) return;  // uniform: before any barrier
     const Geom& g = sp.g;
     const int HD = g.H * D;
     const int b = bh / g.H, h = bh - b * g.H;
     const int tid = threadIdx.x, q = tid & (LPR - 1), grp = tid / LPR, wave = tid >> 6, lane = tid & (kWave - 1);
-    __shared__ __attribute__((aligned(16))) float accl[TB * D];
+    __shared__ __attribute__((aligned(16))) float accl[TB * PITCH];
     __shared__ uint2 sorted[kSortChunk];
     __shared__ int cnt[TB], base[TB], wtot[2];
     const unsigned code = sp.chunk_bin[static_cast<int64_t>(bh) * sp.maxch + c];
@@ -1239,12 +1255,15 @@ __global__ __launch_bounds__(256) void sort_reduce_kernel(SortParams sp) {
     const int eb0 = bs[bin], eb1 = bs[bin + 1];
     const uint2* __restrict__ src = sp.entries + static_cast<int64_t>(bh) * sp.cap;
     const T* __restrict__ go = static_cast<const T*>(sp.grad_out) + q * VL;
-    for (int i = tid; i < TB * D / 4; i += NTH) reinterpret_cast<f32x4*>(accl)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = tid; i < TB * PITCH / 4; i += NTH) reinterpret_cast<f32x4*>(accl)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint2 ex[PER];
+    if (eb0 < eb1) {  // uniform: the first round's entries (clamped: all in flight)
+        const int n = min(eb1 - eb0, kSortChunk);
+#pragma unroll
+        for (int u = 0; u < PER; ++u) ex[u] = src[eb0 + min(tid + u * NTH, n - 1)];
+    }
     for (int r0 = eb0; r0 < eb1; r0 += kSortChunk) {  // uniform: every barrier is reached by the whole workgroup
         const int n = min(eb1 - r0, kSortChunk);
-        uint2 ex[PER];
-#pragma unroll
-        for (int u = 0; u < PER; ++u) ex[u] = src[r0 + min(tid + u * NTH, n - 1)];  // clamped: all in flight
         if (tid < TB) cnt[tid] = 0;
         __syncthreads();  // the counts are clear (and, the first time, the sums)
         int rk[PER], key[PER];
@@ -1255,6 +1274,12 @@ __global__ __launch_bounds__(256) void sort_reduce_kernel(SortParams sp) {
             in[u] = tid + u * NTH < n && static_cast<unsigned>(r) < static_cast<unsigned>(width);
             key[u] = in[u] ? (r & (NG - 1)) * tpg + r / NG : 0;
             rk[u] = atomicAdd(&cnt[key[u]], in[u] ? 1 : 0);  // no branch: the four atomics in flight together
+        }
+        uint2 exn[PER];  // the next round's entries, loaded while this round is processed
+        if (r0 + kSortChunk < eb1) {  // uniform
+            const int nn = min(eb1 - r0 - kSortChunk, kSortChunk);
+#pragma unroll
+            for (int u = 0; u < PER; ++u) exn[u] = src[r0 + kSortChunk + min(tid + u * NTH, nn - 1)];
         }
         __syncthreads();  // the counts are final
         if (tid < 128) {  // the first two wavefronts, every lane active: scan of the TB counts
@@ -1287,7 +1312,7 @@ __global__ __launch_bounds__(256) void sort_reduce_kernel(SortParams sp) {
                 if (i0 + u >= se) continue;  // (no break: the loop stays unrolled, its arrays in registers)
                 float v[VL];
                 IO::unpack(raw[u], v);
-                f32x4* a = reinterpret_cast<f32x4*>(accl + tl[u] * D + q * VL);
+                f32x4* a = reinterpret_cast<f32x4*>(accl + tl[u] * PITCH + q * VL);
                 f32x4 s4 = *a;
 #pragma unroll
                 for (int e = 0; e < VL; ++e) s4[e] += cf[u] * v[e];
@@ -1295,13 +1320,15 @@ __global__ __launch_bounds__(256) void sort_reduce_kernel(SortParams sp) {
             }
         }
         __syncthreads();  // the entries, counts and starts are free for the next round
+#pragma unroll
+        for (int u = 0; u < PER; ++u) ex[u] = exn[u];
     }
     __syncthreads();  // the sums are final (also where the bin has no entries)
     T* __restrict__ out = static_cast<T*>(sp.grad_value) + static_cast<int64_t>(b) * g.N * HD + h * D;
     for (int i = tid; i < width * LPR; i += NTH) {
         const int tl = i / LPR, qq = i & (LPR - 1), t = bin * TB + lo + tl;
         if (t >= g.N) continue;
-        const f32x4 s4 = reinterpret_cast<const f32x4*>(accl + tl * D)[qq];
+        const f32x4 s4 = reinterpret_cast<const f32x4*>(accl + tl * PITCH)[qq];
         const float v[VL] = {s4[0], s4[1], s4[2], s4[3]};
         IO::store(out + static_cast<int64_t>(t) * HD + qq * VL, v);
     }
