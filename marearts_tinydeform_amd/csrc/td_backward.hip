@@ -1004,28 +1004,32 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(6))) void s
 // (decoders: 2-4 per token and head) the atomic scatter runs at the GPU's float-atomic rate (about 320 G lane-adds/s,
 // one 128-byte line per corner at D = 32) and needs a zeroed float32 accumulator and a rounding pass. LDS float
 // atomics are no way out: ds_add_f32 runs at about 0.33 lanes per clock per CU (about 200 G lane-adds/s over the GPU,
-// whatever the bank pattern), against about 13 for integer LDS atomics. Instead, per (image b, head h), with bins of
-// TB consecutive tokens (TB = 128, 64 at D = 64):
+// whatever the bank pattern), against about 13 for integer LDS atomics. Instead, per (image b, head h):
+//   * bins: level l's tokens go in bins of 2^shift_l consecutive tokens, the widest power of two from the minimum
+//     (8 or more, chosen on the host so that the bins fit) to TB (128; 64 at D = 64) whose bin expects at most
+//     kSortTarget entries (4 Q P_l corners over the level's n_l tokens): the small, densely sampled levels get narrow
+//     bins (sort_levels, from the device-resident level shapes);
 //   * sort_count_kernel: each query tile counts its corners into the bins (LDS counters);
 //   * sort_scan_kernel: one workgroup per (b, h) scans the counts, bin-major, into each tile's start within each bin
-//     and each bin's start; then it gives every bin j = 1, 2, 4 ... workgroups, enough that each of the bin's j token
-//     ranges (TB / j tokens) averages at most kSortChunk entries, and lists them;
-//   * sort_fill_kernel: each tile writes its corners as entries {a * w_c, row << 7 | token % TB} into their bins
-//     (ranks within the tile from LDS atomics);
-//   * sort_reduce_kernel: one workgroup per (bin, token range) reads the bin's entries kSortChunk at a time and sorts
-//     those of its range in LDS (a counting sort: integer LDS atomics for the ranks) so that each lane group's
-//     tokens' entries lie together; each group then streams through its entries, 16 grad_out rows in flight per
-//     lane, adding the products a * w_c * g_row into its own tokens' float sums in LDS; finally the workgroup writes
-//     its tokens' rows, in the element type. The small levels' bins (many corners on few tokens) are so split over
-//     several workgroups, each reading the whole bin's entries (8 bytes each) but loading only its own grad_out rows.
+//     and each bin's start; then it lists the reduce items: one per bin, or, for a bin above kSortChunk entries (a
+//     hot spot), 2^j token ranges, the fewest averaging at most kSortChunk entries each;
+//   * sort_fill_kernel: each tile writes its corners as entries {a * w_c, row << 7 | position in the bin} into their
+//     bins (ranks within the tile from LDS atomics);
+//   * sort_reduce_kernel: one workgroup per item reads its bin's entries kSortChunk at a time and sorts those of its
+//     range in LDS (a counting sort: integer LDS atomics for the ranks) so that each lane group's tokens' entries lie
+//     together; each group then streams through its entries, 16 grad_out rows in flight per lane, adding the products
+//     a * w_c * g_row into its own tokens' float sums in LDS; finally the workgroup writes its tokens' rows, in the
+//     element type.
 // No float atomics, no zero fill, no rounding pass. Within a token the products are added in the order the LDS ranks
-// give, so the result agrees with the atomic scatter's to float rounding. The scratch (entries, counts, starts,
-// workgroup list) lives in the caller's float32 accumulator buffer. grad_loc and grad_attn come from
+// give, so the result agrees with the atomic scatter's to float rounding. The scratch (entries, items, counts,
+// starts) lives in the caller's float32 accumulator buffer. grad_loc and grad_attn come from
 // loc_attn_backward_kernel.
-constexpr int kSortMaxBins = 8192;  // bins per (b, h) at most (the tiles' LDS counters; 13 bits of a chunk code)
+constexpr int kSortMaxBins = 8192;  // bins per (b, h) at most (the tiles' LDS counters)
 constexpr int kSortChunk = 1024;    // entries per token range on average at most; entries read per round
+constexpr int kSortTarget = 512;    // expected entries per bin at most (where the bin can be that narrow)
 
-// tokens per bin at head width D: TB x D floats = 16 KB (128 at most: the entry keeps token % TB in 7 bits)
+// tokens per bin at most at head width D: TB x D floats = 16 KB (128 at most: an entry keeps its position in the
+// bin in 7 bits)
 __host__ __device__ constexpr int sort_bin_tokens(int D) { return D >= 64 ? 4096 / D : 128; }
 
 struct SortParams {
@@ -1034,22 +1038,79 @@ struct SortParams {
     const void* grad_out;
     void* grad_value;  // [B, N, H * D] element type
     Geom g;
-    int QT, qtiles, nb;   // queries per tile (256 / (L * P)), tiles per (b, h), bins per (b, h)
-    int tb_shift;         // log2 of the tokens per bin
-    int maxch;            // reduce workgroups per (b, h) at most
+    int QT, qtiles;       // queries per tile (256 / (L * P)), tiles per (b, h)
+    int nb;               // bins per (b, h) at most (the levels' bins, computed on the device, are clamped to it)
+    int tb_shift;         // log2 of the tokens per bin at most
+    int min_shift;        // log2 of the tokens per bin at least
+    int maxch;            // reduce items per (b, h) at most
     int64_t cap;          // entries per (b, h) at most: Q * L * P * 4
     int* hist;            // [B * H][nb][qtiles]: counts, then each tile's start within its bin
-    int* bin_start;       // [B * H][nb + 1]: start of each bin within the (b, h) region of entries
-    unsigned* chunk_bin;  // [B * H][maxch]: bin | range << 13 | log2(ranges) << 20 of each reduce workgroup
-    int* nch;             // [B * H]: reduce workgroups of the (b, h)
+    uint4* items;         // [B * H * maxch]: the reduce items of every (b, h) (sort_item)
+    int* counters;        // [1]: items listed (zeroed by sort_count_kernel)
     uint2* entries;       // [B * H][cap]
     FastDiv d_lp;
 };
 
-// Thread tid of tile (bh, qt): its sample's four corners (tokens, -1 outside) and coefficients, and its row.
+// The bins of the levels: level l's tokens start[l] .. start[l] + n[l] - 1 (clamped into [0, N)) in bins of
+// 2^shift[l] tokens, numbered base[l] .. base[l + 1] - 1 (base[L] = the bins in use, at most sp.nb).
+struct SortLevels {
+    int base[kMaxLevelPoints + 1];
+    int shift[kMaxLevelPoints];
+    int start[kMaxLevelPoints];
+    int n[kMaxLevelPoints];
+};
+
+// A reduce item: bin tokens t0 .. t0 + 2^shift - 1 of (b, h) = bh, of which `tokens` exist, range k of 2^j of them;
+// its entries first .. end - 1 of the (b, h)'s. t0 < 2^20 (N / 2^min_shift + L bins of at most 128 tokens stay within
+// kSortMaxBins), bh < 2^23 (checked on the host).
+struct SortItem {
+    int t0, bh, first, end, shift, j, k, tokens;
+};
+__host__ __device__ inline uint4 sort_item_pack(const SortItem& i) {
+    return make_uint4(static_cast<unsigned>(i.t0) | static_cast<unsigned>(i.bh & 0xfff) << 20,
+                      static_cast<unsigned>(i.first), static_cast<unsigned>(i.end),
+                      static_cast<unsigned>(i.shift | i.j << 3 | i.k << 6 | i.tokens << 13 | (i.bh >> 12) << 21));
+}
+__device__ inline SortItem sort_item_unpack(const uint4& u) {
+    SortItem i;
+    i.t0 = static_cast<int>(u.x & 0xfffffu);
+    i.bh = static_cast<int>(u.x >> 20 | (u.w >> 21) << 12);
+    i.first = static_cast<int>(u.y);
+    i.end = static_cast<int>(u.z);
+    i.shift = static_cast<int>(u.w & 7u);
+    i.j = static_cast<int>((u.w >> 3) & 7u);
+    i.k = static_cast<int>((u.w >> 6) & 0x7fu);
+    i.tokens = static_cast<int>((u.w >> 13) & 0xffu);
+    return i;
+}
+
+// Fills lv; called by a whole wavefront (every lane active), the caller's barrier publishes it.
+__device__ void sort_levels(const SortParams& sp, SortLevels& lv) {
+    const Geom& g = sp.g;
+    const int l = lane_id();
+    int nbins = 0;
+    if (l < g.L) {
+        const int64_t st = g.starts[l], n64 = g.shapes[2 * l] * g.shapes[2 * l + 1];
+        const int64_t s0 = st < 0 ? 0 : (st > g.N ? g.N : st);
+        const int64_t n = n64 < 0 ? 0 : (n64 > g.N - s0 ? g.N - s0 : n64);
+        const int pl = g.P > 0 ? g.P : g.level_end[l] - (l > 0 ? g.level_end[l - 1] : 0);
+        const int64_t corners = int64_t{4} * g.Q * pl;
+        int shift = sp.min_shift;
+        while (shift < sp.tb_shift && (corners << (shift + 1)) <= int64_t{kSortTarget} * n) ++shift;
+        nbins = static_cast<int>((n + (int64_t{1} << shift) - 1) >> shift);
+        lv.shift[l] = shift;
+        lv.start[l] = static_cast<int>(s0);
+        lv.n[l] = static_cast<int>(n);
+    }
+    const int incl = wave_incl_scan(nbins);
+    if (l < g.L) lv.base[l + 1] = min(incl, sp.nb);
+    if (l == 0) lv.base[0] = 0;
+}
+
+// Thread tid of tile (bh, qt): its sample's four corners (tokens, -1 outside) and coefficients, its level and row.
 template <typename T>
 __device__ __forceinline__ bool sort_sample(const SortParams& sp, int bh, int qt, int tid, int (&tk)[4],
-                                            float (&cf)[4], int& row) {
+                                            float (&cf)[4], int& lev, int& row) {
     const Geom& g = sp.g;
     if (tid >= sp.QT * g.LP) return false;
     const int r = static_cast<int>(fast_div(sp.d_lp, static_cast<uint32_t>(tid))), j = tid - r * g.LP;
@@ -1068,7 +1129,8 @@ __device__ __forceinline__ bool sort_sample(const SortParams& sp, int bh, int qt
         ly = cvt<float>(static_cast<const T*>(sp.loc)[2 * idx + 1]);
         a = cvt<float>(static_cast<const T*>(sp.attn)[idx]);
     }
-    const Taps<float> t = taps_at_b<float>(lx, ly, level_of(g, j), g, b);
+    lev = level_of(g, j);
+    const Taps<float> t = taps_at_b<float>(lx, ly, lev, g, b);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         tk[k] = t.tok[k];
@@ -1077,29 +1139,44 @@ __device__ __forceinline__ bool sort_sample(const SortParams& sp, int bh, int qt
     return true;
 }
 
+// The bin of token tk of level l and its position in the bin (-1 for a token outside the level's clamped range)
+__device__ __forceinline__ int sort_bin_of(const SortLevels& lv, int l, int tk, int& pos) {
+    const int rel = tk - lv.start[l];
+    if (static_cast<unsigned>(rel) >= static_cast<unsigned>(lv.n[l])) return -1;
+    const int bin = lv.base[l] + (rel >> lv.shift[l]);
+    pos = rel & ((1 << lv.shift[l]) - 1);
+    return bin < lv.base[l + 1] ? bin : -1;
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void sort_count_kernel(SortParams sp) {
     extern __shared__ int lc[];  // [nb]
+    __shared__ SortLevels lv;
     const int bh = blockIdx.x / sp.qtiles, qt = blockIdx.x - bh * sp.qtiles;
+    if (blockIdx.x == 0 && threadIdx.x == 0) sp.counters[0] = 0;  // for sort_scan_kernel's reservations
+    if (threadIdx.x < kWave) sort_levels(sp, lv);
     for (int i = threadIdx.x; i < sp.nb; i += 256) lc[i] = 0;
     __syncthreads();
-    int tk[4], row;
+    const int nb = lv.base[sp.g.L];
+    int tk[4], lev, row;
     float cf[4];
-    if (sort_sample<T>(sp, bh, qt, threadIdx.x, tk, cf, row)) {
+    if (sort_sample<T>(sp, bh, qt, threadIdx.x, tk, cf, lev, row)) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-            if (tk[k] >= 0) atomicAdd(&lc[tk[k] >> sp.tb_shift], 1);
+        for (int k = 0; k < 4; ++k) {
+            int pos;
+            const int bin = tk[k] >= 0 ? sort_bin_of(lv, lev, tk[k], pos) : -1;
+            if (bin >= 0) atomicAdd(&lc[bin], 1);
+        }
     }
     __syncthreads();
     int* hist = sp.hist + static_cast<int64_t>(bh) * sp.nb * sp.qtiles;
-    for (int i = threadIdx.x; i < sp.nb; i += 256) hist[static_cast<int64_t>(i) * sp.qtiles + qt] = lc[i];
+    for (int i = threadIdx.x; i < nb; i += 256) hist[static_cast<int64_t>(i) * sp.qtiles + qt] = lc[i];
 }
 
 // One workgroup per (b, h). First the exclusive scan of the nb * qtiles counts (bin-major) in chunks of 4096, each
 // loaded into LDS with coalesced reads, thread t owning 8 consecutive counts (LDS pitch 9 words: the owners' reads
 // spread over the banks), a wavefront scan of the owners' totals, and coalesced writes back; the bins' starts are the
-// scanned values at the bins' first counts (kept in LDS too, bst). Then, 512 bins at a time, each bin's number of
-// token ranges (a block scan gives their places in the list) and the list of reduce workgroups.
+// scanned values at the bins' first counts (kept in LDS, bst). Then the reduce items of the (b, h)'s bins.
 constexpr int kScanTh = 512, kScanK = 8, kScanChunk = kScanTh * kScanK;
 
 __device__ __forceinline__ int block_excl_scan(int x, int* wt, int wave, int lane, int& total) {
@@ -1120,11 +1197,14 @@ __device__ __forceinline__ int block_excl_scan(int x, int* wt, int wave, int lan
 __global__ __launch_bounds__(kScanTh) void sort_scan_kernel(SortParams sp) {
     __shared__ int v[kScanTh * (kScanK + 1)];
     __shared__ int wtot[kScanTh / kWave];
+    __shared__ SortLevels lv;
     extern __shared__ int bst[];  // [nb + 1]: the bins' starts
     const int bh = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
+    if (tid < kWave) sort_levels(sp, lv);
+    __syncthreads();
+    const int nb = lv.base[sp.g.L];
     int* hist = sp.hist + static_cast<int64_t>(bh) * sp.nb * sp.qtiles;
-    int* bs = sp.bin_start + static_cast<int64_t>(bh) * (sp.nb + 1);
-    const int n = sp.nb * sp.qtiles;  // < 2^30 (checked on the host)
+    const int n = nb * sp.qtiles;  // < 2^30 (checked on the host)
     int* mine = v + tid * (kScanK + 1);
     int carry = 0;
     for (int c0 = 0; c0 < n; c0 += kScanChunk) {  // uniform: every barrier is reached by the whole workgroup
@@ -1155,183 +1235,236 @@ __global__ __launch_bounds__(kScanTh) void sort_scan_kernel(SortParams sp) {
         for (int bb = (c0 + sp.qtiles - 1) / sp.qtiles + tid; static_cast<int64_t>(bb) * sp.qtiles < c0 + len;
              bb += kScanTh) {
             const int j = bb * sp.qtiles - c0;
-            const int st = v[(j / kScanK) * (kScanK + 1) + j % kScanK];
-            bs[bb] = st;
-            bst[bb] = st;
+            bst[bb] = v[(j / kScanK) * (kScanK + 1) + j % kScanK];
         }
         carry += tot;
         __syncthreads();  // v and wtot are free for the next chunk
     }
-    if (tid == 0) {
-        bs[sp.nb] = carry;
-        bst[sp.nb] = carry;
-    }
+    if (tid == 0) bst[nb] = carry;
     __syncthreads();  // every bin's start is in bst
-    // the list: first the split bins' workgroups (those read several rounds of entries: the longest), then one per
-    // other bin, so that the long ones start first
-    unsigned* list = sp.chunk_bin + static_cast<int64_t>(bh) * sp.maxch;
-    int nsplit = 0;
-    for (int b0 = 0; b0 < sp.nb; b0 += kScanTh) {  // uniform: the split bins' workgroups
+    // the items: one per bin, or 2^lj token ranges of a bin above kSortChunk entries (the fewest averaging at most
+    // kSortChunk entries each), the split ones first (they read several rounds of entries: the longest); the (b, h)
+    // reserves its places in the list with one atomic
+    auto level_of_bin = [&](int bin) {
+        int l = 0;
+        while (l + 1 < sp.g.L && bin >= lv.base[l + 1]) ++l;
+        return l;
+    };
+    auto split_of = [&](int bin, int l) {
+        const int cnt = bst[bin + 1] - bst[bin];
+        int lj = 0;
+        while (lj < lv.shift[l] && (cnt >> lj) > kSortChunk) ++lj;
+        return lj;
+    };
+    int own_split = 0, own_other = 0;
+    for (int bin = tid; bin < nb; bin += kScanTh) {
+        const int lj = split_of(bin, level_of_bin(bin));
+        own_split += lj > 0 ? 1 << lj : 0;
+        own_other += lj > 0 ? 0 : 1;
+    }
+    __shared__ int place;
+    int tot_split, tot_other;
+    block_excl_scan(own_split, wtot, wave, lane, tot_split);
+    __syncthreads();  // wtot is free
+    block_excl_scan(own_other, wtot, wave, lane, tot_other);
+    if (tid == 0) place = atomicAdd(sp.counters, tot_split + tot_other);
+    __syncthreads();  // the place is known; wtot is free
+    uint4* list = sp.items + place;
+    int run_split = 0, run_other = tot_split;
+    for (int b0 = 0; b0 < nb; b0 += kScanTh) {  // uniform
         const int bin = b0 + tid;
-        const int cnt = bin < sp.nb ? bst[bin + 1] - bst[bin] : 0;
-        int lj = 0;  // 2^lj token ranges: the fewest with at most kSortChunk entries each on average, TB at most
-        while (lj < sp.tb_shift && (cnt >> lj) > kSortChunk) ++lj;
-        const int nk = lj > 0 ? 1 << lj : 0;
-        int tn;
-        const int fn = nsplit + block_excl_scan(nk, wtot, wave, lane, tn);
-        for (int k = 0; k < nk; ++k)
-            list[fn + k] = static_cast<unsigned>(bin) | static_cast<unsigned>(k) << 13 | static_cast<unsigned>(lj) << 20;
-        nsplit += tn;
+        const int l = bin < nb ? level_of_bin(bin) : 0, lj = bin < nb ? split_of(bin, l) : 0;
+        const int nk = bin < nb && lj > 0 ? 1 << lj : 0, one = bin < nb && lj == 0 ? 1 : 0;
+        int tn, to;
+        const int fn = run_split + block_excl_scan(nk, wtot, wave, lane, tn);
+        __syncthreads();  // wtot is free
+        const int fo = run_other + block_excl_scan(one, wtot, wave, lane, to);
+        if (bin < nb) {
+            SortItem it;
+            it.bh = bh;
+            it.shift = lv.shift[l];
+            const int off = (bin - lv.base[l]) << it.shift;
+            it.t0 = lv.start[l] + off;
+            it.tokens = min(1 << it.shift, lv.n[l] - off);
+            it.first = bst[bin];
+            it.end = bst[bin + 1];
+            it.j = lj;
+            for (int k = 0; k < (lj > 0 ? 1 << lj : 1); ++k) {
+                it.k = k;
+                list[lj > 0 ? fn + k : fo] = sort_item_pack(it);
+            }
+        }
+        run_split += tn;
+        run_other += to;
         __syncthreads();  // wtot is free for the next bins
     }
-    int ch_carry = nsplit;
-    for (int b0 = 0; b0 < sp.nb; b0 += kScanTh) {  // uniform: one workgroup per other bin
-        const int bin = b0 + tid;
-        const int cnt = bin < sp.nb ? bst[bin + 1] - bst[bin] : 0;
-        const int one = bin < sp.nb && cnt <= kSortChunk ? 1 : 0;
-        int tn;
-        const int fn = ch_carry + block_excl_scan(one, wtot, wave, lane, tn);
-        if (one) list[fn] = static_cast<unsigned>(bin);
-        ch_carry += tn;
-        __syncthreads();
-    }
-    if (tid == 0) sp.nch[bh] = ch_carry;
 }
 
 template <typename T>
 __global__ __launch_bounds__(256) void sort_fill_kernel(SortParams sp) {
     extern __shared__ int lc[];  // [nb]: this tile's running rank per bin
+    __shared__ SortLevels lv;
     const int bh = blockIdx.x / sp.qtiles, qt = blockIdx.x - bh * sp.qtiles;
+    if (threadIdx.x < kWave) sort_levels(sp, lv);
     for (int i = threadIdx.x; i < sp.nb; i += 256) lc[i] = 0;
     __syncthreads();
-    int tk[4], row;
+    int tk[4], lev, row;
     float cf[4];
-    if (sort_sample<T>(sp, bh, qt, threadIdx.x, tk, cf, row)) {
+    if (sort_sample<T>(sp, bh, qt, threadIdx.x, tk, cf, lev, row)) {
         const int* off = sp.hist + static_cast<int64_t>(bh) * sp.nb * sp.qtiles + qt;
         uint2* ent = sp.entries + static_cast<int64_t>(bh) * sp.cap;
-        const int tmask = (1 << sp.tb_shift) - 1;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            if (tk[k] < 0) continue;
-            const int bin = tk[k] >> sp.tb_shift;
+            int pos;
+            const int bin = tk[k] >= 0 ? sort_bin_of(lv, lev, tk[k], pos) : -1;
+            if (bin < 0) continue;
             const int rank = atomicAdd(&lc[bin], 1);
             ent[off[static_cast<int64_t>(bin) * sp.qtiles] + rank] =
-                make_uint2(__float_as_uint(cf[k]), static_cast<unsigned>(row) << 7 | static_cast<unsigned>(tk[k] & tmask));
+                make_uint2(__float_as_uint(cf[k]), static_cast<unsigned>(row) << 7 | static_cast<unsigned>(pos));
         }
     }
 }
 
-// One workgroup of 256 threads per (bin, token range) (grid: maxch x B * H, chunk-major; those past the (b, h)'s
-// count return at once); the range's width x D float sums in LDS. A grad_out row is loaded by LPR = D / 4 lanes,
-// 4 elements (8 bytes) each; the NG = 256 / LPR lane groups each own the range's tokens r with r % NG == grp (tokens
-// of a neighbourhood go to different groups). Rounds of kSortChunk of the bin's entries: loaded 4 a thread (all in
-// flight; the next round's during this one), those in the range ranked (integer LDS atomics) by the key
-// (r % NG) * tpg + r / NG and written to LDS in key order, so that each group's entries lie together, token by
-// token; then each group streams through its own entries, 16 grad_out rows in flight per lane, adding each product
-// into its tokens' LDS sums (no other group writes them, so plain LDS read-modify-writes). The sums are written
-// once, in the element type.
+// Persistent: workgroup w of G (the GPU's resident count) takes items w, w + G, ... of the list (the split bins'
+// items, the longest, first in each (b, h)'s part); each item's width x D float sums in LDS. A grad_out row is loaded
+// by LPR = D / 4 lanes, 4 elements (8 bytes) each; the NG = 256 / LPR lane groups each own the item's tokens r with
+// r % NG == grp (tokens of a neighbourhood go to different groups). Rounds of kSortChunk of the bin's entries, loaded
+// 4 a thread: those in the range ranked (integer LDS atomics) by the key (r % NG) * tpg + r / NG and written to LDS in
+// key order, so that each group's entries lie together, token by token; then each group streams through its own
+// entries, 16 grad_out rows in flight per lane, adding each product into its tokens' LDS sums (no other group writes
+// them, so plain LDS read-modify-writes). The sums are written once, in the element type. The next item is read an
+// item ahead, and the next round's entries (of this item or the next) during this round, so that the loads a
+// workgroup waits on are the grad_out rows alone.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void sort_reduce_kernel(SortParams sp) {
     constexpr int NTH = 256, VL = 4, LPR = D / VL, NG = NTH / LPR, TB = sort_bin_tokens(D), U = 16;
     constexpr int PER = kSortChunk / NTH;
+    constexpr int PITCH = D + 4;  // LDS floats per token's sums: the groups' rows start in different banks
     using IO = VecIO<T, VL>;
     static_assert(D >= 8 && TB <= 128 && NG <= TB, "reduce shape");
-    constexpr int PITCH = D + 4;  // LDS floats per token's sums: the groups' rows start in different banks
-    const int BH = sp.g.B * sp.g.H;
-    const int c = blockIdx.x / BH, bh = blockIdx.x - c * BH;  // chunk-major: every (b, h)'s first (longest) ones first
-    if (c >= sp.nch[bh]) return;  // uniform: before any barrier
     const Geom& g = sp.g;
     const int HD = g.H * D;
-    const int b = bh / g.H, h = bh - b * g.H;
     const int tid = threadIdx.x, q = tid & (LPR - 1), grp = tid / LPR, wave = tid >> 6, lane = tid & (kWave - 1);
+    const int total = sp.counters[0];
+    int gi = static_cast<int>(blockIdx.x);
+    if (gi >= total) return;  // uniform: before any barrier
     __shared__ __attribute__((aligned(16))) float accl[TB * PITCH];
     __shared__ uint2 sorted[kSortChunk];
     __shared__ int cnt[TB], base[TB], wtot[2];
-    const unsigned code = sp.chunk_bin[static_cast<int64_t>(bh) * sp.maxch + c];
-    const int bin = static_cast<int>(code & 0x1fffu), width = TB >> (code >> 20);
-    const int lo = static_cast<int>((code >> 13) & 0x7fu) * width;
-    const int tpg = width >= NG ? width / NG : 1;  // keys per group (width and NG are powers of two)
-    const int* bs = sp.bin_start + static_cast<int64_t>(bh) * (sp.nb + 1);
-    const int eb0 = bs[bin], eb1 = bs[bin + 1];
-    const uint2* __restrict__ src = sp.entries + static_cast<int64_t>(bh) * sp.cap;
-    const T* __restrict__ go = static_cast<const T*>(sp.grad_out) + q * VL;
     for (int i = tid; i < TB * PITCH / 4; i += NTH) reinterpret_cast<f32x4*>(accl)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // a round's entries, 4 a thread at clamped indexes (no branch: all in flight); n >= 1
+    auto load_round = [&](uint2 (&e)[PER], int bh, int r0, int n) {
+        const uint2* __restrict__ src = sp.entries + static_cast<int64_t>(bh) * sp.cap + r0;
+#pragma unroll
+        for (int u = 0; u < PER; ++u) e[u] = src[min(tid + u * NTH, n - 1)];
+    };
+    SortItem it = sort_item_unpack(sp.items[gi]);
     uint2 ex[PER];
-    if (eb0 < eb1) {  // uniform: the first round's entries (clamped: all in flight)
-        const int n = min(eb1 - eb0, kSortChunk);
+    if (it.first < it.end) load_round(ex, it.bh, it.first, min(it.end - it.first, kSortChunk));
+    while (true) {  // uniform: one item per pass
+        const int gn = gi + static_cast<int>(gridDim.x);
+        const SortItem itn = sort_item_unpack(sp.items[min(gn, total - 1)]);  // the next item (clamped: no branch)
+        const int width = (1 << it.shift) >> it.j, lo = it.k * width;
+        const int tpg = width >= NG ? width / NG : 1;  // keys per group (width and NG are powers of two)
+        const T* __restrict__ go = static_cast<const T*>(sp.grad_out) + q * VL;
+        bool next_loaded = false;
+        for (int r0 = it.first; r0 < it.end; r0 += kSortChunk) {  // uniform: every barrier is reached by all
+            const int n = min(it.end - r0, kSortChunk);
+            if (tid < TB) cnt[tid] = 0;
+            __syncthreads();  // the counts are clear (and the sums, after the previous item's write)
+            int rk[PER], key[PER];
+            bool in[PER];
 #pragma unroll
-        for (int u = 0; u < PER; ++u) ex[u] = src[eb0 + min(tid + u * NTH, n - 1)];
-    }
-    for (int r0 = eb0; r0 < eb1; r0 += kSortChunk) {  // uniform: every barrier is reached by the whole workgroup
-        const int n = min(eb1 - r0, kSortChunk);
-        if (tid < TB) cnt[tid] = 0;
-        __syncthreads();  // the counts are clear (and, the first time, the sums)
-        int rk[PER], key[PER];
-        bool in[PER];
-#pragma unroll
-        for (int u = 0; u < PER; ++u) {
-            const int r = static_cast<int>(ex[u].y & (TB - 1)) - lo;
-            in[u] = tid + u * NTH < n && static_cast<unsigned>(r) < static_cast<unsigned>(width);
-            key[u] = in[u] ? (r & (NG - 1)) * tpg + r / NG : 0;
-            rk[u] = atomicAdd(&cnt[key[u]], in[u] ? 1 : 0);  // no branch: the four atomics in flight together
-        }
-        uint2 exn[PER];  // the next round's entries, loaded while this round is processed
-        if (r0 + kSortChunk < eb1) {  // uniform
-            const int nn = min(eb1 - r0 - kSortChunk, kSortChunk);
-#pragma unroll
-            for (int u = 0; u < PER; ++u) exn[u] = src[r0 + kSortChunk + min(tid + u * NTH, nn - 1)];
-        }
-        __syncthreads();  // the counts are final
-        if (tid < 128) {  // the first two wavefronts, every lane active: scan of the TB counts
-            const int cv = tid < TB ? cnt[tid] : 0;
-            const int incl = wave_incl_scan(cv);
-            if (lane == kWave - 1) wtot[wave] = incl;
-            if (tid < TB) base[tid] = incl - cv;
-        }
-        __syncthreads();
-        if (tid >= kWave && tid < TB) base[tid] += wtot[0];
-        __syncthreads();  // every key's start is known
-#pragma unroll
-        for (int u = 0; u < PER; ++u)
-            if (in[u]) sorted[base[key[u]] + rk[u]] = ex[u];
-        __syncthreads();  // the range's entries are in key order
-        const int k0 = grp * tpg, sb = base[k0], se = base[k0 + tpg - 1] + cnt[k0 + tpg - 1];
-        for (int i0 = sb; i0 < se; i0 += U) {  // this group's entries, U at a time
-            typename IO::raw_t raw[U];
-            float cf[U];
-            int tl[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {  // clamped: no branch around the loads
-                const uint2 x = sorted[min(i0 + u, se - 1)];
-                cf[u] = __uint_as_float(x.x);
-                tl[u] = static_cast<int>(x.y & (TB - 1)) - lo;
-                raw[u] = IO::load(go + static_cast<int64_t>(x.y >> 7) * D);
+            for (int u = 0; u < PER; ++u) {
+                const int r = static_cast<int>(ex[u].y & 0x7fu) - lo;
+                in[u] = tid + u * NTH < n && static_cast<unsigned>(r) < static_cast<unsigned>(width);
+                key[u] = in[u] ? (r & (NG - 1)) * tpg + r / NG : 0;
+                if (in[u]) rk[u] = atomicAdd(&cnt[key[u]], 1);
             }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                if (i0 + u >= se) continue;  // (no break: the loop stays unrolled, its arrays in registers)
-                float v[VL];
-                IO::unpack(raw[u], v);
-                f32x4* a = reinterpret_cast<f32x4*>(accl + tl[u] * PITCH + q * VL);
-                f32x4 s4 = *a;
-#pragma unroll
-                for (int e = 0; e < VL; ++e) s4[e] += cf[u] * v[e];
-                *a = s4;
+            // the next round's entries: this item's, else the next item's first (else a reload of this round's)
+            uint2 exn[PER];
+            {
+                int nbh = it.bh, nr0 = r0, nn = 1;
+                if (r0 + kSortChunk < it.end) {
+                    nr0 = r0 + kSortChunk;
+                    nn = min(it.end - nr0, kSortChunk);
+                } else if (gn < total && itn.first < itn.end) {
+                    nbh = itn.bh;
+                    nr0 = itn.first;
+                    nn = min(itn.end - itn.first, kSortChunk);
+                    next_loaded = true;
+                }
+                load_round(exn, nbh, nr0, nn);
             }
-        }
-        __syncthreads();  // the entries, counts and starts are free for the next round
+            __syncthreads();  // the counts are final
+            if (tid < 128) {  // the first two wavefronts, every lane active: scan of the TB counts
+                const int cv = tid < TB ? cnt[tid] : 0;
+                const int incl = wave_incl_scan(cv);
+                if (lane == kWave - 1) wtot[wave] = incl;
+                if (tid < TB) base[tid] = incl - cv;
+            }
+            __syncthreads();
+            if (tid >= kWave && tid < TB) base[tid] += wtot[0];
+            __syncthreads();  // every key's start is known
 #pragma unroll
-        for (int u = 0; u < PER; ++u) ex[u] = exn[u];
+            for (int u = 0; u < PER; ++u)
+                if (in[u]) sorted[base[key[u]] + rk[u]] = ex[u];
+            __syncthreads();  // the range's entries are in key order
+            const int k0 = grp * tpg, sb = base[k0], se = base[k0 + tpg - 1] + cnt[k0 + tpg - 1];
+            for (int i0 = sb; i0 < se; i0 += U) {  // this group's entries, U at a time
+                typename IO::raw_t raw[U];
+                float cf[U];
+                int tl[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {  // clamped: no branch around the loads
+                    const uint2 x = sorted[min(i0 + u, se - 1)];
+                    cf[u] = __uint_as_float(x.x);
+                    tl[u] = static_cast<int>(x.y & 0x7fu) - lo;
+                    raw[u] = IO::load(go + static_cast<int64_t>(x.y >> 7) * D);
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    if (i0 + u >= se) continue;  // (no break: the loop stays unrolled, its arrays in registers)
+                    float v[VL];
+                    IO::unpack(raw[u], v);
+                    f32x4* a = reinterpret_cast<f32x4*>(accl + tl[u] * PITCH + q * VL);
+                    f32x4 s4 = *a;
+#pragma unroll
+                    for (int e = 0; e < VL; ++e) s4[e] += cf[u] * v[e];
+                    *a = s4;
+                }
+            }
+            __syncthreads();  // the sums are final for this round; the entries, counts and starts are free
+#pragma unroll
+            for (int u = 0; u < PER; ++u) ex[u] = exn[u];
+        }
+        // this item's rows, in the element type; each thread clears the sums it wrote out (the next item's first
+        // barrier orders that before any new sums, and each thread writes out the same places in every item)
+        const int b = it.bh / g.H, h = it.bh - b * g.H;
+        T* __restrict__ out = static_cast<T*>(sp.grad_value) + static_cast<int64_t>(b) * g.N * HD + h * D;
+        for (int i = tid; i < width * LPR; i += NTH) {
+            const int tl = i / LPR, qq = i & (LPR - 1);
+            f32x4* a = reinterpret_cast<f32x4*>(accl + tl * PITCH) + qq;
+            const f32x4 s4 = *a;
+            *a = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (lo + tl >= it.tokens) continue;
+            const float v[VL] = {s4[0], s4[1], s4[2], s4[3]};
+            IO::store(out + static_cast<int64_t>(it.t0 + lo + tl) * HD + qq * VL, v);
+        }
+        if (gn >= total) break;
+        gi = gn;
+        it = itn;
+        if (!next_loaded && it.first < it.end)  // uniform: no round of the last item loaded this one's entries
+            load_round(ex, it.bh, it.first, min(it.end - it.first, kSortChunk));
     }
-    __syncthreads();  // the sums are final (also where the bin has no entries)
-    T* __restrict__ out = static_cast<T*>(sp.grad_value) + static_cast<int64_t>(b) * g.N * HD + h * D;
-    for (int i = tid; i < width * LPR; i += NTH) {
-        const int tl = i / LPR, qq = i & (LPR - 1), t = bin * TB + lo + tl;
-        if (t >= g.N) continue;
-        const f32x4 s4 = reinterpret_cast<const f32x4*>(accl + tl * PITCH)[qq];
-        const float v[VL] = {s4[0], s4[1], s4[2], s4[3]};
-        IO::store(out + static_cast<int64_t>(t) * HD + qq * VL, v);
-    }
+}
+
+// resident workgroups of 256 threads of the kernel on the current device (at least the CU count)
+template <typename K>
+int resident_workgroups(K kernel) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu < 1) per_cu = 1;
+    return per_cu * cu_count();
 }
 
 template <typename T, typename A>
@@ -1743,8 +1876,8 @@ template <typename T>
 int sample_backward_sorted(const BackParams& p, void* grad_value_t, int64_t acc_bytes, hipStream_t stream) {
     const Geom& g = p.g;
     if (grad_value_t == nullptr || grad_value_t == p.grad_value || reinterpret_cast<uintptr_t>(grad_value_t) % 8 != 0 ||
-        !is_pow2(g.D) || g.D < 8 || g.D > 64 ||
-        g.LP <= 0 || g.LP > 256 || bucket_scatter_pays(g))
+        reinterpret_cast<uintptr_t>(p.grad_value) % 16 != 0 || !is_pow2(g.D) || g.D < 8 || g.D > 64 || g.LP <= 0 ||
+        g.LP > 256 || g.L > kMaxLevelPoints || bucket_scatter_pays(g))
         return 1;
     const int64_t rows = static_cast<int64_t>(g.B) * g.Q * g.H;
     if (rows * g.LP * 4 < kSortMinCorners || rows >= (int64_t{1} << 25)) return 1;
@@ -1756,28 +1889,35 @@ int sample_backward_sorted(const BackParams& p, void* grad_value_t, int64_t acc_
     sp.g = g;
     sp.QT = 256 / g.LP;
     sp.qtiles = (g.Q + sp.QT - 1) / sp.QT;
-    const int tb = sort_bin_tokens(g.D);
-    sp.tb_shift = ilog2(tb);
-    const int64_t nb = (static_cast<int64_t>(g.N) + tb - 1) / tb, BH = static_cast<int64_t>(g.B) * g.H;
+    sp.tb_shift = ilog2(sort_bin_tokens(g.D));
     sp.cap = static_cast<int64_t>(g.Q) * g.LP * 4;
-    // reduce workgroups: a bin of count entries takes j = 1 or the least power of two with count / j <= kSortChunk
-    // (so j < 2 count / kSortChunk), hence at most nb + 2 cap / kSortChunk of them per (b, h)
-    const int64_t maxch = nb + 2 * sp.cap / kSortChunk + 1;
-    if (nb > kSortMaxBins || nb * sp.qtiles >= (int64_t{1} << 30) || BH * maxch >= (int64_t{1} << 31)) return 1;
+    const int64_t BH = static_cast<int64_t>(g.B) * g.H;
+    if (sp.cap >= (int64_t{1} << 31) || BH >= (int64_t{1} << 23)) return 1;
+    // the narrowest bins (8 tokens or more) for which the bins (N / 2^min_shift + L at most: each level's last bin
+    // may be partial) stay within kSortMaxBins and the scratch (entries, items, counts, starts) fits in acc_bytes;
+    // items: one per bin, or 2^j < 2 count / kSortChunk for a split bin, so at most nb + 2 cap / kSortChunk
+    const int64_t ent_bytes = (BH * sp.cap * 8 + 15) / 16 * 16;
+    int64_t nb = 0, maxch = 0, item_bytes = 0;
+    for (sp.min_shift = 3;; ++sp.min_shift) {
+        if (sp.min_shift > sp.tb_shift) return 1;
+        nb = ((static_cast<int64_t>(g.N) >> sp.min_shift) + 1) + g.L;
+        maxch = nb + 2 * sp.cap / kSortChunk + 1;
+        item_bytes = BH * maxch * 16;
+        const int64_t ints = BH * nb * sp.qtiles + 1;
+        if (nb <= kSortMaxBins && nb * sp.qtiles < (int64_t{1} << 30) && BH * maxch < (int64_t{1} << 31) &&
+            ent_bytes + item_bytes + 4 * ints <= acc_bytes)
+            break;
+    }
     sp.nb = static_cast<int>(nb);
     sp.maxch = static_cast<int>(maxch);
-    const int64_t ent_bytes = BH * sp.cap * 8;
-    const int64_t ints = BH * nb * sp.qtiles + BH * (nb + 1) + BH * maxch + BH;
-    if (ent_bytes + 4 * ints > acc_bytes) return 1;
     // the location and weight gradients first (1: its 16-byte loads do not fit these sizes)
     const int rc = loc_attn_backward_go<T>(p, stream);
     if (rc != 0) return rc;
-    unsigned char* scratch = static_cast<unsigned char*>(p.grad_value);
+    unsigned char* scratch = static_cast<unsigned char*>(p.grad_value);  // 16-byte aligned (checked above)
     sp.entries = reinterpret_cast<uint2*>(scratch);
-    sp.hist = reinterpret_cast<int*>(scratch + ent_bytes);
-    sp.bin_start = sp.hist + BH * nb * sp.qtiles;
-    sp.chunk_bin = reinterpret_cast<unsigned*>(sp.bin_start + BH * (nb + 1));
-    sp.nch = reinterpret_cast<int*>(sp.chunk_bin + BH * maxch);
+    sp.items = reinterpret_cast<uint4*>(scratch + ent_bytes);
+    sp.hist = reinterpret_cast<int*>(scratch + ent_bytes + item_bytes);
+    sp.counters = sp.hist + BH * nb * sp.qtiles;
     sp.d_lp = make_fastdiv(static_cast<uint32_t>(g.LP));
     const unsigned tiles = static_cast<unsigned>(BH * sp.qtiles);
     const size_t lds = static_cast<size_t>(nb) * sizeof(int);
@@ -1790,12 +1930,17 @@ int sample_backward_sorted(const BackParams& p, void* grad_value_t, int64_t acc_
     hipLaunchKernelGGL(sort_fill_kernel<T>, dim3(tiles), dim3(256), lds, stream, sp);
     r2 = launched("sample backward fill");
     if (r2 != 0) return r2;
-    const dim3 rgrid(static_cast<unsigned>(BH * maxch));
+    // persistent: the resident count (at most the items' bound)
+    auto go = [&](auto kernel) {
+        static const int resident = resident_workgroups(kernel);
+        const int64_t grid = std::min<int64_t>(resident, BH * maxch);
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream, sp);
+    };
     switch (g.D) {
-        case 8: hipLaunchKernelGGL((sort_reduce_kernel<T, 8>), rgrid, dim3(256), 0, stream, sp); break;
-        case 16: hipLaunchKernelGGL((sort_reduce_kernel<T, 16>), rgrid, dim3(256), 0, stream, sp); break;
-        case 32: hipLaunchKernelGGL((sort_reduce_kernel<T, 32>), rgrid, dim3(256), 0, stream, sp); break;
-        default: hipLaunchKernelGGL((sort_reduce_kernel<T, 64>), rgrid, dim3(256), 0, stream, sp); break;
+        case 8: go(sort_reduce_kernel<T, 8>); break;
+        case 16: go(sort_reduce_kernel<T, 16>); break;
+        case 32: go(sort_reduce_kernel<T, 32>); break;
+        default: go(sort_reduce_kernel<T, 64>); break;
     }
     return launched("sample backward reduce");
 }

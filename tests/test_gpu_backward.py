@@ -197,19 +197,22 @@ def test_headline_shape_backward():
 
 
 SORT_LEVELS = {'four': [(48, 64), (24, 32), (12, 16), (6, 8)], 'wide': [(64, 80), (32, 40), (16, 20)],
-               'big': [(96, 128), (48, 64)]}
+               'big': [(96, 128), (48, 64)], 'dino': [(50, 84), (25, 42), (13, 21)]}
 
 
 @pytest.mark.parametrize('dtype,D,shape,Q', [(torch.float16, 32, 'four', 901), (torch.bfloat16, 32, 'four', 901),
                                              (torch.float16, 64, 'four', 901), (torch.bfloat16, 16, 'wide', 901),
                                              (torch.float16, 8, 'big', 600), (torch.bfloat16, 8, 'big', 700),
-                                             (torch.bfloat16, 4, 'big', 600)])
+                                             (torch.bfloat16, 4, 'big', 600), (torch.float16, 32, 'dino', 400),
+                                             (torch.bfloat16, 64, 'dino', 400)])
 @pytest.mark.parametrize('with_mask', [False, True])
 def test_decoder_sorted_value_gradients(dtype, D, shape, Q, with_mask):
     # decoder density with many corners (2^18 and more, 16-bit): the value gradient by binning the corners by token
     # (sort_count_kernel .. sort_reduce_kernel, written once in the element type) and the location and weight
     # gradients by loc_attn_backward_kernel; Q ragged against the query tiles, clustered and uniform locations.
-    # D = 4 (16-bit): narrower than loc_attn_backward_kernel's 16-byte loads, so the atomic scatter instead
+    # Bins per level: where the scratch is tight ('four', 'wide') wide bins, the small levels' bins then split into
+    # token ranges; 'dino' has room for narrow bins on its small levels (8-16 tokens), with hot spots split when
+    # clustered. D = 4 (16-bit): narrower than loc_attn_backward_kernel's 16-byte loads, so the atomic scatter
     levels = SORT_LEVELS[shape]
     L, P = len(levels), 4
     N = sum(h * w for h, w in levels)
