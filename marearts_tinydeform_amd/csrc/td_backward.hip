@@ -1017,7 +1017,7 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(6))) void s
 //     bins (ranks within the tile from LDS atomics);
 //   * sort_reduce_kernel: one workgroup per item reads its bin's entries kSortChunk at a time and sorts those of its
 //     range in LDS (a counting sort: integer LDS atomics for the ranks) so that each lane group's tokens' entries lie
-//     together; each group then streams through its entries, 16 grad_out rows in flight per lane, adding the products
+//     together; each group then streams through its entries, 8 grad_out rows in flight per lane, adding the products
 //     a * w_c * g_row into its own tokens' float sums in LDS; finally the workgroup writes its tokens' rows, in the
 //     element type.
 // No float atomics, no zero fill, no rounding pass. Within a token the products are added in the order the LDS ranks
@@ -1025,7 +1025,7 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(6))) void s
 // starts) lives in the caller's float32 accumulator buffer. grad_loc and grad_attn come from
 // loc_attn_backward_kernel.
 constexpr int kSortMaxBins = 8192;  // bins per (b, h) at most (the tiles' LDS counters)
-constexpr int kSortChunk = 1024;    // entries per token range on average at most; entries read per round
+constexpr int kSortChunk = 512;     // entries per token range on average at most; entries read per round
 constexpr int kSortTarget = 512;    // expected entries per bin at most (where the bin can be that narrow)
 
 // tokens per bin at most at head width D: TB x D floats = 16 KB (128 at most: an entry keeps its position in the
@@ -1154,13 +1154,14 @@ __global__ __launch_bounds__(256) void sort_count_kernel(SortParams sp) {
     __shared__ SortLevels lv;
     const int bh = blockIdx.x / sp.qtiles, qt = blockIdx.x - bh * sp.qtiles;
     if (blockIdx.x == 0 && threadIdx.x == 0) sp.counters[0] = 0;  // for sort_scan_kernel's reservations
-    if (threadIdx.x < kWave) sort_levels(sp, lv);
     for (int i = threadIdx.x; i < sp.nb; i += 256) lc[i] = 0;
-    __syncthreads();
-    const int nb = lv.base[sp.g.L];
     int tk[4], lev, row;
     float cf[4];
-    if (sort_sample<T>(sp, bh, qt, threadIdx.x, tk, cf, lev, row)) {
+    const bool has = sort_sample<T>(sp, bh, qt, threadIdx.x, tk, cf, lev, row);  // its loads overlap the table's
+    if (threadIdx.x < kWave) sort_levels(sp, lv);
+    __syncthreads();  // the level table and the cleared counters
+    const int nb = lv.base[sp.g.L];
+    if (has) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             int pos;
@@ -1207,16 +1208,22 @@ __global__ __launch_bounds__(kScanTh) void sort_scan_kernel(SortParams sp) {
     const int n = nb * sp.qtiles;  // < 2^30 (checked on the host)
     int* mine = v + tid * (kScanK + 1);
     int carry = 0;
+    int hv[kScanK];  // a chunk's counts, loaded at clamped indexes (all in flight together) a chunk ahead
+    if (n > 0) {
+#pragma unroll
+        for (int u = 0; u < kScanK; ++u) hv[u] = hist[min(tid + u * kScanTh, min(n, kScanChunk) - 1)];
+    }
     for (int c0 = 0; c0 < n; c0 += kScanChunk) {  // uniform: every barrier is reached by the whole workgroup
         const int len = n - c0 < kScanChunk ? n - c0 : kScanChunk;
-        int hv[kScanK];  // loads at clamped indexes, all in flight together
-#pragma unroll
-        for (int u = 0; u < kScanK; ++u) hv[u] = hist[c0 + min(tid + u * kScanTh, len - 1)];
 #pragma unroll
         for (int u = 0; u < kScanK; ++u) {
             const int j = tid + u * kScanTh;
             v[(j / kScanK) * (kScanK + 1) + j % kScanK] = j < len ? hv[u] : 0;
         }
+        // the next chunk's counts (no branch, so that the loads stay in flight: past the end they reread the last
+        // count, unused)
+#pragma unroll
+        for (int u = 0; u < kScanK; ++u) hv[u] = hist[min(c0 + kScanChunk + tid + u * kScanTh, n - 1)];
         __syncthreads();  // the chunk is in LDS
         int own = 0;
 #pragma unroll
@@ -1305,12 +1312,13 @@ __global__ __launch_bounds__(256) void sort_fill_kernel(SortParams sp) {
     extern __shared__ int lc[];  // [nb]: this tile's running rank per bin
     __shared__ SortLevels lv;
     const int bh = blockIdx.x / sp.qtiles, qt = blockIdx.x - bh * sp.qtiles;
-    if (threadIdx.x < kWave) sort_levels(sp, lv);
     for (int i = threadIdx.x; i < sp.nb; i += 256) lc[i] = 0;
-    __syncthreads();
     int tk[4], lev, row;
     float cf[4];
-    if (sort_sample<T>(sp, bh, qt, threadIdx.x, tk, cf, lev, row)) {
+    const bool has = sort_sample<T>(sp, bh, qt, threadIdx.x, tk, cf, lev, row);  // its loads overlap the table's
+    if (threadIdx.x < kWave) sort_levels(sp, lv);
+    __syncthreads();  // the level table and the cleared counters
+    if (has) {
         const int* off = sp.hist + static_cast<int64_t>(bh) * sp.nb * sp.qtiles + qt;
         uint2* ent = sp.entries + static_cast<int64_t>(bh) * sp.cap;
 #pragma unroll
@@ -1329,15 +1337,17 @@ __global__ __launch_bounds__(256) void sort_fill_kernel(SortParams sp) {
 // items, the longest, first in each (b, h)'s part); each item's width x D float sums in LDS. A grad_out row is loaded
 // by LPR = D / 4 lanes, 4 elements (8 bytes) each; the NG = 256 / LPR lane groups each own the item's tokens r with
 // r % NG == grp (tokens of a neighbourhood go to different groups). Rounds of kSortChunk of the bin's entries, loaded
-// 4 a thread: those in the range ranked (integer LDS atomics) by the key (r % NG) * tpg + r / NG and written to LDS in
+// 2 a thread: those in the range ranked (integer LDS atomics) by the key (r % NG) * tpg + r / NG and written to LDS in
 // key order, so that each group's entries lie together, token by token; then each group streams through its own
-// entries, 16 grad_out rows in flight per lane, adding each product into its tokens' LDS sums (no other group writes
-// them, so plain LDS read-modify-writes). The sums are written once, in the element type. The next item is read an
-// item ahead, and the next round's entries (of this item or the next) during this round, so that the loads a
-// workgroup waits on are the grad_out rows alone.
+// entries, 8 grad_out rows in flight per lane (at most 80 VGPRs and 24 KB of LDS: six workgroups a CU), adding
+// each product into its tokens' LDS sums (no other group writes them, so plain LDS read-modify-writes). The sums are
+// written once, in the element type. The next item is read an item ahead, and the next round's entries (of this item
+// or the next) during this round, so that the loads a workgroup waits on are the grad_out rows alone. (Sums in
+// registers instead, each lane holding its TB / NG tokens' 4 columns and adding every product under a per-token
+// select, measured slower: 65 against 50 us at DINO B4.)
 template <typename T, int D>
 __global__ __launch_bounds__(256) void sort_reduce_kernel(SortParams sp) {
-    constexpr int NTH = 256, VL = 4, LPR = D / VL, NG = NTH / LPR, TB = sort_bin_tokens(D), U = 16;
+    constexpr int NTH = 256, VL = 4, LPR = D / VL, NG = NTH / LPR, TB = sort_bin_tokens(D), U = 8;
     constexpr int PER = kSortChunk / NTH;
     constexpr int PITCH = D + 4;  // LDS floats per token's sums: the groups' rows start in different banks
     using IO = VecIO<T, VL>;
@@ -1352,7 +1362,7 @@ __global__ __launch_bounds__(256) void sort_reduce_kernel(SortParams sp) {
     __shared__ uint2 sorted[kSortChunk];
     __shared__ int cnt[TB], base[TB], wtot[2];
     for (int i = tid; i < TB * PITCH / 4; i += NTH) reinterpret_cast<f32x4*>(accl)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // a round's entries, 4 a thread at clamped indexes (no branch: all in flight); n >= 1
+    // a round's entries, PER a thread at clamped indexes (no branch: all in flight); n >= 1
     auto load_round = [&](uint2 (&e)[PER], int bh, int r0, int n) {
         const uint2* __restrict__ src = sp.entries + static_cast<int64_t>(bh) * sp.cap + r0;
 #pragma unroll
