@@ -269,11 +269,17 @@ def test_dense_query_gradients_nine_levels(dtype, loc_dist):
             check(f'nine levels Q={Q} {dtype} {loc_dist} d{n}', grads[n], ref[n], dtype)
 
 
-def test_training_step_graph_replays_match_oracle():
+@pytest.mark.parametrize('shape', ['rtdetr-b1', 'binned'])
+def test_training_step_graph_replays_match_oracle(shape):
     # the training step (gradients set to None, forward, backward) captured in a graph, as the benchmark times it:
     # every replay must give all five gradients (the backward's accumulator is cleared by a kernel, not a memset),
-    # each checked against the float64 oracle, with eager work on the device between the replays
-    args = workload(1, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.float16, seed=11)
+    # each checked against the float64 oracle, with eager work on the device between the replays. 'binned': a decoder
+    # shape of 2^18 corners and more, whose value gradient takes the binned kernels (their item counter is reset by
+    # sort_count_kernel, their bin table computed from the device-resident shapes at every replay)
+    if shape == 'rtdetr-b1':
+        args = workload(1, 300, 8, 32, 256, RTDETR_LEVELS, 4, torch.float16, seed=11)
+    else:
+        args = workload(2, 400, 8, 32, 256, SORT_LEVELS['dino'], 4, torch.float16, loc_dist='clustered', seed=11)
     go = grad_out_for(args)
     ref = gridsample.deform_attn_grads(*args, go.to(torch.float16))
     dev = [None if t is None else t.cuda() for t in args]
@@ -302,7 +308,7 @@ def test_training_step_graph_replays_match_oracle():
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
-        say(f'  training step graph replay {i}')
+        say(f'  training step graph replay {i} ({shape})')
         grads = {n: None if leaves[j] is None else leaves[j].grad for n, j in zip(NAMES, (0, 1, 2, 5, 6))}
         for n in NAMES:
             check(f'replay {i} d{n}', grads[n], ref[n], torch.float16)
