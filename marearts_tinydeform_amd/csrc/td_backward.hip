@@ -1321,14 +1321,19 @@ __global__ __launch_bounds__(256) void sort_fill_kernel(SortParams sp) {
     if (has) {
         const int* off = sp.hist + static_cast<int64_t>(bh) * sp.nb * sp.qtiles + qt;
         uint2* ent = sp.entries + static_cast<int64_t>(bh) * sp.cap;
+        int bin[4], pos[4], o[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bin[k] = tk[k] >= 0 ? sort_bin_of(lv, lev, tk[k], pos[k]) : -1;
+        // the four tile starts at once (bin 0's for a dropped corner: no branch around the loads, which would each
+        // be waited for at the branch's end)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k] = off[static_cast<int64_t>(bin[k] >= 0 ? bin[k] : 0) * sp.qtiles];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            int pos;
-            const int bin = tk[k] >= 0 ? sort_bin_of(lv, lev, tk[k], pos) : -1;
-            if (bin < 0) continue;
-            const int rank = atomicAdd(&lc[bin], 1);
-            ent[off[static_cast<int64_t>(bin) * sp.qtiles] + rank] =
-                make_uint2(__float_as_uint(cf[k]), static_cast<unsigned>(row) << 7 | static_cast<unsigned>(pos));
+            if (bin[k] < 0) continue;
+            const int rank = atomicAdd(&lc[bin[k]], 1);
+            ent[o[k] + rank] =
+                make_uint2(__float_as_uint(cf[k]), static_cast<unsigned>(row) << 7 | static_cast<unsigned>(pos[k]));
         }
     }
 }
