@@ -1678,11 +1678,12 @@ __global__ __launch_bounds__(256) void wgrad_kernel(WgradParams p) {
 // nothing of each other, and each alone leaves most of the GPU idle at those sizes (about 500 and 260 workgroups of
 // a few rounds of loads each). Workgroups [0, gemm_blocks) take GEMM tiles (numbered as the GEMM's own launch numbers
 // them), the rest the weight gradient's tiles and splits; both run in the same 256 threads on one LDS buffer.
-template <typename T>
-using InGradGemm = GemmMfmaTile<T, 4, 1, 1, 4, 4, 2>;
-template <typename T, bool VEC>
+// WT (16-bit): the GEMM reads W as stored, [HD, C], through LDS transpose reads, instead of a transposed copy.
+template <typename T, bool WT>
+using InGradGemm = GemmMfmaTile<T, 4, 1, 1, 4, 4, 2, false, false, WT>;
+template <typename T, bool VEC, bool WT = false>
 __global__ __launch_bounds__(256) void input_weight_grad_kernel(GemmParams gp, WgradParams wp, int gemm_blocks) {
-    using G = InGradGemm<T>;
+    using G = InGradGemm<T, WT>;
     constexpr size_t kW = wgrad_slice_bytes<T>();
     constexpr size_t kL = G::kLds > 2 * kW ? G::kLds : 2 * kW;
     static_assert(G::NTH == 256, "the GEMM tile runs in the weight gradient's 256 threads");
@@ -2069,13 +2070,21 @@ int launch_transpose(int dtype, const void* src, void* dst, int64_t R, int64_t C
 int launch_input_weight_grad(int dtype, const void* G, const void* W, void* Wt, const void* X, void* gm, void* gw,
                              void* gb, int64_t M, int64_t HD, int64_t C, void* workspace, int64_t ws_bytes,
                              hipStream_t stream) {
+    if (value_proj_plan(dtype, G, Wt, nullptr, gm, M, HD, C, 0, 0) == 25) {
+        // 16-bit with C a multiple of 8 and W 16-byte aligned: the GEMM reads W as stored (no transpose launch,
+        // Wt is left unwritten)
+        const bool stored = (dtype == kF16 || dtype == kBF16) && C % 8 == 0 &&
+                            reinterpret_cast<uintptr_t>(W) % 16 == 0;
+        if (!stored) {
+            const int rc = launch_transpose(dtype, W, Wt, HD, C, stream);
+            if (rc != 0) return rc;
+        }
+        const GemmParams gp{G, stored ? W : Wt, nullptr, gm, static_cast<int>(M), static_cast<int>(HD),
+                            static_cast<int>(C), 0, 0, 0};
+        return launch_wgrad(dtype, G, X, gw, gb, M, HD, C, workspace, ws_bytes, stream, &gp, stored);
+    }
     int rc = launch_transpose(dtype, W, Wt, HD, C, stream);
     if (rc != 0) return rc;
-    if (value_proj_plan(dtype, G, Wt, nullptr, gm, M, HD, C, 0, 0) == 25) {
-        const GemmParams gp{G, Wt, nullptr, gm, static_cast<int>(M), static_cast<int>(HD), static_cast<int>(C),
-                            0, 0, 0};
-        return launch_wgrad(dtype, G, X, gw, gb, M, HD, C, workspace, ws_bytes, stream, &gp);
-    }
     rc = launch_value_proj(dtype, G, Wt, nullptr, gm, M, HD, C, stream);
     if (rc != 0) return rc;
     return launch_wgrad(dtype, G, X, gw, gb, M, HD, C, workspace, ws_bytes, stream);
@@ -2106,7 +2115,7 @@ void wgrad_plan(int64_t M, int64_t NO, int64_t K, int dtype, int* splits, int* c
 }
 
 int launch_wgrad(int dtype, const void* G, const void* X, void* gw, void* gb, int64_t M, int64_t NO, int64_t K,
-                 void* workspace, int64_t ws_bytes, hipStream_t stream, const GemmParams* with_gemm) {
+                 void* workspace, int64_t ws_bytes, hipStream_t stream, const GemmParams* with_gemm, bool gemm_wt) {
     int splits = 1, chunk = 32;
     int64_t need = 0;
     wgrad_plan(M, NO, K, dtype, &splits, &chunk, &need);
@@ -2162,20 +2171,36 @@ int launch_wgrad(int dtype, const void* G, const void* X, void* gw, void* gb, in
                                    gemm_blocks);
                 break;
             case kF16 * 2:
-                hipLaunchKernelGGL((input_weight_grad_kernel<f16, false>), cgrid, dim3(256), 0, stream, gp, p,
-                                   gemm_blocks);
+                if (gemm_wt)
+                    hipLaunchKernelGGL((input_weight_grad_kernel<f16, false, true>), cgrid, dim3(256), 0, stream, gp,
+                                       p, gemm_blocks);
+                else
+                    hipLaunchKernelGGL((input_weight_grad_kernel<f16, false>), cgrid, dim3(256), 0, stream, gp, p,
+                                       gemm_blocks);
                 break;
             case kF16 * 2 + 1:
-                hipLaunchKernelGGL((input_weight_grad_kernel<f16, true>), cgrid, dim3(256), 0, stream, gp, p,
-                                   gemm_blocks);
+                if (gemm_wt)
+                    hipLaunchKernelGGL((input_weight_grad_kernel<f16, true, true>), cgrid, dim3(256), 0, stream, gp,
+                                       p, gemm_blocks);
+                else
+                    hipLaunchKernelGGL((input_weight_grad_kernel<f16, true>), cgrid, dim3(256), 0, stream, gp, p,
+                                       gemm_blocks);
                 break;
             case kBF16 * 2:
-                hipLaunchKernelGGL((input_weight_grad_kernel<bf16, false>), cgrid, dim3(256), 0, stream, gp, p,
-                                   gemm_blocks);
+                if (gemm_wt)
+                    hipLaunchKernelGGL((input_weight_grad_kernel<bf16, false, true>), cgrid, dim3(256), 0, stream, gp,
+                                       p, gemm_blocks);
+                else
+                    hipLaunchKernelGGL((input_weight_grad_kernel<bf16, false>), cgrid, dim3(256), 0, stream, gp, p,
+                                       gemm_blocks);
                 break;
             case kBF16 * 2 + 1:
-                hipLaunchKernelGGL((input_weight_grad_kernel<bf16, true>), cgrid, dim3(256), 0, stream, gp, p,
-                                   gemm_blocks);
+                if (gemm_wt)
+                    hipLaunchKernelGGL((input_weight_grad_kernel<bf16, true, true>), cgrid, dim3(256), 0, stream, gp,
+                                       p, gemm_blocks);
+                else
+                    hipLaunchKernelGGL((input_weight_grad_kernel<bf16, true>), cgrid, dim3(256), 0, stream, gp, p,
+                                       gemm_blocks);
                 break;
             default: return set_error(-2, "unknown dtype code %d", dtype);
         }

@@ -17,7 +17,14 @@ namespace td {
 // Epilogue: bias, one rounding to T, the tile transposed through LDS and written with 16-byte stores.
 // DUAL: C = A . W^T + A2 . W^T + bias with A2 the same shape as A (two MFMAs per block; the sum A + A2 is never
 // rounded to T). F32OUT: C is float32, the accumulators stored unrounded.
-template <typename T, int WM, int WN, int TM, int TN, int NKB, int STAGES, bool DUAL = false, bool F32OUT = false>
+// WT (16-bit types): W is given as stored by its owner, [K, NO] with NO contiguous (C = A . W), so no transposed copy
+// is needed: the K x BN slice is staged as K rows (pitch BN + 16 elements: measured at the RT-DETR training step's
+// input gradient against BN + 4 and BN + 8, 57.1 and 56.3 against 56.1 us), and each B fragment (8 consecutive k
+// of one column) is read by two LDS transpose reads (ds_read_b64_tr_b16: within each 16 lanes, lane i receives
+// element i % 4 of the 8-byte pieces the lanes i / 4, 4 + i / 4, 8 + i / 4 and 12 + i / 4 point at, so lanes
+// pointing at rows k .. k + 3, columns c + 4 (lane % 4) give lane i the four k of column c + i).
+template <typename T, int WM, int WN, int TM, int TN, int NKB, int STAGES, bool DUAL = false, bool F32OUT = false,
+          bool WT = false>
 struct GemmMfmaTile {
     using O = typename std::conditional<F32OUT, float, T>::type;  // output element
     static constexpr int NTH = WM * WN * kWave;
@@ -27,10 +34,13 @@ struct GemmMfmaTile {
     static constexpr int KC = NKB * KBK;                         // K per chunk
     static constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
     static constexpr int LDK = KC + E;                           // LDS pitch (elements) of a staged W row
+    static constexpr int LDN = BN + 16;                          // WT: LDS pitch (elements) of a staged k row
     static constexpr int B_CHUNKS = BN * KC / E;                 // 16-byte pieces of one staged W slice
     static constexpr int B_PER_T = (B_CHUNKS + NTH - 1) / NTH;
     static constexpr int LDC = BN + EO;                          // LDS pitch of the output tile
-    static constexpr size_t kStage = static_cast<size_t>(BN) * LDK * sizeof(T);
+    static_assert(!WT || sizeof(T) == 2, "the transposed-W form reads 16-bit fragments");
+    static constexpr size_t kStage =
+        WT ? static_cast<size_t>(KC) * LDN * sizeof(T) : static_cast<size_t>(BN) * LDK * sizeof(T);
     static constexpr size_t kOut = static_cast<size_t>(BM) * LDC * sizeof(O);
     static constexpr size_t kLds = STAGES * kStage > kOut ? STAGES * kStage : kOut;
 
@@ -72,11 +82,19 @@ struct GemmMfmaTile {
 #pragma unroll
             for (int u = 0; u < B_PER_T; ++u) {
                 const int c = tid + u * NTH;
-                const int row = c / (KC / E), kc = (c % (KC / E)) * E;
-                const int n = n0 + row, k = k0 + kc;
-                rb[u] = (c < B_CHUNKS && n < NO && k < K)
-                            ? *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(n) * K + k)
-                            : zero;
+                if constexpr (WT) {  // piece c: k row c / (BN / E), columns (c % (BN / E)) * E .. + E - 1
+                    const int kk = c / (BN / E), nn = (c % (BN / E)) * E;
+                    const int n = n0 + nn, k = k0 + kk;
+                    rb[u] = (c < B_CHUNKS && n < NO && k < K)
+                                ? *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(k) * NO + n)
+                                : zero;
+                } else {
+                    const int row = c / (KC / E), kc = (c % (KC / E)) * E;
+                    const int n = n0 + row, k = k0 + kc;
+                    rb[u] = (c < B_CHUNKS && n < NO && k < K)
+                                ? *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(n) * K + k)
+                                : zero;
+                }
             }
         };
         auto store_b = [&](T* buf) {
@@ -84,8 +102,13 @@ struct GemmMfmaTile {
             for (int u = 0; u < B_PER_T; ++u) {
                 const int c = tid + u * NTH;
                 if (c < B_CHUNKS) {
-                    const int row = c / (KC / E), kc = (c % (KC / E)) * E;
-                    *reinterpret_cast<u32x4*>(buf + row * LDK + kc) = rb[u];
+                    if constexpr (WT) {
+                        const int kk = c / (BN / E), nn = (c % (BN / E)) * E;
+                        *reinterpret_cast<u32x4*>(buf + kk * LDN + nn) = rb[u];
+                    } else {
+                        const int row = c / (KC / E), kc = (c % (KC / E)) * E;
+                        *reinterpret_cast<u32x4*>(buf + row * LDK + kc) = rb[u];
+                    }
                 }
             }
         };
@@ -102,8 +125,19 @@ struct GemmMfmaTile {
             for (int j = 0; j < NKB; ++j) {
                 u32x4 b[TN];
 #pragma unroll
-                for (int t = 0; t < TN; ++t)
-                    b[t] = *reinterpret_cast<const u32x4*>(bs + ((wn * TN + t) * 16 + r16) * LDK + j * KBK + kg * E);
+                for (int t = 0; t < TN; ++t) {
+                    if constexpr (WT) {  // k rows j * KBK + 8 kg + lane16 / 4 (+ 4), columns 4 (lane16 % 4) on
+                        using v4s = short __attribute__((ext_vector_type(4)));
+                        using lds_v4s = __attribute__((address_space(3))) v4s;
+                        const T* q = bs + (j * KBK + kg * 8 + (r16 >> 2)) * LDN + (wn * TN + t) * 16 + 4 * (r16 & 3);
+                        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(q));
+                        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(q + 4 * LDN));
+                        b[t] = __builtin_bit_cast(u32x4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                    } else {
+                        b[t] = *reinterpret_cast<const u32x4*>(bs + ((wn * TN + t) * 16 + r16) * LDK + j * KBK +
+                                                               kg * E);
+                    }
+                }
 #pragma unroll
                 for (int o = 0; o < NA; ++o)
 #pragma unroll

@@ -129,10 +129,12 @@ int launch_convert(int dtype, const void* src_acc, void* dst, int64_t n, hipStre
 int launch_transpose(int dtype, const void* src, void* dst, int64_t R, int64_t Cc, hipStream_t stream);
 // weight / bias gradient split over tokens: partials in the workspace, summed in a fixed order
 void wgrad_plan(int64_t M, int64_t NO, int64_t K, int dtype, int* splits, int* chunk, int64_t* ws_bytes);
-// with_gemm: a GEMM run in the same launch on the 64 x 64 two-stage tiles (launch_input_weight_grad)
+// with_gemm: a GEMM run in the same launch on the 64 x 64 two-stage tiles (launch_input_weight_grad); gemm_wt: its W
+// is given as stored, [K, NO] (16-bit types only)
 struct GemmParams;
 int launch_wgrad(int dtype, const void* G, const void* X, void* gw, void* gb, int64_t M, int64_t NO, int64_t K,
-                 void* workspace, int64_t ws_bytes, hipStream_t stream, const GemmParams* with_gemm = nullptr);
+                 void* workspace, int64_t ws_bytes, hipStream_t stream, const GemmParams* with_gemm = nullptr,
+                 bool gemm_wt = false);
 int launch_input_weight_grad(int dtype, const void* G, const void* W, void* Wt, const void* X, void* gm, void* gw,
                              void* gb, int64_t M, int64_t HD, int64_t C, void* workspace, int64_t ws_bytes,
                              hipStream_t stream);
