@@ -291,9 +291,9 @@ int td_weight_grad(int dtype, const void* grad_value, const void* memory, void* 
  * workspace (td_weight_grad_workspace; TD_E_WORKSPACE before anything is launched when it is smaller). Where the
  * input gradient's GEMM takes the small-grid tiles (below about 14000 tokens of 256 channels in 16 bits) its tiles
  * and the weight gradient's share one launch; no counterpart in the reference, whose operator is inference only.
- * There, in 16 bits with C a multiple of 8 and value_weight 16-byte aligned, the GEMM reads value_weight as stored
- * (LDS transpose reads) and weight_t is left unwritten; otherwise weight_t receives value_weight^T as in
- * td_input_grad.
+ * There, and where the input gradient takes the streaming GEMM (C = 256, HD = 128 or 256, many tokens), in 16 bits
+ * with C a multiple of 8 and value_weight 16-byte aligned, the GEMM reads value_weight as stored (LDS transpose
+ * reads) and weight_t is left unwritten; otherwise weight_t receives value_weight^T as in td_input_grad.
  */
 int td_input_weight_grad(int dtype, const void* grad_value, const void* value_weight, void* weight_t,
                          const void* memory, void* grad_memory, void* grad_weight, void* grad_bias, int64_t M,

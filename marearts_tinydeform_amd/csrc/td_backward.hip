@@ -2083,7 +2083,15 @@ int launch_input_weight_grad(int dtype, const void* G, const void* W, void* Wt, 
                             static_cast<int>(C), 0, 0, 0};
         return launch_wgrad(dtype, G, X, gw, gb, M, HD, C, workspace, ws_bytes, stream, &gp, stored);
     }
-    int rc = launch_transpose(dtype, W, Wt, HD, C, stream);
+    // the streaming GEMM (16-bit, C = 256, HD = 128 or 256, many tokens) reads W as stored too
+    const GemmParams sp{G, W, nullptr, gm, static_cast<int>(M), static_cast<int>(HD), static_cast<int>(C), 0, 0, 0};
+    int rc = 0;
+    if (value_proj_plan(dtype, G, W, nullptr, gm, M, HD, C, 0, 0) == 22 && gemm_stream_fits(dtype, sp)) {
+        rc = launch_gemm_stream(dtype, sp, stream, true);
+        if (rc != 0) return rc;
+        return launch_wgrad(dtype, G, X, gw, gb, M, HD, C, workspace, ws_bytes, stream);
+    }
+    rc = launch_transpose(dtype, W, Wt, HD, C, stream);
     if (rc != 0) return rc;
     rc = launch_value_proj(dtype, G, Wt, nullptr, gm, M, HD, C, stream);
     if (rc != 0) return rc;

@@ -86,6 +86,7 @@ int launch_gemm_dma(int dtype, GemmParams p, hipStream_t stream, int variant);
 // The streaming kernel for narrow K (td_gemm_stream.hip): 16-bit, NO = 256, K = 128 or 256, 16-byte aligned a, w, c
 // and bias (or no bias); a head-major output needs hm_D a multiple of 8.
 bool gemm_stream_fits(int dtype, const GemmParams& p);
-int launch_gemm_stream(int dtype, GemmParams p, hipStream_t stream);
+// w_stored: p.w is [K, 256] as its owner stores it (C = A . W) instead of [256, K]
+int launch_gemm_stream(int dtype, GemmParams p, hipStream_t stream, bool w_stored = false);
 
 }  // namespace td

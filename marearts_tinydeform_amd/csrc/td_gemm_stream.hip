@@ -67,7 +67,13 @@ __device__ __forceinline__ void meet() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <typename T, int KB>
+// WT: W is given as stored by its owner, [K, 256] with the 256 output channels contiguous (C = A . W: the input
+// gradient grad_memory = G . value_weight), instead of [256, K]. Its LDS copy then holds K rows of 256 channels in
+// order (the same 1 KB direct loads), and each wavefront reads its W quarter into registers once by LDS transpose
+// reads (ds_read_b64_tr_b16: within each 16 lanes, lane i receives element i % 4 of the 8-byte pieces lanes i / 4,
+// 4 + i / 4, 8 + i / 4 and 12 + i / 4 point at), lane j pointing at k row 8 kg + j / 4 (+ 4) and at the column of
+// its fragment layout's channel group j % 4, so that lane r receives the 8 k of the channel the layout gives it.
+template <typename T, int KB, bool WT>
 __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_stream_kernel(
     GemmParams p) {
     constexpr int NTQ = kStreamNO / 16 / kStreamWaves;  // 16-channel tiles per wavefront: 4
@@ -132,8 +138,14 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
 #pragma unroll 4
         for (int jj = 0; jj < WDL; ++jj) {
             const int j = wave * WDL + (jj + rot) % WDL;  // the CUs of an XCD start on different runs
-            const int sl = j * kWave + lane, ch = sl / CHR, c = (sl % CHR) ^ wkey(ch);
-            load_lds16(W + static_cast<size_t>(ch) * K + c * 8, wl + j * 1024);
+            const int sl = j * kWave + lane;
+            if constexpr (WT) {  // slot sl: k row sl / 32, channels (sl % 32) * 8 .. + 7
+                load_lds16(W + static_cast<size_t>(sl / (kStreamNO / 8)) * kStreamNO + (sl % (kStreamNO / 8)) * 8,
+                           wl + j * 1024);
+            } else {
+                const int ch = sl / CHR, c = (sl % CHR) ^ wkey(ch);
+                load_lds16(W + static_cast<size_t>(ch) * K + c * 8, wl + j * 1024);
+            }
         }
     }
     // the bias is loaded unconditionally (W's first row stands in for a missing one) so that the count of loads in
@@ -193,8 +205,19 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int t = 0; t < NTQ; ++t) {
-            const int ch = qc + 32 * (t >> 1) + 8 * (r >> 2) + 4 * (t & 1) + (r & 3);
-            wf[t][kb] = *reinterpret_cast<const u32x4*>(wl + (ch * CHR + ((kb * 4 + kg) ^ wkey(ch))) * 16);
+            if constexpr (WT) {
+                using v4s = short __attribute__((ext_vector_type(4)));
+                using lds_v4s = __attribute__((address_space(3))) v4s;
+                const int k = kb * 32 + kg * 8 + (r >> 2);
+                const int col = qc + 32 * (t >> 1) + 8 * (r & 3) + 4 * (t & 1);
+                const unsigned char* q = wl + (k * kStreamNO + col) * 2;
+                const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(q));
+                const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(q + 4 * kStreamNO * 2));
+                wf[t][kb] = __builtin_bit_cast(u32x4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            } else {
+                const int ch = qc + 32 * (t >> 1) + 8 * (r >> 2) + 4 * (t & 1) + (r & 3);
+                wf[t][kb] = *reinterpret_cast<const u32x4*>(wl + (ch * CHR + ((kb * 4 + kg) ^ wkey(ch))) * 16);
+            }
         }
     step(0);
     for (int i = 1; i < ns; ++i) {
@@ -207,31 +230,31 @@ __global__ __launch_bounds__(kStreamWaves* kWave) __attribute__((amdgpu_waves_pe
     __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
 }
 
-template <typename T, int KB>
+template <typename T, int KB, bool WT>
 int go_stream(GemmParams p, int64_t grid, hipStream_t stream) {
     // two token stages and W: 160 KB at K = 256, 80 KB at K = 128
     constexpr size_t lds = static_cast<size_t>(2) * kStreamStep * KB * 64 + static_cast<size_t>(kStreamNO) * KB * 64;
     if constexpr (lds > 65536) {
         static std::atomic<uint64_t> done{0};
         const hipError_t attr =
-            allow_dynamic_lds(reinterpret_cast<const void*>(gemm_stream_kernel<T, KB>), static_cast<int>(lds), done);
+            allow_dynamic_lds(reinterpret_cast<const void*>(gemm_stream_kernel<T, KB, WT>), static_cast<int>(lds), done);
         if (attr != hipSuccess)
             return set_error(-3, "value_proj: LDS size attribute refused: %s", hipGetErrorString(attr));
     }
-    hipLaunchKernelGGL((gemm_stream_kernel<T, KB>), dim3(static_cast<unsigned>(grid)), dim3(kStreamWaves * kWave), lds,
+    hipLaunchKernelGGL((gemm_stream_kernel<T, KB, WT>), dim3(static_cast<unsigned>(grid)), dim3(kStreamWaves * kWave), lds,
                        stream, p);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : set_error(-3, "value_proj launch failed: %s", hipGetErrorString(e));
 }
 
 // One workgroup per CU (at least one step of tokens each); the workgroups' shares differ by at most one token.
-template <typename T>
+template <typename T, bool WT>
 int stream_t(GemmParams p, hipStream_t stream) {
     int64_t grid = (static_cast<int64_t>(p.M) + kStreamStep - 1) / kStreamStep;
     const int cus = cu_count();
     if (grid > cus) grid = cus;
     if (grid < 1) grid = 1;
-    return p.K == 256 ? go_stream<T, 8>(p, grid, stream) : go_stream<T, 4>(p, grid, stream);
+    return p.K == 256 ? go_stream<T, 8, WT>(p, grid, stream) : go_stream<T, 4, WT>(p, grid, stream);
 }
 
 }  // namespace
@@ -244,9 +267,10 @@ bool gemm_stream_fits(int dtype, const GemmParams& p) {
            al % 16 == 0 && p.hm_D % 8 == 0;
 }
 
-int launch_gemm_stream(int dtype, GemmParams p, hipStream_t stream) {
+int launch_gemm_stream(int dtype, GemmParams p, hipStream_t stream, bool w_stored) {
     if (!gemm_stream_fits(dtype, p)) return set_error(-1, "value_proj: the streaming kernel does not take this shape");
-    return dtype == kF16 ? stream_t<f16>(p, stream) : stream_t<bf16>(p, stream);
+    if (w_stored) return dtype == kF16 ? stream_t<f16, true>(p, stream) : stream_t<bf16, true>(p, stream);
+    return dtype == kF16 ? stream_t<f16, false>(p, stream) : stream_t<bf16, false>(p, stream);
 }
 
 }  // namespace td

@@ -154,10 +154,12 @@ def test_projection_gradients_alone(dtype):
 def test_input_and_weight_gradients_in_one_call(dtype):
     # td_input_weight_grad against td_input_grad and td_weight_grad, bit for bit: (1, 8400, 256, 256) and the two
     # ragged shapes (M, N and K off the tiles; C a multiple of 8 or not, so the weight gradient stages 16-byte pieces
-    # or scalars) share one launch in 16/32 bits; the others take the two kernels one after the other
+    # or scalars) share one launch in 16/32 bits (in 16 bits with C % 8 = 0 reading W as stored); (1, 16800, 256,
+    # 256) and (2, 5000, 256, 128) take the streaming GEMM, in 16 bits also with W as stored, against td_input_grad's
+    # transposed copy; the others take the two kernels one after the other
     g = torch.Generator().manual_seed(12)
     for (B, N, C, HD) in ((1, 8400, 256, 256), (1, 5000, 264, 136), (1, 5000, 260, 136), (2, 77, 40, 48),
-                          (1, 1000, 1024, 96)):
+                          (1, 1000, 1024, 96), (1, 16800, 256, 256), (2, 5000, 256, 128)):
         gv = torch.randn(B, N, HD, generator=g).to(dtype).cuda()
         mem = torch.randn(B, N, C, generator=g).to(dtype).cuda()
         w = (torch.randn(HD, C, generator=g) / C ** 0.5).to(dtype).cuda()
