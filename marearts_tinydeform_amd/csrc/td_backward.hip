@@ -556,8 +556,12 @@ struct LocAttnParams {
     FastDiv d_lp, d_gs, d_dv, d_q, d_h;  // divisions by L * P, DV * SG, DV, Q and H
 };
 
+// LDS of loc_attn_backward_body: corner byte offsets and dots, [RB][S] each (RB * LP <= 256)
+constexpr size_t kLocAttnLds = 2 * 4 * 256 * sizeof(int);
+
+// Workgroup `wg` of loc_attn_backward_kernel's grid, with `lds` its kLocAttnLds bytes (16-byte aligned).
 template <typename T, int V, int NB>
-__global__ __launch_bounds__(256) void loc_attn_backward_kernel(LocAttnParams lp) {
+__device__ __forceinline__ void loc_attn_backward_body(const LocAttnParams& lp, int wg, unsigned char* lds) {
     constexpr int NTH = 256;
     using A = float;
     using IO = VecIO<T, V>;
@@ -565,10 +569,10 @@ __global__ __launch_bounds__(256) void loc_attn_backward_kernel(LocAttnParams lp
     const BackParams& p = lp.p;
     const Geom& g = p.g;
     const int LP = g.LP, S = 4 * LP, D = g.D, HD = g.H * D, DV = D / V, SG = lp.SG, GS = DV * SG, RB = lp.RB;
-    __shared__ int off[4 * NTH];  // [RB][S] corner byte offsets (RB * LP <= NTH)
-    __shared__ A dots[4 * NTH];   // [RB][S] value row . grad_out row
+    int* off = reinterpret_cast<int*>(lds);             // [RB][S] corner byte offsets (RB * LP <= NTH)
+    A* dots = reinterpret_cast<A*>(lds) + 4 * NTH;      // [RB][S] value row . grad_out row
     const int tid = threadIdx.x;
-    const int blk = (blockIdx.x % kXcds) * lp.per_xcd + blockIdx.x / kXcds;
+    const int blk = (wg % kXcds) * lp.per_xcd + wg / kXcds;
     if (blk >= lp.blocks) return;  // the whole workgroup
     const int rows = g.B * g.Q * g.H, i0 = blk * RB;
     // row (b, q, h) of the i-th row in (b, h, q) order
@@ -673,6 +677,12 @@ __global__ __launch_bounds__(256) void loc_attn_backward_kernel(LocAttnParams lp
             static_cast<T*>(p.grad_attn)[idx] = static_cast<T>(ga);
         }
     }
+}
+
+template <typename T, int V, int NB>
+__global__ __launch_bounds__(256) void loc_attn_backward_kernel(LocAttnParams lp) {
+    __shared__ __align__(16) unsigned char lds[kLocAttnLds];
+    loc_attn_backward_body<T, V, NB>(lp, static_cast<int>(blockIdx.x), lds);
 }
 
 // The value-gradient scatter where many queries sample the same neighbourhood (encoder self-attention: every token
@@ -1010,9 +1020,10 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(6))) void s
 //     kSortTarget entries (4 Q P_l corners over the level's n_l tokens): the small, densely sampled levels get narrow
 //     bins (sort_levels, from the device-resident level shapes);
 //   * sort_count_kernel: each query tile counts its corners into the bins (LDS counters);
-//   * sort_scan_kernel: one workgroup per (b, h) scans the counts, bin-major, into each tile's start within each bin
-//     and each bin's start; then it lists the reduce items: one per bin, or, for a bin above kSortChunk entries (a
-//     hot spot), 2^j token ranges, the fewest averaging at most kSortChunk entries each;
+//   * sort_scan_body (in scan_loc_attn_kernel, beside the location and weight gradients): one workgroup per (b, h)
+//     scans the counts, bin-major, into each tile's start within each bin and each bin's start; then it lists the
+//     reduce items: one per bin, or, for a bin above kSortChunk entries (a hot spot), 2^j token ranges, the fewest
+//     averaging at most kSortChunk entries each;
 //   * sort_fill_kernel: each tile writes its corners as entries {a * w_c, row << 7 | position in the bin} into their
 //     bins (ranks within the tile from LDS atomics);
 //   * sort_reduce_kernel: one workgroup per item reads its bin's entries kSortChunk at a time and sorts those of its
@@ -1045,6 +1056,7 @@ struct SortParams {
     int maxch;            // reduce items per (b, h) at most
     int64_t cap;          // entries per (b, h) at most: Q * L * P * 4
     int* hist;            // [B * H][nb][qtiles]: counts, then each tile's start within its bin
+    int* bin_start;       // [B * H][nb + 1]: each bin's first entry (sort_scan_body)
     uint4* items;         // [B * H * maxch]: the reduce items of every (b, h) (sort_item)
     int* counters;        // [1]: items listed (zeroed by sort_count_kernel)
     uint2* entries;       // [B * H][cap]
@@ -1153,7 +1165,7 @@ __global__ __launch_bounds__(256) void sort_count_kernel(SortParams sp) {
     extern __shared__ int lc[];  // [nb]
     __shared__ SortLevels lv;
     const int bh = blockIdx.x / sp.qtiles, qt = blockIdx.x - bh * sp.qtiles;
-    if (blockIdx.x == 0 && threadIdx.x == 0) sp.counters[0] = 0;  // for sort_scan_kernel's reservations
+    if (blockIdx.x == 0 && threadIdx.x == 0) sp.counters[0] = 0;  // for sort_scan_body's reservations
     for (int i = threadIdx.x; i < sp.nb; i += 256) lc[i] = 0;
     int tk[4], lev, row;
     float cf[4];
@@ -1178,7 +1190,7 @@ __global__ __launch_bounds__(256) void sort_count_kernel(SortParams sp) {
 // loaded into LDS with coalesced reads, thread t owning 8 consecutive counts (LDS pitch 9 words: the owners' reads
 // spread over the banks), a wavefront scan of the owners' totals, and coalesced writes back; the bins' starts are the
 // scanned values at the bins' first counts (kept in LDS, bst). Then the reduce items of the (b, h)'s bins.
-constexpr int kScanTh = 512, kScanK = 8, kScanChunk = kScanTh * kScanK;
+constexpr int kScanTh = 256, kScanK = 8, kScanChunk = kScanTh * kScanK;
 
 __device__ __forceinline__ int block_excl_scan(int x, int* wt, int wave, int lane, int& total) {
     constexpr int NW = kScanTh / kWave;
@@ -1195,12 +1207,19 @@ __device__ __forceinline__ int block_excl_scan(int x, int* wt, int wave, int lan
     return run;
 }
 
-__global__ __launch_bounds__(kScanTh) void sort_scan_kernel(SortParams sp) {
-    __shared__ int v[kScanTh * (kScanK + 1)];
-    __shared__ int wtot[kScanTh / kWave];
-    __shared__ SortLevels lv;
-    extern __shared__ int bst[];  // [nb + 1]: the bins' starts
-    const int bh = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
+// LDS of sort_scan_body: the chunk (pitch kScanK + 1), the wavefront totals, the place in the item list, the level
+// table
+constexpr size_t kScanV = static_cast<size_t>(kScanTh) * (kScanK + 1) * sizeof(int);
+constexpr size_t kScanLds = kScanV + (kScanTh / kWave + 4) * sizeof(int) + sizeof(SortLevels);
+
+// Workgroup of (b, h) = bh, with `lds` its kScanLds bytes (16-byte aligned).
+__device__ __forceinline__ void sort_scan_body(const SortParams& sp, int bh, unsigned char* lds) {
+    int* v = reinterpret_cast<int*>(lds);
+    int* wtot = reinterpret_cast<int*>(lds + kScanV);
+    int& place = wtot[kScanTh / kWave];
+    SortLevels& lv = *reinterpret_cast<SortLevels*>(lds + kScanV + (kScanTh / kWave + 4) * sizeof(int));
+    int* bst = sp.bin_start + static_cast<int64_t>(bh) * (sp.nb + 1);  // the bins' starts (read back after a barrier)
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
     if (tid < kWave) sort_levels(sp, lv);
     __syncthreads();
     const int nb = lv.base[sp.g.L];
@@ -1269,7 +1288,6 @@ __global__ __launch_bounds__(kScanTh) void sort_scan_kernel(SortParams sp) {
         own_split += lj > 0 ? 1 << lj : 0;
         own_other += lj > 0 ? 0 : 1;
     }
-    __shared__ int place;
     int tot_split, tot_other;
     block_excl_scan(own_split, wtot, wave, lane, tot_split);
     __syncthreads();  // wtot is free
@@ -1305,6 +1323,19 @@ __global__ __launch_bounds__(kScanTh) void sort_scan_kernel(SortParams sp) {
         run_other += to;
         __syncthreads();  // wtot is free for the next bins
     }
+}
+
+// The scan and the location and weight gradients (which do not depend on it) in one launch: workgroups [0, B * H) run
+// the scan, the rest loc_attn_backward_kernel's grid; the scan's B * H workgroups alone would leave the GPU idle.
+template <typename T, int V, int NB>
+__global__ __launch_bounds__(256) void scan_loc_attn_kernel(SortParams sp, LocAttnParams lp) {
+    constexpr size_t kL = kScanLds > kLocAttnLds ? kScanLds : kLocAttnLds;
+    __shared__ __align__(16) unsigned char lds[kL];
+    const int BH = sp.g.B * sp.g.H, wg = static_cast<int>(blockIdx.x);
+    if (wg < BH)
+        sort_scan_body(sp, wg, lds);
+    else
+        loc_attn_backward_body<T, V, NB>(lp, wg - BH, lds);
 }
 
 template <typename T>
@@ -1850,8 +1881,9 @@ int scatter_bucket_go(const BackParams& p, hipStream_t stream) {
 // loc_attn_backward_kernel's shape: RB = 256 / LP rows a workgroup, SG corner groups a row (every thread a lane
 // where RB * DV <= 256); 1 without launching when the kernel does not fit (the caller then takes
 // sample_backward_vec_kernel or the atomic scatter)
+// loc_attn_backward_kernel's parameters for p; 1 when the kernel does not fit (see above)
 template <typename T>
-int loc_attn_backward_go(const BackParams& p, hipStream_t stream) {
+int loc_attn_plan(const BackParams& p, LocAttnParams& lp) {
     constexpr int V = 16 / static_cast<int>(sizeof(T)), NTH = 256;
     const Geom& g = p.g;
     const int64_t rows = static_cast<int64_t>(g.B) * g.Q * g.H;
@@ -1862,7 +1894,7 @@ int loc_attn_backward_go(const BackParams& p, hipStream_t stream) {
         reinterpret_cast<uintptr_t>(p.grad_out) % 16 != 0 || g.LP <= 0 || g.LP > NTH ||
         rows * g.LP >= (int64_t{1} << 31) || vbytes >= (int64_t{1} << 31))
         return 1;
-    LocAttnParams lp{p, 0, 0, 0, 0, 0, {}, {}, {}, {}, {}};
+    lp = LocAttnParams{p, 0, 0, 0, 0, 0, {}, {}, {}, {}, {}};
     lp.RB = NTH / g.LP;
     lp.SG = NTH / (lp.RB * DV) > 0 ? NTH / (lp.RB * DV) : 1;
     const int64_t blocks = (rows + lp.RB - 1) / lp.RB;
@@ -1874,8 +1906,17 @@ int loc_attn_backward_go(const BackParams& p, hipStream_t stream) {
     lp.d_dv = make_fastdiv(static_cast<uint32_t>(DV));
     lp.d_q = make_fastdiv(static_cast<uint32_t>(g.Q));
     lp.d_h = make_fastdiv(static_cast<uint32_t>(g.H));
-    if (rows == 0) return 0;
-    hipLaunchKernelGGL((loc_attn_backward_kernel<T, V, 8>), dim3(static_cast<unsigned>(lp.per_xcd * kXcds)), dim3(NTH),
+    return 0;
+}
+
+template <typename T>
+int loc_attn_backward_go(const BackParams& p, hipStream_t stream) {
+    constexpr int V = 16 / static_cast<int>(sizeof(T));
+    LocAttnParams lp;
+    const int rc = loc_attn_plan<T>(p, lp);
+    if (rc != 0) return rc;
+    if (lp.blocks == 0) return 0;
+    hipLaunchKernelGGL((loc_attn_backward_kernel<T, V, 8>), dim3(static_cast<unsigned>(lp.per_xcd * kXcds)), dim3(256),
                        0, stream, lp);
     return launched("sample backward locations");
 }
@@ -1919,29 +1960,36 @@ int sample_backward_sorted(const BackParams& p, void* grad_value_t, int64_t acc_
         nb = ((static_cast<int64_t>(g.N) >> sp.min_shift) + 1) + g.L;
         maxch = nb + 2 * sp.cap / kSortChunk + 1;
         item_bytes = BH * maxch * 16;
-        const int64_t ints = BH * nb * sp.qtiles + 1;
+        const int64_t ints = BH * nb * sp.qtiles + BH * (nb + 1) + 1;
         if (nb <= kSortMaxBins && nb * sp.qtiles < (int64_t{1} << 30) && BH * maxch < (int64_t{1} << 31) &&
             ent_bytes + item_bytes + 4 * ints <= acc_bytes)
             break;
     }
     sp.nb = static_cast<int>(nb);
     sp.maxch = static_cast<int>(maxch);
-    // the location and weight gradients first (1: its 16-byte loads do not fit these sizes)
-    const int rc = loc_attn_backward_go<T>(p, stream);
+    // the location and weight gradients' plan (1: its 16-byte loads do not fit these sizes); they run beside the scan
+    LocAttnParams lp;
+    const int rc = loc_attn_plan<T>(p, lp);
     if (rc != 0) return rc;
     unsigned char* scratch = static_cast<unsigned char*>(p.grad_value);  // 16-byte aligned (checked above)
     sp.entries = reinterpret_cast<uint2*>(scratch);
     sp.items = reinterpret_cast<uint4*>(scratch + ent_bytes);
     sp.hist = reinterpret_cast<int*>(scratch + ent_bytes + item_bytes);
-    sp.counters = sp.hist + BH * nb * sp.qtiles;
+    sp.bin_start = sp.hist + BH * nb * sp.qtiles;
+    sp.counters = sp.bin_start + BH * (nb + 1);
     sp.d_lp = make_fastdiv(static_cast<uint32_t>(g.LP));
     const unsigned tiles = static_cast<unsigned>(BH * sp.qtiles);
     const size_t lds = static_cast<size_t>(nb) * sizeof(int);
     hipLaunchKernelGGL(sort_count_kernel<T>, dim3(tiles), dim3(256), lds, stream, sp);
     int r2 = launched("sample backward count");
     if (r2 != 0) return r2;
-    hipLaunchKernelGGL(sort_scan_kernel, dim3(static_cast<unsigned>(BH)), dim3(kScanTh), lds + sizeof(int), stream, sp);
-    r2 = launched("sample backward scan");
+    {  // the scan and the location and weight gradients in one launch
+        constexpr int V = 16 / static_cast<int>(sizeof(T));
+        const unsigned lblocks = lp.blocks > 0 ? static_cast<unsigned>(lp.per_xcd * kXcds) : 0u;
+        hipLaunchKernelGGL((scan_loc_attn_kernel<T, V, 8>), dim3(static_cast<unsigned>(BH) + lblocks), dim3(256), 0,
+                           stream, sp, lp);
+    }
+    r2 = launched("sample backward scan and locations");
     if (r2 != 0) return r2;
     hipLaunchKernelGGL(sort_fill_kernel<T>, dim3(tiles), dim3(256), lds, stream, sp);
     r2 = launched("sample backward fill");
