@@ -1592,17 +1592,19 @@ constexpr size_t wgrad_slice_bytes() {
     return sizeof(T) * kWgTile * (KBlock<T>::kK + 16 / sizeof(T));
 }
 
-// Workgroup `bid` of the weight gradient's grid (tile and split), with gs and xs its two LDS slices.
-template <typename T, bool VEC>
+// Workgroup `bid` of the weight gradient's grid (tile and split), with gs and xs its two LDS slices. TW = 2 widens
+// the tile to 128 (n) x 256 (c), wavefronts of 64 x 128 (32 MFMAs per token step): three quarters of the staged
+// bytes, LDS reads and barriers per MFMA of the 128 x 128 tile. xs then holds 256 rows.
+template <typename T, bool VEC, int TW = 1>
 __device__ __forceinline__ void wgrad_tile(const WgradParams& p, int bid, T* __restrict__ gs, T* __restrict__ xs) {
     constexpr int E = 16 / static_cast<int>(sizeof(T));  // elements per 16 bytes
     constexpr int KB = KBlock<T>::kK;                     // tokens per MFMA step
     constexpr int LD = KB + E;                            // LDS pitch (elements) of a staged transposed row
-    constexpr int TL = kWgTile, PIECES = KB * (TL / E) / 256;
+    constexpr int TL = kWgTile, TC = TW * kWgTile, PIECES = KB * (TL / E) / 256;
     static_assert(PIECES == 2, "two pieces per thread");
     const int tiles = p.nt * p.ct;
     const int s = bid / tiles, tile = bid - s * tiles;
-    const int n0 = (tile / p.ct) * TL, c0 = (tile % p.ct) * TL;
+    const int n0 = (tile / p.ct) * TL, c0 = (tile % p.ct) * TC;
     const int m_begin = s * p.chunk, m_end = min(p.M, m_begin + p.chunk);
     const T* __restrict__ G = static_cast<const T*>(p.G);
     const T* __restrict__ X = static_cast<const T*>(p.X);
@@ -1611,18 +1613,19 @@ __device__ __forceinline__ void wgrad_tile(const WgradParams& p, int bid, T* __r
     // this thread's pieces: token rows mm[0] = 2 rp and mm[1] = 2 rp + 1, columns cc[u] = cb .. cb + E - 1; the KB / 2
     // token pairs run across consecutive lanes, so that a transposed store instruction (rows cb + e, 2 rp) spreads
     // over the LDS banks (2-way at most), where 16 column groups of one pair would meet in one or two banks
+    // (X's TW column blocks of 128 are staged by the same threads, block w at columns cb + 128 w)
     const int rp = tid % (KB / 2), cb = (tid / (KB / 2)) * E;
     const int mm[PIECES] = {2 * rp, 2 * rp + 1};
     const int cc[PIECES] = {cb, cb};
-    f32x4 acc[4][4];
+    f32x4 acc[4][4 * TW];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < 4 * TW; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     float bsum = 0.f;  // thread tid < 128: column n0 + tid of G (c tile 0)
     const bool do_b = c0 == 0;
 
-    T pg[PIECES][E], px[PIECES][E];
+    T pg[PIECES][E], px[TW][PIECES][E];
     auto load = [&](int m0) {
 #pragma unroll
         for (int u = 0; u < PIECES; ++u) {
@@ -1632,22 +1635,29 @@ __device__ __forceinline__ void wgrad_tile(const WgradParams& p, int bid, T* __r
                 const u32x4 vg = (m < m_end && n0 + cc[u] < p.NO)
                                      ? *reinterpret_cast<const u32x4*>(G + static_cast<int64_t>(m) * p.NO + n0 + cc[u])
                                      : zero;
-                const u32x4 vx = (m < m_end && c0 + cc[u] < p.K)
-                                     ? *reinterpret_cast<const u32x4*>(X + static_cast<int64_t>(m) * p.K + c0 + cc[u])
-                                     : zero;
                 const T* eg = reinterpret_cast<const T*>(&vg);
-                const T* ex = reinterpret_cast<const T*>(&vx);
 #pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    pg[u][e] = eg[e];
-                    px[u][e] = ex[e];
+                for (int e = 0; e < E; ++e) pg[u][e] = eg[e];
+#pragma unroll
+                for (int w = 0; w < TW; ++w) {
+                    const int c = c0 + w * kWgTile + cc[u];
+                    const u32x4 vx =
+                        (m < m_end && c < p.K) ? *reinterpret_cast<const u32x4*>(X + static_cast<int64_t>(m) * p.K + c)
+                                               : zero;
+                    const T* ex = reinterpret_cast<const T*>(&vx);
+#pragma unroll
+                    for (int e = 0; e < E; ++e) px[w][u][e] = ex[e];
                 }
             } else {
 #pragma unroll
                 for (int e = 0; e < E; ++e) {
-                    const int n = n0 + cc[u] + e, c = c0 + cc[u] + e;
+                    const int n = n0 + cc[u] + e;
                     pg[u][e] = (m < m_end && n < p.NO) ? G[static_cast<int64_t>(m) * p.NO + n] : T(0);
-                    px[u][e] = (m < m_end && c < p.K) ? X[static_cast<int64_t>(m) * p.K + c] : T(0);
+#pragma unroll
+                    for (int w = 0; w < TW; ++w) {
+                        const int c = c0 + w * kWgTile + cc[u] + e;
+                        px[w][u][e] = (m < m_end && c < p.K) ? X[static_cast<int64_t>(m) * p.K + c] : T(0);
+                    }
                 }
             }
         }
@@ -1656,39 +1666,43 @@ __device__ __forceinline__ void wgrad_tile(const WgradParams& p, int bid, T* __r
     for (int m0 = m_begin; m0 < m_end; m0 += KB) {
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            Pair<T> g2, x2;
+            Pair<T> g2;
             g2.v[0] = pg[0][e];
             g2.v[1] = pg[1][e];
-            x2.v[0] = px[0][e];
-            x2.v[1] = px[1][e];
             *reinterpret_cast<Pair<T>*>(gs + (cb + e) * LD + 2 * rp) = g2;
-            *reinterpret_cast<Pair<T>*>(xs + (cb + e) * LD + 2 * rp) = x2;
+#pragma unroll
+            for (int w = 0; w < TW; ++w) {
+                Pair<T> x2;
+                x2.v[0] = px[w][0][e];
+                x2.v[1] = px[w][1][e];
+                *reinterpret_cast<Pair<T>*>(xs + (w * kWgTile + cb + e) * LD + 2 * rp) = x2;
+            }
         }
         __syncthreads();
         if (m0 + KB < m_end) load(m0 + KB);  // in flight during this step's MFMAs
         if (do_b && tid < TL) {
             for (int k = 0; k < KB; ++k) bsum += static_cast<float>(gs[tid * LD + k]);
         }
-        u32x4 fa[4], fb[4];
+        u32x4 fa[4], fb[4 * TW];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             fa[i] = *reinterpret_cast<const u32x4*>(gs + (wm * 64 + i * 16 + r16) * LD + kg * E);
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-            fb[t] = *reinterpret_cast<const u32x4*>(xs + (wn * 64 + t * 16 + r16) * LD + kg * E);
+        for (int t = 0; t < 4 * TW; ++t)
+            fb[t] = *reinterpret_cast<const u32x4*>(xs + (wn * 64 * TW + t * 16 + r16) * LD + kg * E);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc[i][t] = KBlock<T>::mma(fa[i], fb[t], acc[i][t]);
+            for (int t = 0; t < 4 * TW; ++t) acc[i][t] = KBlock<T>::mma(fa[i], fb[t], acc[i][t]);
         __syncthreads();
     }
-    // acc[i][t][e]: row n0 + wm*64 + i*16 + kg*4 + e, column c0 + wn*64 + t*16 + r16
+    // acc[i][t][e]: row n0 + wm*64 + i*16 + kg*4 + e, column c0 + wn*64*TW + t*16 + r16
     float* part = p.part + static_cast<int64_t>(s) * p.NO * p.K;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int c = c0 + wn * 64 + t * 16 + r16;
+        for (int t = 0; t < 4 * TW; ++t) {
+            const int c = c0 + wn * 64 * TW + t * 16 + r16;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int n = n0 + wm * 64 + i * 16 + kg * 4 + e;
@@ -1698,10 +1712,11 @@ __device__ __forceinline__ void wgrad_tile(const WgradParams& p, int bid, T* __r
     if (do_b && tid < TL && n0 + tid < p.NO) p.bpart[static_cast<int64_t>(s) * p.NO + n0 + tid] = bsum;
 }
 
-template <typename T, bool VEC>
+template <typename T, bool VEC, int TW = 1>
 __global__ __launch_bounds__(256) void wgrad_kernel(WgradParams p) {
-    __shared__ __align__(16) unsigned char lds[2 * wgrad_slice_bytes<T>()];
-    wgrad_tile<T, VEC>(p, blockIdx.x, reinterpret_cast<T*>(lds), reinterpret_cast<T*>(lds + wgrad_slice_bytes<T>()));
+    __shared__ __align__(16) unsigned char lds[(1 + TW) * wgrad_slice_bytes<T>()];
+    wgrad_tile<T, VEC, TW>(p, blockIdx.x, reinterpret_cast<T*>(lds),
+                           reinterpret_cast<T*>(lds + wgrad_slice_bytes<T>()));
 }
 
 // The input gradient's GEMM (grad_memory = G . W, on the 64 x 64 two-stage tiles the value projection's size rule
@@ -2146,12 +2161,19 @@ int launch_input_weight_grad(int dtype, const void* G, const void* W, void* Wt, 
     return launch_wgrad(dtype, G, X, gw, gb, M, HD, C, workspace, ws_bytes, stream);
 }
 
-// Split count and workspace of the weight gradient: about 512 workgroups (1024 for large outputs), at least four
-// token steps per split (64 tokens in float32, 128 otherwise). Measured on the training step at 8400 tokens
-// (256 x 256), against 256 tokens per split: float32 117.0 -> 99.0 us with 64-token splits (105.8 with 128), 16-bit
-// 63.3 -> 62.7 with 128 (63.4 with 64); problems of 32768 tokens and more already had their 512 workgroups.
-void wgrad_plan(int64_t M, int64_t NO, int64_t K, int dtype, int* splits, int* chunk, int64_t* ws_bytes) {
-    const int64_t tiles = ((NO + kWgTile - 1) / kWgTile) * ((K + kWgTile - 1) / kWgTile);
+// Column tiles of 256 (TW = 2) for the weight gradient's own launch from this many input channels on: training
+// step at C = 1024 bf16 B2 Q300 544.1 -> 494.1 us; from 256 channels on, DINO B4 Q900 168.7 -> 176.1 and RT-DETR bf16
+// B8 124.6 -> 129.0 (half the tiles, so twice the splits and partials)
+constexpr int64_t kWgWideMinK = 512;
+
+int wgrad_width(int64_t K, int dtype) { return dtype != kF64 && K >= kWgWideMinK ? 2 : 1; }
+
+// Split count of the weight gradient: about 512 workgroups (1024 for large outputs), at least four token steps per
+// split (64 tokens in float32, 128 otherwise). Measured on the training step at 8400 tokens (256 x 256), against 256
+// tokens per split: float32 117.0 -> 99.0 us with 64-token splits (105.8 with 128), 16-bit 63.3 -> 62.7 with 128
+// (63.4 with 64); problems of 32768 tokens and more already had their 512 workgroups.
+static void wgrad_split(int64_t M, int64_t NO, int64_t K, int dtype, int tw, int* splits, int* chunk) {
+    const int64_t tiles = ((NO + kWgTile - 1) / kWgTile) * ((K + tw * kWgTile - 1) / (tw * kWgTile));
     const int kb = dtype == kF32 ? 16 : 32;
     // 1024 workgroups from 64 output tiles (C = 1024): training step at C = 1024 bf16 B2 Q300 913.0 -> 895.2 us; at
     // 4 tiles (C = 256) 1024 lost 1.5-5% (DINO B4 Q900, bf16 B8 Q300, the DINO encoder: more partials to reduce)
@@ -2166,8 +2188,19 @@ void wgrad_plan(int64_t M, int64_t NO, int64_t K, int dtype, int* splits, int* c
     if (s < 1) s = 1;
     *splits = static_cast<int>(s);
     *chunk = static_cast<int>(c > 0 ? c : kb);
+}
+
+// Splits, tokens per split and workspace of the weight gradient's own launch; the workspace also covers the 128-wide
+// tiles of the launch combined with the input gradient's GEMM.
+void wgrad_plan(int64_t M, int64_t NO, int64_t K, int dtype, int* splits, int* chunk, int64_t* ws_bytes) {
+    int s1 = 1, c1 = 32;
+    wgrad_split(M, NO, K, dtype, 1, &s1, &c1);
+    const int tw = wgrad_width(K, dtype);
+    *splits = s1;
+    *chunk = c1;
+    if (tw != 1) wgrad_split(M, NO, K, dtype, tw, splits, chunk);
     const int64_t elem = dtype == kF64 ? 8 : 4;
-    *ws_bytes = s * (NO * K + NO) * elem;
+    *ws_bytes = (s1 > *splits ? s1 : *splits) * (NO * K + NO) * elem;
 }
 
 int launch_wgrad(int dtype, const void* G, const void* X, void* gw, void* gb, int64_t M, int64_t NO, int64_t K,
@@ -2179,9 +2212,11 @@ int launch_wgrad(int dtype, const void* G, const void* X, void* gw, void* gb, in
         return set_error(-4, "weight gradient: workspace of %lld bytes needed, %lld given", static_cast<long long>(need),
                          static_cast<long long>(ws_bytes));
     if (NO * K == 0) return 0;
+    const int tw = with_gemm != nullptr ? 1 : wgrad_width(K, dtype);
+    if (tw != wgrad_width(K, dtype)) wgrad_split(M, NO, K, dtype, tw, &splits, &chunk);
     WgradParams p{G, X, nullptr, nullptr, static_cast<int>(M), static_cast<int>(NO), static_cast<int>(K),
-                  static_cast<int>((NO + kWgTile - 1) / kWgTile), static_cast<int>((K + kWgTile - 1) / kWgTile), splits,
-                  chunk};
+                  static_cast<int>((NO + kWgTile - 1) / kWgTile),
+                  static_cast<int>((K + tw * kWgTile - 1) / (tw * kWgTile)), splits, chunk};
     const int64_t n_out = NO * K;
     const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(p.nt) * p.ct * splits));
     const dim3 rgrid(static_cast<unsigned>((n_out + 63) / 64));
@@ -2261,13 +2296,17 @@ int launch_wgrad(int dtype, const void* G, const void* X, void* gw, void* gb, in
             default: return set_error(-2, "unknown dtype code %d", dtype);
         }
     } else {
-        switch (dtype * 2 + (vec ? 1 : 0)) {
-            case kF32 * 2: hipLaunchKernelGGL((wgrad_kernel<float, false>), grid, dim3(256), 0, stream, p); break;
-            case kF32 * 2 + 1: hipLaunchKernelGGL((wgrad_kernel<float, true>), grid, dim3(256), 0, stream, p); break;
-            case kF16 * 2: hipLaunchKernelGGL((wgrad_kernel<f16, false>), grid, dim3(256), 0, stream, p); break;
-            case kF16 * 2 + 1: hipLaunchKernelGGL((wgrad_kernel<f16, true>), grid, dim3(256), 0, stream, p); break;
-            case kBF16 * 2: hipLaunchKernelGGL((wgrad_kernel<bf16, false>), grid, dim3(256), 0, stream, p); break;
-            case kBF16 * 2 + 1: hipLaunchKernelGGL((wgrad_kernel<bf16, true>), grid, dim3(256), 0, stream, p); break;
+        switch ((dtype * 2 + (vec ? 1 : 0)) * 2 + (tw == 2 ? 1 : 0)) {
+#define TD_WG(code, T, V)                                                                                     \
+    case (code * 2 + V) * 2: hipLaunchKernelGGL((wgrad_kernel<T, V, 1>), grid, dim3(256), 0, stream, p); break; \
+    case (code * 2 + V) * 2 + 1: hipLaunchKernelGGL((wgrad_kernel<T, V, 2>), grid, dim3(256), 0, stream, p); break;
+            TD_WG(kF32, float, false)
+            TD_WG(kF32, float, true)
+            TD_WG(kF16, f16, false)
+            TD_WG(kF16, f16, true)
+            TD_WG(kBF16, bf16, false)
+            TD_WG(kBF16, bf16, true)
+#undef TD_WG
             default: return set_error(-2, "unknown dtype code %d", dtype);
         }
     }
