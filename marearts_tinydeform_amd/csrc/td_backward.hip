@@ -1712,11 +1712,15 @@ __device__ __forceinline__ void wgrad_tile(const WgradParams& p, int bid, T* __r
     if (do_b && tid < TL && n0 + tid < p.NO) p.bpart[static_cast<int64_t>(s) * p.NO + n0 + tid] = bsum;
 }
 
+// Workgroups go to the XCDs round-robin (blockIdx.x % kXcds); the grid is kXcds * per_xcd workgroups, and XCD x takes
+// the contiguous range [x * per_xcd, (x + 1) * per_xcd) of the (split, tile) order, so that the tiles of one split,
+// which read the same token rows, share one XCD's L2 instead of pulling the rows into several.
 template <typename T, bool VEC, int TW = 1>
-__global__ __launch_bounds__(256) void wgrad_kernel(WgradParams p) {
+__global__ __launch_bounds__(256) void wgrad_kernel(WgradParams p, int per_xcd) {
     __shared__ __align__(16) unsigned char lds[(1 + TW) * wgrad_slice_bytes<T>()];
-    wgrad_tile<T, VEC, TW>(p, blockIdx.x, reinterpret_cast<T*>(lds),
-                           reinterpret_cast<T*>(lds + wgrad_slice_bytes<T>()));
+    const int idx = static_cast<int>(blockIdx.x % kXcds) * per_xcd + static_cast<int>(blockIdx.x / kXcds);
+    if (idx >= p.nt * p.ct * p.splits) return;  // the last XCD's spare workgroups
+    wgrad_tile<T, VEC, TW>(p, idx, reinterpret_cast<T*>(lds), reinterpret_cast<T*>(lds + wgrad_slice_bytes<T>()));
 }
 
 // The input gradient's GEMM (grad_memory = G . W, on the 64 x 64 two-stage tiles the value projection's size rule
@@ -2296,10 +2300,16 @@ int launch_wgrad(int dtype, const void* G, const void* X, void* gw, void* gb, in
             default: return set_error(-2, "unknown dtype code %d", dtype);
         }
     } else {
+        const int per_xcd = static_cast<int>((static_cast<int64_t>(grid.x) + kXcds - 1) / kXcds);
+        const dim3 xgrid(static_cast<unsigned>(per_xcd * kXcds));
         switch ((dtype * 2 + (vec ? 1 : 0)) * 2 + (tw == 2 ? 1 : 0)) {
-#define TD_WG(code, T, V)                                                                                     \
-    case (code * 2 + V) * 2: hipLaunchKernelGGL((wgrad_kernel<T, V, 1>), grid, dim3(256), 0, stream, p); break; \
-    case (code * 2 + V) * 2 + 1: hipLaunchKernelGGL((wgrad_kernel<T, V, 2>), grid, dim3(256), 0, stream, p); break;
+#define TD_WG(code, T, V)                                                                                          \
+    case (code * 2 + V) * 2:                                                                                       \
+        hipLaunchKernelGGL((wgrad_kernel<T, V, 1>), xgrid, dim3(256), 0, stream, p, per_xcd);                      \
+        break;                                                                                                     \
+    case (code * 2 + V) * 2 + 1:                                                                                   \
+        hipLaunchKernelGGL((wgrad_kernel<T, V, 2>), xgrid, dim3(256), 0, stream, p, per_xcd);                      \
+        break;
             TD_WG(kF32, float, false)
             TD_WG(kF32, float, true)
             TD_WG(kF16, f16, false)
