@@ -135,9 +135,11 @@ def test_projection_gradients_alone(dtype):
     g = torch.Generator().manual_seed(8)
     # (the last shape has C and H * D off the 16-byte vector width: scalar staging in the weight gradient; 1024 x 1024
     # is 64 output tiles, planned for 1024 workgroups; from C = 512 on the weight gradient's column tiles are 256 wide,
-    # and C = 520 and 516 leave the last one 8 and 4 columns, with 16-byte and scalar staging)
+    # and C = 520 and 516 leave the last one 8 and 4 columns, with 16-byte and scalar staging; 520 x 520 and 516 x 516
+    # are ragged in both the row and the column tiles)
     for (B, N, C, HD) in ((1, 8400, 256, 256), (2, 77, 40, 48), (1, 1000, 1024, 96), (3, 5, 8, 16), (1, 50, 36, 30),
-                          (1, 3000, 1024, 1024), (1, 700, 520, 64), (1, 300, 516, 40)):
+                          (1, 3000, 1024, 1024), (1, 700, 520, 64), (1, 300, 516, 40), (1, 400, 520, 520),
+                          (1, 300, 516, 516)):
         gv = torch.randn(B, N, HD, generator=g).to(dtype)
         mem = torch.randn(B, N, C, generator=g).to(dtype)
         w = (torch.randn(HD, C, generator=g) / C ** 0.5).to(dtype)
