@@ -2183,7 +2183,11 @@ static void wgrad_split(int64_t M, int64_t NO, int64_t K, int dtype, int tw, int
     // 4 tiles (C = 256) 1024 lost 1.5-5% (DINO B4 Q900, bf16 B8 Q300, the DINO encoder: more partials to reduce)
     const int64_t target = tiles >= 64 ? 1024 : 512;
     int64_t s = (target + tiles - 1) / tiles;
-    const int64_t max_s = (M + 4 * kb - 1) / (4 * kb);
+    // at least four token steps per split; in 16 bits below 16384 tokens (where the input gradient's GEMM shares the
+    // launch) eight: training step at RT-DETR B1 fp16 Q300 55.6 -> 55.1 us, Q100 48.7 -> 48.2 (half the partials to
+    // reduce); float32 lost with eight (95.2 -> 97.4)
+    const int64_t min_tok = kb * ((dtype == kF16 || dtype == kBF16) && M < 16384 ? 8 : 4);
+    const int64_t max_s = (M + min_tok - 1) / min_tok;
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;
     int64_t c = (M + s - 1) / s;
