@@ -234,17 +234,22 @@ def test_probe_argument_errors(lib):
 
 
 @pytest.mark.parametrize('dtype,M,NO,K', [(1, 8400, 256, 256), (2, 43520, 1024, 1024), (0, 100, 48, 40),
-                                          (3, 5, 16, 8), (1, 0, 64, 64)])
+                                          (3, 5, 16, 8), (1, 0, 64, 64), (0, 8400, 256, 256), (2, 20000, 256, 256),
+                                          (1, 3000, 520, 600)])
 def test_weight_grad_workspace_plan(lib, dtype, M, NO, K):
-    # split-K plan: about 512 workgroups of 128 x 128 outputs (1024 from 64 tiles), splits of at least four MFMA K
-    # steps (64 tokens for float32, 128 otherwise) rounded up to the MFMA K (16 tokens for float32, 32 otherwise),
-    # float32 partials (float64 for float64) plus bias partials
-    tiles = -(-NO // 128) * -(-K // 128)
-    kb = 16 if dtype == 0 else 32
-    target = 1024 if tiles >= 64 else 512  # 1024 workgroups for 64 output tiles and more
-    s = max(1, min(-(-target // tiles), -(-M // (4 * kb))))
-    chunk = -(-M // s) if M else 0
-    chunk = -(-chunk // kb) * kb
-    s = -(-M // chunk) if chunk else 1
+    # split-K plan: about 512 workgroups of 128 x 128 outputs (128 x 256 from K = 512 on, except float64; 1024
+    # workgroups from 64 tiles), splits of at least four MFMA K steps (eight in 16 bits below 16384 tokens; 16 tokens
+    # for float32, 32 otherwise) rounded up to the MFMA K, float32 partials (float64 for float64) plus bias partials;
+    # the workspace covers the 128 x 128 plan as well (the launch combined with the input gradient)
+    def splits(tw):
+        tiles = -(-NO // 128) * -(-K // (128 * tw))
+        kb = 16 if dtype == 0 else 32
+        target = 1024 if tiles >= 64 else 512  # 1024 workgroups for 64 output tiles and more
+        steps = 8 if dtype in (1, 2) and M < 16384 else 4
+        s = max(1, min(-(-target // tiles), -(-M // (steps * kb))))
+        chunk = -(-M // s) if M else 0
+        chunk = -(-chunk // kb) * kb
+        return -(-M // chunk) if chunk else 1
+    s = max(splits(1), splits(2 if dtype != 3 and K >= 512 else 1))
     elem = 8 if dtype == 3 else 4
     assert lib.td_weight_grad_workspace(dtype, M, NO, K) == s * (NO * K + NO) * elem
